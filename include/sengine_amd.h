@@ -1,0 +1,172 @@
+/*
+ * sengine_amd.h — C ABI of the MI355X (gfx950) fused 2:4-sparse Conv+BN+LIF operator.
+ *
+ * Every entry point takes plain device pointers, plain integers and a HIP stream,
+ * never allocates device memory, never synchronises, and returns 0 on success.
+ * A negative return is an argument error detected on the host (nothing was
+ * launched; sengine_amd_last_error() describes it); a positive return is the
+ * hipError_t reported by the launch.  All launches are safe under stream capture.
+ *
+ * Reference interfaces replaced (paths relative to the SparseSNN repository):
+ *   - the per-node kernel ABI `int init(void)` / `int call(ptrs..., stream)`
+ *     exported by sengine/build/export_standalone.py:1-8,37-103 and dlopen'd by
+ *     sengine/csrc/cpp_executor.cu:631-662, called with six pointers
+ *     (data, weight, state, bn_scale, bn_bias, spikes) at cpp_executor.cu:909-913;
+ *   - the fused operator conv2d_bn_if_interleaved_kernel
+ *     (sengine/kernels/conv2d_bn_if_t4.py:918-1022) and conv1x1_bn_lif / conv1x1_bn_if
+ *     (sengine/kernels/interleaved_templates.py:28-154), i.e. the node variants
+ *     KernelVariant.FusedSparseConvBNLIF / TileLangFusedConvBNIF /
+ *     TileLangFusedConv1x1BNIF (sengine/ir.py:53,78-79);
+ *   - the unfused fallback conv2d_bn_t4_kernel / conv1x1_bn_t4_kernel
+ *     (sengine/kernels/conv2d_bn_if_t4.py:551-673) followed by lif_neuron_kernel /
+ *     if_neuron_kernel (sengine/csrc/kernels.cuh:18-54).
+ *
+ * Data layouts (all NHWC, rows ordered t-major then b, oh, ow — the order of
+ * models/layers.py:26-31 SeqToANNContainer and of the reference kernels):
+ *   spike bits : uint32 words, position p = ((t*B + b)*H + h)*W + w holds C/32 words;
+ *                channel c is bit (c % 32) of word c/32.
+ *   fp16 dense : _Float16 [(t*B + b)*H + h][w][c]  (the reference's io dtype).
+ *   membrane   : float [B*OH*OW][C_out]  (cuda_graph_runtime.py:385-390).
+ *   BN         : folded per-channel scale / bias, fp32 (sengine/optimizer.py:159-183).
+ *   weights    : an opaque "sparse blob" produced by sengine_amd_compress_2_4
+ *                (2:4 values in SMFMAC operand order + 2-bit position metadata),
+ *                or a "dense blob" from sengine_amd_pack_dense_weights.
+ */
+#ifndef SENGINE_AMD_H
+#define SENGINE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Activation / spike encodings. */
+enum {
+  SENGINE_ENC_BITS = 0, /* 1 bit per value, value = bit (binary spikes) */
+  SENGINE_ENC_F16 = 1,  /* fp16 NHWC (any fp16 value on input; 0.0 / 1.0 on output) */
+  SENGINE_ENC_F32 = 2   /* fp32 NHWC (pack/unpack and weights only) */
+};
+
+/* Neuron models (sengine/ir.py:44-48 NeuronType, models/neurons.py). */
+enum { SENGINE_NEURON_LIF = 0, SENGINE_NEURON_IF = 1 };
+
+/* Weight tensor layouts accepted by the compressors. */
+enum {
+  SENGINE_WLAYOUT_OIHW = 0, /* torch nn.Conv2d weight (C_out, C_in, KH, KW) */
+  SENGINE_WLAYOUT_HWIO = 1  /* reference runtime layout (KH, KW, C_in, C_out), cuda_graph_runtime.py:233-235 */
+};
+
+/*
+ * Shape + neuron descriptor of one Conv+BN+LIF node.  Mirrors ConvParams +
+ * NeuronParams (sengine/ir.py:179-201) plus the batch/time extents the
+ * reference bakes into each compiled kernel (tilelang_compiler.py:551-553).
+ */
+typedef struct sengine_conv_lif_desc {
+  int32_t T, B;                 /* timesteps, batch */
+  int32_t C_in, H, W, C_out;    /* input channels/spatial, output channels */
+  int32_t KH, KW;               /* kernel */
+  int32_t stride_h, stride_w;
+  int32_t pad_h, pad_w;
+  int32_t dil_h, dil_w;
+  int32_t neuron;               /* SENGINE_NEURON_LIF / SENGINE_NEURON_IF */
+  int32_t hard_reset;           /* 1: v <- v_reset after a spike; 0: v <- v - v_threshold */
+  float tau, v_threshold, v_reset;
+  int32_t in_enc;               /* SENGINE_ENC_BITS or SENGINE_ENC_F16 */
+  int32_t out_enc;              /* SENGINE_ENC_BITS or SENGINE_ENC_F16 */
+  int32_t weight_planes;        /* 1: fp16 weights; 2: fp16 hi + fp16 lo (fp32-faithful) */
+} sengine_conv_lif_desc;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int sengine_amd_version(void);
+
+/* Human-readable description of the last negative return on this thread. */
+const char* sengine_amd_last_error(void);
+
+/* Output spatial size, M = B*OH*OW rows per timestep and K_red = KH*KW*C_in. */
+int sengine_amd_conv_geometry(const sengine_conv_lif_desc* d, int32_t* OH, int32_t* OW,
+                              int64_t* M_per_t, int64_t* K_red);
+
+/*
+ * Byte sizes of the weight blobs for a descriptor (sparse: values + metadata;
+ * dense: values).  The fused kernel reads the sparse blob; the fallback the dense one.
+ */
+int sengine_amd_sparse_blob_bytes(const sengine_conv_lif_desc* d, size_t* value_bytes, size_t* meta_bytes);
+int sengine_amd_dense_blob_bytes(const sengine_conv_lif_desc* d, size_t* value_bytes);
+
+/*
+ * 2:4 weight compressor (new in this build; the reference only validates 2:4,
+ * sengine/optimizer.py:499-553, and leaves compression to TensorRT).
+ * weight: fp32 (w_enc = SENGINE_ENC_F32) or fp16 (SENGINE_ENC_F16) in layout w_layout.
+ * Each group of 4 consecutive input channels at one (c_out, kh, kw) must hold at most
+ * two entries with |w| >= 1e-10 (the zero test of validate_2_4_pattern); entries below
+ * that are dropped.  violations (device, optional): receives, per 4-group, 1 if the
+ * group had more than two such entries (the group is then truncated to its first two).
+ * The blob is laid out for the descriptor's C_out/C_in/KH/KW and weight_planes only.
+ */
+int sengine_amd_compress_2_4(const sengine_conv_lif_desc* d, const void* weight, int32_t w_enc,
+                             int32_t w_layout, void* blob_values, void* blob_meta,
+                             int32_t* violations, hipStream_t stream);
+
+/* Number of 4-groups the compressor checks (= C_out*KH*KW*C_in/4): size of `violations`. */
+int64_t sengine_amd_num_groups(const sengine_conv_lif_desc* d);
+
+/* Dense weight packer for the unfused fallback (any weights). */
+int sengine_amd_pack_dense_weights(const sengine_conv_lif_desc* d, const void* weight, int32_t w_enc,
+                                   int32_t w_layout, void* blob_values, hipStream_t stream);
+
+/*
+ * Fused 2:4-sparse Conv + folded BN + multi-step LIF/IF over T (one launch).
+ * Replaces conv2d_bn_if_interleaved_kernel / conv1x1_bn_lif (see above).
+ *   data     : input activations, encoding d->in_enc, (T*B, H, W, C_in)
+ *   blob_*   : from sengine_amd_compress_2_4
+ *   state    : optional (may be NULL => V0 = 0, not written back) fp32 (B*OH*OW, C_out);
+ *              read as the initial membrane and overwritten with the final one.
+ *   bn_scale, bn_bias : fp32 (C_out)
+ *   spikes   : output, encoding d->out_enc, (T*B, OH, OW, C_out)
+ *   h_trace  : optional fp32 (T, B*OH*OW, C_out): charged membrane at each t (pre-reset)
+ *   x_trace  : optional fp32 (T, B*OH*OW, C_out): BN output (LIF input current)
+ * Requires C_in % 64 == 0, C_out % 64 == 0, T in {1,2,4,8}.
+ */
+int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const void* data,
+                                         const void* blob_values, const void* blob_meta,
+                                         float* state, const float* bn_scale, const float* bn_bias,
+                                         void* spikes, float* h_trace, float* x_trace,
+                                         hipStream_t stream);
+
+/*
+ * Unfused fallback, half 1: dense Conv + folded BN, fp32 output (T*B*OH*OW, C_out).
+ * Mirrors conv2d_bn_t4_kernel / conv1x1_bn_t4_kernel (conv2d_bn_if_t4.py:551-673), but
+ * keeps the BN output in fp32 (the reference rounds it to fp16).
+ * Requires C_in % 32 == 0, C_out % 64 == 0.
+ */
+int sengine_amd_dense_conv_bn(const sengine_conv_lif_desc* d, const void* data, const void* blob_values,
+                              const float* bn_scale, const float* bn_bias, float* out,
+                              hipStream_t stream);
+
+/*
+ * Unfused fallback, half 2: standalone multi-step neuron over T.
+ * x: fp32 (T, n) with n = spatial elements per timestep; state: optional fp32 (n).
+ * spikes: encoding out_enc (bits need n % 32 == 0), h_trace optional fp32 (T, n).
+ * Mirrors lif_neuron_kernel / if_neuron_kernel (sengine/csrc/kernels.cuh:18-54) with the
+ * reset and leak of models/neurons.py:121-146,169-184.
+ */
+int sengine_amd_multistep_neuron(int32_t T, int64_t n, int32_t neuron, int32_t hard_reset, float tau,
+                                 float v_threshold, float v_reset, const float* x, float* state,
+                                 int32_t out_enc, void* spikes, float* h_trace, hipStream_t stream);
+
+/* Pack a dense NHWC tensor (n_pos, C) into spike bits (value != 0 -> 1); C % 32 == 0. */
+int sengine_amd_pack_spikes(const void* x, int32_t x_enc, int64_t n_pos, int32_t C, uint32_t* bits,
+                            hipStream_t stream);
+
+/* Unpack spike bits (n_pos, C) into fp16 / fp32 0.0 / 1.0; C % 32 == 0. */
+int sengine_amd_unpack_spikes(const uint32_t* bits, int64_t n_pos, int32_t C, void* out, int32_t out_enc,
+                              hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SENGINE_AMD_H */

@@ -1,0 +1,96 @@
+// Shared device helpers for the gfx950 kernels of sengine_amd.
+//
+// Operand layouts of the CDNA4 matrix instructions used here (measured on the
+// MI355X with a known-answer probe, not taken from any document):
+//   v_smfmac_f32_16x16x64_f16  D(16x16) += A(16x64, 2:4 sparse along k) * B(64x16)
+//     A lane l : row l%16, 8 compressed fp16 values j=0..7; value j sits in 4-group
+//                j/2 of k-range [16*(l/16), 16*(l/16)+16) at position idx[2j+1:2j]
+//                (idx = 16-bit metadata selected by ABID).
+//     B lane l : column l%16, 16 fp16 values; value j<8 is k = 8*(l/16)+j,
+//                value j>=8 is k = 32 + 8*(l/16) + (j-8).
+//     D lane l : value i is row 4*(l/16)+i, column l%16.
+//   v_mfma_f32_16x16x32_f16    (dense)
+//     A lane l : row l%16, k = 8*(l/16)+j;  B lane l: k = 8*(l/16)+j, column l%16.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sengine_amd.h"
+
+namespace sengine {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half16_t __attribute__((ext_vector_type(16)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
+
+// Spike value fed to the matrix cores for a set bit: fp16 2.0 (0x4000) is a single
+// set bit, so expansion is one shift + one mask per register.  The factor 2 is exact
+// and folded into the epilogue scale.
+constexpr float kBitSpikeValue = 2.0f;
+
+// Spread 16 spike bits x (bit j -> B value j) into a 16-value fp16 B fragment.
+// X = x | x<<15 holds bit j at position j and at 15+j; shifting left by 14-2j moves
+// bit 2j to 14 and bit 2j+1 (upper copy) to 30, the exponent MSB of each half.
+__device__ __forceinline__ half16_t expand_bits16(uint32_t x) {
+  const uint32_t X = x | (x << 15);
+  u32x8_t r;
+  r[0] = (X << 14) & 0x40004000u;
+  r[1] = (X << 12) & 0x40004000u;
+  r[2] = (X << 10) & 0x40004000u;
+  r[3] = (X << 8) & 0x40004000u;
+  r[4] = (X << 6) & 0x40004000u;
+  r[5] = (X << 4) & 0x40004000u;
+  r[6] = (X << 2) & 0x40004000u;
+  r[7] = X & 0x40004000u;
+  return __builtin_bit_cast(half16_t, r);
+}
+
+// Same for 8 bits -> 8 fp16 values (dense 16x16x32 B fragment).
+__device__ __forceinline__ half8_t expand_bits8(uint32_t x) {
+  const uint32_t X = x | (x << 15);
+  u32x4_t r;
+  r[0] = (X << 14) & 0x40004000u;
+  r[1] = (X << 12) & 0x40004000u;
+  r[2] = (X << 10) & 0x40004000u;
+  r[3] = (X << 8) & 0x40004000u;
+  return __builtin_bit_cast(half8_t, r);
+}
+
+__device__ __forceinline__ half16_t concat8(half8_t lo, half8_t hi) {
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+}
+
+// Neuron parameters as the kernels consume them.  The recurrences follow
+// models/neurons.py:121-146 (LIF) and :169-184 (IF) operation by operation:
+//   LIF: v = v*(1 - 1/tau) + x/tau ; IF: v = v + x
+//   spike = (v - v_th) >= 0  (== v >= v_th for finite IEEE values)
+//   hard reset: v = spike ? v_reset : v ; soft reset: v = spike ? v - v_th : v
+// When 1/tau is a power of two (tau = 2 in every reference config) the division and
+// the decay product are exact, so x/tau is folded into the BN scale/bias and the
+// charge becomes one fused multiply-add with the same rounding as the two-step form.
+struct NeuronParams {
+  int neuron;      // SENGINE_NEURON_LIF / IF
+  int hard_reset;
+  int pow2;        // 1/tau is an exact power of two (LIF only)
+  float tau;       // fp32 tau (division operand)
+  float decay;     // fp32(1 - 1/tau), rounded like the reference's python scalar
+  float rtau;      // 1/tau when pow2
+  float vth, vreset;
+};
+
+// One charge step: returns the charged membrane h given the previous membrane v and
+// the input x.  xf is x/tau already folded (pow2 LIF) or the raw BN output.
+__device__ __forceinline__ float neuron_charge(const NeuronParams& np, float v, float xf) {
+  if (np.neuron == SENGINE_NEURON_IF) return __fadd_rn(v, xf);
+  if (np.pow2) return __builtin_fmaf(v, np.decay, xf);  // v*decay exact => single rounding
+  return __fadd_rn(__fmul_rn(v, np.decay), __fdiv_rn(xf, np.tau));
+}
+
+__device__ __forceinline__ float neuron_reset(const NeuronParams& np, float h, bool spike) {
+  if (np.hard_reset) return spike ? np.vreset : h;
+  return spike ? __fsub_rn(h, np.vth) : h;
+}
+
+}  // namespace sengine

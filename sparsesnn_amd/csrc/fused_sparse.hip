@@ -1,0 +1,259 @@
+// Fused 2:4-sparse Conv + folded BN + multi-step LIF/IF for gfx950.
+//
+// Replaces the reference operator conv2d_bn_if_interleaved_kernel
+// (sengine/kernels/conv2d_bn_if_t4.py:918-1022) and conv1x1_bn_lif / conv1x1_bn_if
+// (sengine/kernels/interleaved_templates.py:28-154).  Same contract: one launch
+// processes all T timesteps of a (T*B, H, W, C_in) input; each workgroup owns its
+// output tile across every timestep, so the membrane never leaves registers and no
+// two workgroups touch the same membrane (unlike the T-batched kernels at
+// conv2d_bn_if_t4.py:214-217).
+//
+// GEMM view: out^T[C_out, M] = W[C_out, K_red] (2:4 sparse along C_in) x act^T[K_red, M]
+// with K_red ordered (kh, kw, c_in), c_in fastest — the order of the reference's
+// (KH, KW, C_in, F) weight (cuda_graph_runtime.py:233-235) and of its 2:4 groups
+// (sparse/utils.py:87-109).  The weights are the sparse A operand of
+// v_smfmac_f32_16x16x64_f16; activations are the dense B operand, gathered straight
+// from the NHWC input (implicit im2col) and expanded from spike bits in registers.
+//
+// Work decomposition: workgroup = 4 waves = 64 output channels x 64 output positions
+// (positions flattened over (b, oh, ow), as the reference's M_per_t).  Each wave owns
+// 64 channels x 16 positions and accumulates all T timesteps at once (T*4 MFMA tiles),
+// so every weight fragment fetched is reused T times from registers.  The weight blob
+// permutes rows so that lane group g = lane/16 holds output channels 16g..16g+15 of
+// its 64-channel group: the epilogue then forms 16 spike bits per lane with no
+// cross-lane traffic.
+#include "common.h"
+#include "internal.h"
+
+namespace sengine {
+
+struct FusedParams {
+  const uint8_t* in;
+  const half8_t* wvals;
+  const uint32_t* wmeta;
+  float* state;
+  const float* scale;
+  const float* bias;
+  uint8_t* out;
+  float* h_trace;
+  float* x_trace;
+  int B, C, H, W, F, KW, SH, SW, PH, PW, DH, DW, OH, OW;
+  int M;    // B*OH*OW
+  int nq;   // K_red / 64
+  int64_t in_t_stride;  // pixels per timestep = B*H*W
+  NeuronParams np;
+  float enc_scale;      // 1/value of a spike fed to the MFMA
+};
+
+template <int T, int IN_ENC, int OUT_ENC, int PLANES>
+__global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+  const int G = blockIdx.y;  // 64-channel output group
+  const int m = blockIdx.x * 64 + wave * 16 + col;
+  const bool mvalid = m < p.M;
+  int b = 0, oh = 0, ow = 0;
+  if (mvalid) {
+    const int ohw = p.OH * p.OW;
+    b = m / ohw;
+    const int r = m - b * ohw;
+    oh = r / p.OW;
+    ow = r - oh * p.OW;
+  }
+
+  float4_t acc[T][4];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) acc[t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nq = p.nq;
+  const int chunks_per_tap = p.C >> 6;
+  const half8_t* wv = p.wvals + (size_t)G * nq * PLANES * 4 * 64 + lane;
+  const uint32_t* wm = p.wmeta + (size_t)G * nq * 4 * 64 + lane;
+  // Byte selector pulling bits [8g, 8g+8) of each 32-bit half of a 64-channel chunk.
+  const uint32_t sel = 0x0c0c0000u | ((uint32_t)(4 + g) << 8) | (uint32_t)g;
+
+  for (int q = 0; q < nq; ++q) {
+    const int tap = q / chunks_per_tap;
+    const int c0 = (q - tap * chunks_per_tap) << 6;
+    const int kr = tap / p.KW;
+    const int ks = tap - kr * p.KW;
+    const int ih = oh * p.SH - p.PH + kr * p.DH;
+    const int iw = ow * p.SW - p.PW + ks * p.DW;
+    const bool ok = mvalid && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
+    const int64_t pix0 = ((int64_t)b * p.H + ih) * p.W + iw;
+
+    half8_t av[PLANES][4];
+    uint32_t ix[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+#pragma unroll
+      for (int pl = 0; pl < PLANES; ++pl) av[pl][a] = wv[((size_t)(q * PLANES + pl) * 4 + a) * 64];
+      ix[a] = wm[((size_t)q * 4 + a) * 64];
+    }
+
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      half16_t bf;
+      const int64_t pix = pix0 + (int64_t)t * p.in_t_stride;
+      if (IN_ENC == SENGINE_ENC_BITS) {
+        uint2 w = {0u, 0u};
+        if (ok) w = *reinterpret_cast<const uint2*>(p.in + pix * (p.C >> 3) + (c0 >> 3));
+        bf = expand_bits16(__builtin_amdgcn_perm(w.y, w.x, sel));
+      } else {
+        half8_t lo = {}, hi = {};
+        if (ok) {
+          const half8_t* src =
+              reinterpret_cast<const half8_t*>(reinterpret_cast<const _Float16*>(p.in) + pix * p.C + c0 + 8 * g);
+          lo = src[0];
+          hi = src[4];
+        }
+        bf = concat8(lo, hi);
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int pl = 0; pl < PLANES; ++pl)
+          acc[t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(av[pl][a], bf, acc[t][a], ix[a], 0, 0);
+    }
+  }
+
+  // ---- epilogue: folded BN + T-step neuron, all in registers ----
+  if (!mvalid) return;
+  const int cob = G * 64 + g * 16;  // this lane's 16 output channels
+  const NeuronParams np = p.np;
+  float sc[16], bi[16], xs[16], v[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float s = p.scale[cob + j] * p.enc_scale;  // exact: enc_scale is a power of two
+    const float bb = p.bias[cob + j];
+    sc[j] = s;
+    bi[j] = bb;
+    xs[j] = 0.f;
+  }
+  const bool fold = np.neuron == SENGINE_NEURON_LIF && np.pow2;
+  float fsc[16], fbi[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    fsc[j] = fold ? sc[j] * np.rtau : sc[j];
+    fbi[j] = fold ? bi[j] * np.rtau : bi[j];
+  }
+  float* st = p.state ? p.state + (size_t)m * p.F + cob : nullptr;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = st ? st[j] : 0.f;
+
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    uint32_t word = 0;
+    const size_t row = ((size_t)t * p.M + m) * p.F + cob;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 4 * a + i;
+        const float accv = acc[t][a][i];
+        const float xin = __builtin_fmaf(accv, fsc[j], fbi[j]);
+        const float h = neuron_charge(np, v[j], xin);
+        const bool spike = h >= np.vth;
+        word |= (uint32_t)spike << j;
+        v[j] = neuron_reset(np, h, spike);
+        if (p.h_trace) p.h_trace[row + j] = h;
+        if (p.x_trace) p.x_trace[row + j] = fold ? __builtin_fmaf(accv, sc[j], bi[j]) : xin;
+      }
+    if (OUT_ENC == SENGINE_ENC_BITS) {
+      *reinterpret_cast<uint16_t*>(p.out + (row >> 3)) = (uint16_t)word;
+    } else {
+      half8_t o0, o1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        o0[j] = (word >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+        o1[j] = (word >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+      }
+      half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(p.out) + row);
+      dst[0] = o0;
+      dst[1] = o1;
+    }
+  }
+  if (st) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) st[j] = v[j];
+  }
+}
+
+template <int T, int IN_ENC, int OUT_ENC, int PLANES>
+static hipError_t launch_fused_t(const FusedParams& p, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((fused_sparse_conv_bn_lif_kernel<T, IN_ENC, OUT_ENC, PLANES>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int T>
+static hipError_t launch_fused_enc(const FusedParams& p, int in_enc, int out_enc, int planes, dim3 grid,
+                                   hipStream_t s) {
+#define SENGINE_FUSED_CASE(IE, OE, PL) \
+  if (in_enc == IE && out_enc == OE && planes == PL) return launch_fused_t<T, IE, OE, PL>(p, grid, s);
+  SENGINE_FUSED_CASE(SENGINE_ENC_BITS, SENGINE_ENC_BITS, 1)
+  SENGINE_FUSED_CASE(SENGINE_ENC_BITS, SENGINE_ENC_BITS, 2)
+  SENGINE_FUSED_CASE(SENGINE_ENC_BITS, SENGINE_ENC_F16, 1)
+  SENGINE_FUSED_CASE(SENGINE_ENC_BITS, SENGINE_ENC_F16, 2)
+  SENGINE_FUSED_CASE(SENGINE_ENC_F16, SENGINE_ENC_BITS, 1)
+  SENGINE_FUSED_CASE(SENGINE_ENC_F16, SENGINE_ENC_BITS, 2)
+  SENGINE_FUSED_CASE(SENGINE_ENC_F16, SENGINE_ENC_F16, 1)
+  SENGINE_FUSED_CASE(SENGINE_ENC_F16, SENGINE_ENC_F16, 2)
+#undef SENGINE_FUSED_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace sengine
+
+using namespace sengine;
+
+extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const void* data,
+                                                    const void* blob_values, const void* blob_meta,
+                                                    float* state, const float* bn_scale, const float* bn_bias,
+                                                    void* spikes, float* h_trace, float* x_trace,
+                                                    hipStream_t stream) {
+  Geometry geo;
+  int rc = check_desc(d, &geo, /*sparse=*/true);
+  if (rc) return rc;
+  if (!data || !blob_values || !blob_meta || !bn_scale || !bn_bias || !spikes)
+    return set_error(-1, "fused_sparse_conv_bn_lif: null data/weight/bn/spikes pointer");
+  if (d->T != 1 && d->T != 2 && d->T != 4 && d->T != 8)
+    return set_error(-3, "fused_sparse_conv_bn_lif: T must be 1, 2, 4 or 8");
+  if (d->in_enc != SENGINE_ENC_BITS && d->in_enc != SENGINE_ENC_F16)
+    return set_error(-2, "fused_sparse_conv_bn_lif: in_enc must be BITS or F16");
+  if (d->out_enc != SENGINE_ENC_BITS && d->out_enc != SENGINE_ENC_F16)
+    return set_error(-2, "fused_sparse_conv_bn_lif: out_enc must be BITS or F16");
+  if (geo.M > (1ll << 30)) return set_error(-2, "fused_sparse_conv_bn_lif: B*OH*OW too large");
+
+  FusedParams p;
+  p.in = static_cast<const uint8_t*>(data);
+  p.wvals = static_cast<const half8_t*>(blob_values);
+  p.wmeta = static_cast<const uint32_t*>(blob_meta);
+  p.state = state;
+  p.scale = bn_scale;
+  p.bias = bn_bias;
+  p.out = static_cast<uint8_t*>(spikes);
+  p.h_trace = h_trace;
+  p.x_trace = x_trace;
+  p.B = d->B; p.C = d->C_in; p.H = d->H; p.W = d->W; p.F = d->C_out; p.KW = d->KW;
+  p.SH = d->stride_h; p.SW = d->stride_w; p.PH = d->pad_h; p.PW = d->pad_w;
+  p.DH = d->dil_h; p.DW = d->dil_w; p.OH = geo.OH; p.OW = geo.OW;
+  p.M = (int)geo.M;
+  p.nq = (int)(geo.K_red / 64);
+  p.in_t_stride = (int64_t)d->B * d->H * d->W;
+  p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
+  p.enc_scale = d->in_enc == SENGINE_ENC_BITS ? 1.0f / kBitSpikeValue : 1.0f;
+
+  dim3 grid((unsigned)((geo.M + 63) / 64), (unsigned)(d->C_out / 64));
+  hipError_t e;
+  switch (d->T) {
+    case 1: e = launch_fused_enc<1>(p, d->in_enc, d->out_enc, d->weight_planes, grid, stream); break;
+    case 2: e = launch_fused_enc<2>(p, d->in_enc, d->out_enc, d->weight_planes, grid, stream); break;
+    case 4: e = launch_fused_enc<4>(p, d->in_enc, d->out_enc, d->weight_planes, grid, stream); break;
+    default: e = launch_fused_enc<8>(p, d->in_enc, d->out_enc, d->weight_planes, grid, stream); break;
+  }
+  return (int)e;
+}

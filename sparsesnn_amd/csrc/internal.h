@@ -1,0 +1,26 @@
+// Host-side helpers shared by the C-ABI entry points.
+#pragma once
+#include <stdint.h>
+
+#include "common.h"
+
+namespace sengine {
+
+struct Geometry {
+  int OH, OW;
+  int64_t M;      // B*OH*OW rows per timestep
+  int64_t K_red;  // KH*KW*C_in
+};
+
+// Records msg as this thread's last error and returns code (negative).
+int set_error(int code, const char* msg);
+
+// Validates a descriptor and derives the output geometry.  sparse=true adds the
+// constraints of the 2:4 fused path (C_in % 64), otherwise the dense fallback's (C_in % 32).
+int check_desc(const sengine_conv_lif_desc* d, Geometry* geo, bool sparse);
+
+// fp32 neuron parameters with the rounding of the reference's python scalars:
+// decay = float(1.0 - 1.0/tau) computed in double (models/neurons.py:124).
+NeuronParams make_neuron_params(int neuron, int hard_reset, float tau, float vth, float vreset);
+
+}  // namespace sengine

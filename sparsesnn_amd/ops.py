@@ -1,0 +1,287 @@
+"""Torch-facing wrappers over the C ABI of libsengine_amd.so.
+
+PyTorch is used for device memory and the current stream only; every op launches a
+hand-written gfx950 HIP kernel and there is no fallback path.  Each wrapper checks the
+tensors against the descriptor on the host before launching (the C ABI takes raw
+pointers and cannot check buffer sizes itself).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import (ENC_BITS, ENC_F16, ENC_F32, NEURON_IF, NEURON_LIF, WLAYOUT_HWIO, WLAYOUT_OIHW,
+                   ConvLifDesc, SEngineError, check)
+
+__all__ = [
+    "ConvSpec", "make_desc", "geometry", "compress_2_4", "pack_dense_weights", "pack_spikes",
+    "unpack_spikes", "fused_sparse_conv_bn_lif", "dense_conv_bn", "multistep_neuron", "SEngineError",
+    "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
+]
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_cuda(t: torch.Tensor, name: str):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise SEngineError(f"{name} must be on a HIP device (got {t.device})")
+    if not t.is_contiguous():
+        raise SEngineError(f"{name} must be contiguous")
+
+
+def _require_numel(t: torch.Tensor, n: int, dtype, name: str):
+    if t.dtype != dtype:
+        raise SEngineError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+    if t.numel() != n:
+        raise SEngineError(f"{name}: expected {n} elements, got {t.numel()}")
+
+
+@dataclass(frozen=True)
+class ConvSpec:
+    """Shape + neuron parameters of one Conv+BN+neuron node (ConvParams + NeuronParams,
+    sengine/ir.py:179-201, plus the T/B extents the reference bakes into each kernel)."""
+
+    T: int
+    B: int
+    C_in: int
+    H: int
+    W: int
+    C_out: int
+    KH: int = 3
+    KW: int = 3
+    stride: int = 1
+    padding: int = 1
+    dilation: int = 1
+    neuron: str = "lif"          # "lif" | "if"
+    hard_reset: bool = True
+    tau: float = 2.0
+    v_threshold: float = 1.0
+    v_reset: float = 0.0
+    in_enc: int = ENC_BITS
+    out_enc: int = ENC_BITS
+    weight_planes: int = 1
+
+    def desc(self) -> ConvLifDesc:
+        return make_desc(self)
+
+
+def make_desc(s: ConvSpec) -> ConvLifDesc:
+    if s.neuron not in ("lif", "if"):
+        raise ValueError(f"neuron must be 'lif' or 'if', got {s.neuron!r}")
+    return ConvLifDesc(
+        T=s.T, B=s.B, C_in=s.C_in, H=s.H, W=s.W, C_out=s.C_out, KH=s.KH, KW=s.KW,
+        stride_h=s.stride, stride_w=s.stride, pad_h=s.padding, pad_w=s.padding,
+        dil_h=s.dilation, dil_w=s.dilation,
+        neuron=NEURON_LIF if s.neuron == "lif" else NEURON_IF, hard_reset=int(bool(s.hard_reset)),
+        tau=float(s.tau), v_threshold=float(s.v_threshold), v_reset=float(s.v_reset),
+        in_enc=s.in_enc, out_enc=s.out_enc, weight_planes=s.weight_planes)
+
+
+def geometry(s: ConvSpec):
+    """(OH, OW, M_per_t, K_red) of a node."""
+    lib = _lib.load()
+    d = make_desc(s)
+    oh, ow = ctypes.c_int32(), ctypes.c_int32()
+    m, k = ctypes.c_int64(), ctypes.c_int64()
+    check(lib.sengine_amd_conv_geometry(ctypes.byref(d), ctypes.byref(oh), ctypes.byref(ow),
+                                        ctypes.byref(m), ctypes.byref(k)), "conv_geometry")
+    return oh.value, ow.value, m.value, k.value
+
+
+def _enc_numel(enc: int, n_values: int) -> tuple:
+    """(dtype, numel) of a tensor holding n_values activations in encoding enc."""
+    if enc == ENC_BITS:
+        if n_values % 32:
+            raise SEngineError("bit-encoded tensors need a multiple of 32 values")
+        return torch.int32, n_values // 32
+    if enc == ENC_F16:
+        return torch.float16, n_values
+    if enc == ENC_F32:
+        return torch.float32, n_values
+    raise SEngineError(f"unknown encoding {enc}")
+
+
+def _weight_enc(w: torch.Tensor) -> int:
+    if w.dtype == torch.float32:
+        return ENC_F32
+    if w.dtype == torch.float16:
+        return ENC_F16
+    raise SEngineError(f"weights must be fp32 or fp16, got {w.dtype}")
+
+
+def _check_weight(s: ConvSpec, w: torch.Tensor, layout: int):
+    _require_cuda(w, "weight")
+    shape = (s.C_out, s.C_in, s.KH, s.KW) if layout == WLAYOUT_OIHW else (s.KH, s.KW, s.C_in, s.C_out)
+    if tuple(w.shape) != shape:
+        raise SEngineError(f"weight: expected shape {shape}, got {tuple(w.shape)}")
+
+
+def compress_2_4(s: ConvSpec, weight: torch.Tensor, layout: int = WLAYOUT_OIHW, check_pattern: bool = True):
+    """2:4-compress a conv weight on the GPU -> (values int16 tensor, meta int32 tensor, violations).
+
+    Raises if check_pattern and any 4-group along C_in holds more than two entries with
+    |w| >= 1e-10 (such weights belong on the dense fallback, sengine/optimizer.py:845-853)."""
+    lib = _lib.load()
+    _check_weight(s, weight, layout)
+    d = make_desc(s)
+    vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+    check(lib.sengine_amd_sparse_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)), "sparse_blob_bytes")
+    dev = weight.device
+    values = torch.empty(vb.value // 2, dtype=torch.int16, device=dev)
+    meta = torch.empty(mb.value // 4, dtype=torch.int32, device=dev)
+    n_groups = lib.sengine_amd_num_groups(ctypes.byref(d))
+    viol = torch.empty(n_groups, dtype=torch.int32, device=dev)
+    check(lib.sengine_amd_compress_2_4(ctypes.byref(d), _ptr(weight), _weight_enc(weight), layout,
+                                       _ptr(values), _ptr(meta), _ptr(viol), _stream(dev)), "compress_2_4")
+    if check_pattern:
+        n_bad = int(viol.sum().item())
+        if n_bad:
+            raise SEngineError(f"compress_2_4: {n_bad} 4-groups have more than two non-zero weights")
+    return values, meta, viol
+
+
+def pack_dense_weights(s: ConvSpec, weight: torch.Tensor, layout: int = WLAYOUT_OIHW) -> torch.Tensor:
+    lib = _lib.load()
+    _check_weight(s, weight, layout)
+    d = make_desc(s)
+    vb = ctypes.c_size_t()
+    check(lib.sengine_amd_dense_blob_bytes(ctypes.byref(d), ctypes.byref(vb)), "dense_blob_bytes")
+    values = torch.empty(vb.value // 2, dtype=torch.int16, device=weight.device)
+    check(lib.sengine_amd_pack_dense_weights(ctypes.byref(d), _ptr(weight), _weight_enc(weight), layout,
+                                             _ptr(values), _stream(weight.device)), "pack_dense_weights")
+    return values
+
+
+def pack_spikes(x: torch.Tensor) -> torch.Tensor:
+    """Dense (..., C) fp16/fp32 -> spike bits int32 (..., C/32) (value != 0 -> 1)."""
+    lib = _lib.load()
+    _require_cuda(x, "x")
+    C = x.shape[-1]
+    if C % 32:
+        raise SEngineError("pack_spikes: last dim must be a multiple of 32")
+    enc = ENC_F16 if x.dtype == torch.float16 else ENC_F32 if x.dtype == torch.float32 else None
+    if enc is None:
+        raise SEngineError("pack_spikes: x must be fp16 or fp32")
+    n_pos = x.numel() // C
+    out = torch.empty(*x.shape[:-1], C // 32, dtype=torch.int32, device=x.device)
+    check(lib.sengine_amd_pack_spikes(_ptr(x), enc, n_pos, C, _ptr(out), _stream(x.device)), "pack_spikes")
+    return out
+
+
+def unpack_spikes(bits: torch.Tensor, C: int, dtype=torch.float16) -> torch.Tensor:
+    lib = _lib.load()
+    _require_cuda(bits, "bits")
+    if C % 32 or bits.shape[-1] != C // 32 or bits.dtype != torch.int32:
+        raise SEngineError("unpack_spikes: bits must be int32 (..., C/32)")
+    enc = ENC_F16 if dtype == torch.float16 else ENC_F32 if dtype == torch.float32 else None
+    if enc is None:
+        raise SEngineError("unpack_spikes: dtype must be fp16 or fp32")
+    n_pos = bits.numel() // (C // 32)
+    out = torch.empty(*bits.shape[:-1], C, dtype=dtype, device=bits.device)
+    check(lib.sengine_amd_unpack_spikes(_ptr(bits), n_pos, C, _ptr(out), enc, _stream(bits.device)), "unpack_spikes")
+    return out
+
+
+def fused_sparse_conv_bn_lif(s: ConvSpec, data: torch.Tensor, values: torch.Tensor, meta: torch.Tensor,
+                             bn_scale: torch.Tensor, bn_bias: torch.Tensor, state: Optional[torch.Tensor] = None,
+                             out: Optional[torch.Tensor] = None, h_trace: Optional[torch.Tensor] = None,
+                             x_trace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused 2:4 Conv + BN + multi-step neuron (one launch).  Returns the spike tensor:
+    bits int32 (T*B, OH, OW, C_out/32) or fp16 (T*B, OH, OW, C_out) per s.out_enc."""
+    lib = _lib.load()
+    OH, OW, M, _ = geometry(s)
+    d = make_desc(s)
+    vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+    check(lib.sengine_amd_sparse_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)), "sparse_blob_bytes")
+    for t, n in ((data, "data"), (values, "values"), (meta, "meta"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    dev = data.device
+    dt, n_in = _enc_numel(s.in_enc, s.T * s.B * s.H * s.W * s.C_in)
+    _require_numel(data, n_in, dt, "data")
+    if values.numel() * values.element_size() != vb.value or meta.numel() * meta.element_size() != mb.value:
+        raise SEngineError("fused_sparse_conv_bn_lif: weight blob does not match the descriptor")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    if state is not None:
+        _require_cuda(state, "state")
+        _require_numel(state, M * s.C_out, torch.float32, "state")
+    for tr, n in ((h_trace, "h_trace"), (x_trace, "x_trace")):
+        if tr is not None:
+            _require_cuda(tr, n)
+            _require_numel(tr, s.T * M * s.C_out, torch.float32, n)
+    odt, n_out = _enc_numel(s.out_enc, s.T * M * s.C_out)
+    if out is None:
+        last = s.C_out // 32 if s.out_enc == ENC_BITS else s.C_out
+        out = torch.empty(s.T * s.B, OH, OW, last, dtype=odt, device=dev)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, n_out, odt, "out")
+    rc = lib.sengine_amd_fused_sparse_conv_bn_lif(
+        ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta), _ptr(state), _ptr(bn_scale), _ptr(bn_bias),
+        _ptr(out), _ptr(h_trace), _ptr(x_trace), _stream(dev))
+    check(rc, "fused_sparse_conv_bn_lif")
+    return out
+
+
+def dense_conv_bn(s: ConvSpec, data: torch.Tensor, values: torch.Tensor, bn_scale: torch.Tensor,
+                  bn_bias: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense Conv + folded BN -> fp32 (T*B, OH, OW, C_out)."""
+    lib = _lib.load()
+    OH, OW, M, _ = geometry(s)
+    d = make_desc(s)
+    vb = ctypes.c_size_t()
+    check(lib.sengine_amd_dense_blob_bytes(ctypes.byref(d), ctypes.byref(vb)), "dense_blob_bytes")
+    for t, n in ((data, "data"), (values, "values"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    dt, n_in = _enc_numel(s.in_enc, s.T * s.B * s.H * s.W * s.C_in)
+    _require_numel(data, n_in, dt, "data")
+    if values.numel() * values.element_size() != vb.value:
+        raise SEngineError("dense_conv_bn: weight blob does not match the descriptor")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    if out is None:
+        out = torch.empty(s.T * s.B, OH, OW, s.C_out, dtype=torch.float32, device=data.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, s.T * M * s.C_out, torch.float32, "out")
+    check(lib.sengine_amd_dense_conv_bn(ctypes.byref(d), _ptr(data), _ptr(values), _ptr(bn_scale), _ptr(bn_bias),
+                                        _ptr(out), _stream(data.device)), "dense_conv_bn")
+    return out
+
+
+def multistep_neuron(x: torch.Tensor, T: int, neuron: str = "lif", tau: float = 2.0, v_threshold: float = 1.0,
+                     v_reset: Optional[float] = 0.0, state: Optional[torch.Tensor] = None, out_enc: int = ENC_BITS,
+                     h_trace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Standalone multi-step LIF/IF over T on x (T, ...) fp32 (n = x.numel()/T per step).
+    v_reset=None selects soft reset (models/neurons.py:135-137).  Returns spikes as bits
+    int32 (T, n/32) or fp16 (T, n)."""
+    lib = _lib.load()
+    _require_cuda(x, "x")
+    if x.dtype != torch.float32 or x.numel() % T:
+        raise SEngineError("multistep_neuron: x must be fp32 with T * n elements")
+    n = x.numel() // T
+    if state is not None:
+        _require_cuda(state, "state")
+        _require_numel(state, n, torch.float32, "state")
+    if h_trace is not None:
+        _require_cuda(h_trace, "h_trace")
+        _require_numel(h_trace, T * n, torch.float32, "h_trace")
+    odt, n_out = _enc_numel(out_enc, T * n)
+    out = torch.empty(n_out, dtype=odt, device=x.device)
+    hard = v_reset is not None
+    check(lib.sengine_amd_multistep_neuron(T, n, NEURON_LIF if neuron == "lif" else NEURON_IF, int(hard), float(tau),
+                                           float(v_threshold), float(v_reset if hard else 0.0), _ptr(x), _ptr(state),
+                                           out_enc, _ptr(out), _ptr(h_trace), _stream(x.device)), "multistep_neuron")
+    return out

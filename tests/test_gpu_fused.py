@@ -1,0 +1,117 @@
+"""GPU parity of the fused 2:4-sparse Conv+BN+LIF kernel against the CPU oracle.
+
+Every case runs the reference PyTorch path (oracle.reference_path) on the CPU and the
+HIP kernel through the C ABI on the same seeded inputs, then applies the acceptance
+rule of tests/parity.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import packing as pk
+from oracle import reference_path as ref
+from sparsesnn_amd import ops
+from tests.parity import compare, nhwc_seq
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, case: ref.LayerCase, neuron="lif", tau=2.0, v_th=1.0, v_reset=0.0, planes=1,
+             in_enc=ops.ENC_BITS, out_enc=ops.ENC_BITS, v0=None, layout=ops.WLAYOUT_OIHW):
+    T, B, C_in, H, W = case.x_seq.shape
+    C_out, _, KH, KW = case.w.shape
+    hard = v_reset is not None
+    spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=KH, KW=KW, stride=case.stride,
+                        padding=case.padding, neuron=neuron, hard_reset=hard, tau=tau, v_threshold=v_th,
+                        v_reset=v_reset if hard else 0.0, in_enc=in_enc, out_enc=out_enc, weight_planes=planes)
+    OH, OW, M, _ = ops.geometry(spec)
+    w_dev = case.w.to(dev) if layout == ops.WLAYOUT_OIHW else case.w.permute(2, 3, 1, 0).contiguous().to(dev)
+    values, meta, _ = ops.compress_2_4(spec, w_dev, layout)
+    scale, bias = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
+    scale_d = torch.from_numpy(scale).to(dev)
+    bias_d = torch.from_numpy(bias).to(dev)
+    x_nhwc = case.x_seq.permute(0, 1, 3, 4, 2).reshape(T * B, H, W, C_in).contiguous()
+    if in_enc == ops.ENC_BITS:
+        data = torch.from_numpy(pk.seq_to_nhwc_bits(case.x_seq.numpy()).view(np.int32)).to(dev)
+    else:
+        data = x_nhwc.half().to(dev)
+    state = None
+    if v0 is not None:
+        state = v0.permute(0, 2, 3, 1).reshape(M, C_out).contiguous().to(dev)
+    h_tr = torch.empty(T, M, C_out, dtype=torch.float32, device=dev)
+    x_tr = torch.empty(T, M, C_out, dtype=torch.float32, device=dev)
+    out = ops.fused_sparse_conv_bn_lif(spec, data, values, meta, scale_d, bias_d, state=state,
+                                       h_trace=h_tr, x_trace=x_tr)
+    torch.cuda.synchronize()
+    if out_enc == ops.ENC_BITS:
+        s_gpu = pk.unpack_bits(out.cpu().numpy().view(np.uint32).reshape(-1, C_out // 32), C_out)
+        s_gpu = torch.from_numpy(s_gpu.reshape(T * B, OH, OW, C_out))
+    else:
+        s_gpu = out.float().cpu()
+    r = ref.fused_layer(case.x_seq, case.w, case.bn, case.stride, case.padding, 1, neuron, tau, v_th, v_reset, v0)
+    h_gpu = nhwc_seq(h_tr.view(T * B, OH, OW, C_out), T)
+    rep = compare(nhwc_seq(s_gpu, T), h_gpu, r.spikes.numpy(), r.h.numpy(), v_th)
+    x_gpu = nhwc_seq(x_tr.view(T * B, OH, OW, C_out), T)
+    x_err = float(np.max(np.abs(x_gpu - r.x.numpy())))
+    v_fin = None
+    if state is not None:
+        v_fin = state.view(B, OH, OW, C_out).permute(0, 3, 1, 2).cpu()
+    return rep, x_err, r, v_fin
+
+
+def test_cfg0_lif_bits(dev):
+    case = ref.make_layer_case(0, T=4, B=1, C_in=64, C_out=64, H=32, W=32, k=3)
+    rep, x_err, r, _ = run_case(dev, case, planes=2)
+    print(rep, "x_err", x_err, "spike rate", float(r.spikes.mean()))
+    assert rep.ok, str(rep)
+    assert x_err < 1e-4
+
+
+@pytest.mark.parametrize("planes", [1, 2])
+@pytest.mark.parametrize("in_enc,out_enc", [(ops.ENC_BITS, ops.ENC_BITS), (ops.ENC_F16, ops.ENC_F16),
+                                            (ops.ENC_BITS, ops.ENC_F16), (ops.ENC_F16, ops.ENC_BITS)])
+def test_encodings(dev, planes, in_enc, out_enc):
+    case = ref.make_layer_case(1, T=4, B=2, C_in=64, C_out=128, H=10, W=12, k=3, fp16_weights=(planes == 1))
+    rep, x_err, _, _ = run_case(dev, case, planes=planes, in_enc=in_enc, out_enc=out_enc)
+    print(rep, x_err)
+    assert rep.ok, str(rep)
+
+
+@pytest.mark.parametrize("k,stride,pad", [(3, 1, 1), (3, 2, 1), (1, 1, 0), (1, 2, 0), (3, 1, 0), (5, 2, 2)])
+def test_shapes(dev, k, stride, pad):
+    case = ref.make_layer_case(2 + k + stride, T=4, B=3, C_in=128, C_out=64, H=13, W=11, k=k, stride=stride,
+                               padding=pad, fp16_weights=True)
+    rep, x_err, _, _ = run_case(dev, case)
+    print(rep, x_err)
+    assert rep.ok, str(rep)
+
+
+@pytest.mark.parametrize("T", [1, 2, 8])
+def test_timesteps(dev, T):
+    case = ref.make_layer_case(10 + T, T=T, B=2, C_in=64, C_out=64, H=9, W=9, k=3, fp16_weights=True)
+    rep, _, _, _ = run_case(dev, case)
+    assert rep.ok, str(rep)
+
+
+@pytest.mark.parametrize("neuron,tau,v_reset", [("if", 2.0, 0.0), ("lif", 2.0, None), ("if", 2.0, None),
+                                                ("lif", 3.0, 0.0), ("lif", 1.5, 0.2), ("lif", 4.0, None)])
+def test_neuron_variants(dev, neuron, tau, v_reset):
+    case = ref.make_layer_case(20, T=4, B=2, C_in=64, C_out=64, H=8, W=8, k=3, fp16_weights=True, p_spike=0.3)
+    rep, _, r, _ = run_case(dev, case, neuron=neuron, tau=tau, v_reset=v_reset, v_th=0.5)
+    print(neuron, tau, v_reset, rep, float(r.spikes.mean()))
+    assert rep.ok, str(rep)
+
+
+def test_state_in_out(dev):
+    case = ref.make_layer_case(30, T=4, B=2, C_in=64, C_out=64, H=6, W=7, k=3, fp16_weights=True)
+    g = torch.Generator().manual_seed(5)
+    v0 = torch.rand((2, 64, 6, 7), generator=g) * 0.9
+    rep, _, r, v_fin = run_case(dev, case, v0=v0)
+    assert rep.ok, str(rep)
+    assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
+
+
+def test_hwio_layout(dev):
+    case = ref.make_layer_case(31, T=4, B=1, C_in=64, C_out=64, H=8, W=8, k=3, fp16_weights=True)
+    rep, _, _, _ = run_case(dev, case, layout=ops.WLAYOUT_HWIO)
+    assert rep.ok, str(rep)
