@@ -1,0 +1,258 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused 2:4-sparse Conv+BN+LIF operator on one MI355X.
+
+Workload: the layer sweep at T=4, batch 32, fp16 2:4 weights,
+1-bit spike inputs with density p in {0.05, 0.15, 0.30}, BN + LIF(tau=2, V_th=1, hard
+reset) as config 0; shapes 64->64 56x56 k3, 128->128 28x28 k3, 256->256 14x14 k3,
+512->512 7x7 k3, 256->1024 14x14 k1.  One "step" = the 15 fused layer calls (5 shapes x
+3 densities), inputs resident in HBM, replayed from a hipGraph (the reference benchmarks
+graph replays too, sengine/csrc/cpp_executor.cu:1298-1315).
+
+Score: per layer, ideal time = max(F / P_sparse, B_min / BW) with
+F = 2*M*N*K_red dense-equivalent FLOPs and B_min the algorithmic HBM bytes (1 bit per
+spike in and out, fp16 2:4 values + 2-bit metadata, BN vectors); value = sum(ideal) /
+measured step time, in percent.
+
+Prints ONE JSON line on stdout.  Per-layer details go to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+P_SPARSE = 5.0e15   # MI355X fp16 2:4 SMFMAC, dense-equivalent FLOP/s (= 2.5 PFLOP/s dense x 2)
+BW_HBM = 8.0e12     # MI355X HBM3E bytes/s
+
+SHAPES = [  # (C_in, C_out, H, W, k)
+    (64, 64, 56, 56, 3),
+    (128, 128, 28, 28, 3),
+    (256, 256, 14, 14, 3),
+    (512, 512, 7, 7, 3),
+    (256, 1024, 14, 14, 1),
+]
+DENSITIES = (0.05, 0.15, 0.30)
+T_STEPS, BATCH = 4, 32
+
+
+def layer_work(C_in, C_out, H, W, k, T, B):
+    OH, OW = H, W  # stride 1, same padding for every sweep layer
+    M = T * B * OH * OW
+    K_red = k * k * C_in
+    flops = 2.0 * M * C_out * K_red
+    bytes_min = (T * B * H * W * C_in) / 8 + (M * C_out) / 8 + C_out * K_red / 2 * 2 + C_out * K_red / 8 + 8 * C_out
+    return flops, bytes_min
+
+
+def build_workloads(dev, T, B, seed=1234):
+    import torch
+    from sparsesnn_amd import ops
+    from sparsesnn_amd.sparsity import fold_batchnorm, prune_conv_2_4
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    work = []
+    for (C_in, C_out, H, W, k) in SHAPES:
+        std = (2.0 / (k * k * C_in)) ** 0.5
+        w = torch.randn((C_out, C_in, k, k), generator=g, device=dev) * std
+        w = prune_conv_2_4(w).half()
+        gamma = torch.rand(C_out, generator=g, device=dev) + 0.5
+        beta = torch.randn(C_out, generator=g, device=dev) * 0.1
+        mean = torch.randn(C_out, generator=g, device=dev) * 0.1
+        var = torch.rand(C_out, generator=g, device=dev) + 0.5
+        scale, bias = fold_batchnorm(gamma, beta, mean, var, 1e-5)
+        spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=k, KW=k, stride=1, padding=k // 2,
+                            neuron="lif", tau=2.0, v_threshold=1.0, v_reset=0.0)
+        values, meta, _ = ops.compress_2_4(spec, w)
+        scale, bias = scale.to(dev), bias.to(dev)
+        for p in DENSITIES:
+            x = (torch.rand((T * B, H, W, C_in), generator=g, device=dev) < p).half()
+            data = ops.pack_spikes(x)
+            del x
+            OH, OW, M, _ = ops.geometry(spec)
+            out = torch.empty(T * B, OH, OW, C_out // 32, dtype=torch.int32, device=dev)
+            flops, bmin = layer_work(C_in, C_out, H, W, k, T, B)
+            work.append(dict(name=f"{C_in}->{C_out} {H}x{W} k{k} p{p}", spec=spec, data=data, values=values,
+                             meta=meta, scale=scale, bias=bias, out=out, flops=flops, bytes_min=bmin,
+                             ideal=max(flops / P_SPARSE, bmin / BW_HBM)))
+    torch.cuda.synchronize(dev)
+    return work
+
+
+def run_layer(wk):
+    from sparsesnn_amd import ops
+    ops.fused_sparse_conv_bn_lif(wk["spec"], wk["data"], wk["values"], wk["meta"], wk["scale"], wk["bias"],
+                                 out=wk["out"])
+
+
+def cpu_baseline(sample_batch=4, runs=10, warmup=3):
+    """The oracle (restated reference PyTorch path, torch CPU fp32) on a bounded sample:
+    the 5 sweep shapes at p=0.15 with batch `sample_batch`; scaled linearly to batch 32 and to
+    the 3 densities (CPU conv cost does not depend on spike density)."""
+    import torch
+    from oracle import reference_path as ref
+
+    cores = os.cpu_count() or 1
+    try:
+        phys = len({(l.split(":")[1].strip()) for l in open("/proc/cpuinfo") if l.startswith("core id")}) or cores
+    except OSError:
+        phys = cores
+    torch.set_num_threads(max(1, min(phys, cores)))
+    cases = [ref.make_layer_case(7 + i, T=T_STEPS, B=sample_batch, C_in=ci, C_out=co, H=h, W=w, k=k,
+                                 fp16_weights=True) for i, (ci, co, h, w, k) in enumerate(SHAPES)]
+
+    def sweep():
+        for c in cases:
+            ref.fused_layer(c.x_seq, c.w, c.bn, c.stride, c.padding, 1, "lif", 2.0, 1.0, 0.0)
+
+    for _ in range(warmup):
+        sweep()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        sweep()
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    step_s = med * (BATCH / sample_batch) * len(DENSITIES)
+    model = ""
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return dict(step_s=step_s, sample_s=med, threads=torch.get_num_threads(), cpu_count=cores, model=model,
+                sample=f"5 sweep shapes at p=0.15, batch {sample_batch}, T=4 (median of {runs} after {warmup} "
+                       f"warmups), scaled x{BATCH // sample_batch} to batch {BATCH} and x{len(DENSITIES)} densities")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--json-out", default="")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the single-GPU fused operator only; multi-GPU runs are not part of this "
+              "build (the operator shards by batch with no communication, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from sparsesnn_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    work = build_workloads(dev, T_STEPS, BATCH)
+
+    # per-launch durations: HIP events on the launch stream around each eager call
+    per = {wk["name"]: [] for wk in work}
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(max(1, args.warmup)):
+        for wk in work:
+            run_layer(wk)
+    torch.cuda.synchronize(dev)
+    reps = max(3, min(args.steps, 20))
+    evs = []
+    for _ in range(reps):
+        for wk in work:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            run_layer(wk)
+            b.record(stream)
+            evs.append((wk["name"], a, b))
+    torch.cuda.synchronize(dev)
+    for name, a, b in evs:
+        per[name].append(a.elapsed_time(b) * 1e-3)
+
+    # the step: all 15 launches captured once in a hipGraph, replayed K times
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        for wk in work:
+            run_layer(wk)
+    stream.wait_stream(cap)
+    torch.cuda.synchronize(dev)
+    with torch.cuda.graph(graph):
+        for wk in work:
+            run_layer(wk)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(args.steps):
+        graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize(dev)
+    step_s = t0.elapsed_time(t1) * 1e-3 / args.steps
+
+    ideal = sum(wk["ideal"] for wk in work)
+    flops = sum(wk["flops"] for wk in work)
+    launches = sum(len(v) for v in per.values())
+    launch_sum = sum(sum(v) for v in per.values())
+    avg_launch = launch_sum / launches
+    avg_flops = sum(wk["flops"] * len(per[wk["name"]]) for wk in work) / launches
+    for wk in work:
+        t = statistics.median(per[wk["name"]])
+        print(f"{wk['name']:28s} {t * 1e6:9.1f} us  {wk['flops'] / t / 1e12:8.1f} TFLOP/s(de)  "
+              f"roofline {100 * wk['ideal'] / t:5.1f}%", file=sys.stderr)
+
+    result = {
+        "metric": "fused sparse conv+BN+LIF: % sparse-MFMA/HBM roofline; e2e images/sec @T=4",
+        "value": round(100.0 * ideal / step_s, 3),
+        "unit": "% of roofline (sum of per-layer max(F/5.0 PFLOP/s, B_min/8 TB/s) / step time)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (2:4 fp16 weights x {0,1} spikes, fp32 accumulate, fp32 BN/LIF)",
+        "data": "synthetic (seeded Bernoulli spikes, N(0,2/fan_in) weights 2:4-pruned, random BN)",
+        "config": {
+            "workload": "BASELINE configs[1] layer sweep: 5 shapes x p{0.05,0.15,0.30}, T=4, batch 32, "
+                        "fp16 2:4 weights, 1-bit NHWC spikes in/out, LIF tau=2 V_th=1 hard reset",
+            "global_batch": BATCH, "timesteps": T_STEPS, "launches_per_step": len(work),
+            "step": "hipGraph replay of the 15 fused launches",
+            "tflops_dense_equiv": round(flops / step_s / 1e12, 2),
+            "per_layer_us": {wk["name"]: round(statistics.median(per[wk["name"]]) * 1e6, 2) for wk in work},
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(avg_flops / avg_launch / 1e12, 2),
+            "peak": P_SPARSE / 1e12,
+            "unit": "TFLOP/s",
+            "frac": round(avg_flops / avg_launch / P_SPARSE, 4),
+            "traffic": None,
+            "kernel": "fused_sparse_conv_bn_lif_kernel<4,BITS,BITS,1> (all 15 sweep launches)",
+            "avg_launch_us": round(avg_launch * 1e6, 3),
+            "note": "dense-equivalent FLOPs vs the 5.0 PFLOP/s 2:4 peak == useful FLOPs vs the 2.5 PFLOP/s dense peak",
+        },
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline()
+        result["cpu_baseline"] = {
+            "value": round(100.0 * ideal / cb["step_s"], 6),
+            "unit": result["unit"],
+            "cores": cb["threads"],
+            "kind": "port",
+            "sample": cb["sample"],
+            "ms_per_step": round(cb["step_s"] * 1e3, 2),
+            "cpu": cb["model"],
+            "cpu_count": cb["cpu_count"],
+            "gpu_speedup": round(cb["step_s"] / step_s, 1),
+        }
+    line = json.dumps(result)
+    print(line)
+    if args.json_out:
+        with open(args.json_out, "w") as f:
+            f.write(line + "\n")
+
+
+if __name__ == "__main__":
+    main()
