@@ -1,0 +1,253 @@
+"""Kernel-object contract: compile_all() -> {nid: kernel} (sengine/build/tilelang_compiler.py:404-491).
+
+Kernel objects are cached per shape key (tilelang_compiler.py:551-553) and called the way
+the reference runtime calls them (sengine/cuda_graph_runtime.py:616-643):
+
+    spikes = kern(data, weight, state, bn_scale, bn_bias)   # fused node with a membrane
+    spikes = kern(data, weight, bn_scale, bn_bias)          # no membrane: V0 = 0, not kept
+
+`data` is the reference's fp16 NHWC (T*B, H, W, C_in) activation or an int32 spike-bit
+tensor (T*B, H, W, C_in/32); the output uses the same encoding unless out_enc is given,
+and is freshly allocated like a TileLang out_idx=[-1] result.  `weight` may be the
+prepared SparseWeight blob (kern.prepare_weight) or the raw weight tensor in the
+runtime's (KH, KW, C_in, C_out) layout (cuda_graph_runtime.py:233-235) or torch's
+(C_out, C_in, KH, KW); raw tensors are compressed once and cached.
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import torch
+
+from . import ops
+from .ops import ENC_BITS, ENC_F16, ConvSpec, SEngineError
+
+FUSED_VARIANTS = {"FusedSparseConvBNLIF", "TileLangFusedConvBNIF", "TileLangFusedConv1x1BNIF"}
+DENSE_VARIANTS = {"TileLangConvBN", "TileLangConv1x1BN"}
+NEURON_VARIANTS = {"CUDAVec4LIF", "CUDAVec4IF"}
+
+
+class SparseWeight:
+    """One contiguous device blob [2:4 values | position metadata] for a fused node: a single
+    pointer carries both, which is what the 6-pointer call() ABI passes as `weight`."""
+
+    def __init__(self, spec: ConvSpec, blob: torch.Tensor, value_bytes: int):
+        self.spec = spec
+        self.blob = blob
+        self.value_bytes = value_bytes
+        self.values = blob[:value_bytes].view(torch.int16)
+        self.meta = blob[value_bytes:].view(torch.int32)
+
+    def data_ptr(self) -> int:
+        return self.blob.data_ptr()
+
+    @classmethod
+    def from_weight(cls, spec: ConvSpec, w: torch.Tensor, device=None, check_pattern=True) -> "SparseWeight":
+        if isinstance(w, np.ndarray):
+            w = torch.from_numpy(np.ascontiguousarray(w))
+        device = device or (w.device if w.is_cuda else torch.device("cuda"))
+        w = w.to(device).contiguous()
+        layout = _weight_layout(spec, w)
+        values, meta, _ = ops.compress_2_4(spec, w, layout, check_pattern=check_pattern)
+        vb = values.numel() * 2
+        blob = torch.empty(vb + meta.numel() * 4, dtype=torch.uint8, device=device)
+        blob[:vb].copy_(values.view(torch.uint8))
+        blob[vb:].copy_(meta.view(torch.uint8))
+        return cls(spec, blob, vb)
+
+
+def _weight_layout(spec: ConvSpec, w: torch.Tensor) -> int:
+    if tuple(w.shape) == (spec.C_out, spec.C_in, spec.KH, spec.KW):
+        return ops.WLAYOUT_OIHW
+    if tuple(w.shape) == (spec.KH, spec.KW, spec.C_in, spec.C_out):
+        return ops.WLAYOUT_HWIO
+    raise SEngineError(f"weight shape {tuple(w.shape)} matches neither OIHW nor HWIO for {spec}")
+
+
+class FusedSparseConvBNLIFKernel:
+    """The fused 2:4 Conv+BN+neuron node (one HIP launch per call)."""
+
+    def __init__(self, spec: ConvSpec, key: str):
+        self.spec = spec  # in_enc/out_enc of `spec` are ignored; chosen per call
+        self.key = key
+        self._wcache: dict = {}
+        self.OH, self.OW, self.M, self.K_red = ops.geometry(spec)
+
+    def spec_for(self, in_enc: int, out_enc: int) -> ConvSpec:
+        return dataclasses.replace(self.spec, in_enc=in_enc, out_enc=out_enc)
+
+    def prepare_weight(self, w, device=None) -> SparseWeight:
+        return SparseWeight.from_weight(self.spec, w, device)
+
+    def _weight(self, w) -> SparseWeight:
+        if isinstance(w, SparseWeight):
+            return w
+        if not isinstance(w, torch.Tensor):
+            raise TypeError("weight must be a SparseWeight or a torch.Tensor")
+        k = (w.data_ptr(), w._version, tuple(w.shape), w.dtype)
+        sw = self._wcache.get(k)
+        if sw is None:
+            sw = self.prepare_weight(w)
+            self._wcache = {k: sw}
+        return sw
+
+    def __call__(self, data: torch.Tensor, weight, *args, out_enc=None, out=None, h_trace=None, x_trace=None):
+        if len(args) == 3:
+            state, bn_scale, bn_bias = args
+        elif len(args) == 2:
+            state, (bn_scale, bn_bias) = None, args
+        else:
+            raise TypeError("call as kern(data, weight, state, bn_scale, bn_bias) or kern(data, weight, bn_scale, bn_bias)")
+        in_enc = ENC_BITS if data.dtype == torch.int32 else ENC_F16 if data.dtype == torch.float16 else None
+        if in_enc is None:
+            raise SEngineError("data must be fp16 NHWC or int32 spike bits")
+        spec = self.spec_for(in_enc, in_enc if out_enc is None else out_enc)
+        sw = self._weight(weight)
+        return ops.fused_sparse_conv_bn_lif(spec, data, sw.values, sw.meta, bn_scale, bn_bias, state=state, out=out,
+                                            h_trace=h_trace, x_trace=x_trace)
+
+
+class DenseConvBNKernel:
+    """Unfused fallback, Conv+BN half: kern(data, weight, bn_scale, bn_bias) -> fp32 (T*B, OH, OW, C_out)."""
+
+    def __init__(self, spec: ConvSpec, key: str):
+        self.spec = spec
+        self.key = key
+        self._wcache: dict = {}
+
+    def prepare_weight(self, w, device=None) -> torch.Tensor:
+        if isinstance(w, np.ndarray):
+            w = torch.from_numpy(np.ascontiguousarray(w))
+        device = device or (w.device if w.is_cuda else torch.device("cuda"))
+        w = w.to(device).contiguous()
+        return ops.pack_dense_weights(self.spec, w, _weight_layout(self.spec, w))
+
+    def __call__(self, data: torch.Tensor, weight, bn_scale, bn_bias, out=None):
+        in_enc = ENC_BITS if data.dtype == torch.int32 else ENC_F16 if data.dtype == torch.float16 else None
+        if in_enc is None:
+            raise SEngineError("data must be fp16 NHWC or int32 spike bits")
+        spec = dataclasses.replace(self.spec, in_enc=in_enc)
+        if isinstance(weight, torch.Tensor) and weight.dtype == torch.int16:
+            blob = weight
+        else:
+            k = (weight.data_ptr(), weight._version, tuple(weight.shape))
+            blob = self._wcache.get(k)
+            if blob is None:
+                blob = self.prepare_weight(weight)
+                self._wcache = {k: blob}
+        return ops.dense_conv_bn(spec, data, blob, bn_scale, bn_bias, out=out)
+
+
+class NeuronExt:
+    """Standalone temporal neuron with the torch-extension API the reference JIT-builds
+    (if_neuron / lif_neuron, sengine/csrc/green_context/if_neuron.cu:75-126):
+    input (T*S, F) or any (T*spatial...) tensor, membrane with `spatial` elements; T =
+    input.numel() / membrane.numel(); hard reset to 0; returns fp16 spikes shaped like input.
+    The membrane is updated in place with the final state."""
+
+    @staticmethod
+    def _run(inp, membrane, v_threshold, neuron, tau):
+        x = inp if inp.dtype == torch.float32 else inp.float()
+        x = x.contiguous()
+        n = membrane.numel()
+        if x.numel() % n:
+            raise SEngineError("input size must be a multiple of the membrane size")
+        T = x.numel() // n
+        s = ops.multistep_neuron(x, T, neuron, tau, v_threshold, 0.0, state=membrane, out_enc=ENC_F16)
+        return s.view(inp.shape)
+
+    def if_neuron(self, input, membrane, v_threshold=1.0):
+        return self._run(input, membrane, v_threshold, "if", 1.0)
+
+    def lif_neuron(self, input, membrane, v_threshold=1.0, recip_tau=0.5):
+        return self._run(input, membrane, v_threshold, "lif", 1.0 / float(recip_tau))
+
+
+_NEURON_EXT = NeuronExt()
+
+
+def get_cuda_if() -> NeuronExt:
+    """Name kept from tilelang_compiler.py (the neuron extension loader)."""
+    return _NEURON_EXT
+
+
+def _kname(node) -> str:
+    kv = node.assigned_kernel
+    return getattr(kv, "name", str(kv))
+
+
+def _neuron_params(ir, node):
+    ids = list(node.extra_attrs.get("absorbed_nids", [])) + list(ir.successors(node.id))
+    for nid in ids:
+        n = ir.nodes.get(nid)
+        if n is not None and getattr(n, "neuron_params", None) is not None:
+            return n.op_type.name, n.neuron_params
+    return None, None
+
+
+class SparseKernelCompiler:
+    """compile_all() for the nodes this build serves; mirrors TileLangCompiler's contract.
+
+    precision 'fp16': weights rounded to fp16 (one SMFMAC plane, the reference engine's
+    io dtype); 'fp32': fp32-faithful weights as an fp16 hi + lo pair (two planes)."""
+
+    def __init__(self, ir, batch_size: int = 1, precision: str = "fp16"):
+        if precision not in ("fp16", "fp32"):
+            raise ValueError("precision must be 'fp16' or 'fp32'")
+        self.ir = ir
+        self.T = int(getattr(ir, "T", 4) or 4)
+        self.B = int(batch_size)
+        self.precision = precision
+        self._kernel_cache: dict = {}
+
+    def _spec(self, node, neuron_kind, np_) -> ConvSpec:
+        cp = node.conv_params
+        N, C, H, W = node.input_shapes[0]
+        if N != self.T * self.B:
+            raise SEngineError(f"node {node.name}: input batch {N} != T*B = {self.T * self.B}")
+        if cp.stride_h != cp.stride_w or cp.pad_h != cp.pad_w or cp.dilation_h != cp.dilation_w or cp.groups != 1:
+            raise SEngineError(f"node {node.name}: only square stride/pad/dilation and groups=1 are supported")
+        is_lif = neuron_kind == "LIF"
+        hard = True if np_ is None else bool(np_.hard_reset)
+        return ConvSpec(T=self.T, B=self.B, C_in=cp.in_channels, H=H, W=W, C_out=cp.out_channels,
+                        KH=cp.kernel_h, KW=cp.kernel_w, stride=cp.stride_h, padding=cp.pad_h,
+                        dilation=cp.dilation_h, neuron="lif" if is_lif else "if", hard_reset=hard,
+                        tau=float(np_.tau) if (np_ is not None and is_lif) else 2.0,
+                        v_threshold=float(np_.v_threshold) if np_ is not None else 1.0,
+                        v_reset=float(np_.v_reset) if np_ is not None else 0.0,
+                        weight_planes=1 if self.precision == "fp16" else 2)
+
+    def compile_all(self, skip_nids=None) -> dict:
+        skip = skip_nids or set()
+        kernels = {}
+        for nid in self.ir.topo_order:
+            if nid in skip:
+                continue
+            node = self.ir.nodes[nid]
+            name = _kname(node)
+            if name in FUSED_VARIANTS:
+                if not node.sparse_weight:
+                    raise SEngineError(f"node {node.name}: {name} needs 2:4 weights on this build "
+                                       "(dense weights take the TileLangConvBN + neuron fallback)")
+                kind, np_ = _neuron_params(self.ir, node)
+                spec = self._spec(node, kind or "IF", np_)
+                key = f"sparse_{spec}_{self.precision}"
+                kern = self._kernel_cache.get(key)
+                if kern is None:
+                    kern = FusedSparseConvBNLIFKernel(spec, key)
+                    self._kernel_cache[key] = kern
+                node.tilelang_config = {"kernel": "fused_sparse_conv_bn_lif", "T": self.T, "waves": 4,
+                                        "tile_channels": 64, "tile_positions": 64}
+                kernels[nid] = kern
+            elif name in DENSE_VARIANTS:
+                spec = self._spec(node, "IF", None)
+                key = f"dense_{spec}_{self.precision}"
+                kern = self._kernel_cache.get(key)
+                if kern is None:
+                    kern = DenseConvBNKernel(spec, key)
+                    self._kernel_cache[key] = kern
+                kernels[nid] = kern
+            elif name in NEURON_VARIANTS:
+                kernels[nid] = get_cuda_if()
+        return kernels
