@@ -85,6 +85,14 @@ int sengine_amd_version(void);
 /* Human-readable description of the last negative return on this thread. */
 const char* sengine_amd_last_error(void);
 
+/*
+ * Kernel selection for sengine_amd_fused_sparse_conv_bn_lif with spike-bit input:
+ * 0 = automatic (LDS-staged kernel, the default), 1 = direct-gather kernel (the kernel
+ * fp16 inputs always use).  Process-wide; the environment variable
+ * SENGINE_AMD_FUSED_KERNEL=direct sets 1 at load time.  Both give identical results.
+ */
+int sengine_amd_set_fused_kernel(int32_t choice);
+
 /* Output spatial size, M = B*OH*OW rows per timestep and K_red = KH*KW*C_in. */
 int sengine_amd_conv_geometry(const sengine_conv_lif_desc* d, int32_t* OH, int32_t* OW,
                               int64_t* M_per_t, int64_t* K_red);

@@ -40,6 +40,7 @@ _SZP = ctypes.POINTER(ctypes.c_size_t)
 SIGNATURES = {
     "sengine_amd_version": (ctypes.c_int, []),
     "sengine_amd_last_error": (ctypes.c_char_p, []),
+    "sengine_amd_set_fused_kernel": (ctypes.c_int, [_I32]),
     "sengine_amd_conv_geometry": (ctypes.c_int, [_DP, ctypes.POINTER(_I32), ctypes.POINTER(_I32),
                                                  ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "sengine_amd_sparse_blob_bytes": (ctypes.c_int, [_DP, _SZP, _SZP]),

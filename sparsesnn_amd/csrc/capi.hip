@@ -1,5 +1,6 @@
 // Host-side C-ABI utilities: versioning, error strings, geometry and blob sizes.
 #include <math.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -40,6 +41,16 @@ int check_desc(const sengine_conv_lif_desc* d, Geometry* geo, bool sparse) {
   return 0;
 }
 
+static int g_kernel_choice = -1;
+
+int fused_kernel_choice() {
+  if (g_kernel_choice < 0) {
+    const char* e = getenv("SENGINE_AMD_FUSED_KERNEL");
+    g_kernel_choice = (e && strcmp(e, "direct") == 0) ? 1 : 0;
+  }
+  return g_kernel_choice;
+}
+
 NeuronParams make_neuron_params(int neuron, int hard_reset, float tau, float vth, float vreset) {
   NeuronParams np;
   np.neuron = neuron;
@@ -76,6 +87,12 @@ using namespace sengine;
 extern "C" int sengine_amd_version(void) { return 100; }
 
 extern "C" const char* sengine_amd_last_error(void) { return g_last_error; }
+
+extern "C" int sengine_amd_set_fused_kernel(int32_t choice) {
+  if (choice != 0 && choice != 1) return set_error(-2, "set_fused_kernel: choice must be 0 (auto) or 1 (direct)");
+  g_kernel_choice = choice;
+  return 0;
+}
 
 extern "C" int sengine_amd_conv_geometry(const sengine_conv_lif_desc* d, int32_t* OH, int32_t* OW,
                                          int64_t* M_per_t, int64_t* K_red) {

@@ -23,6 +23,7 @@
 // its 64-channel group: the epilogue then forms 16 spike bits per lane with no
 // cross-lane traffic.
 #include "common.h"
+#include "epilogue.h"
 #include "internal.h"
 
 namespace sengine {
@@ -123,64 +124,8 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
 
   // ---- epilogue: folded BN + T-step neuron, all in registers ----
   if (!mvalid) return;
-  const int cob = G * 64 + g * 16;  // this lane's 16 output channels
-  const NeuronParams np = p.np;
-  float sc[16], bi[16], xs[16], v[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float s = p.scale[cob + j] * p.enc_scale;  // exact: enc_scale is a power of two
-    const float bb = p.bias[cob + j];
-    sc[j] = s;
-    bi[j] = bb;
-    xs[j] = 0.f;
-  }
-  const bool fold = np.neuron == SENGINE_NEURON_LIF && np.pow2;
-  float fsc[16], fbi[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    fsc[j] = fold ? sc[j] * np.rtau : sc[j];
-    fbi[j] = fold ? bi[j] * np.rtau : bi[j];
-  }
-  float* st = p.state ? p.state + (size_t)m * p.F + cob : nullptr;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = st ? st[j] : 0.f;
-
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    uint32_t word = 0;
-    const size_t row = ((size_t)t * p.M + m) * p.F + cob;
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = 4 * a + i;
-        const float accv = acc[t][a][i];
-        const float xin = __builtin_fmaf(accv, fsc[j], fbi[j]);
-        const float h = neuron_charge(np, v[j], xin);
-        const bool spike = h >= np.vth;
-        word |= (uint32_t)spike << j;
-        v[j] = neuron_reset(np, h, spike);
-        if (p.h_trace) p.h_trace[row + j] = h;
-        if (p.x_trace) p.x_trace[row + j] = fold ? __builtin_fmaf(accv, sc[j], bi[j]) : xin;
-      }
-    if (OUT_ENC == SENGINE_ENC_BITS) {
-      *reinterpret_cast<uint16_t*>(p.out + (row >> 3)) = (uint16_t)word;
-    } else {
-      half8_t o0, o1;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        o0[j] = (word >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
-        o1[j] = (word >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
-      }
-      half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(p.out) + row);
-      dst[0] = o0;
-      dst[1] = o1;
-    }
-  }
-  if (st) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) st[j] = v[j];
-  }
+  lif_epilogue<T, OUT_ENC, EPI_GENERIC>(acc, m, p.M, p.F, G * 64 + g * 16, p.np, p.scale, p.bias, p.enc_scale,
+                                        p.state, p.out, p.h_trace, p.x_trace);
 }
 
 template <int T, int IN_ENC, int OUT_ENC, int PLANES>
@@ -227,6 +172,11 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
   if (d->out_enc != SENGINE_ENC_BITS && d->out_enc != SENGINE_ENC_F16)
     return set_error(-2, "fused_sparse_conv_bn_lif: out_enc must be BITS or F16");
   if (geo.M > (1ll << 30)) return set_error(-2, "fused_sparse_conv_bn_lif: B*OH*OW too large");
+
+  if (d->in_enc == SENGINE_ENC_BITS && fused_kernel_choice() == 0) {
+    const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace};
+    return (int)launch_fused_bits_lds(d, geo, args, stream);
+  }
 
   FusedParams p;
   p.in = static_cast<const uint8_t*>(data);

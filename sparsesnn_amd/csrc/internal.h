@@ -23,4 +23,26 @@ int check_desc(const sengine_conv_lif_desc* d, Geometry* geo, bool sparse);
 // decay = float(1.0 - 1.0/tau) computed in double (models/neurons.py:124).
 NeuronParams make_neuron_params(int neuron, int hard_reset, float tau, float vth, float vreset);
 
+// Pointers of one fused call (already validated).
+struct FusedArgs {
+  const void* data;
+  const void* wvals;
+  const void* wmeta;
+  float* state;
+  const float* scale;
+  const float* bias;
+  void* out;
+  float* h_trace;
+  float* x_trace;
+};
+
+// LDS-staged kernel for spike-bit inputs (fused_sparse_lds.hip).
+hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+                                 hipStream_t stream);
+
+// Kernel selection for the fused op: 0 = automatic (LDS-staged kernel for bit inputs),
+// 1 = always the direct-gather kernel.  Read once from SENGINE_AMD_FUSED_KERNEL
+// ("auto" | "direct").
+int fused_kernel_choice();
+
 }  // namespace sengine

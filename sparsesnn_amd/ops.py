@@ -18,7 +18,7 @@ from ._lib import (ENC_BITS, ENC_F16, ENC_F32, NEURON_IF, NEURON_LIF, WLAYOUT_HW
                    ConvLifDesc, SEngineError, check)
 
 __all__ = [
-    "ConvSpec", "make_desc", "geometry", "compress_2_4", "pack_dense_weights", "pack_spikes",
+    "ConvSpec", "make_desc", "geometry", "set_fused_kernel", "compress_2_4", "pack_dense_weights", "pack_spikes",
     "unpack_spikes", "fused_sparse_conv_bn_lif", "dense_conv_bn", "multistep_neuron", "SEngineError",
     "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
 ]
@@ -87,6 +87,12 @@ def make_desc(s: ConvSpec) -> ConvLifDesc:
         neuron=NEURON_LIF if s.neuron == "lif" else NEURON_IF, hard_reset=int(bool(s.hard_reset)),
         tau=float(s.tau), v_threshold=float(s.v_threshold), v_reset=float(s.v_reset),
         in_enc=s.in_enc, out_enc=s.out_enc, weight_planes=s.weight_planes)
+
+
+def set_fused_kernel(choice: str) -> None:
+    """'auto' (LDS-staged kernel for spike-bit inputs) or 'direct' (direct-gather kernel)."""
+    lib = _lib.load()
+    check(lib.sengine_amd_set_fused_kernel({"auto": 0, "direct": 1}[choice]), "set_fused_kernel")
 
 
 def geometry(s: ConvSpec):

@@ -115,3 +115,20 @@ def test_hwio_layout(dev):
     case = ref.make_layer_case(31, T=4, B=1, C_in=64, C_out=64, H=8, W=8, k=3, fp16_weights=True)
     rep, _, _, _ = run_case(dev, case, layout=ops.WLAYOUT_HWIO)
     assert rep.ok, str(rep)
+
+
+@pytest.mark.parametrize("kernel", ["direct", "auto"])
+@pytest.mark.parametrize("k,stride,pad,B,C_in,C_out,H,W", [(3, 1, 1, 5, 64, 128, 13, 11), (3, 2, 1, 3, 128, 64, 15, 9),
+                                                           (1, 1, 0, 2, 256, 192, 7, 7), (1, 2, 0, 2, 64, 64, 9, 10)])
+def test_bit_kernels_agree_and_match_oracle(dev, kernel, k, stride, pad, B, C_in, C_out, H, W):
+    """Both spike-bit kernels (LDS-staged and direct-gather) against the oracle, on shapes whose
+    position count is not a multiple of the workgroup tile."""
+    ops.set_fused_kernel(kernel)
+    try:
+        case = ref.make_layer_case(40 + k + stride + B, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
+                                   stride=stride, padding=pad, fp16_weights=True)
+        rep, x_err, _, v_fin = run_case(dev, case)
+        assert rep.ok, str(rep)
+        assert x_err < 1e-4
+    finally:
+        ops.set_fused_kernel("auto")
