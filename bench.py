@@ -229,7 +229,8 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(avg_flops / avg_launch / P_SPARSE, 4),
             "traffic": None,
-            "kernel": "fused_sparse_conv_bn_lif_kernel<4,BITS,BITS,1> (all 15 sweep launches)",
+            "kernel": "sengine::fused_sparse_lds_kernel<T=4,...> (spike-bit LDS-staged kernel; "
+                      "mean over all 15 sweep launches)",
             "avg_launch_us": round(avg_launch * 1e6, 3),
             "note": "dense-equivalent FLOPs vs the 5.0 PFLOP/s 2:4 peak == useful FLOPs vs the 2.5 PFLOP/s dense peak",
         },

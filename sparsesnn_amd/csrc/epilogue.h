@@ -18,6 +18,37 @@ namespace sengine {
 
 enum { EPI_GENERIC = 0, EPI_LIF_HARD = 1, EPI_IF_HARD = 2 };
 
+// One hard-reset fire step: spike = h >= v_th (VCC), v = spike ? v_reset : h, and the spike
+// shifted into `word` as its new lowest bit (word = 2*word + spike, with VCC as carry-in).
+// Three VALU ops; the compiler's form needs a separate select to materialise the bit.
+__device__ __forceinline__ void fire_hard(float h, float vth, float vreset, float& v, uint32_t& word) {
+  asm("v_cmp_le_f32_e32 vcc, %[th], %[h]\n\t"
+      "v_cndmask_b32_e32 %[v], %[h], %[vr], vcc\n\t"
+      "v_addc_co_u32_e32 %[w], vcc, %[w], %[w], vcc"
+      : [v] "=&v"(v), [w] "+v"(word)
+      : [h] "v"(h), [th] "s"(vth), [vr] "v"(vreset)
+      : "vcc");
+}
+
+// Same without the reset (last timestep, membrane not kept).
+__device__ __forceinline__ void fire_only(float h, float vth, uint32_t& word) {
+  asm("v_cmp_le_f32_e32 vcc, %[th], %[h]\n\t"
+      "v_addc_co_u32_e32 %[w], vcc, %[w], %[w], vcc"
+      : [w] "+v"(word)
+      : [h] "v"(h), [th] "s"(vth)
+      : "vcc");
+}
+
+// Per-lane BN coefficients for its 16 channels: folded scale/bias (x/tau folded in for the
+// power-of-two LIF case, spike encoding factor folded into the scale) and the unfolded
+// pair (for the BN-output trace).
+struct EpiCoeffs {
+  const float* fsc;
+  const float* fbi;
+  const float* sc;
+  const float* bi;
+};
+
 __host__ __device__ inline int epilogue_mode(const NeuronParams& np, bool traces) {
   if (traces || !np.hard_reset) return EPI_GENERIC;
   if (np.neuron == SENGINE_NEURON_LIF && np.pow2) return EPI_LIF_HARD;
@@ -25,69 +56,63 @@ __host__ __device__ inline int epilogue_mode(const NeuronParams& np, bool traces
   return EPI_GENERIC;
 }
 
+// `valid` false (a padding position past M) computes but stores nothing: keeping the call
+// unconditional avoids a divergent branch whose join reshuffles the accumulators.
 template <int T, int OUT_ENC, int MODE>
-__device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], int m, int M, int F, int cob,
-                                             const NeuronParams& np, const float* __restrict__ scale,
-                                             const float* __restrict__ bias, float enc_scale, float* state,
+__device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool valid, int m, int M, int F, int cob,
+                                             const NeuronParams& np, const EpiCoeffs& cf, float* state,
                                              uint8_t* __restrict__ out, float* h_trace, float* x_trace) {
-  float sc[16], bi[16], fsc[16], fbi[16], v[16];
+  float fsc[16], fbi[16], v[16];
   const bool fold = MODE == EPI_LIF_HARD || (MODE == EPI_GENERIC && np.neuron == SENGINE_NEURON_LIF && np.pow2);
 #pragma unroll
   for (int j = 0; j < 16; j += 4) {
-    const float4_t s4 = *reinterpret_cast<const float4_t*>(scale + cob + j);
-    const float4_t b4 = *reinterpret_cast<const float4_t*>(bias + cob + j);
+    const float4_t s4 = *reinterpret_cast<const float4_t*>(cf.fsc + j);
+    const float4_t b4 = *reinterpret_cast<const float4_t*>(cf.fbi + j);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      sc[j + e] = s4[e] * enc_scale;  // exact: enc_scale is a power of two
-      bi[j + e] = b4[e];
+      fsc[j + e] = s4[e];
+      fbi[j + e] = b4[e];
     }
-  }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    fsc[j] = fold ? sc[j] * np.rtau : sc[j];  // exact: rtau is a power of two when fold
-    fbi[j] = fold ? bi[j] * np.rtau : bi[j];
   }
   float* st = state ? state + (size_t)m * F + cob : nullptr;
   const bool has_state = st != nullptr;
-  if (has_state) {
 #pragma unroll
-    for (int j = 0; j < 16; j += 4) {
-      const float4_t v4 = *reinterpret_cast<const float4_t*>(st + j);
+  for (int j = 0; j < 16; j += 4) {
+    float4_t v4 = float4_t{0.f, 0.f, 0.f, 0.f};
+    if (has_state && valid) v4 = *reinterpret_cast<const float4_t*>(st + j);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[j + e] = v4[e];
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = 0.f;
+    for (int e = 0; e < 4; ++e) v[j + e] = v4[e];
   }
+  const float vreset = np.vreset;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     uint32_t word = 0;
     const size_t row = ((size_t)t * M + m) * F + cob;
+    if (MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD) {
+      // Branch-free: with no state v starts at 0 and fma(0, decay, x) == x exactly; the
+      // reset is computed at every step (the last one is simply not stored).  Channels
+      // 15..0 so that channel j ends in bit j of the shifted-in word.
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float accv = acc[t][j >> 2][j & 3];
-      const float xin = __builtin_fmaf(accv, fsc[j], fbi[j]);
-      float h;
-      bool spike;
-      if (MODE == EPI_LIF_HARD) {
-        // v*decay is exact (decay a power of two): one rounding, as v*decay + x/tau
-        h = (t == 0 && !has_state) ? xin : __builtin_fmaf(v[j], np.decay, xin);
-        spike = h >= np.vth;
-        if (t + 1 < T || has_state) v[j] = spike ? np.vreset : h;
-      } else if (MODE == EPI_IF_HARD) {
-        h = (t == 0 && !has_state) ? xin : __fadd_rn(v[j], xin);
-        spike = h >= np.vth;
-        if (t + 1 < T || has_state) v[j] = spike ? np.vreset : h;
-      } else {
-        h = neuron_charge(np, v[j], xin);
-        spike = h >= np.vth;
-        v[j] = neuron_reset(np, h, spike);
-        if (h_trace) h_trace[row + j] = h;
-        if (x_trace) x_trace[row + j] = fold ? __builtin_fmaf(accv, sc[j], bi[j]) : xin;
+      for (int j = 15; j >= 0; --j) {
+        const float xin = __builtin_fmaf(acc[t][j >> 2][j & 3], fsc[j], fbi[j]);
+        const float h = MODE == EPI_LIF_HARD ? __builtin_fmaf(v[j], np.decay, xin)  // v*decay exact: one rounding
+                                             : __fadd_rn(v[j], xin);
+        fire_hard(h, np.vth, vreset, v[j], word);
       }
-      word |= (uint32_t)spike << j;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float accv = acc[t][j >> 2][j & 3];
+        const float xin = __builtin_fmaf(accv, fsc[j], fbi[j]);
+        const float h = neuron_charge(np, v[j], xin);
+        const bool spike = h >= np.vth;
+        v[j] = neuron_reset(np, h, spike);
+        if (h_trace && valid) h_trace[row + j] = h;
+        if (x_trace && valid) x_trace[row + j] = fold ? __builtin_fmaf(accv, cf.sc[j], cf.bi[j]) : xin;
+        word |= (uint32_t)spike << j;
+      }
     }
+    if (!valid) continue;
     if (OUT_ENC == SENGINE_ENC_BITS) {
       *reinterpret_cast<uint16_t*>(out + (row >> 3)) = (uint16_t)word;
     } else {
@@ -102,7 +127,7 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], int m,
       dst[1] = o1;
     }
   }
-  if (has_state) {
+  if (has_state && valid) {
 #pragma unroll
     for (int j = 0; j < 16; j += 4) *reinterpret_cast<float4_t*>(st + j) = float4_t{v[j], v[j + 1], v[j + 2], v[j + 3]};
   }

@@ -54,6 +54,20 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
   const int col = lane & 15;
   const int G = blockIdx.y;  // 64-channel output group
   const int m = blockIdx.x * 64 + wave * 16 + col;
+  // folded BN coefficients of the workgroup's 64 channels (see epilogue.h)
+  __shared__ float sCoef[4][64];
+  {
+    const bool fold = p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2;
+    if (threadIdx.x < 64) {
+      const float sc = p.scale[G * 64 + threadIdx.x] * p.enc_scale;
+      const float bi = p.bias[G * 64 + threadIdx.x];
+      sCoef[0][threadIdx.x] = fold ? sc * p.np.rtau : sc;
+      sCoef[1][threadIdx.x] = fold ? bi * p.np.rtau : bi;
+      sCoef[2][threadIdx.x] = sc;
+      sCoef[3][threadIdx.x] = bi;
+    }
+    __syncthreads();
+  }
   const bool mvalid = m < p.M;
   int b = 0, oh = 0, ow = 0;
   if (mvalid) {
@@ -124,8 +138,9 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
 
   // ---- epilogue: folded BN + T-step neuron, all in registers ----
   if (!mvalid) return;
-  lif_epilogue<T, OUT_ENC, EPI_GENERIC>(acc, m, p.M, p.F, G * 64 + g * 16, p.np, p.scale, p.bias, p.enc_scale,
-                                        p.state, p.out, p.h_trace, p.x_trace);
+  const EpiCoeffs cf{&sCoef[0][g * 16], &sCoef[1][g * 16], &sCoef[2][g * 16], &sCoef[3][g * 16]};
+  lif_epilogue<T, OUT_ENC, EPI_GENERIC>(acc, true, m, p.M, p.F, G * 64 + g * 16, p.np, cf, p.state, p.out,
+                                        p.h_trace, p.x_trace);
 }
 
 template <int T, int IN_ENC, int OUT_ENC, int PLANES>
@@ -173,7 +188,8 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
     return set_error(-2, "fused_sparse_conv_bn_lif: out_enc must be BITS or F16");
   if (geo.M > (1ll << 30)) return set_error(-2, "fused_sparse_conv_bn_lif: B*OH*OW too large");
 
-  if (d->in_enc == SENGINE_ENC_BITS && fused_kernel_choice() == 0) {
+  // LDS-staged kernel for bit inputs (its per-thread tap mask holds up to 64 taps)
+  if (d->in_enc == SENGINE_ENC_BITS && fused_kernel_choice() == 0 && d->KH * d->KW <= 64) {
     const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace};
     return (int)launch_fused_bits_lds(d, geo, args, stream);
   }

@@ -39,7 +39,7 @@ struct LdsParams {
   uint8_t* out;
   float* h_trace;
   float* x_trace;
-  int B, C, H, W, F, KW, SH, SW, PH, PW, DH, DW, OH, OW;
+  int B, C, H, W, F, KH, KW, SH, SW, PH, PW, DH, DW, OH, OW;
   int M, nq;
   int64_t in_t_bytes;  // bytes of one timestep of input spike bits
   NeuronParams np;
@@ -52,11 +52,11 @@ __device__ __forceinline__ uint2 interleave_bytes(uint2 w) {
 }
 
 // Registers holding one chunk's staged data between its global load and its LDS store.
-template <int NW, int PL>
+template <int NW, int GPW, int PL>
 struct StageRegs {
   uint2 bw[NW];
-  u32x4_t aw[PL];
-  uint32_t mw;
+  u32x4_t aw[GPW][PL];
+  uint32_t mw[GPW];
 };
 
 // Workgroup order: hardware dispatches consecutive workgroup ids round-robin over the 8
@@ -68,22 +68,37 @@ __device__ __forceinline__ int xcd_tile(int id, int n) {
   return (id & 7) * per + (id >> 3);
 }
 
-template <int T, int PT, int PL, int OUT_ENC, int MODE>
+// T timesteps, PT*64 positions per workgroup, GPW 64-channel output groups per wave,
+// PL weight planes, output encoding, epilogue mode, CPS reduction chunks per LDS stage.
+template <int T, int PT, int GPW, int PL, int OUT_ENC, int MODE, int CPS>
 __global__ __launch_bounds__(256) void fused_sparse_lds_kernel(LdsParams p) {
   constexpr int NPOS = 64 * PT;                  // positions per workgroup
   constexpr int TSTEP = 256 / NPOS;              // timesteps covered by one pass of 256 threads
   constexpr int NW = (T + TSTEP - 1) / TSTEP;    // spike words staged per thread per chunk
-  __shared__ uint2 sB[2][T][NPOS];
-  __shared__ u32x4_t sA[2][PL][256];
-  __shared__ uint32_t sM[2][256];
+  constexpr int NCH = 64 * GPW;                  // output channels per workgroup
+  __shared__ uint2 sB[2][CPS][T][NPOS];
+  __shared__ u32x4_t sA[2][CPS][GPW][PL][256];
+  __shared__ uint32_t sM[2][CPS][GPW][256];
+  __shared__ float sCoef[4][NCH];                // folded scale, folded bias, scale, bias
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int g = lane >> 4;
   const int col = lane & 15;
-  const int G = blockIdx.y;
+  const int G0 = blockIdx.y * GPW;  // first 64-channel output group of this workgroup
   const int m0 = xcd_tile(blockIdx.x, gridDim.x) * NPOS;
+
+  // Folded BN coefficients of this workgroup's channels (written before the first barrier).
+  const bool fold = MODE == EPI_LIF_HARD || (MODE == EPI_GENERIC && p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2);
+  if (tid < NCH) {
+    const float sc = p.scale[G0 * 64 + tid] * p.enc_scale;  // exact: enc_scale is a power of two
+    const float bi = p.bias[G0 * 64 + tid];
+    sCoef[0][tid] = fold ? sc * p.np.rtau : sc;             // exact: rtau is a power of two
+    sCoef[1][tid] = fold ? bi * p.np.rtau : bi;
+    sCoef[2][tid] = sc;
+    sCoef[3][tid] = bi;
+  }
 
   // ---- staging identity: one position, timesteps st0, st0+TSTEP, ...
   const int spos = tid % NPOS;
@@ -101,137 +116,198 @@ __global__ __launch_bounds__(256) void fused_sparse_lds_kernel(LdsParams p) {
   const int ih0 = soh * p.SH - p.PH;
   const int iw0 = sow * p.SW - p.PW;
   const int cbytes = p.C >> 3;
-  const u32x4_t* wv = p.wvals + (size_t)G * p.nq * PL * 256 + tid;
-  const uint32_t* wm = p.wmeta + (size_t)G * p.nq * 256 + tid;
-
-  // chunk counters of the next chunk to load: q = (kr, ks, c0), uniform in the workgroup
-  int lq = 0, kr = 0, ks = 0, c0 = 0;
-  auto load_next = [&](StageRegs<NW, PL>& R) {
-    if (lq < p.nq) {
+  // Taps whose input pixel lies inside the image (bit kr*KW + ks; KH*KW <= 64).
+  uint64_t tapmask = 0;
+  if (svalid)
+    for (int kr = 0; kr < p.KH; ++kr) {
       const int ih = ih0 + kr * p.DH;
-      const int iw = iw0 + ks * p.DW;
-      const bool ok = svalid && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
-      const int64_t base = (((int64_t)sb * p.H + ih) * p.W + iw) * cbytes + (c0 >> 3);
+      if (ih < 0 || ih >= p.H) continue;
+      for (int ks = 0; ks < p.KW; ++ks) {
+        const int iw = iw0 + ks * p.DW;
+        if (iw >= 0 && iw < p.W) tapmask |= 1ull << (kr * p.KW + ks);
+      }
+    }
+  // Byte offset of tap (0, 0), channel 0, timestep st0 (only dereferenced for valid taps).
+  const int64_t off00 = (((int64_t)sb * p.H + ih0) * p.W + iw0) * cbytes + (int64_t)st0 * p.in_t_bytes;
+  const int64_t dks = (int64_t)p.DW * cbytes;                       // next tap in a kernel row
+  const int64_t dkr = (int64_t)p.DH * p.W * cbytes - p.KW * dks;     // wrap to the next kernel row
+  const int64_t tstride = (int64_t)TSTEP * p.in_t_bytes;
+
+  const u32x4_t* wv = p.wvals + (size_t)G0 * p.nq * PL * 256 + tid;
+  const uint32_t* wm = p.wmeta + (size_t)G0 * p.nq * 256 + tid;
+  const size_t wv_group = (size_t)p.nq * PL * 256, wm_group = (size_t)p.nq * 256;
+
+  // counters of the next chunk to load: q = (tap, c0), uniform in the workgroup
+  int lq = 0, tap = 0, ks = 0, c0 = 0;
+  int64_t tap_off = 0;
+  auto load_chunk = [&](StageRegs<NW, GPW, PL>& R) {
+    if (lq < p.nq) {
+      const bool ok = (tapmask >> tap) & 1;
+      const int64_t base = off00 + tap_off + (c0 >> 3);
 #pragma unroll
       for (int k = 0; k < NW; ++k) {
-        const int t = st0 + k * TSTEP;
         R.bw[k] = uint2{0u, 0u};
-        if (ok && t < T) R.bw[k] = *reinterpret_cast<const uint2*>(p.in + base + t * p.in_t_bytes);
+        if (ok && st0 + k * TSTEP < T) R.bw[k] = *reinterpret_cast<const uint2*>(p.in + base + k * tstride);
       }
 #pragma unroll
-      for (int pl = 0; pl < PL; ++pl) R.aw[pl] = wv[((size_t)lq * PL + pl) * 256];
-      R.mw = wm[(size_t)lq * 256];
+      for (int gg = 0; gg < GPW; ++gg) {
+#pragma unroll
+        for (int pl = 0; pl < PL; ++pl) R.aw[gg][pl] = wv[gg * wv_group + ((size_t)lq * PL + pl) * 256];
+        R.mw[gg] = wm[gg * wm_group + (size_t)lq * 256];
+      }
       c0 += 64;
       if (c0 == p.C) {
         c0 = 0;
+        ++tap;
+        tap_off += dks;
         if (++ks == p.KW) {
           ks = 0;
-          ++kr;
+          tap_off += dkr;
         }
       }
     }
     ++lq;
   };
-  auto store_stage = [&](const StageRegs<NW, PL>& R, int buf) {
+  auto store_chunk = [&](const StageRegs<NW, GPW, PL>& R, int buf, int c) {
 #pragma unroll
     for (int k = 0; k < NW; ++k) {
       const int t = st0 + k * TSTEP;
-      if (t < T) sB[buf][t][spos] = interleave_bytes(R.bw[k]);
+      if (t < T) sB[buf][c][t][spos] = interleave_bytes(R.bw[k]);
     }
 #pragma unroll
-    for (int pl = 0; pl < PL; ++pl) sA[buf][pl][tid] = R.aw[pl];
-    sM[buf][tid] = R.mw;
+    for (int gg = 0; gg < GPW; ++gg) {
+#pragma unroll
+      for (int pl = 0; pl < PL; ++pl) sA[buf][c][gg][pl][tid] = R.aw[gg][pl];
+      sM[buf][c][gg][tid] = R.mw[gg];
+    }
   };
 
-  float4_t acc[PT][T][4];
+  float4_t acc[PT][GPW][T][4];
 #pragma unroll
   for (int pp = 0; pp < PT; ++pp)
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+    for (int gg = 0; gg < GPW; ++gg)
 #pragma unroll
-      for (int a = 0; a < 4; ++a) acc[pp][t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) acc[pp][gg][t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   const int wpos = wave * 16 * PT + col;
-  auto compute = [&](int buf) {
-    half8_t av[PL][4];
-    uint32_t ix[4];
+  auto compute = [&](int buf, int c) {
+    half8_t av[GPW][PL][4];
+    uint32_t ix[GPW][4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
+    for (int gg = 0; gg < GPW; ++gg)
 #pragma unroll
-      for (int pl = 0; pl < PL; ++pl) av[pl][a] = __builtin_bit_cast(half8_t, sA[buf][pl][a * 64 + lane]);
-      ix[a] = sM[buf][a * 64 + lane];
-    }
+      for (int a = 0; a < 4; ++a) {
+#pragma unroll
+        for (int pl = 0; pl < PL; ++pl)
+          av[gg][pl][a] = __builtin_bit_cast(half8_t, sA[buf][c][gg][pl][a * 64 + lane]);
+        ix[gg][a] = sM[buf][c][gg][a * 64 + lane];
+      }
     uint32_t xb[T][PT];
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int pp = 0; pp < PT; ++pp)
-        xb[t][pp] = reinterpret_cast<const uint16_t*>(&sB[buf][t][wpos + 16 * pp])[g];
+        xb[t][pp] = reinterpret_cast<const uint16_t*>(&sB[buf][c][t][wpos + 16 * pp])[g];
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int pp = 0; pp < PT; ++pp) {
         const half16_t bf = expand_bits16(xb[t][pp]);
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int gg = 0; gg < GPW; ++gg)
 #pragma unroll
-          for (int pl = 0; pl < PL; ++pl)
-            acc[pp][t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(av[pl][a], bf, acc[pp][t][a], ix[a], 0, 0);
+          for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int pl = 0; pl < PL; ++pl)
+              acc[pp][gg][t][a] =
+                  __builtin_amdgcn_smfmac_f32_16x16x64_f16(av[gg][pl][a], bf, acc[pp][gg][t][a], ix[gg][a], 0, 0);
       }
   };
 
-  // Double-buffered LDS: the global loads of chunk q+1 are issued before chunk q is
-  // multiplied and written to the other buffer after it.
-  StageRegs<NW, PL> R;
-  load_next(R);
-  store_stage(R, 0);
+  // Double-buffered LDS stages of CPS chunks: the global loads of stage s+1 are issued
+  // before stage s is multiplied and written to the other buffer after it.  (A two-stage
+  // deep register prefetch measured slower: the second register set costs occupancy.)
+  StageRegs<NW, GPW, PL> R[CPS];
+#pragma unroll
+  for (int c = 0; c < CPS; ++c) load_chunk(R[c]);
+#pragma unroll
+  for (int c = 0; c < CPS; ++c) store_chunk(R[c], 0, c);
   __syncthreads();
-  for (int q = 0; q < p.nq; ++q) {
-    const bool more = q + 1 < p.nq;
-    if (more) load_next(R);
-    compute(q & 1);
-    if (more) store_stage(R, (q & 1) ^ 1);
+  const int nstage = (p.nq + CPS - 1) / CPS;
+  for (int st = 0; st < nstage; ++st) {
+    const int buf = st & 1;
+    const bool more = st + 1 < nstage;
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < CPS; ++c) load_chunk(R[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < CPS; ++c)
+      if (c == 0 || st * CPS + c < p.nq) compute(buf, c);
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < CPS; ++c) store_chunk(R[c], buf ^ 1, c);
+    }
     __syncthreads();
   }
 
-  const int cob = G * 64 + g * 16;
 #pragma unroll
   for (int pp = 0; pp < PT; ++pp) {
     const int m = m0 + wpos + 16 * pp;
-    if (m < p.M)
-      lif_epilogue<T, OUT_ENC, MODE>(acc[pp], m, p.M, p.F, cob, p.np, p.scale, p.bias, p.enc_scale, p.state, p.out,
-                                     p.h_trace, p.x_trace);
+#pragma unroll
+    for (int gg = 0; gg < GPW; ++gg) {
+      const int lc = gg * 64 + g * 16;  // workgroup-local channel of this lane's first output
+      const EpiCoeffs cf{&sCoef[0][lc], &sCoef[1][lc], &sCoef[2][lc], &sCoef[3][lc]};
+      lif_epilogue<T, OUT_ENC, MODE>(acc[pp][gg], m < p.M, m, p.M, p.F, (G0 + gg) * 64 + g * 16, p.np, cf,
+                                     p.state, p.out, p.h_trace, p.x_trace);
+    }
   }
-}
-
-template <int T, int PT, int PL, int OE, int MODE>
-static hipError_t launch_lds_t(const LdsParams& p, hipStream_t s) {
-  dim3 grid((unsigned)((p.M + 64 * PT - 1) / (64 * PT)), (unsigned)(p.F / 64));
-  hipLaunchKernelGGL((fused_sparse_lds_kernel<T, PT, PL, OE, MODE>), grid, dim3(256), 0, s, p);
-  return hipGetLastError();
-}
-
-template <int T, int PT>
-static hipError_t launch_lds_pt(const LdsParams& p, int planes, int out_enc, int mode, hipStream_t s) {
-  if (out_enc == SENGINE_ENC_BITS && mode == EPI_LIF_HARD) {
-    if (planes == 1) return launch_lds_t<T, PT, 1, SENGINE_ENC_BITS, EPI_LIF_HARD>(p, s);
-    return launch_lds_t<T, PT, 2, SENGINE_ENC_BITS, EPI_LIF_HARD>(p, s);
-  }
-  if (out_enc == SENGINE_ENC_BITS && mode == EPI_IF_HARD) {
-    if (planes == 1) return launch_lds_t<T, PT, 1, SENGINE_ENC_BITS, EPI_IF_HARD>(p, s);
-    return launch_lds_t<T, PT, 2, SENGINE_ENC_BITS, EPI_IF_HARD>(p, s);
-  }
-  if (planes == 1 && out_enc == SENGINE_ENC_BITS) return launch_lds_t<T, PT, 1, SENGINE_ENC_BITS, EPI_GENERIC>(p, s);
-  if (planes == 2 && out_enc == SENGINE_ENC_BITS) return launch_lds_t<T, PT, 2, SENGINE_ENC_BITS, EPI_GENERIC>(p, s);
-  if (planes == 1 && out_enc == SENGINE_ENC_F16) return launch_lds_t<T, PT, 1, SENGINE_ENC_F16, EPI_GENERIC>(p, s);
-  if (planes == 2 && out_enc == SENGINE_ENC_F16) return launch_lds_t<T, PT, 2, SENGINE_ENC_F16, EPI_GENERIC>(p, s);
-  return hipErrorInvalidValue;
 }
 
 static int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
   return e ? atoi(e) : dflt;
 }
+
+// Reduction chunks per LDS stage.  2 halves the barriers but the larger staging set pushes
+// the kernel to the VGPR limit and measured slower on every layer tried, so 1 is the default;
+// SENGINE_AMD_LDS_CPS=2 selects the other variant (tuning; one-plane weights only).
+static int choose_cps(int planes) {
+  static const int forced = env_int("SENGINE_AMD_LDS_CPS", 0);
+  if (planes == 2) return 1;
+  return forced == 2 ? 2 : 1;
+}
+
+template <int T, int PT, int GPW, int PL, int OE, int MODE>
+static hipError_t launch_lds_t(const LdsParams& p, hipStream_t s) {
+  dim3 grid((unsigned)((p.M + 64 * PT - 1) / (64 * PT)), (unsigned)(p.F / (64 * GPW)));
+  if (PL == 1 && choose_cps(PL) == 2)
+    hipLaunchKernelGGL((fused_sparse_lds_kernel<T, PT, GPW, PL, OE, MODE, 2>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((fused_sparse_lds_kernel<T, PT, GPW, PL, OE, MODE, 1>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int T, int PT, int GPW>
+static hipError_t launch_lds_pt(const LdsParams& p, int planes, int out_enc, int mode, hipStream_t s) {
+  if (out_enc == SENGINE_ENC_BITS && mode == EPI_LIF_HARD) {
+    if (planes == 1) return launch_lds_t<T, PT, GPW, 1, SENGINE_ENC_BITS, EPI_LIF_HARD>(p, s);
+    return launch_lds_t<T, PT, GPW, 2, SENGINE_ENC_BITS, EPI_LIF_HARD>(p, s);
+  }
+  if (out_enc == SENGINE_ENC_BITS && mode == EPI_IF_HARD) {
+    if (planes == 1) return launch_lds_t<T, PT, GPW, 1, SENGINE_ENC_BITS, EPI_IF_HARD>(p, s);
+    return launch_lds_t<T, PT, GPW, 2, SENGINE_ENC_BITS, EPI_IF_HARD>(p, s);
+  }
+  if (planes == 1 && out_enc == SENGINE_ENC_BITS) return launch_lds_t<T, PT, GPW, 1, SENGINE_ENC_BITS, EPI_GENERIC>(p, s);
+  if (planes == 2 && out_enc == SENGINE_ENC_BITS) return launch_lds_t<T, PT, GPW, 2, SENGINE_ENC_BITS, EPI_GENERIC>(p, s);
+  if (planes == 1 && out_enc == SENGINE_ENC_F16) return launch_lds_t<T, PT, GPW, 1, SENGINE_ENC_F16, EPI_GENERIC>(p, s);
+  if (planes == 2 && out_enc == SENGINE_ENC_F16) return launch_lds_t<T, PT, GPW, 2, SENGINE_ENC_F16, EPI_GENERIC>(p, s);
+  return hipErrorInvalidValue;
+}
+
 
 // Positions per workgroup: 64 (PT=1) measured faster than 128 on every config-1 layer
 // (more waves in flight, fewer registers); 128 only for T <= 2, where the accumulators are
@@ -240,6 +316,18 @@ static int choose_pt(int T) {
   static const int forced = env_int("SENGINE_AMD_LDS_PT", 0);
   if (forced == 1 || forced == 2) return T > 4 ? 1 : forced;
   return T <= 2 ? 2 : 1;
+}
+
+// Output-channel groups (of 64) per wave: 2 halves the spike-bit expansion work per
+// SMFMAC (each B fragment feeds 8 instead of 4), at the cost of twice the accumulators and
+// half the workgroups.  Used when C_out % 128 == 0 and the grid still holds >= 1 wave per
+// SIMD.  SENGINE_AMD_LDS_GPW=1|2 overrides (tuning).
+static int choose_gpw(int T, int pt, int64_t M, int F) {
+  static const int forced = env_int("SENGINE_AMD_LDS_GPW", 0);
+  if (pt != 1 || T > 4 || F % 128 != 0) return 1;
+  if (forced == 1 || forced == 2) return forced;
+  const int64_t waves = ((M + 63) / 64) * (F / 128) * 4;
+  return waves >= 1024 ? 2 : 1;
 }
 
 hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
@@ -254,7 +342,7 @@ hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry&
   p.out = static_cast<uint8_t*>(a.out);
   p.h_trace = a.h_trace;
   p.x_trace = a.x_trace;
-  p.B = d->B; p.C = d->C_in; p.H = d->H; p.W = d->W; p.F = d->C_out; p.KW = d->KW;
+  p.B = d->B; p.C = d->C_in; p.H = d->H; p.W = d->W; p.F = d->C_out; p.KH = d->KH; p.KW = d->KW;
   p.SH = d->stride_h; p.SW = d->stride_w; p.PH = d->pad_h; p.PW = d->pad_w;
   p.DH = d->dil_h; p.DW = d->dil_w; p.OH = geo.OH; p.OW = geo.OW;
   p.M = (int)geo.M;
@@ -263,18 +351,20 @@ hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry&
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
   p.enc_scale = 1.0f / kBitSpikeValue;
   const int pt = choose_pt(d->T);
+  const int gpw = choose_gpw(d->T, pt, geo.M, d->C_out);
   const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr);
   const int pl = d->weight_planes, oe = d->out_enc;
 #define SENGINE_LDS_T(TT)                                                                      \
   case TT:                                                                                     \
-    return pt == 2 ? launch_lds_pt<TT, 2>(p, pl, oe, mode, stream)                      \
-                   : launch_lds_pt<TT, 1>(p, pl, oe, mode, stream);
+    if (pt == 2) return launch_lds_pt<TT, 2, 1>(p, pl, oe, mode, stream);                     \
+    return gpw == 2 ? launch_lds_pt<TT, 1, 2>(p, pl, oe, mode, stream)                         \
+                    : launch_lds_pt<TT, 1, 1>(p, pl, oe, mode, stream);
   switch (d->T) {
     SENGINE_LDS_T(1)
     SENGINE_LDS_T(2)
     SENGINE_LDS_T(4)
     case 8:
-      return launch_lds_pt<8, 1>(p, pl, oe, mode, stream);
+      return launch_lds_pt<8, 1, 1>(p, pl, oe, mode, stream);
     default:
       return hipErrorInvalidValue;
   }
