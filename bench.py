@@ -37,6 +37,7 @@ SHAPES = [  # (C_in, C_out, H, W, k)
 ]
 DENSITIES = (0.05, 0.15, 0.30)
 T_STEPS, BATCH = 4, 32
+BURST = 10  # launches per timed burst for the per-launch durations
 
 
 def layer_work(C_in, C_out, H, W, k, T, B):
@@ -88,10 +89,11 @@ def run_layer(wk):
                                  out=wk["out"])
 
 
-def cpu_baseline(sample_batch=4, runs=10, warmup=3):
-    """The oracle (restated reference PyTorch path, torch CPU fp32) on a bounded sample:
-    the 5 sweep shapes at p=0.15 with batch `sample_batch`; scaled linearly to batch 32 and to
-    the 3 densities (CPU conv cost does not depend on spike density)."""
+def cpu_baseline(budget_s=12.0, min_runs=2):
+    """The oracle (restated reference PyTorch path, torch CPU fp32) on the full sweep: the 15
+    layers (5 shapes x 3 densities) at batch 32, T=4 -- the same workload as the GPU step.
+    One untimed warmup sweep, then whole sweeps until `budget_s` of timed CPU work (at least
+    `min_runs`); the median sweep time is the step time."""
     import torch
     from oracle import reference_path as ref
 
@@ -101,30 +103,70 @@ def cpu_baseline(sample_batch=4, runs=10, warmup=3):
     except OSError:
         phys = cores
     torch.set_num_threads(max(1, min(phys, cores)))
-    cases = [ref.make_layer_case(7 + i, T=T_STEPS, B=sample_batch, C_in=ci, C_out=co, H=h, W=w, k=k,
-                                 fp16_weights=True) for i, (ci, co, h, w, k) in enumerate(SHAPES)]
+    cases = [ref.make_layer_case(7 + 3 * i + j, T=T_STEPS, B=BATCH, C_in=ci, C_out=co, H=h, W=w, k=k,
+                                 p_spike=p, fp16_weights=True)
+             for i, (ci, co, h, w, k) in enumerate(SHAPES) for j, p in enumerate(DENSITIES)]
 
     def sweep():
         for c in cases:
             ref.fused_layer(c.x_seq, c.w, c.bn, c.stride, c.padding, 1, "lif", 2.0, 1.0, 0.0)
 
-    for _ in range(warmup):
-        sweep()
+    sweep()
     ts = []
-    for _ in range(runs):
+    while len(ts) < min_runs or sum(ts) < budget_s:
         t0 = time.perf_counter()
         sweep()
         ts.append(time.perf_counter() - t0)
-    med = statistics.median(ts)
-    step_s = med * (BATCH / sample_batch) * len(DENSITIES)
     model = ""
     try:
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except (OSError, StopIteration):
         pass
-    return dict(step_s=step_s, sample_s=med, threads=torch.get_num_threads(), cpu_count=cores, model=model,
-                sample=f"5 sweep shapes at p=0.15, batch {sample_batch}, T=4 (median of {runs} after {warmup} "
-                       f"warmups), scaled x{BATCH // sample_batch} to batch {BATCH} and x{len(DENSITIES)} densities")
+    return dict(step_s=statistics.median(ts), threads=torch.get_num_threads(), cpu_count=cores, model=model,
+                sample=f"the full step (15 sweep layers, batch {BATCH}, T={T_STEPS}) on the oracle: median of "
+                       f"{len(ts)} sweeps ({sum(ts):.1f} s timed) after 1 warmup")
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "fused_sparse_lds_cfg1_traffic.md")
+
+
+def kernel_source_hash() -> str:
+    """sha256 over the HIP sources of the library (ties a counter profile to a kernel build)."""
+    import glob
+    import hashlib
+    h = hashlib.sha256()
+    root = os.path.join(os.path.dirname(os.path.abspath(__file__)), "sparsesnn_amd", "csrc")
+    for f in sorted(glob.glob(os.path.join(root, "*"))):
+        with open(f, "rb") as fh:
+            h.update(os.path.basename(f).encode() + b"\0" + fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic():
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, if it
+    was taken on the current kernel sources (else None: counters cannot be read in this run)."""
+    try:
+        lines = open(TRAFFIC_FILE).read().splitlines()
+    except OSError:
+        return None
+    kv = dict(l.split(":", 1) for l in lines if l.startswith(("traffic_bytes_per_launch:", "kernel_source_sha256:")))
+    if kv.get("kernel_source_sha256", "").strip() != kernel_source_hash():
+        return None
+    return float(kv["traffic_bytes_per_launch"])
+
+
+def copy_calibration(dev, nbytes=256 << 20, reps=3):
+    """A plain device-to-device copy of known size, launched `reps` times, so that rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters can be scaled to bytes (each launch reads and writes
+    exactly `nbytes`)."""
+    import torch
+    a = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize(dev)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize(dev)
+    print(f"copy calibration: {reps} launches of a {nbytes} B device copy", file=sys.stderr)
 
 
 def main():
@@ -134,6 +176,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--json-out", default="")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="counter-collection pass for rocprofv3 --pmc: eager launches only (no graph, no "
+                         "JSON line), followed by the copy-calibration kernel")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU fused operator only; multi-GPU runs are not part of this "
@@ -147,25 +192,34 @@ def main():
     dev = torch.device("cuda:0")
     work = build_workloads(dev, T_STEPS, BATCH)
 
-    # per-launch durations: HIP events on the launch stream around each eager call
+    # per-launch durations: HIP events on the launch stream around bursts of BURST back-to-back
+    # launches of one layer (a single launch between two events also times the event and
+    # dispatch gaps, ~2-3 us here)
     per = {wk["name"]: [] for wk in work}
     stream = torch.cuda.current_stream(dev)
     for _ in range(max(1, args.warmup)):
         for wk in work:
             run_layer(wk)
     torch.cuda.synchronize(dev)
-    reps = max(3, min(args.steps, 20))
+    reps = 3
     evs = []
     for _ in range(reps):
         for wk in work:
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)
-            run_layer(wk)
+            for _ in range(BURST):
+                run_layer(wk)
             b.record(stream)
             evs.append((wk["name"], a, b))
     torch.cuda.synchronize(dev)
     for name, a, b in evs:
-        per[name].append(a.elapsed_time(b) * 1e-3)
+        per[name].append(a.elapsed_time(b) * 1e-3 / BURST)
+    if args.profile_pass:
+        copy_calibration(dev)
+        print(f"profile pass: {reps} x {BURST} eager launches of each of {len(work)} layers after "
+              f"{max(1, args.warmup)} warmup sweeps",
+              file=sys.stderr)
+        return
 
     # the step: all 15 launches captured once in a hipGraph, replayed K times
     graph = torch.cuda.CUDAGraph()
@@ -228,7 +282,8 @@ def main():
             "peak": P_SPARSE / 1e12,
             "unit": "TFLOP/s",
             "frac": round(avg_flops / avg_launch / P_SPARSE, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_algorithmic": round(sum(wk["bytes_min"] for wk in work) / len(work)),
             "kernel": "sengine::fused_sparse_lds_kernel<T=4,...> (spike-bit LDS-staged kernel; "
                       "mean over all 15 sweep launches)",
             "avg_launch_us": round(avg_launch * 1e6, 3),
