@@ -87,9 +87,11 @@ const char* sengine_amd_last_error(void);
 
 /*
  * Kernel selection for sengine_amd_fused_sparse_conv_bn_lif with spike-bit input:
- * 0 = automatic (LDS-staged kernel, the default), 1 = direct-gather kernel (the kernel
- * fp16 inputs always use).  Process-wide; the environment variable
- * SENGINE_AMD_FUSED_KERNEL=direct sets 1 at load time.  Both give identical results.
+ * 0 = automatic (the default: halo-tiled kernel for 3x3 / stride 1 / pad 1 / one weight
+ * plane / T <= 4, else the LDS-staged kernel), 1 = direct-gather kernel (the kernel fp16
+ * inputs always use), 2 = LDS-staged kernel.  Process-wide; the environment variable
+ * SENGINE_AMD_FUSED_KERNEL=direct|lds sets 1|2 at load time.  Every choice computes the
+ * same operator (the tests hold each one to the same oracle).
  */
 int sengine_amd_set_fused_kernel(int32_t choice);
 

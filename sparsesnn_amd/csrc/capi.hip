@@ -46,7 +46,7 @@ static int g_kernel_choice = -1;
 int fused_kernel_choice() {
   if (g_kernel_choice < 0) {
     const char* e = getenv("SENGINE_AMD_FUSED_KERNEL");
-    g_kernel_choice = (e && strcmp(e, "direct") == 0) ? 1 : 0;
+    g_kernel_choice = !e ? 0 : strcmp(e, "direct") == 0 ? 1 : strcmp(e, "lds") == 0 ? 2 : 0;
   }
   return g_kernel_choice;
 }
@@ -89,7 +89,8 @@ extern "C" int sengine_amd_version(void) { return 100; }
 extern "C" const char* sengine_amd_last_error(void) { return g_last_error; }
 
 extern "C" int sengine_amd_set_fused_kernel(int32_t choice) {
-  if (choice != 0 && choice != 1) return set_error(-2, "set_fused_kernel: choice must be 0 (auto) or 1 (direct)");
+  if (choice < 0 || choice > 2)
+    return set_error(-2, "set_fused_kernel: choice must be 0 (auto), 1 (direct) or 2 (lds)");
   g_kernel_choice = choice;
   return 0;
 }

@@ -40,9 +40,14 @@ struct FusedArgs {
 hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
                                  hipStream_t stream);
 
-// Kernel selection for the fused op: 0 = automatic (LDS-staged kernel for bit inputs),
-// 1 = always the direct-gather kernel.  Read once from SENGINE_AMD_FUSED_KERNEL
-// ("auto" | "direct").
+// Halo-tiled kernel for spike-bit 3x3 / stride 1 / pad 1 convolutions (fused_sparse_halo.hip).
+bool halo_eligible(const sengine_conv_lif_desc* d);
+hipError_t launch_fused_bits_halo(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+                                  hipStream_t stream);
+
+// Kernel selection for the fused op with spike-bit input: 0 = automatic (halo-tiled kernel
+// where eligible, else the LDS-staged kernel), 1 = always the direct-gather kernel, 2 = always
+// the LDS-staged kernel.  Read once from SENGINE_AMD_FUSED_KERNEL ("auto" | "direct" | "lds").
 int fused_kernel_choice();
 
 }  // namespace sengine

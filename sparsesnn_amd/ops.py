@@ -90,9 +90,10 @@ def make_desc(s: ConvSpec) -> ConvLifDesc:
 
 
 def set_fused_kernel(choice: str) -> None:
-    """'auto' (LDS-staged kernel for spike-bit inputs) or 'direct' (direct-gather kernel)."""
+    """Kernel for spike-bit inputs: 'auto' (halo-tiled kernel for 3x3 / stride 1 / pad 1, else
+    the LDS-staged kernel), 'direct' (direct-gather kernel) or 'lds' (LDS-staged kernel)."""
     lib = _lib.load()
-    check(lib.sengine_amd_set_fused_kernel({"auto": 0, "direct": 1}[choice]), "set_fused_kernel")
+    check(lib.sengine_amd_set_fused_kernel({"auto": 0, "direct": 1, "lds": 2}[choice]), "set_fused_kernel")
 
 
 def geometry(s: ConvSpec):

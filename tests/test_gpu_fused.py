@@ -117,12 +117,12 @@ def test_hwio_layout(dev):
     assert rep.ok, str(rep)
 
 
-@pytest.mark.parametrize("kernel", ["direct", "auto"])
+@pytest.mark.parametrize("kernel", ["direct", "lds", "auto"])
 @pytest.mark.parametrize("k,stride,pad,B,C_in,C_out,H,W", [(3, 1, 1, 5, 64, 128, 13, 11), (3, 2, 1, 3, 128, 64, 15, 9),
                                                            (1, 1, 0, 2, 256, 192, 7, 7), (1, 2, 0, 2, 64, 64, 9, 10)])
 def test_bit_kernels_agree_and_match_oracle(dev, kernel, k, stride, pad, B, C_in, C_out, H, W):
-    """Both spike-bit kernels (LDS-staged and direct-gather) against the oracle, on shapes whose
-    position count is not a multiple of the workgroup tile."""
+    """Every spike-bit kernel (halo-tiled via 'auto' where eligible, LDS-staged, direct-gather)
+    against the oracle, on shapes whose position count is not a multiple of the workgroup tile."""
     ops.set_fused_kernel(kernel)
     try:
         case = ref.make_layer_case(40 + k + stride + B, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
@@ -132,3 +132,35 @@ def test_bit_kernels_agree_and_match_oracle(dev, kernel, k, stride, pad, B, C_in
         assert x_err < 1e-4
     finally:
         ops.set_fused_kernel("auto")
+
+
+@pytest.mark.parametrize("tile", ["8x8", "4x14", "7x7"])
+@pytest.mark.parametrize("H,W,C_in,C_out,B", [(13, 11, 64, 64, 2), (7, 7, 128, 128, 3), (28, 14, 192, 64, 1),
+                                              (4, 17, 64, 192, 2)])
+def test_halo_tiles_against_oracle(dev, tile, H, W, C_in, C_out, B):
+    """Halo-tiled 3x3 kernel with each tile shape forced, on images that leave ragged tiles,
+    one to three input-channel chunks and several output-channel groups."""
+    import os
+    os.environ["SENGINE_AMD_HALO_TILE"] = tile
+    try:
+        case = ref.make_layer_case(60 + H + W + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
+                                   fp16_weights=True)
+        rep, x_err, _, _ = run_case(dev, case)
+        assert rep.ok, str(rep)
+        assert x_err < 1e-4
+        rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=None, out_enc=ops.ENC_F16)
+        assert rep2.ok, str(rep2)
+    finally:
+        del os.environ["SENGINE_AMD_HALO_TILE"]
+
+
+@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("neuron,v_reset", [("lif", 0.0), ("if", 0.0), ("lif", None)])
+def test_halo_short_sequences_and_state(dev, T, neuron, v_reset):
+    case = ref.make_layer_case(70 + T, T=T, B=2, C_in=128, C_out=64, H=9, W=10, k=3, fp16_weights=True,
+                               p_spike=0.3)
+    g = torch.Generator().manual_seed(9)
+    v0 = torch.rand((2, 64, 9, 10), generator=g) * 0.5
+    rep, _, r, v_fin = run_case(dev, case, neuron=neuron, v_reset=v_reset, v_th=0.6, v0=v0)
+    assert rep.ok, str(rep)
+    assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
