@@ -87,8 +87,8 @@ const char* sengine_amd_last_error(void);
 
 /*
  * Kernel selection for sengine_amd_fused_sparse_conv_bn_lif with spike-bit input:
- * 0 = automatic (the default: halo-tiled kernel for 3x3 / stride 1 / pad 1 / one weight
- * plane / T <= 4, else the LDS-staged kernel), 1 = direct-gather kernel (the kernel fp16
+ * 0 = automatic (the default: tile kernel for 3x3 / stride 1 / pad 1 and 1x1 / pad 0 with
+ * one weight plane and T <= 4, else the LDS-staged kernel), 1 = direct-gather kernel (the kernel fp16
  * inputs always use), 2 = LDS-staged kernel.  Process-wide; the environment variable
  * SENGINE_AMD_FUSED_KERNEL=direct|lds sets 1|2 at load time.  Every choice computes the
  * same operator (the tests hold each one to the same oracle).

@@ -22,8 +22,8 @@ LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libsengine_amd.so")
 ARCH = "gfx950"
 
-SOURCES = ["capi.hip", "fused_sparse.hip", "fused_sparse_lds.hip", "fused_sparse_halo.hip", "compress.hip",
-           "fallback.hip"]
+SOURCES = ["capi.hip", "fused_sparse.hip", "fused_sparse_lds.hip", "fused_tile1.hip", "fused_tile3.hip",
+           "compress.hip", "fallback.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -56,12 +56,65 @@ __host__ __device__ inline int epilogue_mode(const NeuronParams& np, bool traces
   return EPI_GENERIC;
 }
 
+// Hard-reset fast modes without a state buffer: V0 = 0, so t = 0 charges h = x exactly
+// (fma(0, decay, x) == x), and the membrane after the last step is not kept (no reset).
+template <int T, int OUT_ENC, int MODE>
+__device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T][4], bool valid, int m, int M, int F,
+                                                        int cob, const NeuronParams& np, const EpiCoeffs& cf,
+                                                        uint8_t* __restrict__ out) {
+  float fsc[16], fbi[16], v[16];
+#pragma unroll
+  for (int j = 0; j < 16; j += 4) {
+    const float4_t s4 = *reinterpret_cast<const float4_t*>(cf.fsc + j);
+    const float4_t b4 = *reinterpret_cast<const float4_t*>(cf.fbi + j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      fsc[j + e] = s4[e];
+      fbi[j + e] = b4[e];
+    }
+  }
+  const float vreset = np.vreset;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 15; j >= 0; --j) {
+      const float xin = __builtin_fmaf(acc[t][j >> 2][j & 3], fsc[j], fbi[j]);
+      const float h = t == 0 ? xin
+                             : (MODE == EPI_LIF_HARD ? __builtin_fmaf(v[j], np.decay, xin) : __fadd_rn(v[j], xin));
+      if (t + 1 < T)
+        fire_hard(h, np.vth, vreset, v[j], word);
+      else
+        fire_only(h, np.vth, word);
+    }
+    if (!valid) continue;
+    const size_t row = ((size_t)t * M + m) * F + cob;
+    if (OUT_ENC == SENGINE_ENC_BITS) {
+      *reinterpret_cast<uint16_t*>(out + (row >> 3)) = (uint16_t)word;
+    } else {
+      half8_t o0, o1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        o0[j] = (word >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+        o1[j] = (word >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+      }
+      half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(out) + row);
+      dst[0] = o0;
+      dst[1] = o1;
+    }
+  }
+}
+
 // `valid` false (a padding position past M) computes but stores nothing: keeping the call
 // unconditional avoids a divergent branch whose join reshuffles the accumulators.
 template <int T, int OUT_ENC, int MODE>
 __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool valid, int m, int M, int F, int cob,
                                              const NeuronParams& np, const EpiCoeffs& cf, float* state,
                                              uint8_t* __restrict__ out, float* h_trace, float* x_trace) {
+  if ((MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD) && state == nullptr) {  // uniform branch
+    fast_epilogue_stateless<T, OUT_ENC, MODE>(acc, valid, m, M, F, cob, np, cf, out);
+    return;
+  }
   float fsc[16], fbi[16], v[16];
   const bool fold = MODE == EPI_LIF_HARD || (MODE == EPI_GENERIC && np.neuron == SENGINE_NEURON_LIF && np.pow2);
 #pragma unroll

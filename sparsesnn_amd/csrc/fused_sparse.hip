@@ -188,12 +188,12 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
     return set_error(-2, "fused_sparse_conv_bn_lif: out_enc must be BITS or F16");
   if (geo.M > (1ll << 30)) return set_error(-2, "fused_sparse_conv_bn_lif: B*OH*OW too large");
 
-  // Bit inputs: halo-tiled kernel for 3x3 / stride 1 / pad 1, else the LDS-staged kernel
-  // (its per-thread tap mask holds up to 64 taps), else the direct-gather kernel below.
+  // Bit inputs: tile kernel for 3x3 / stride 1 / pad 1 and 1x1 / pad 0, else the LDS-staged
+  // kernel (its per-thread tap mask holds up to 64 taps), else the direct-gather kernel below.
   const int choice = fused_kernel_choice();
   if (d->in_enc == SENGINE_ENC_BITS && choice != 1) {
     const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace};
-    if (choice == 0 && halo_eligible(d)) return (int)launch_fused_bits_halo(d, geo, args, stream);
+    if (choice == 0 && tile_eligible(d)) return (int)launch_fused_bits_tile(d, geo, args, stream);
     if (d->KH * d->KW <= 64) return (int)launch_fused_bits_lds(d, geo, args, stream);
   }
 

@@ -1,0 +1,111 @@
+// Instantiations of the tile kernel (tile_kernel.h) for 1x1 / pad 0 convolutions (any
+// stride), and the host-side choice between tile shapes and channel blocking.
+#include "tile_kernel.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+namespace sengine {
+
+hipError_t launch_tile1(const TileParams& p, int T, int gpw, int oe, int mode, hipStream_t s) {
+  switch (T) {
+    case 1:
+      return launch_tile<1, 1, 0, 0, 1, 1>(p, oe, mode, s);
+    case 2:
+      return launch_tile<2, 1, 0, 0, 1, 1>(p, oe, mode, s);
+    case 4:
+      return gpw == 2 ? launch_tile<4, 1, 0, 0, 1, 2>(p, oe, mode, s) : launch_tile<4, 1, 0, 0, 1, 1>(p, oe, mode, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+namespace {
+
+constexpr TileShape kShapes3[] = {{3, 8, 8, 8}, {3, 14, 4, 8}, {3, 7, 7, 7}};
+
+int env_int_now(const char* name, int dflt) {  // read per call: tests switch these between cases
+  const char* e = getenv(name);
+  return e ? atoi(e) : dflt;
+}
+
+// Relative cost of a 3x3 tile shape: SMFMAC issue over all position slots (valid or not)
+// plus the halo expansion (~72 VALU ops of ~4 cycles per 64-bit spike word), per image.
+double shape_cost(const TileShape& s, int H, int W) {
+  const int tiles = ((H + s.TR - 1) / s.TR) * ((W + s.TC - 1) / s.TC);
+  const int slots = 16 * ((s.TC + 1) / 2) * ((s.TR + s.GR - 1) / s.GR);
+  const double mfma = (double)slots / 16 * 9 * 4 * 26;
+  const double stage = (double)(s.TR + 2) * (s.TC + 2) * 4 * 72.0 / 64 * 4;
+  return tiles * (mfma + stage);
+}
+
+}  // namespace
+
+bool tile_eligible(const sengine_conv_lif_desc* d) {
+  if (d->in_enc != SENGINE_ENC_BITS || d->weight_planes != 1 || d->dil_h != 1 || d->dil_w != 1) return false;
+  // 32-bit input offsets in the kernel
+  if ((int64_t)d->T * d->B * d->H * d->W * (d->C_in / 8) >= ((int64_t)1 << 31)) return false;
+  if (d->T != 1 && d->T != 2 && d->T != 4) return false;
+  const bool k3 = d->KH == 3 && d->KW == 3 && d->stride_h == 1 && d->stride_w == 1 && d->pad_h == 1 && d->pad_w == 1;
+  const bool k1 = d->KH == 1 && d->KW == 1 && d->pad_h == 0 && d->pad_w == 0 && d->stride_h == d->stride_w;
+  return k3 || k1;
+}
+
+hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+                                  hipStream_t stream) {
+  TileParams p;
+  p.in = static_cast<const uint8_t*>(a.data);
+  p.wvals = static_cast<const u32x4_t*>(a.wvals);
+  p.wmeta = static_cast<const uint32_t*>(a.wmeta);
+  p.state = a.state;
+  p.scale = a.scale;
+  p.bias = a.bias;
+  p.out = static_cast<uint8_t*>(a.out);
+  p.h_trace = a.h_trace;
+  p.x_trace = a.x_trace;
+  p.B = d->B; p.C = d->C_in; p.H = d->H; p.W = d->W; p.F = d->C_out;
+  p.OH = geo.OH; p.OW = geo.OW; p.S = d->stride_h;
+  p.M = (int)geo.M;
+  p.nchunk = d->C_in / 64;
+  p.nq = d->KH * d->KW * p.nchunk;
+  p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
+  p.enc_scale = 1.0f / kBitSpikeValue;
+  const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr);
+  const bool k3 = d->KH == 3;
+
+  int shape = 0;
+  if (k3) {
+    if (d->T == 4) {
+      const int forced = env_int_now("SENGINE_AMD_TILE_SHAPE", -1);  // tuning: 0, 1, 2
+      if (forced >= 0 && forced < 3) {
+        shape = forced;
+      } else {
+        double best = 0;
+        for (int i = 0; i < 3; ++i) {
+          const double c = shape_cost(kShapes3[i], geo.OH, geo.OW);
+          if (i == 0 || c < best) best = c, shape = i;
+        }
+      }
+    }
+    const TileShape s = kShapes3[shape];
+    p.tiles_w = (geo.OW + s.TC - 1) / s.TC;
+    p.tiles_per_image = ((geo.OH + s.TR - 1) / s.TR) * p.tiles_w;
+    p.ntiles = d->B * p.tiles_per_image;
+  } else {
+    p.tiles_w = p.tiles_per_image = 0;
+    p.ntiles = (int)((geo.M + 63) / 64);
+  }
+
+  // Two 64-channel groups per wave halve the B bytes per SMFMAC but double the
+  // accumulators (2 waves per SIMD instead of 3) and halve the workgroup count; used when
+  // the grid still gives every CU two workgroups.  SENGINE_AMD_TILE_GPW=1|2 overrides.
+  int gpw = (!k3 && d->T == 4 && d->C_out % 128 == 0 && (int64_t)p.ntiles * (d->C_out / 128) >= 512) ? 2 : 1;
+  const int fg = env_int_now("SENGINE_AMD_TILE_GPW", 0);
+  if (d->T == 4 && d->C_out % 128 == 0 && (fg == 1 || fg == 2)) gpw = fg;
+  if ((int64_t)p.ntiles * (d->C_out / (64 * gpw)) > 0x7fffffff) return hipErrorInvalidValue;
+
+  if (k3) return launch_tile3(p, d->T, shape, gpw, d->out_enc, mode, stream);
+  return launch_tile1(p, d->T, gpw, d->out_enc, mode, stream);
+}
+
+}  // namespace sengine

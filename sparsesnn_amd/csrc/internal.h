@@ -40,13 +40,14 @@ struct FusedArgs {
 hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
                                  hipStream_t stream);
 
-// Halo-tiled kernel for spike-bit 3x3 / stride 1 / pad 1 convolutions (fused_sparse_halo.hip).
-bool halo_eligible(const sengine_conv_lif_desc* d);
-hipError_t launch_fused_bits_halo(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+// Tile kernels for spike-bit 3x3 / stride 1 / pad 1 and 1x1 / pad 0 convolutions with one
+// weight plane and T <= 4 (tile_kernel.h, fused_tile1.hip, fused_tile3.hip).
+bool tile_eligible(const sengine_conv_lif_desc* d);
+hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
                                   hipStream_t stream);
 
-// Kernel selection for the fused op with spike-bit input: 0 = automatic (halo-tiled kernel
-// where eligible, else the LDS-staged kernel), 1 = always the direct-gather kernel, 2 = always
+// Kernel selection for the fused op with spike-bit input: 0 = automatic (tile kernel where
+// eligible, else the LDS-staged kernel), 1 = always the direct-gather kernel, 2 = always
 // the LDS-staged kernel.  Read once from SENGINE_AMD_FUSED_KERNEL ("auto" | "direct" | "lds").
 int fused_kernel_choice();
 

@@ -1,0 +1,350 @@
+// Fused 2:4-sparse Conv + BN + multi-step LIF/IF for spike-bit inputs, with the spikes
+// expanded to fp16 once per workgroup in LDS ("tile" kernels; gfx950 fast path).
+//
+// Same operator, GEMM view and weight blob as fused_sparse.hip / fused_sparse_lds.hip
+// (the reference's conv2d_bn_if_interleaved_kernel and conv1x1_bn_lif,
+// sengine/kernels/conv2d_bn_if_t4.py:918-1022, interleaved_templates.py:95-154).
+//
+// On the MI355X the v_smfmac_f32_16x16x64_f16 issue rate is limited less by the
+// matrix cores than by everything else the SIMD must do per SMFMAC: VALU ops (~4 cycles
+// each, not overlapped with the SMFMAC) and operand bytes returned into VGPRs by LDS
+// and global loads (~16 cycles per KB per SIMD, measured).  The design minimises both:
+//
+//  * The spike bits are expanded to fp16 (value 2.0, factor 1/2 folded into the BN scale)
+//    once per workgroup and input pixel, into LDS, instead of once per wave, tap and
+//    fragment: a B fragment is then two ds_read_b128 (channels 8g..8g+7 and
+//    32+8g..32+8g+7 of the pixel) and no VALU.
+//  * KS == 3 (3x3, stride 1, pad 1): a workgroup owns a TR x TC tile of output pixels of
+//    one image; LDS holds the (TR+2) x (TC+2) halo of input pixels, so the 9 taps are
+//    compile-time offsets from a per-lane base and every input pixel is expanded once,
+//    not 9 times.  Each wave owns a GR-row x 2-column block of the tile (lane column l is
+//    block pixel (l/2, l%2)); with a halo row length HC = 2 (mod 4) (or GR = 7, HC = 9)
+//    the 16 pixels of a block land in 16 distinct 16-byte bank groups for every tap.
+//  * KS == 1 (1x1, any stride, pad 0): a workgroup owns 64 consecutive output positions
+//    (flattened b, oh, ow); LDS holds their input pixels, double-buffered across the
+//    64-channel reduction chunks (one barrier per chunk).
+//  * A wave owns 16 positions x 64*GPW output channels x all T: T*4*GPW accumulator tiles
+//    in VGPRs, so the LIF recurrence over t runs in registers (the membrane never touches
+//    HBM).  GPW = 2 halves the B bytes per SMFMAC (each fragment feeds 8 SMFMACs).
+//  * A operands (2:4 values + metadata) come from global memory (L2-resident, shared by
+//    every workgroup of a channel group), one tap ahead of their use.
+//  * LDS layout: 8-byte half-pieces [t][half h][piece i][pixel]; piece i holds channels
+//    8i..8i+7 (half h: 8i+4h..8i+4h+3), so a lane group's 16 lanes read 16 distinct
+//    half-pieces (conflict-free), staging writes are consecutive, and a fragment is four
+//    8-byte reads (measured cheaper for the SIMD than two 16-byte reads; the halves of a
+//    piece are kept more than 2 KB apart so they are not merged into one 16-byte access).
+//  * Workgroup ids are remapped so each XCD (own L2) runs a contiguous range of
+//    (channel block, tile) ids: an XCD touches few channel blocks' weights.
+#pragma once
+#include "common.h"
+#include "epilogue.h"
+#include "internal.h"
+
+namespace sengine {
+
+struct TileParams {
+  const uint8_t* in;
+  const u32x4_t* wvals;
+  const uint32_t* wmeta;
+  float* state;
+  const float* scale;
+  const float* bias;
+  uint8_t* out;
+  float* h_trace;
+  float* x_trace;
+  int B, C, H, W, F, OH, OW, S;  // S: stride (KS == 1 only)
+  int M;                         // B*OH*OW positions per timestep
+  int nchunk;                    // C / 64
+  int nq;                        // KS*KS*nchunk reduction chunks in the blob
+  int tiles_w, tiles_per_image;  // KS == 3: spatial tiles
+  int ntiles;                    // tiles per channel block
+  NeuronParams np;
+  float enc_scale;
+};
+
+template <int KS, int TR, int TC, int GR>
+struct TileGeom {
+  static constexpr int HC = KS == 3 ? TC + 2 : 0;
+  static constexpr int NPIX = KS == 3 ? (TR + 2) * (TC + 2) : 64;
+  static constexpr int NCP = KS == 3 ? (TC + 1) / 2 : 1;
+  static constexpr int NWAVE = KS == 3 ? NCP * ((TR + GR - 1) / GR) : 4;
+  static constexpr int NTHR = 64 * NWAVE;
+  static constexpr int NTAP = KS * KS;
+  static constexpr int NBUF = KS == 3 ? 1 : 2;
+};
+
+// Consecutive hardware workgroup ids go round-robin over the 8 XCDs; give XCD x the
+// logical ids [x*per, (x+1)*per) instead (ragged tail unchanged).
+__device__ __forceinline__ int tile_remap(int id, int n) {
+  const int per = n >> 3;
+  if (id >= per * 8) return id;
+  return (id & 7) * per + (id >> 3);
+}
+
+// 64 spike bits (channel c = bit c) -> 64 fp16 values in 8 pieces of 8 channels.
+__device__ __forceinline__ void expand_word64(uint2 w, u32x4_t (&pc)[8]) {
+  const uint32_t parts[4] = {w.x & 0xffffu, w.x >> 16, w.y & 0xffffu, w.y >> 16};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const u32x8_t e = __builtin_bit_cast(u32x8_t, expand_bits16(parts[k]));
+    pc[2 * k] = u32x4_t{e[0], e[1], e[2], e[3]};
+    pc[2 * k + 1] = u32x4_t{e[4], e[5], e[6], e[7]};
+  }
+}
+
+template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE>
+__global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR))
+__attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(TileParams p) {
+  using Gm = TileGeom<KS, TR, TC, GR>;
+  constexpr int NPIX = Gm::NPIX;
+  constexpr int NTHR = Gm::NTHR;
+  constexpr int NTAP = Gm::NTAP;
+  constexpr int NBUF = Gm::NBUF;
+  constexpr int NCH = 64 * GPW;
+  constexpr int UNITS = T * NPIX;                 // (t, pixel) spike words per chunk
+  constexpr int UPT = (UNITS + NTHR - 1) / NTHR;  // per thread
+  __shared__ uint2 sB[NBUF][T * 16 * NPIX];
+  __shared__ float sCoef[4][NCH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+
+  const int L = tile_remap(blockIdx.x, gridDim.x);
+  const int Gb = L / p.ntiles;  // channel block: 64-channel groups Gb*GPW .. Gb*GPW+GPW-1
+  const int tile = L - Gb * p.ntiles;
+  const int G0 = Gb * GPW;
+  int b = 0, oh0 = 0, ow0 = 0, m0 = 0;
+  if (KS == 3) {
+    b = tile / p.tiles_per_image;
+    const int trc = tile - b * p.tiles_per_image;
+    const int tr = trc / p.tiles_w;
+    oh0 = tr * TR;
+    ow0 = (trc - tr * p.tiles_w) * TC;
+  } else {
+    m0 = tile * 64;
+  }
+
+  const bool fold = MODE == EPI_LIF_HARD || (MODE == EPI_GENERIC && p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2);
+  if (tid < NCH) {
+    const float sc = p.scale[G0 * 64 + tid] * p.enc_scale;  // exact: enc_scale is a power of two
+    const float bi = p.bias[G0 * 64 + tid];
+    sCoef[0][tid] = fold ? sc * p.np.rtau : sc;             // exact: rtau is a power of two
+    sCoef[1][tid] = fold ? bi * p.np.rtau : bi;
+    sCoef[2][tid] = sc;
+    sCoef[3][tid] = bi;
+  }
+
+  // ---- staging identity: units u = tid + j*NTHR -> (t, pixel); goff -1 = zero word
+  const int cbytes = p.C >> 3;
+  int goff[UPT];  // byte offsets: the host guarantees the input spans < 2^31 bytes
+  int soff[UPT];
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) {
+    const int u = tid + j * NTHR;
+    const int t = u / NPIX;
+    const int px = u - t * NPIX;
+    int ib = b, ih, iw;
+    bool inb;
+    if (KS == 3) {
+      const int hr = px / Gm::HC;
+      ih = oh0 - 1 + hr;
+      iw = ow0 - 1 + (px - hr * Gm::HC);
+      inb = u < UNITS && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
+    } else {
+      const int m = m0 + px;
+      inb = u < UNITS && m < p.M;
+      const int ohw = p.OH * p.OW;
+      ib = inb ? m / ohw : 0;
+      const int r = m - ib * ohw;
+      const int oh = inb ? r / p.OW : 0;
+      ih = oh * p.S;
+      iw = (r - oh * p.OW) * p.S;
+    }
+    goff[j] = inb ? (((t * p.B + ib) * p.H + ih) * p.W + iw) * cbytes : -1;
+    soff[j] = t * 16 * NPIX + px;
+  }
+  auto load_units = [&](uint2 (&v)[UPT], int c) {
+#pragma unroll
+    for (int j = 0; j < UPT; ++j)
+      v[j] = goff[j] >= 0 ? *reinterpret_cast<const uint2*>(p.in + goff[j] + c * 8) : uint2{0u, 0u};
+  };
+  auto store_units = [&](int buf, const uint2 (&v)[UPT]) {
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+      if ((j + 1) * NTHR <= UNITS || tid + j * NTHR < UNITS) {
+        u32x4_t pc[8];
+        expand_word64(v[j], pc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          sB[buf][soff[j] + i * NPIX] = uint2{pc[i][0], pc[i][1]};
+          sB[buf][soff[j] + (8 + i) * NPIX] = uint2{pc[i][2], pc[i][3]};
+        }
+      }
+    }
+  };
+
+  // ---- compute identity: this lane's B column / accumulator column
+  int bbase, m;
+  bool valid;
+  if (KS == 3) {
+    const int rb = wave / Gm::NCP;
+    const int r_in = col >> 1;
+    const int pr_ = rb * GR + r_in;
+    const int pc0 = (wave - rb * Gm::NCP) * 2 + (col & 1);
+    const bool pin = r_in < GR && pr_ < TR && pc0 < TC;
+    const int pr = pin ? pr_ : 0;
+    const int pc = pin ? pc0 : 0;
+    const int oh = oh0 + pr, ow = ow0 + pc;
+    valid = pin && oh < p.OH && ow < p.OW;
+    bbase = g * NPIX + pr * Gm::HC + pc;  // piece g of halo pixel (pr, pc) = tap (0, 0)
+    m = valid ? (b * p.OH + oh) * p.OW + ow : 0;
+  } else {
+    const int pos = wave * 16 + col;
+    valid = m0 + pos < p.M;
+    bbase = g * NPIX + pos;
+    m = valid ? m0 + pos : 0;
+  }
+
+  // LDS byte address of this lane's tap-(0,0) half-piece g (half 0) in buffer 0; the four
+  // 8-byte reads of a fragment are at compile-time offsets from it.
+  const uint32_t lds0 =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint2*)&sB[0][0] + (uint32_t)bbase * 8u;
+  const size_t wgroup = (size_t)p.nq * 4 * 64;
+  const u32x4_t* wv = p.wvals + (size_t)G0 * wgroup + lane;
+  const uint32_t* wm = p.wmeta + (size_t)G0 * wgroup + lane;
+
+  float4_t acc[GPW][T][4];
+#pragma unroll
+  for (int gg = 0; gg < GPW; ++gg)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) acc[gg][t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint2 stg[UPT];
+  load_units(stg, 0);
+  store_units(0, stg);
+  __syncthreads();
+
+  // A operands of (chunk c, tap) -> registers
+  auto load_a = [&](int c, int tap, u32x4_t (&av)[GPW][4], uint32_t (&ix)[GPW][4]) {
+    const size_t q = (size_t)(tap * p.nchunk + c) * 4 * 64;
+#pragma unroll
+    for (int gg = 0; gg < GPW; ++gg)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        av[gg][a] = wv[gg * wgroup + q + a * 64];
+        ix[gg][a] = wm[gg * wgroup + q + a * 64];
+      }
+  };
+
+  u32x4_t av[GPW][4];
+  uint32_t ix[GPW][4];
+  load_a(0, 0, av, ix);
+  for (int c = 0; c < p.nchunk; ++c) {
+    const bool more = c + 1 < p.nchunk;
+    const int buf = NBUF == 2 ? (c & 1) : 0;
+    if (more) load_units(stg, c + 1);
+    // B fragments: four ds_read_b64 per (tap, t), issued one step ahead of their SMFMACs
+    // and waited for with an explicit lgkmcnt (the loop issues no other LDS operation).
+    // Written as asm so the compiler neither fuses them into 16-byte or paired reads nor
+    // hoists them further (both measured slower / register-starved).
+    const uint32_t lbase = lds0 + (uint32_t)buf * (uint32_t)(T * 16 * NPIX * 8);
+    uint2 fr[2][4];
+    auto issue = [&](int step, uint2 (&f)[4]) {
+      const int tp = step / T, t = step - (step / T) * T;
+      const int toff = KS == 3 ? (tp / 3) * Gm::HC + (tp % 3) : 0;
+      const int o = (t * 16 * NPIX + toff) * 8;
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[0]) : "v"(lbase), "i"(o));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[1]) : "v"(lbase), "i"(o + 8 * NPIX * 8));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[2]) : "v"(lbase), "i"(o + 4 * NPIX * 8));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[3]) : "v"(lbase), "i"(o + 12 * NPIX * 8));
+    };
+    issue(0, fr[0]);
+#pragma unroll
+    for (int tap = 0; tap < NTAP; ++tap) {
+      u32x4_t avn[GPW][4];
+      uint32_t ixn[GPW][4];
+      if (tap + 1 < NTAP) load_a(c, tap + 1, avn, ixn);
+      else if (more) load_a(c + 1, 0, avn, ixn);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int step = tap * T + t;
+        uint2(&f)[4] = fr[step & 1];
+        // The wait names the fragment registers as operands, so every use of them is
+        // ordered after it.
+        if (step + 1 < NTAP * T) {
+          issue(step + 1, fr[(step + 1) & 1]);
+          asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) :: "memory");
+        } else {
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) :: "memory");
+        }
+        const half16_t bf = __builtin_bit_cast(
+            half16_t, u32x8_t{f[0].x, f[0].y, f[1].x, f[1].y, f[2].x, f[2].y, f[3].x, f[3].y});
+#pragma unroll
+        for (int gg = 0; gg < GPW; ++gg)
+#pragma unroll
+          for (int a = 0; a < 4; ++a)
+            acc[gg][t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(half8_t, av[gg][a]), bf,
+                                                                     acc[gg][t][a], (int)ix[gg][a], 0, 0);
+      }
+      if (tap + 1 < NTAP || more) {
+#pragma unroll
+        for (int gg = 0; gg < GPW; ++gg)
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            av[gg][a] = avn[gg][a];
+            ix[gg][a] = ixn[gg][a];
+          }
+      }
+    }
+    if (more) {
+      if (NBUF == 1) __syncthreads();  // every wave is done reading the single buffer
+      store_units(NBUF == 2 ? (buf ^ 1) : 0, stg);
+      __syncthreads();
+    }
+  }
+
+#pragma unroll
+  for (int gg = 0; gg < GPW; ++gg) {
+    const int cl = gg * 64 + g * 16;  // this lane's 16 channels within the block
+    const EpiCoeffs cf{&sCoef[0][cl], &sCoef[1][cl], &sCoef[2][cl], &sCoef[3][cl]};
+    lif_epilogue<T, OUT_ENC, MODE>(acc[gg], valid, m, p.M, p.F, G0 * 64 + cl, p.np, cf, p.state, p.out, p.h_trace,
+                                   p.x_trace);
+  }
+}
+
+// Host side (fused_tile_host.hip).
+struct TileShape {
+  int KS, TR, TC, GR;
+};
+
+template <int T, int KS, int TR, int TC, int GR, int GPW>
+hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s) {
+  constexpr int NTHR = TileGeom<KS, TR, TC, GR>::NTHR;
+  const dim3 grid((unsigned)(p.ntiles * (p.F / (64 * GPW))));
+  if (out_enc == SENGINE_ENC_BITS) {
+    if (mode == EPI_LIF_HARD)
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_LIF_HARD>), grid,
+                         dim3(NTHR), 0, s, p);
+    else if (mode == EPI_IF_HARD)
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_IF_HARD>), grid,
+                         dim3(NTHR), 0, s, p);
+    else
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_GENERIC>), grid,
+                         dim3(NTHR), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16, EPI_GENERIC>), grid, dim3(NTHR),
+                       0, s, p);
+  }
+  return hipGetLastError();
+}
+
+// Launchers compiled in fused_tile3.hip (KS = 3) and fused_tile1.hip (KS = 1).
+hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int out_enc, int mode, hipStream_t s);
+hipError_t launch_tile1(const TileParams& p, int T, int gpw, int out_enc, int mode, hipStream_t s);
+
+}  // namespace sengine

@@ -134,14 +134,14 @@ def test_bit_kernels_agree_and_match_oracle(dev, kernel, k, stride, pad, B, C_in
         ops.set_fused_kernel("auto")
 
 
-@pytest.mark.parametrize("tile", ["8x8", "4x14", "7x7"])
+@pytest.mark.parametrize("tile", ["0", "1", "2"])
 @pytest.mark.parametrize("H,W,C_in,C_out,B", [(13, 11, 64, 64, 2), (7, 7, 128, 128, 3), (28, 14, 192, 64, 1),
                                               (4, 17, 64, 192, 2)])
 def test_halo_tiles_against_oracle(dev, tile, H, W, C_in, C_out, B):
-    """Halo-tiled 3x3 kernel with each tile shape forced, on images that leave ragged tiles,
-    one to three input-channel chunks and several output-channel groups."""
+    """3x3 tile kernel with each tile shape forced (0: 8x8, 1: 14x4, 2: 7x7), on images that
+    leave ragged tiles, one to three input-channel chunks and several output-channel groups."""
     import os
-    os.environ["SENGINE_AMD_HALO_TILE"] = tile
+    os.environ["SENGINE_AMD_TILE_SHAPE"] = tile
     try:
         case = ref.make_layer_case(60 + H + W + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
                                    fp16_weights=True)
@@ -151,7 +151,7 @@ def test_halo_tiles_against_oracle(dev, tile, H, W, C_in, C_out, B):
         rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=None, out_enc=ops.ENC_F16)
         assert rep2.ok, str(rep2)
     finally:
-        del os.environ["SENGINE_AMD_HALO_TILE"]
+        del os.environ["SENGINE_AMD_TILE_SHAPE"]
 
 
 @pytest.mark.parametrize("T", [1, 2])
@@ -164,3 +164,23 @@ def test_halo_short_sequences_and_state(dev, T, neuron, v_reset):
     rep, _, r, v_fin = run_case(dev, case, neuron=neuron, v_reset=v_reset, v_th=0.6, v0=v0)
     assert rep.ok, str(rep)
     assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("gpw", ["1", "2"])
+@pytest.mark.parametrize("k,stride,H,W,C_in,C_out,B", [(3, 1, 9, 10, 128, 128, 2), (1, 1, 7, 9, 256, 256, 3),
+                                                       (1, 2, 11, 10, 128, 128, 2), (1, 1, 5, 5, 64, 192, 1)])
+def test_tile_channel_blocking(dev, gpw, k, stride, H, W, C_in, C_out, B):
+    """Tile kernels with one or two 64-channel groups per wave (SENGINE_AMD_TILE_GPW), for
+    3x3 halo tiles and flat 1x1 tiles (stride 1 and 2), against the oracle."""
+    import os
+    os.environ["SENGINE_AMD_TILE_GPW"] = gpw
+    try:
+        case = ref.make_layer_case(80 + k + stride + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
+                                   stride=stride, padding=k // 2, fp16_weights=True)
+        rep, x_err, _, _ = run_case(dev, case)
+        assert rep.ok, str(rep)
+        assert x_err < 1e-4
+        rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0)
+        assert rep2.ok, str(rep2)
+    finally:
+        del os.environ["SENGINE_AMD_TILE_GPW"]
