@@ -155,6 +155,53 @@ def measured_traffic():
     return float(kv["traffic_bytes_per_launch"])
 
 
+E2E_BATCH, E2E_HW, E2E_CLASSES = 64, 32, 100
+
+
+def bench_e2e(dev, warmup: int, iters: int):
+    """SEW-ResNet-18 (reference init, convs 2:4 except the stem, LIF
+    tau=2 V_th=1, ADD), 3x32x32 images ~U(0,1), batch 64, T=4, one hipGraph replay per
+    batch; images/s from HIP events around `iters` replays (the reference times graph
+    replays the same way, sengine/csrc/cpp_executor.cu:1298-1315)."""
+    import torch
+    from sparsesnn_amd.sew_resnet import SEWResNet18Engine, random_params
+
+    params = random_params(2024, E2E_CLASSES)
+    eng = SEWResNet18Engine(params, batch=E2E_BATCH, T=T_STEPS, device=dev)
+    g = torch.Generator().manual_seed(7)
+    x = torch.rand((E2E_BATCH, 3, E2E_HW, E2E_HW), generator=g).to(dev)
+    eng.forward(x)
+    eng.capture()
+    for _ in range(warmup):
+        eng.forward(x)
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    eng.x_buf.copy_(x)
+    a.record(stream)
+    for _ in range(iters):
+        eng.graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize(dev)
+    s = a.elapsed_time(b) * 1e-3 / iters
+    return dict(params=params, x=x.cpu(), batch_s=s, launches=3 + sum(3 if blk.downsample is not None else 2
+                                                                        for blk in eng.blocks) + 1)
+
+
+def cpu_e2e(params, x, budget_s=6.0, min_runs=2):
+    """The oracle SEW-ResNet-18 (torch CPU fp32) on the same batch: median of whole batches."""
+    import torch
+    from oracle import sew_resnet as sr
+    with torch.no_grad():
+        sr.forward(params, x)
+        ts = []
+        while len(ts) < min_runs or sum(ts) < budget_s:
+            t0 = time.perf_counter()
+            sr.forward(params, x)
+            ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), len(ts), torch.get_num_threads()
+
+
 def copy_calibration(dev, nbytes=256 << 20, reps=3):
     """A plain device-to-device copy of known size, launched `reps` times, so that rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters can be scaled to bytes (each launch reads and writes
@@ -176,6 +223,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--json-out", default="")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the SEW-ResNet-18 end-to-end measurement")
     ap.add_argument("--profile-pass", action="store_true",
                     help="counter-collection pass for rocprofv3 --pmc: eager launches only (no graph, no "
                          "JSON line), followed by the copy-calibration kernel")
@@ -303,6 +351,22 @@ def main():
             "cpu_count": cb["cpu_count"],
             "gpu_speedup": round(cb["step_s"] / step_s, 1),
         }
+    if not args.no_e2e:
+        e2e = bench_e2e(dev, warmup=20, iters=max(50, args.steps * 5))
+        result["e2e"] = {
+            "metric": "images/sec", "model": "SEW-ResNet-18 (ADD, LIF tau=2 V_th=1, 2:4 convs except the stem)",
+            "value": round(E2E_BATCH / e2e["batch_s"], 1), "batch": E2E_BATCH, "timesteps": T_STEPS,
+            "input": f"3x{E2E_HW}x{E2E_HW} ~U(0,1), direct-encoded", "ms_per_batch": round(e2e["batch_s"] * 1e3, 4),
+            "launches_per_batch": e2e["launches"], "step": "one hipGraph replay per batch",
+            "data": "synthetic images, reference random init (models/sewresnet.py:155-160)",
+        }
+        if not args.no_cpu_baseline:
+            cs, runs, thr = cpu_e2e(e2e["params"], e2e["x"])
+            result["e2e"]["cpu_baseline"] = {"value": round(E2E_BATCH / cs, 2), "unit": "images/sec", "cores": thr,
+                                             "kind": "port", "sample": f"the same batch of {E2E_BATCH} images, "
+                                                                       f"median of {runs} batches",
+                                             "ms_per_batch": round(cs * 1e3, 2)}
+            result["e2e"]["speedup_vs_cpu"] = round(cs / e2e["batch_s"], 1)
     line = json.dumps(result)
     print(line)
     if args.json_out:

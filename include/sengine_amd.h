@@ -147,6 +147,61 @@ int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const v
                                          hipStream_t stream);
 
 /*
+ * Fused Conv + BN + neuron with the SEW 'ADD' residual connection in the epilogue:
+ * out = spike + residual (models/sewresnet.py:58-59; replaces conv2d_bn_if_add_t4_kernel,
+ * sengine/kernels/conv2d_bn_if_t4.py:813-911, whose output is fp16 spike + residual).
+ * Integer-valued activations are stored as bit planes interleaved per position: a tensor
+ * with P planes is an NHWC spike-bit tensor with P*C channels, channel p*C + c holding bit p
+ * of channel c's value.  residual: (T*B, OH, OW) positions x residual_planes*C_out bits;
+ * out: out_planes*C_out bits per position; 1 <= residual_planes <= out_planes <= 3 and the
+ * caller chooses out_planes so that spike + residual fits (SEW-ResNet-18: 2 planes).
+ * A conv whose input is such a P-plane tensor is an ordinary spike-bit conv with C_in =
+ * P*C and weights [W, 2W, 4W, ...] along the input channels (sparsesnn_amd.sparsity).
+ * Requires out_enc = BITS; state may be NULL; no traces.
+ */
+int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_desc* d, const void* data,
+                                             const void* blob_values, const void* blob_meta, float* state,
+                                             const float* bn_scale, const float* bn_bias, const void* residual,
+                                             int32_t residual_planes, void* out, int32_t out_planes,
+                                             hipStream_t stream);
+
+/*
+ * Dense stem convolution on images + folded BN (the reference runs it through cuDNN,
+ * sengine/csrc/cpp_executor.cu:306-347; models/sewresnet.py:140-141,199-200):
+ * x NCHW fp32 (d->B images, d->C_in, d->H, d->W), weight OIHW fp32, out NHWC fp32
+ * (d->B, OH, OW, d->C_out).  Any C_in / kernel / stride / pad (dilation 1); T is ignored.
+ */
+int sengine_amd_stem_conv_bn(const sengine_conv_lif_desc* d, const float* x, const float* weight,
+                             const float* bn_scale, const float* bn_bias, float* out, hipStream_t stream);
+
+/*
+ * Multi-step neuron on an input repeated at every timestep (the stem output,
+ * x.unsqueeze(0).repeat(T), models/sewresnet.py:201-202): x fp32 (n), V0 = 0,
+ * spikes bits (T, n); n % 32 == 0.
+ */
+int sengine_amd_multistep_neuron_repeat(int32_t T, int64_t n, int32_t neuron, int32_t hard_reset, float tau,
+                                        float v_threshold, float v_reset, const float* x, uint32_t* spikes,
+                                        hipStream_t stream);
+
+/*
+ * Max-pooling of spike bits (SeqToANNContainer(MaxPool2d(k, stride, pad)),
+ * models/sewresnet.py:143,203; the reference runtime's pool kernels,
+ * sengine/csrc/cpp_executor.cu:77-139): in (NT, H, W) x C bits -> out (NT, OH, OW) x C
+ * bits; for {0,1} values the max is the OR.  C % 32 == 0, pad <= k/2.
+ */
+int sengine_amd_maxpool_spikes(int32_t NT, int32_t H, int32_t W, int32_t C, int32_t k, int32_t stride, int32_t pad,
+                               const uint32_t* in, uint32_t* out, hipStream_t stream);
+
+/*
+ * Head: AdaptiveAvgPool2d(1) per timestep, mean over T, Linear (models/sewresnet.py:152-153,
+ * 208-210).  in: integer activations as `planes` bit planes, (T*B, HW) positions x planes*C
+ * bits; fc_weight (N_out, C) fp32, fc_bias (N_out); out (B, N_out) fp32.
+ */
+int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t planes, const uint32_t* in,
+                         const float* fc_weight, const float* fc_bias, int32_t N_out, float* out,
+                         hipStream_t stream);
+
+/*
  * Unfused fallback, half 1: dense Conv + folded BN, fp32 output (T*B*OH*OW, C_out).
  * Mirrors conv2d_bn_t4_kernel / conv1x1_bn_t4_kernel (conv2d_bn_if_t4.py:551-673), but
  * keeps the BN output in fp32 (the reference rounds it to fp16).

@@ -52,6 +52,22 @@ def nhwc_bits_to_seq(words: np.ndarray, T, B, C, H, W) -> np.ndarray:
     return np.ascontiguousarray(np.transpose(x, (0, 1, 4, 2, 3)))
 
 
+def seq_to_planes(x_seq: np.ndarray, planes: int) -> np.ndarray:
+    """Integer activations (T, B, C, H, W), values 0 .. 2^planes - 1 -> packed NHWC bit planes
+    (T*B*H*W, planes*C/32): channel p*C + c holds bit p of channel c (the layout of the SEW
+    residual output)."""
+    x = np.asarray(x_seq).astype(np.int64)
+    assert x.min() >= 0 and x.max() < (1 << planes)
+    stacked = np.concatenate([(x >> p) & 1 for p in range(planes)], axis=2)
+    return seq_to_nhwc_bits(stacked)
+
+
+def planes_to_seq(words: np.ndarray, planes: int, T, B, C, H, W) -> np.ndarray:
+    """Inverse of seq_to_planes: (T*B*H*W, planes*C/32) -> integer (T, B, C, H, W) float32."""
+    x = nhwc_bits_to_seq(words, T, B, planes * C, H, W)
+    return sum(x[:, :, p * C:(p + 1) * C] * float(1 << p) for p in range(planes)).astype(np.float32)
+
+
 def _row_to_channel(G: int, a: int, r: np.ndarray) -> np.ndarray:
     return 64 * G + 16 * (r // 4) + 4 * a + (r % 4)
 

@@ -80,6 +80,18 @@ struct NeuronParams {
   float vth, vreset;
 };
 
+// SEW 'ADD' connection fused into a fused layer's output (models/sewresnet.py:58-59; the
+// reference's conv2d_bn_if_add_t4_kernel, sengine/kernels/conv2d_bn_if_t4.py:813-911):
+// out = spike + residual, integer-valued.  Integer activations are stored as bit planes
+// interleaved per position: an activation with P planes is an NHWC spike-bit tensor of P*C
+// channels, plane p holding bit p of every channel's value (channel c of plane p is channel
+// p*C + c).  res == nullptr: plain spike output.
+struct SewAdd {
+  const uint8_t* res;
+  int res_planes;  // planes of the residual (1..3)
+  int out_planes;  // planes written (>= res_planes; the caller sizes it so no carry is lost)
+};
+
 // One charge step: returns the charged membrane h given the previous membrane v and
 // the input x.  xf is x/tau already folded (pow2 LIF) or the raw BN output.
 __device__ __forceinline__ float neuron_charge(const NeuronParams& np, float v, float xf) {

@@ -49,6 +49,24 @@ struct EpiCoeffs {
   const float* bi;
 };
 
+// Store the 16 spike bits of (position row_pos = t*M + m, channels cob..cob+15).
+__device__ __forceinline__ void store_spike_word(uint32_t word, size_t row_pos, int F, int cob, uint8_t* out,
+                                                 const SewAdd& sa) {
+  if (sa.res == nullptr) {
+    *reinterpret_cast<uint16_t*>(out + ((row_pos * F + cob) >> 3)) = (uint16_t)word;
+    return;
+  }
+  const size_t rbase = row_pos * (size_t)sa.res_planes * F + cob;
+  const size_t obase = row_pos * (size_t)sa.out_planes * F + cob;
+  uint32_t carry = word;
+  for (int pl = 0; pl < sa.out_planes; ++pl) {
+    const uint32_t r = pl < sa.res_planes ? *reinterpret_cast<const uint16_t*>(sa.res + ((rbase + (size_t)pl * F) >> 3))
+                                           : 0u;
+    *reinterpret_cast<uint16_t*>(out + ((obase + (size_t)pl * F) >> 3)) = (uint16_t)(r ^ carry);
+    carry &= r;
+  }
+}
+
 __host__ __device__ inline int epilogue_mode(const NeuronParams& np, bool traces) {
   if (traces || !np.hard_reset) return EPI_GENERIC;
   if (np.neuron == SENGINE_NEURON_LIF && np.pow2) return EPI_LIF_HARD;
@@ -61,7 +79,7 @@ __host__ __device__ inline int epilogue_mode(const NeuronParams& np, bool traces
 template <int T, int OUT_ENC, int MODE>
 __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T][4], bool valid, int m, int M, int F,
                                                         int cob, const NeuronParams& np, const EpiCoeffs& cf,
-                                                        uint8_t* __restrict__ out) {
+                                                        uint8_t* __restrict__ out, const SewAdd& sa) {
   float fsc[16], fbi[16], v[16];
 #pragma unroll
   for (int j = 0; j < 16; j += 4) {
@@ -90,7 +108,7 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
     if (!valid) continue;
     const size_t row = ((size_t)t * M + m) * F + cob;
     if (OUT_ENC == SENGINE_ENC_BITS) {
-      *reinterpret_cast<uint16_t*>(out + (row >> 3)) = (uint16_t)word;
+      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa);
     } else {
       half8_t o0, o1;
 #pragma unroll
@@ -110,9 +128,10 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
 template <int T, int OUT_ENC, int MODE>
 __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool valid, int m, int M, int F, int cob,
                                              const NeuronParams& np, const EpiCoeffs& cf, float* state,
-                                             uint8_t* __restrict__ out, float* h_trace, float* x_trace) {
+                                             uint8_t* __restrict__ out, float* h_trace, float* x_trace,
+                                             const SewAdd& sa) {
   if ((MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD) && state == nullptr) {  // uniform branch
-    fast_epilogue_stateless<T, OUT_ENC, MODE>(acc, valid, m, M, F, cob, np, cf, out);
+    fast_epilogue_stateless<T, OUT_ENC, MODE>(acc, valid, m, M, F, cob, np, cf, out, sa);
     return;
   }
   float fsc[16], fbi[16], v[16];
@@ -167,7 +186,7 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
     }
     if (!valid) continue;
     if (OUT_ENC == SENGINE_ENC_BITS) {
-      *reinterpret_cast<uint16_t*>(out + (row >> 3)) = (uint16_t)word;
+      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa);
     } else {
       half8_t o0, o1;
 #pragma unroll

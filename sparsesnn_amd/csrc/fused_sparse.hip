@@ -44,6 +44,7 @@ struct FusedParams {
   int64_t in_t_stride;  // pixels per timestep = B*H*W
   NeuronParams np;
   float enc_scale;      // 1/value of a spike fed to the MFMA
+  SewAdd sew;
 };
 
 template <int T, int IN_ENC, int OUT_ENC, int PLANES>
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
   if (!mvalid) return;
   const EpiCoeffs cf{&sCoef[0][g * 16], &sCoef[1][g * 16], &sCoef[2][g * 16], &sCoef[3][g * 16]};
   lif_epilogue<T, OUT_ENC, EPI_GENERIC>(acc, true, m, p.M, p.F, G * 64 + g * 16, p.np, cf, p.state, p.out,
-                                        p.h_trace, p.x_trace);
+                                        p.h_trace, p.x_trace, p.sew);
 }
 
 template <int T, int IN_ENC, int OUT_ENC, int PLANES>
@@ -170,11 +171,9 @@ static hipError_t launch_fused_enc(const FusedParams& p, int in_enc, int out_enc
 
 using namespace sengine;
 
-extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const void* data,
-                                                    const void* blob_values, const void* blob_meta,
-                                                    float* state, const float* bn_scale, const float* bn_bias,
-                                                    void* spikes, float* h_trace, float* x_trace,
-                                                    hipStream_t stream) {
+static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const void* blob_values,
+                       const void* blob_meta, float* state, const float* bn_scale, const float* bn_bias, void* spikes,
+                       float* h_trace, float* x_trace, const SewAdd& sew, hipStream_t stream) {
   Geometry geo;
   int rc = check_desc(d, &geo, /*sparse=*/true);
   if (rc) return rc;
@@ -192,7 +191,7 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
   // kernel (its per-thread tap mask holds up to 64 taps), else the direct-gather kernel below.
   const int choice = fused_kernel_choice();
   if (d->in_enc == SENGINE_ENC_BITS && choice != 1) {
-    const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace};
+    const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace, sew};
     if (choice == 0 && tile_eligible(d)) return (int)launch_fused_bits_tile(d, geo, args, stream);
     if (d->KH * d->KW <= 64) return (int)launch_fused_bits_lds(d, geo, args, stream);
   }
@@ -215,6 +214,7 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
   p.in_t_stride = (int64_t)d->B * d->H * d->W;
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
   p.enc_scale = d->in_enc == SENGINE_ENC_BITS ? 1.0f / kBitSpikeValue : 1.0f;
+  p.sew = sew;
 
   dim3 grid((unsigned)((geo.M + 63) / 64), (unsigned)(d->C_out / 64));
   hipError_t e;
@@ -225,4 +225,28 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
     default: e = launch_fused_enc<8>(p, d->in_enc, d->out_enc, d->weight_planes, grid, stream); break;
   }
   return (int)e;
+}
+
+extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const void* data,
+                                                    const void* blob_values, const void* blob_meta,
+                                                    float* state, const float* bn_scale, const float* bn_bias,
+                                                    void* spikes, float* h_trace, float* x_trace,
+                                                    hipStream_t stream) {
+  return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace,
+                     SewAdd{nullptr, 0, 0}, stream);
+}
+
+extern "C" int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_desc* d, const void* data,
+                                                        const void* blob_values, const void* blob_meta,
+                                                        float* state, const float* bn_scale, const float* bn_bias,
+                                                        const void* residual, int32_t residual_planes, void* out,
+                                                        int32_t out_planes, hipStream_t stream) {
+  if (!d) return set_error(-1, "fused_sparse_conv_bn_lif_add: null descriptor");
+  if (!residual) return set_error(-1, "fused_sparse_conv_bn_lif_add: null residual");
+  if (d->out_enc != SENGINE_ENC_BITS) return set_error(-2, "fused_sparse_conv_bn_lif_add: out_enc must be BITS");
+  if (residual_planes < 1 || residual_planes > 3 || out_planes < residual_planes || out_planes > 3)
+    return set_error(-2, "fused_sparse_conv_bn_lif_add: need 1 <= residual_planes <= out_planes <= 3");
+  if (d->C_out % 32 != 0) return set_error(-2, "fused_sparse_conv_bn_lif_add: C_out % 32 != 0");
+  return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, out, nullptr, nullptr,
+                     SewAdd{static_cast<const uint8_t*>(residual), residual_planes, out_planes}, stream);
 }

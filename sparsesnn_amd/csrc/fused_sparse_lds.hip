@@ -44,6 +44,7 @@ struct LdsParams {
   int64_t in_t_bytes;  // bytes of one timestep of input spike bits
   NeuronParams np;
   float enc_scale;
+  SewAdd sew;
 };
 
 __device__ __forceinline__ uint2 interleave_bytes(uint2 w) {
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(256) void fused_sparse_lds_kernel(LdsParams p) {
       const int lc = gg * 64 + g * 16;  // workgroup-local channel of this lane's first output
       const EpiCoeffs cf{&sCoef[0][lc], &sCoef[1][lc], &sCoef[2][lc], &sCoef[3][lc]};
       lif_epilogue<T, OUT_ENC, MODE>(acc[pp][gg], m < p.M, m, p.M, p.F, (G0 + gg) * 64 + g * 16, p.np, cf,
-                                     p.state, p.out, p.h_trace, p.x_trace);
+                                     p.state, p.out, p.h_trace, p.x_trace, p.sew);
     }
   }
 }
@@ -350,6 +351,7 @@ hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry&
   p.in_t_bytes = (int64_t)d->B * d->H * d->W * (d->C_in / 8);
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
   p.enc_scale = 1.0f / kBitSpikeValue;
+  p.sew = a.sew;
   const int pt = choose_pt(d->T);
   const int gpw = choose_gpw(d->T, pt, geo.M, d->C_out);
   const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr);

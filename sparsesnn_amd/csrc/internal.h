@@ -34,6 +34,7 @@ struct FusedArgs {
   void* out;
   float* h_trace;
   float* x_trace;
+  SewAdd sew;  // fused SEW residual add (sew.res == nullptr: none)
 };
 
 // LDS-staged kernel for spike-bit inputs (fused_sparse_lds.hip).

@@ -60,6 +60,7 @@ struct TileParams {
   int ntiles;                    // tiles per channel block
   NeuronParams np;
   float enc_scale;
+  SewAdd sew;
 };
 
 template <int KS, int TR, int TC, int GR>
@@ -313,7 +314,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(Ti
     const int cl = gg * 64 + g * 16;  // this lane's 16 channels within the block
     const EpiCoeffs cf{&sCoef[0][cl], &sCoef[1][cl], &sCoef[2][cl], &sCoef[3][cl]};
     lif_epilogue<T, OUT_ENC, MODE>(acc[gg], valid, m, p.M, p.F, G0 * 64 + cl, p.np, cf, p.state, p.out, p.h_trace,
-                                   p.x_trace);
+                                   p.x_trace, p.sew);
   }
 }
 

@@ -19,7 +19,8 @@ from ._lib import (ENC_BITS, ENC_F16, ENC_F32, NEURON_IF, NEURON_LIF, WLAYOUT_HW
 
 __all__ = [
     "ConvSpec", "make_desc", "geometry", "set_fused_kernel", "compress_2_4", "pack_dense_weights", "pack_spikes",
-    "unpack_spikes", "fused_sparse_conv_bn_lif", "dense_conv_bn", "multistep_neuron", "SEngineError",
+    "unpack_spikes", "fused_sparse_conv_bn_lif", "fused_sparse_conv_bn_lif_add", "stem_conv_bn",
+    "multistep_neuron_repeat", "maxpool_spikes", "sew_head", "dense_conv_bn", "multistep_neuron", "SEngineError",
     "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
 ]
 
@@ -239,6 +240,126 @@ def fused_sparse_conv_bn_lif(s: ConvSpec, data: torch.Tensor, values: torch.Tens
         ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta), _ptr(state), _ptr(bn_scale), _ptr(bn_bias),
         _ptr(out), _ptr(h_trace), _ptr(x_trace), _stream(dev))
     check(rc, "fused_sparse_conv_bn_lif")
+    return out
+
+
+def fused_sparse_conv_bn_lif_add(s: ConvSpec, data: torch.Tensor, values: torch.Tensor, meta: torch.Tensor,
+                                 bn_scale: torch.Tensor, bn_bias: torch.Tensor, residual: torch.Tensor,
+                                 residual_planes: int, out_planes: int, state: Optional[torch.Tensor] = None,
+                                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused 2:4 Conv + BN + neuron + SEW 'ADD' residual: out = spike + residual as
+    `out_planes` bit planes, int32 (T*B, OH, OW, out_planes*C_out/32)."""
+    lib = _lib.load()
+    if s.out_enc != ENC_BITS:
+        raise SEngineError("fused_sparse_conv_bn_lif_add: out_enc must be ENC_BITS")
+    OH, OW, M, _ = geometry(s)
+    d = make_desc(s)
+    vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+    check(lib.sengine_amd_sparse_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)), "sparse_blob_bytes")
+    for t, n in ((data, "data"), (values, "values"), (meta, "meta"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias"),
+                 (residual, "residual")):
+        _require_cuda(t, n)
+    dev = data.device
+    dt, n_in = _enc_numel(s.in_enc, s.T * s.B * s.H * s.W * s.C_in)
+    _require_numel(data, n_in, dt, "data")
+    if values.numel() * values.element_size() != vb.value or meta.numel() * meta.element_size() != mb.value:
+        raise SEngineError("fused_sparse_conv_bn_lif_add: weight blob does not match the descriptor")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    _require_numel(residual, s.T * M * residual_planes * s.C_out // 32, torch.int32, "residual")
+    if state is not None:
+        _require_cuda(state, "state")
+        _require_numel(state, M * s.C_out, torch.float32, "state")
+    if out is None:
+        out = torch.empty(s.T * s.B, OH, OW, out_planes * s.C_out // 32, dtype=torch.int32, device=dev)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, s.T * M * out_planes * s.C_out // 32, torch.int32, "out")
+    rc = lib.sengine_amd_fused_sparse_conv_bn_lif_add(
+        ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta), _ptr(state), _ptr(bn_scale), _ptr(bn_bias),
+        _ptr(residual), int(residual_planes), _ptr(out), int(out_planes), _stream(dev))
+    check(rc, "fused_sparse_conv_bn_lif_add")
+    return out
+
+
+def stem_conv_bn(s: ConvSpec, x: torch.Tensor, weight: torch.Tensor, bn_scale: torch.Tensor, bn_bias: torch.Tensor,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense fp32 conv + folded BN on NCHW images (s.B images; s.T ignored) -> NHWC fp32."""
+    lib = _lib.load()
+    for t, n in ((x, "x"), (weight, "weight"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    _require_numel(x, s.B * s.C_in * s.H * s.W, torch.float32, "x")
+    _require_numel(weight, s.C_out * s.C_in * s.KH * s.KW, torch.float32, "weight")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    OH = (s.H + 2 * s.padding - s.KH) // s.stride + 1
+    OW = (s.W + 2 * s.padding - s.KW) // s.stride + 1
+    if out is None:
+        out = torch.empty(s.B, OH, OW, s.C_out, dtype=torch.float32, device=x.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, s.B * OH * OW * s.C_out, torch.float32, "out")
+    d = make_desc(s)
+    check(lib.sengine_amd_stem_conv_bn(ctypes.byref(d), _ptr(x), _ptr(weight), _ptr(bn_scale), _ptr(bn_bias),
+                                       _ptr(out), _stream(x.device)), "stem_conv_bn")
+    return out
+
+
+def multistep_neuron_repeat(x: torch.Tensor, T: int, neuron: str = "lif", tau: float = 2.0, v_threshold: float = 1.0,
+                            v_reset: Optional[float] = 0.0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Neuron over T steps of the same input x (fp32, n % 32 == 0): spike bits int32 (T, n/32)."""
+    lib = _lib.load()
+    _require_cuda(x, "x")
+    if x.dtype != torch.float32:
+        raise SEngineError("multistep_neuron_repeat: x must be fp32")
+    n = x.numel()
+    if out is None:
+        out = torch.empty(T, n // 32, dtype=torch.int32, device=x.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, T * n // 32, torch.int32, "out")
+    hard = v_reset is not None
+    check(lib.sengine_amd_multistep_neuron_repeat(int(T), int(n), NEURON_LIF if neuron == "lif" else NEURON_IF,
+                                                  int(hard), float(tau), float(v_threshold),
+                                                  float(v_reset if hard else 0.0), _ptr(x), _ptr(out),
+                                                  _stream(x.device)), "multistep_neuron_repeat")
+    return out
+
+
+def maxpool_spikes(x: torch.Tensor, NT: int, H: int, W: int, C: int, k: int = 3, stride: int = 2, pad: int = 1,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Max-pool spike bits (NT, H, W, C/32 words) -> (NT, OH, OW, C/32)."""
+    lib = _lib.load()
+    _require_cuda(x, "x")
+    _require_numel(x, NT * H * W * C // 32, torch.int32, "x")
+    OH, OW = (H + 2 * pad - k) // stride + 1, (W + 2 * pad - k) // stride + 1
+    if out is None:
+        out = torch.empty(NT, OH, OW, C // 32, dtype=torch.int32, device=x.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, NT * OH * OW * C // 32, torch.int32, "out")
+    check(lib.sengine_amd_maxpool_spikes(NT, H, W, C, k, stride, pad, _ptr(x), _ptr(out), _stream(x.device)),
+          "maxpool_spikes")
+    return out
+
+
+def sew_head(x: torch.Tensor, T: int, B: int, HW: int, C: int, planes: int, fc_weight: torch.Tensor,
+             fc_bias: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Average pool + mean over T + Linear on `planes`-plane integer activations -> (B, N_out) fp32."""
+    lib = _lib.load()
+    for t, n in ((x, "x"), (fc_weight, "fc_weight"), (fc_bias, "fc_bias")):
+        _require_cuda(t, n)
+    _require_numel(x, T * B * HW * planes * C // 32, torch.int32, "x")
+    N_out = fc_weight.shape[0]
+    _require_numel(fc_weight, N_out * C, torch.float32, "fc_weight")
+    _require_numel(fc_bias, N_out, torch.float32, "fc_bias")
+    if out is None:
+        out = torch.empty(B, N_out, dtype=torch.float32, device=x.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, B * N_out, torch.float32, "out")
+    check(lib.sengine_amd_sew_head(T, B, HW, C, planes, _ptr(x), _ptr(fc_weight), _ptr(fc_bias), N_out, _ptr(out),
+                                   _stream(x.device)), "sew_head")
     return out
 
 

@@ -95,3 +95,11 @@ def fold_batchnorm(gamma, beta, running_mean, running_var, eps: float = 1e-5, co
     cb = np.zeros_like(mu) if conv_bias is None else f64(conv_bias)
     bias = scale * (cb - mu) + b
     return torch.from_numpy(scale.astype(np.float32)), torch.from_numpy(bias.astype(np.float32))
+
+
+def expand_planes(w: torch.Tensor, planes: int) -> torch.Tensor:
+    """Weights for a conv whose input is stored as `planes` bit planes (an integer activation
+    x = sum_p 2^p b_p, e.g. a SEW 'ADD' output): conv(x, W) = conv([b_0, b_1, ...], [W, 2W, ...])
+    with the planes stacked along the input channels.  Scaling by 2^p is exact in fp16/fp32 and
+    keeps the 2:4 pattern of every plane's copy."""
+    return torch.cat([w * float(1 << p) for p in range(planes)], dim=1)
