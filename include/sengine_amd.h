@@ -168,10 +168,11 @@ int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_desc* d, con
 /*
  * Dense stem convolution on images + folded BN (the reference runs it through cuDNN,
  * sengine/csrc/cpp_executor.cu:306-347; models/sewresnet.py:140-141,199-200):
- * x NCHW fp32 (d->B images, d->C_in, d->H, d->W), weight OIHW fp32, out NHWC fp32
- * (d->B, OH, OW, d->C_out).  Any C_in / kernel / stride / pad (dilation 1); T is ignored.
+ * x NCHW fp32 (d->B images, d->C_in, d->H, d->W), weight fp32 in w_layout (HWIO reads
+ * coalesced, OIHW does not), out NHWC fp32 (d->B, OH, OW, d->C_out).  Any C_in / kernel /
+ * stride / pad (dilation 1); T is ignored.
  */
-int sengine_amd_stem_conv_bn(const sengine_conv_lif_desc* d, const float* x, const float* weight,
+int sengine_amd_stem_conv_bn(const sengine_conv_lif_desc* d, const float* x, const float* weight, int32_t w_layout,
                              const float* bn_scale, const float* bn_bias, float* out, hipStream_t stream);
 
 /*
@@ -195,10 +196,11 @@ int sengine_amd_maxpool_spikes(int32_t NT, int32_t H, int32_t W, int32_t C, int3
 /*
  * Head: AdaptiveAvgPool2d(1) per timestep, mean over T, Linear (models/sewresnet.py:152-153,
  * 208-210).  in: integer activations as `planes` bit planes, (T*B, HW) positions x planes*C
- * bits; fc_weight (N_out, C) fp32, fc_bias (N_out); out (B, N_out) fp32.
+ * bits; fc_weight_t (C, N_out) fp32 = the transposed nn.Linear weight, fc_bias (N_out);
+ * out (B, N_out) fp32.
  */
 int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t planes, const uint32_t* in,
-                         const float* fc_weight, const float* fc_bias, int32_t N_out, float* out,
+                         const float* fc_weight_t, const float* fc_bias, int32_t N_out, float* out,
                          hipStream_t stream);
 
 /*

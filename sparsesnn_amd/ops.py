@@ -283,8 +283,9 @@ def fused_sparse_conv_bn_lif_add(s: ConvSpec, data: torch.Tensor, values: torch.
 
 
 def stem_conv_bn(s: ConvSpec, x: torch.Tensor, weight: torch.Tensor, bn_scale: torch.Tensor, bn_bias: torch.Tensor,
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Dense fp32 conv + folded BN on NCHW images (s.B images; s.T ignored) -> NHWC fp32."""
+                 out: Optional[torch.Tensor] = None, layout: int = WLAYOUT_OIHW) -> torch.Tensor:
+    """Dense fp32 conv + folded BN on NCHW images (s.B images; s.T ignored) -> NHWC fp32.
+    weight: OIHW, or HWIO (KH, KW, C_in, C_out) with layout=WLAYOUT_HWIO (coalesced reads)."""
     lib = _lib.load()
     for t, n in ((x, "x"), (weight, "weight"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
         _require_cuda(t, n)
@@ -300,8 +301,8 @@ def stem_conv_bn(s: ConvSpec, x: torch.Tensor, weight: torch.Tensor, bn_scale: t
         _require_cuda(out, "out")
         _require_numel(out, s.B * OH * OW * s.C_out, torch.float32, "out")
     d = make_desc(s)
-    check(lib.sengine_amd_stem_conv_bn(ctypes.byref(d), _ptr(x), _ptr(weight), _ptr(bn_scale), _ptr(bn_bias),
-                                       _ptr(out), _stream(x.device)), "stem_conv_bn")
+    check(lib.sengine_amd_stem_conv_bn(ctypes.byref(d), _ptr(x), _ptr(weight), int(layout), _ptr(bn_scale),
+                                       _ptr(bn_bias), _ptr(out), _stream(x.device)), "stem_conv_bn")
     return out
 
 
@@ -345,12 +346,13 @@ def maxpool_spikes(x: torch.Tensor, NT: int, H: int, W: int, C: int, k: int = 3,
 
 def sew_head(x: torch.Tensor, T: int, B: int, HW: int, C: int, planes: int, fc_weight: torch.Tensor,
              fc_bias: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Average pool + mean over T + Linear on `planes`-plane integer activations -> (B, N_out) fp32."""
+    """Average pool + mean over T + Linear on `planes`-plane integer activations -> (B, N_out) fp32.
+    fc_weight: the transposed Linear weight, (C, N_out) contiguous."""
     lib = _lib.load()
     for t, n in ((x, "x"), (fc_weight, "fc_weight"), (fc_bias, "fc_bias")):
         _require_cuda(t, n)
     _require_numel(x, T * B * HW * planes * C // 32, torch.int32, "x")
-    N_out = fc_weight.shape[0]
+    N_out = fc_weight.shape[1]
     _require_numel(fc_weight, N_out * C, torch.float32, "fc_weight")
     _require_numel(fc_bias, N_out, torch.float32, "fc_bias")
     if out is None:

@@ -106,6 +106,7 @@ class Block:
     OH: int
     OW: int
     C_out: int
+    stride: int
     bufs: dict = field(default_factory=dict)
 
 
@@ -128,7 +129,7 @@ class SEWResNet18Engine:
         # ---- stem: dense fp32 conv 7x7/2 + BN, neuron over the repeated output, max-pool
         sc, bi = fold_batchnorm(p["bn1.weight"], p["bn1.bias"], p["bn1.running_mean"], p["bn1.running_var"])
         self.stem_spec = ConvSpec(T=1, B=batch, C_in=in_channels, H=H, W=W, C_out=64, KH=7, KW=7, stride=2, padding=3)
-        self.stem_w = p["conv1.weight"].contiguous().to(self.dev)
+        self.stem_w = p["conv1.weight"].permute(2, 3, 1, 0).contiguous().to(self.dev)  # HWIO: coalesced
         self.stem_scale, self.stem_bias = sc.to(self.dev), bi.to(self.dev)
         self.H1, self.W1 = (H + 6 - 7) // 2 + 1, (W + 6 - 7) // 2 + 1
         self.H2, self.W2 = (self.H1 + 2 - 3) // 2 + 1, (self.W1 + 2 - 3) // 2 + 1
@@ -158,7 +159,7 @@ class SEWResNet18Engine:
                 out_planes = _planes_for(out_max)
                 if out_planes > 3:
                     raise SEngineError("SEW sums above 7 need more than 3 bit planes")
-                blk = Block(pre, conv1, conv2, ds, x_planes, id_planes, out_planes, h, w, oh, ow, planes)
+                blk = Block(pre, conv1, conv2, ds, x_planes, id_planes, out_planes, h, w, oh, ow, planes, s)
                 TB = T * batch
                 blk.bufs["s1"] = torch.empty(TB, oh, ow, planes // 32, dtype=torch.int32, device=self.dev)
                 if ds is not None:
@@ -168,9 +169,9 @@ class SEWResNet18Engine:
                 self.blocks.append(blk)
                 inplanes, h, w, x_planes, x_max = planes, oh, ow, out_planes, out_max
         self.final_planes, self.final_hw, self.final_c = x_planes, h * w, inplanes
-        self.fc_w = p["fc.weight"].contiguous().to(self.dev)
+        self.fc_w = p["fc.weight"].t().contiguous().to(self.dev)  # (C, N_out): coalesced head reads
         self.fc_b = p["fc.bias"].contiguous().to(self.dev)
-        self.logits = torch.empty(batch, self.fc_w.shape[0], dtype=torch.float32, device=self.dev)
+        self.logits = torch.empty(batch, self.fc_w.shape[1], dtype=torch.float32, device=self.dev)
 
     # ------------------------------------------------------------------ build helpers
     def _fused(self, prefix, p, cin, cout, k, stride, pad, h, w, in_planes) -> FusedConv:
@@ -183,10 +184,24 @@ class SEWResNet18Engine:
             raise SEngineError(f"{wkey}: not 2:4 sparse along C_in (prune it, or run it on the dense fallback)")
         sc, bi = fold_batchnorm(p[bn + ".weight"], p[bn + ".bias"], p[bn + ".running_mean"], p[bn + ".running_var"])
         wx = expand_planes(w_, in_planes) if in_planes > 1 else w_
-        spec = ConvSpec(T=self.T, B=self.B, C_in=cin * in_planes, H=h, W=w, C_out=cout, KH=k, KW=k, stride=stride,
-                        padding=pad, neuron=self.neuron, hard_reset=self.vreset is not None, tau=self.tau,
-                        v_threshold=self.vth, v_reset=0.0 if self.vreset is None else self.vreset,
-                        weight_planes=self.planes_w)
+        oh, ow = (h + 2 * pad - k) // stride + 1, (w + 2 * pad - k) // stride + 1
+        geo = dict(C_in=cin * in_planes, H=h, W=w, KH=k, KW=k, stride=stride, padding=pad)
+        if k > 1 and oh == 1 and ow == 1:
+            # One output pixel per image (the last stage on small inputs): the conv is a 1x1
+            # conv over the whole image flattened into channels, NHWC order (pixel, plane, c),
+            # with the weights of the taps that land inside the image and zeros elsewhere.
+            # Same memory, no padded taps multiplied.
+            flat = torch.zeros(cout, h, w, wx.shape[1])
+            for ih in range(h):
+                for iw in range(w):
+                    kh, kw = ih + pad, iw + pad
+                    if kh < k and kw < k:
+                        flat[:, ih, iw, :] = wx[:, :, kh, kw]
+            wx = flat.reshape(cout, h * w * wx.shape[1], 1, 1)
+            geo = dict(C_in=h * w * cin * in_planes, H=1, W=1, KH=1, KW=1, stride=1, padding=0)
+        spec = ConvSpec(T=self.T, B=self.B, C_out=cout, neuron=self.neuron, hard_reset=self.vreset is not None,
+                        tau=self.tau, v_threshold=self.vth, v_reset=0.0 if self.vreset is None else self.vreset,
+                        weight_planes=self.planes_w, **geo)
         wdev = wx.contiguous().to(self.dev)
         if self.planes_w == 1:
             wdev = wdev.half()
@@ -195,7 +210,8 @@ class SEWResNet18Engine:
 
     # ------------------------------------------------------------------ execution
     def run_stem(self):
-        ops.stem_conv_bn(self.stem_spec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias, out=self.stem_out)
+        ops.stem_conv_bn(self.stem_spec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias, out=self.stem_out,
+                         layout=ops.WLAYOUT_HWIO)
         ops.multistep_neuron_repeat(self.stem_out, self.T, self.neuron, self.tau, self.vth, self.vreset,
                                     out=self.stem_spk.view(self.T, -1))
         ops.maxpool_spikes(self.stem_spk, self.T * self.B, self.H1, self.W1, 64, 3, 2, 1, out=self.pool_out)
@@ -207,14 +223,14 @@ class SEWResNet18Engine:
         blk = self.blocks[i]
         x = self.block_input(i) if x is None else x
         c1, c2, ds = blk.conv1, blk.conv2, blk.downsample
-        ops.fused_sparse_conv_bn_lif(c1.spec, x, c1.values, c1.meta, c1.scale, c1.bias, out=blk.bufs["s1"])
+        ops.fused_sparse_conv_bn_lif(c1.spec, x.view(-1), c1.values, c1.meta, c1.scale, c1.bias, out=blk.bufs["s1"])
         if ds is not None:
             ops.fused_sparse_conv_bn_lif(ds.spec, x, ds.values, ds.meta, ds.scale, ds.bias, out=blk.bufs["ds"])
             identity = blk.bufs["ds"]
         else:
             identity = x
-        ops.fused_sparse_conv_bn_lif_add(c2.spec, blk.bufs["s1"], c2.values, c2.meta, c2.scale, c2.bias, identity,
-                                         blk.id_planes, blk.out_planes, out=blk.bufs["out"])
+        ops.fused_sparse_conv_bn_lif_add(c2.spec, blk.bufs["s1"].view(-1), c2.values, c2.meta, c2.scale, c2.bias,
+                                         identity, blk.id_planes, blk.out_planes, out=blk.bufs["out"])
 
     def run_head(self):
         ops.sew_head(self.blocks[-1].bufs["out"], self.T, self.B, self.final_hw, self.final_c, self.final_planes,

@@ -24,13 +24,15 @@ def _bits_to_seq(t: torch.Tensor, T, B, C, H, W, planes=1):
     return pk.planes_to_seq(w, planes, T, B, C, H, W)
 
 
-def test_stem_conv_bn_matches_fp32_conv(dev):
+@pytest.mark.parametrize("layout", [ops.WLAYOUT_OIHW, ops.WLAYOUT_HWIO])
+def test_stem_conv_bn_matches_fp32_conv(dev, layout):
     p = sr.make_params(1, bn_random=True)
     x = sr.make_images(2, 3)
     spec = ops.ConvSpec(T=1, B=3, C_in=3, H=32, W=32, C_out=64, KH=7, KW=7, stride=2, padding=3)
     sc, bi = ref.fold_batchnorm(p["bn1.weight"], p["bn1.bias"], p["bn1.running_mean"], p["bn1.running_var"])
-    out = ops.stem_conv_bn(spec, x.to(dev), p["conv1.weight"].to(dev), torch.from_numpy(sc).to(dev),
-                           torch.from_numpy(bi).to(dev))
+    w = p["conv1.weight"] if layout == ops.WLAYOUT_OIHW else p["conv1.weight"].permute(2, 3, 1, 0).contiguous()
+    out = ops.stem_conv_bn(spec, x.to(dev), w.to(dev), torch.from_numpy(sc).to(dev), torch.from_numpy(bi).to(dev),
+                           layout=layout)
     exp = F.conv2d(x, p["conv1.weight"], None, 2, 3) * torch.from_numpy(sc)[:, None, None] + \
         torch.from_numpy(bi)[:, None, None]
     got = out.cpu().permute(0, 3, 1, 2)
@@ -72,7 +74,7 @@ def test_sew_head(dev, planes, HW):
     bits = torch.from_numpy(pk.seq_to_planes(a, planes).view(np.int32)).to(dev)
     w = torch.randn(10, C) * 0.1
     b = torch.randn(10) * 0.1
-    y = ops.sew_head(bits, T, B, HW, C, planes, w.to(dev), b.to(dev)).cpu()
+    y = ops.sew_head(bits, T, B, HW, C, planes, w.t().contiguous().to(dev), b.to(dev)).cpu()
     feat = torch.from_numpy(a.astype(np.float32)).flatten(3).mean(3).mean(0)
     assert torch.allclose(y, feat @ w.T + b, atol=1e-5)
 
@@ -130,7 +132,7 @@ def test_engine_blocks_teacher_forced(dev, sew_case):
         eng.run_block(i, x=xd)
         torch.cuda.synchronize()
         pre = blk.name
-        s = blk.conv1.spec.stride
+        s = blk.stride  # the block's conv stride (the engine may run a conv in a reduced form)
         bn1 = sr._bn(p, pre + ".conv1.module.1")
         r1 = ref.fused_layer(torch.from_numpy(xin), p[pre + ".conv1.module.0.weight"], bn1, s, 1, 1, "lif", 2.0, 1.0,
                              0.0)
