@@ -127,18 +127,21 @@ def cpu_baseline(budget_s=12.0, min_runs=2):
                        f"{len(ts)} sweeps ({sum(ts):.1f} s timed) after 1 warmup")
 
 
-TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "fused_sparse_lds_cfg1_traffic.md")
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "fused_tile_kernel_cfg1_sweep_traffic.md")
+# the sources the sweep's kernels are built from (the halo-tiled fused kernel and its dispatch)
+SWEEP_KERNEL_SOURCES = ("common.h", "epilogue.h", "internal.h", "tile_kernel.h", "fused_tile1.hip", "fused_tile3.hip",
+                        "fused_sparse.hip")
 
 
 def kernel_source_hash() -> str:
-    """sha256 over the HIP sources of the library (ties a counter profile to a kernel build)."""
-    import glob
+    """sha256 over the HIP sources of the sweep's kernels (ties a counter profile to a kernel build)."""
     import hashlib
     h = hashlib.sha256()
     root = os.path.join(os.path.dirname(os.path.abspath(__file__)), "sparsesnn_amd", "csrc")
-    for f in sorted(glob.glob(os.path.join(root, "*"))):
-        with open(f, "rb") as fh:
-            h.update(os.path.basename(f).encode() + b"\0" + fh.read())
+    for name in SWEEP_KERNEL_SOURCES:
+        with open(os.path.join(root, name), "rb") as fh:
+            h.update(name.encode() + b"\0" + fh.read())
     return h.hexdigest()[:16]
 
 
@@ -224,6 +227,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--json-out", default="")
     ap.add_argument("--no-e2e", action="store_true", help="skip the SEW-ResNet-18 end-to-end measurement")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="only the SEW-ResNet-18 end-to-end measurement (prints its JSON object; for profiling)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="counter-collection pass for rocprofv3 --pmc: eager launches only (no graph, no "
                          "JSON line), followed by the copy-calibration kernel")
@@ -238,6 +243,12 @@ def main():
 
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.e2e_only:
+        e2e = bench_e2e(dev, warmup=args.warmup, iters=args.steps)
+        print(json.dumps({"metric": "images/sec", "value": round(E2E_BATCH / e2e["batch_s"], 1),
+                          "ms_per_batch": round(e2e["batch_s"] * 1e3, 4), "batch": E2E_BATCH, "timesteps": T_STEPS,
+                          "replays": args.steps, "warmup": args.warmup}))
+        return
     work = build_workloads(dev, T_STEPS, BATCH)
 
     # per-launch durations: HIP events on the launch stream around bursts of BURST back-to-back
@@ -332,8 +343,8 @@ def main():
             "frac": round(avg_flops / avg_launch / P_SPARSE, 4),
             "traffic": measured_traffic(),
             "traffic_algorithmic": round(sum(wk["bytes_min"] for wk in work) / len(work)),
-            "kernel": "sengine::fused_sparse_lds_kernel<T=4,...> (spike-bit LDS-staged kernel; "
-                      "mean over all 15 sweep launches)",
+            "kernel": "sengine::fused_tile_kernel<T=4,...> (halo-tiled spike-bit kernel: 3x3 layers KS=3, "
+                      "the 1x1 layer KS=1; mean over all 15 sweep launches)",
             "avg_launch_us": round(avg_launch * 1e6, 3),
             "note": "dense-equivalent FLOPs vs the 5.0 PFLOP/s 2:4 peak == useful FLOPs vs the 2.5 PFLOP/s dense peak",
         },
