@@ -176,6 +176,21 @@ int sengine_amd_stem_conv_bn(const sengine_conv_lif_desc* d, const float* x, con
                              const float* bn_scale, const float* bn_bias, float* out, hipStream_t stream);
 
 /*
+ * The stem, its neuron and the max-pool in one launch (models/sewresnet.py:199-203: conv1,
+ * bn1, repeat over T, sn1, maxpool): conv + folded BN as sengine_amd_stem_conv_bn (HWIO
+ * weights), the neuron of d (V0 = 0) on that output repeated over d->T, then
+ * MaxPool2d(pool_k, pool_stride, pool_pad) of the spikes.  pooled: (T, B, POH, POW) x
+ * C_out bits; spikes (optional, may be NULL): the stem spikes (T, B, OH, OW) x C_out bits.
+ * Bit-identical to the three separate entry points.  Needs C_out % 32 == 0, T <= 16,
+ * OH*OW <= 256 and the image's staged input rows and weights within LDS (a 3x32x32 image
+ * with a 7x7/2 stem fits); returns -2 otherwise.
+ */
+int sengine_amd_stem_conv_bn_lif_pool(const sengine_conv_lif_desc* d, const float* x, const float* weight,
+                                      const float* bn_scale, const float* bn_bias, int32_t pool_k,
+                                      int32_t pool_stride, int32_t pool_pad, uint32_t* spikes, uint32_t* pooled,
+                                      hipStream_t stream);
+
+/*
  * Multi-step neuron on an input repeated at every timestep (the stem output,
  * x.unsqueeze(0).repeat(T), models/sewresnet.py:201-202): x fp32 (n), V0 = 0,
  * spikes bits (T, n); n % 32 == 0.
@@ -196,11 +211,10 @@ int sengine_amd_maxpool_spikes(int32_t NT, int32_t H, int32_t W, int32_t C, int3
 /*
  * Head: AdaptiveAvgPool2d(1) per timestep, mean over T, Linear (models/sewresnet.py:152-153,
  * 208-210).  in: integer activations as `planes` bit planes, (T*B, HW) positions x planes*C
- * bits; fc_weight_t (C, N_out) fp32 = the transposed nn.Linear weight, fc_bias (N_out);
- * out (B, N_out) fp32.
+ * bits; fc_weight (N_out, C) fp32 (nn.Linear layout), fc_bias (N_out); out (B, N_out) fp32.
  */
 int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t planes, const uint32_t* in,
-                         const float* fc_weight_t, const float* fc_bias, int32_t N_out, float* out,
+                         const float* fc_weight, const float* fc_bias, int32_t N_out, float* out,
                          hipStream_t stream);
 
 /*

@@ -126,6 +126,29 @@ def compress_2_4(w: np.ndarray, planes: int = 1):
     return values.view(np.uint16), meta, violations.reshape(-1)
 
 
+def flat_weight(w: np.ndarray, H: int, W: int, stride: int = 1, padding: int = 0, dilation: int = 1) -> np.ndarray:
+    """The flat small-output layout of this build's library: an OIHW conv weight
+    (C_out, C_in, KH, KW) applied to H x W inputs as one matrix (N_flat, K_flat, 1, 1) with
+    rows (oh, ow, c_out) and reduction (ih, iw, c_in) -- NHWC order on both sides -- holding
+    w[f, c, kh, kw] where input pixel (ih, iw) meets output pixel (oh, ow) through tap
+    (kh, kw), and 0 elsewhere.  conv2d(x, w) == x_nhwc_flat @ flat.T (pinned against
+    torch.nn.functional.conv2d in tests/test_oracle.py)."""
+    w = np.asarray(w)
+    C_out, C_in, KH, KW = w.shape
+    OH = (H + 2 * padding - dilation * (KH - 1) - 1) // stride + 1
+    OW = (W + 2 * padding - dilation * (KW - 1) - 1) // stride + 1
+    flat = np.zeros((OH, OW, C_out, H, W, C_in), w.dtype)
+    for oh in range(OH):
+        for ow in range(OW):
+            for kh in range(KH):
+                for kw in range(KW):
+                    ih = oh * stride - padding + kh * dilation
+                    iw = ow * stride - padding + kw * dilation
+                    if 0 <= ih < H and 0 <= iw < W:
+                        flat[oh, ow, :, ih, iw, :] = w[:, :, kh, kw]
+    return flat.reshape(OH * OW * C_out, H * W * C_in, 1, 1)
+
+
 def decompress_2_4(values: np.ndarray, meta: np.ndarray, shape) -> np.ndarray:
     """Inverse of compress_2_4 (planes summed in fp32) -> OIHW float32."""
     C_out, C_in, KH, KW = shape

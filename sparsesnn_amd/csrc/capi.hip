@@ -41,6 +41,16 @@ int check_desc(const sengine_conv_lif_desc* d, Geometry* geo, bool sparse) {
   return 0;
 }
 
+bool flat_layout(const sengine_conv_lif_desc* d, const Geometry& geo) {
+  const int64_t npix = (int64_t)geo.OH * geo.OW;
+  const int64_t kf = (int64_t)d->H * d->W * d->C_in;
+  const int64_t nf = npix * d->C_out;
+  // the flat matrix multiplies H*W / (KH*KW) times the conv's own work (taps outside the
+  // window are zeros): allowed up to kFlatMaxWaste
+  const bool cheap = (int64_t)d->H * d->W <= kFlatMaxWaste * d->KH * d->KW;
+  return npix <= kFlatMaxPixels && kf <= kFlatMaxK && nf * kf <= kFlatMaxEntries && cheap;
+}
+
 static int g_kernel_choice = -1;
 
 int fused_kernel_choice() {
@@ -119,8 +129,9 @@ extern "C" int sengine_amd_sparse_blob_bytes(const sengine_conv_lif_desc* d, siz
   Geometry geo;
   int rc = check_desc(d, &geo, true);
   if (rc) return rc;
-  const size_t groups = (size_t)d->C_out / 64;
-  const size_t nq = (size_t)(geo.K_red / 64);
+  const bool flat = flat_layout(d, geo);
+  const size_t groups = (size_t)(flat ? (int64_t)geo.OH * geo.OW * d->C_out : d->C_out) / 64;
+  const size_t nq = (size_t)((flat ? (int64_t)d->H * d->W * d->C_in : geo.K_red) / 64);
   // per (group, chunk, plane, tile): 64 lanes x 8 fp16; per (group, chunk, tile): 64 lanes x u32
   if (value_bytes) *value_bytes = groups * nq * d->weight_planes * 4 * 64 * 16;
   if (meta_bytes) *meta_bytes = groups * nq * 4 * 64 * 4;

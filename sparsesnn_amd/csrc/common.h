@@ -90,6 +90,7 @@ struct SewAdd {
   const uint8_t* res;
   int res_planes;  // planes of the residual (1..3)
   int out_planes;  // planes written (>= res_planes; the caller sizes it so no carry is lost)
+  int pix_ch;      // channels per output pixel: planes interleave per pixel, (pixel, plane, c)
 };
 
 // One charge step: returns the charged membrane h given the previous membrane v and

@@ -36,7 +36,22 @@ struct WeightParams {
   int C_out, C_in, KH, KW;
   int nq;
   int planes;
+  // flat layout (sparse blob only): rows (opix, c_out), reduction (ipix, c_in)
+  int flat, W, OW, SH, SW, PH, PW, DH, DW;
+  int rows;  // blob rows: C_out, or OH*OW*C_out in the flat layout
 };
+
+// Flat layout: the conv tap that input pixel ipix contributes to output pixel opix
+// through, or false when it falls outside the kernel.
+__device__ __forceinline__ bool flat_tap(const WeightParams& p, int opix, int ipix, int& kh, int& kw) {
+  const int oh = opix / p.OW, ow = opix - (opix / p.OW) * p.OW;
+  const int ih = ipix / p.W, iw = ipix - (ipix / p.W) * p.W;
+  const int dh = ih - oh * p.SH + p.PH, dw = iw - ow * p.SW + p.PW;
+  if (dh < 0 || dw < 0 || dh % p.DH != 0 || dw % p.DW != 0) return false;
+  kh = dh / p.DH;
+  kw = dw / p.DW;
+  return kh < p.KH && kw < p.KW;
+}
 
 // Zero test of validate_2_4_pattern (sengine/optimizer.py:522): |w| < 1e-10.
 __device__ __forceinline__ bool is_kept(float x) { return fabsf(x) >= 1e-10f; }
@@ -44,7 +59,7 @@ __device__ __forceinline__ bool is_kept(float x) { return fabsf(x) >= 1e-10f; }
 __global__ __launch_bounds__(256) void compress_2_4_kernel(WeightParams p, half8_t* vals, uint32_t* meta,
                                                            int32_t* violations) {
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)(p.C_out / 64) * p.nq * 4 * 64;
+  const int64_t total = (int64_t)(p.rows / 64) * p.nq * 4 * 64;
   if (tid >= total) return;
   const int lane = (int)(tid & 63);
   const int a = (int)((tid >> 6) & 3);
@@ -52,12 +67,17 @@ __global__ __launch_bounds__(256) void compress_2_4_kernel(WeightParams p, half8
   const int q = (int)(gq % p.nq);
   const int G = (int)(gq / p.nq);
   const int r = lane & 15;
-  const int co = G * 64 + 16 * (r >> 2) + 4 * a + (r & 3);
+  const int row = G * 64 + 16 * (r >> 2) + 4 * a + (r & 3);
   const int kbase = q * 64 + 16 * (lane >> 4);
-  const int tap = kbase / p.C_in;
+  const int tap = kbase / p.C_in;  // flat layout: the input pixel
   const int cin0 = kbase - tap * p.C_in;
-  const int kh = tap / p.KW;
-  const int kw = tap - kh * p.KW;
+  int co = row, kh = tap / p.KW, kw = tap - (tap / p.KW) * p.KW;
+  bool inside = true;
+  if (p.flat) {
+    const int opix = row / p.C_out;
+    co = row - opix * p.C_out;
+    inside = flat_tap(p, opix, tap, kh, kw);
+  }
 
   float kept[8];
   uint32_t bits = 0;
@@ -66,7 +86,9 @@ __global__ __launch_bounds__(256) void compress_2_4_kernel(WeightParams p, half8
     float w4[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      w4[e] = load_weight(p.w, p.w_enc, p.w_layout, co, cin0 + 4 * gi + e, kh, kw, p.C_out, p.C_in, p.KH, p.KW);
+      w4[e] = inside ? load_weight(p.w, p.w_enc, p.w_layout, co, cin0 + 4 * gi + e, kh, kw, p.C_out, p.C_in, p.KH,
+                                   p.KW)
+                     : 0.f;
     int pos[2] = {-1, -1};
     int n = 0;
 #pragma unroll
@@ -88,7 +110,7 @@ __global__ __launch_bounds__(256) void compress_2_4_kernel(WeightParams p, half8
       kept[2 * gi + s] = is_kept(x) ? x : 0.f;
       bits |= (uint32_t)pos[s] << (2 * (2 * gi + s));
     }
-    if (violations) {
+    if (violations && inside) {  // flat layout: every copy of a group writes the same value
       const int64_t gid = (((int64_t)co * p.KH + kh) * p.KW + kw) * (p.C_in / 4) + (cin0 / 4) + gi;
       violations[gid] = n > 2 ? 1 : 0;
     }
@@ -152,8 +174,15 @@ extern "C" int sengine_amd_compress_2_4(const sengine_conv_lif_desc* d, const vo
     return set_error(-2, "compress_2_4: weight encoding must be F32 or F16");
   if (w_layout != SENGINE_WLAYOUT_OIHW && w_layout != SENGINE_WLAYOUT_HWIO)
     return set_error(-2, "compress_2_4: unknown weight layout");
-  WeightParams p{weight, w_enc, w_layout, d->C_out, d->C_in, d->KH, d->KW, (int)(geo.K_red / 64), d->weight_planes};
-  const int64_t total = (int64_t)(d->C_out / 64) * p.nq * 256;
+  const bool flat = flat_layout(d, geo);
+  WeightParams p{weight, w_enc, w_layout, d->C_out, d->C_in, d->KH, d->KW, (int)(geo.K_red / 64), d->weight_planes,
+                 flat ? 1 : 0, d->W, geo.OW, d->stride_h, d->stride_w, d->pad_h, d->pad_w, d->dil_h, d->dil_w,
+                 d->C_out};
+  if (flat) {
+    p.nq = (int)((int64_t)d->H * d->W * d->C_in / 64);
+    p.rows = geo.OH * geo.OW * d->C_out;
+  }
+  const int64_t total = (int64_t)(p.rows / 64) * p.nq * 256;
   hipLaunchKernelGGL(compress_2_4_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, p,
                      static_cast<half8_t*>(blob_values), static_cast<uint32_t*>(blob_meta), violations);
   return (int)hipGetLastError();
@@ -169,7 +198,8 @@ extern "C" int sengine_amd_pack_dense_weights(const sengine_conv_lif_desc* d, co
     return set_error(-2, "pack_dense_weights: weight encoding must be F32 or F16");
   if (w_layout != SENGINE_WLAYOUT_OIHW && w_layout != SENGINE_WLAYOUT_HWIO)
     return set_error(-2, "pack_dense_weights: unknown weight layout");
-  WeightParams p{weight, w_enc, w_layout, d->C_out, d->C_in, d->KH, d->KW, (int)(geo.K_red / 32), d->weight_planes};
+  WeightParams p{weight, w_enc, w_layout, d->C_out, d->C_in, d->KH, d->KW, (int)(geo.K_red / 32), d->weight_planes,
+                 0, 0, 0, 0, 0, 0, 0, 0, 0, d->C_out};
   const int64_t total = (int64_t)(d->C_out / 64) * p.nq * 256;
   hipLaunchKernelGGL(pack_dense_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, p,
                      static_cast<half8_t*>(blob_values));

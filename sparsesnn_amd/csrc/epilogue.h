@@ -49,21 +49,51 @@ struct EpiCoeffs {
   const float* bi;
 };
 
-// Store the 16 spike bits of (position row_pos = t*M + m, channels cob..cob+15).
+// The residual words (16 channels, each plane, every t) of one lane, loaded together
+// before the epilogue's t loop: the loads cannot move past the previous step's output
+// stores by themselves, so loading them inside the loop costs one memory latency per t.
+// Channel cob of a row is channel c of output pixel `pix` (one pixel per row unless the
+// layer runs in the flat small-output layout); the planes of a pixel sit together.
+template <int T>
+struct SewRes {
+  uint32_t r[T][3];
+};
+
+template <int T>
+__device__ __forceinline__ void load_sew_res(const SewAdd& sa, int M, int m, int F, int cob, bool valid,
+                                             SewRes<T>& o) {
+  if (sa.res == nullptr) return;
+  const int pix = cob / sa.pix_ch;
+  const int c = cob - pix * sa.pix_ch;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const size_t rbase =
+        ((size_t)t * M + m) * sa.res_planes * F + (size_t)pix * sa.res_planes * sa.pix_ch + c;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+      o.r[t][pl] = (valid && pl < sa.res_planes)
+                       ? *reinterpret_cast<const uint16_t*>(sa.res + ((rbase + (size_t)pl * sa.pix_ch) >> 3))
+                       : 0u;
+  }
+}
+
+// Store the 16 spike bits of (position row_pos = t*M + m, channels cob..cob+15), plus the
+// residual r (its planes) when the SEW add is fused.
 __device__ __forceinline__ void store_spike_word(uint32_t word, size_t row_pos, int F, int cob, uint8_t* out,
-                                                 const SewAdd& sa) {
+                                                 const SewAdd& sa, const uint32_t (&r)[3]) {
   if (sa.res == nullptr) {
     *reinterpret_cast<uint16_t*>(out + ((row_pos * F + cob) >> 3)) = (uint16_t)word;
     return;
   }
-  const size_t rbase = row_pos * (size_t)sa.res_planes * F + cob;
-  const size_t obase = row_pos * (size_t)sa.out_planes * F + cob;
+  const int pix = cob / sa.pix_ch;
+  const int c = cob - pix * sa.pix_ch;
+  const size_t obase = row_pos * (size_t)sa.out_planes * F + (size_t)pix * sa.out_planes * sa.pix_ch + c;
   uint32_t carry = word;
-  for (int pl = 0; pl < sa.out_planes; ++pl) {
-    const uint32_t r = pl < sa.res_planes ? *reinterpret_cast<const uint16_t*>(sa.res + ((rbase + (size_t)pl * F) >> 3))
-                                           : 0u;
-    *reinterpret_cast<uint16_t*>(out + ((obase + (size_t)pl * F) >> 3)) = (uint16_t)(r ^ carry);
-    carry &= r;
+#pragma unroll
+  for (int pl = 0; pl < 3; ++pl) {
+    if (pl >= sa.out_planes) break;
+    *reinterpret_cast<uint16_t*>(out + ((obase + (size_t)pl * sa.pix_ch) >> 3)) = (uint16_t)(r[pl] ^ carry);
+    carry &= r[pl];
   }
 }
 
@@ -79,7 +109,11 @@ __host__ __device__ inline int epilogue_mode(const NeuronParams& np, bool traces
 template <int T, int OUT_ENC, int MODE>
 __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T][4], bool valid, int m, int M, int F,
                                                         int cob, const NeuronParams& np, const EpiCoeffs& cf,
-                                                        uint8_t* __restrict__ out, const SewAdd& sa) {
+                                                        uint8_t* __restrict__ out, const SewAdd& sa,
+                                                        const SewRes<T>* pre) {
+  SewRes<T> res;
+  if (pre) res = *pre;
+  else load_sew_res<T>(sa, M, m, F, cob, valid, res);
   float fsc[16], fbi[16], v[16];
 #pragma unroll
   for (int j = 0; j < 16; j += 4) {
@@ -108,7 +142,7 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
     if (!valid) continue;
     const size_t row = ((size_t)t * M + m) * F + cob;
     if (OUT_ENC == SENGINE_ENC_BITS) {
-      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa);
+      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, res.r[t]);
     } else {
       half8_t o0, o1;
 #pragma unroll
@@ -124,16 +158,20 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
 }
 
 // `valid` false (a padding position past M) computes but stores nothing: keeping the call
-// unconditional avoids a divergent branch whose join reshuffles the accumulators.
+// unconditional avoids a divergent branch whose join reshuffles the accumulators.  `pre`:
+// residual words the kernel loaded earlier (else they are loaded here).
 template <int T, int OUT_ENC, int MODE>
 __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool valid, int m, int M, int F, int cob,
                                              const NeuronParams& np, const EpiCoeffs& cf, float* state,
                                              uint8_t* __restrict__ out, float* h_trace, float* x_trace,
-                                             const SewAdd& sa) {
+                                             const SewAdd& sa, const SewRes<T>* pre = nullptr) {
   if ((MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD) && state == nullptr) {  // uniform branch
-    fast_epilogue_stateless<T, OUT_ENC, MODE>(acc, valid, m, M, F, cob, np, cf, out, sa);
+    fast_epilogue_stateless<T, OUT_ENC, MODE>(acc, valid, m, M, F, cob, np, cf, out, sa, pre);
     return;
   }
+  SewRes<T> res;
+  if (pre) res = *pre;
+  else load_sew_res<T>(sa, M, m, F, cob, valid, res);
   float fsc[16], fbi[16], v[16];
   const bool fold = MODE == EPI_LIF_HARD || (MODE == EPI_GENERIC && np.neuron == SENGINE_NEURON_LIF && np.pow2);
 #pragma unroll
@@ -186,7 +224,7 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
     }
     if (!valid) continue;
     if (OUT_ENC == SENGINE_ENC_BITS) {
-      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa);
+      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, res.r[t]);
     } else {
       half8_t o0, o1;
 #pragma unroll

@@ -42,10 +42,26 @@ struct FusedParams {
   int M;    // B*OH*OW
   int nq;   // K_red / 64
   int64_t in_t_stride;  // pixels per timestep = B*H*W
+  int bn_period;        // BN vectors repeat every bn_period output channels (C_out; flat layout: per pixel)
   NeuronParams np;
   float enc_scale;      // 1/value of a spike fed to the MFMA
   SewAdd sew;
 };
+
+// Folded BN coefficients of output channels G*64 .. G*64+63 into LDS (see epilogue.h).
+__device__ __forceinline__ void load_coeffs(const FusedParams& p, int G, float (&sCoef)[4][64]) {
+  const bool fold = p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2;
+  if (threadIdx.x < 64) {
+    const int c = (G * 64) % p.bn_period + threadIdx.x;
+    const float sc = p.scale[c] * p.enc_scale;
+    const float bi = p.bias[c];
+    sCoef[0][threadIdx.x] = fold ? sc * p.np.rtau : sc;
+    sCoef[1][threadIdx.x] = fold ? bi * p.np.rtau : bi;
+    sCoef[2][threadIdx.x] = sc;
+    sCoef[3][threadIdx.x] = bi;
+  }
+  __syncthreads();
+}
 
 template <int T, int IN_ENC, int OUT_ENC, int PLANES>
 __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedParams p) {
@@ -57,18 +73,7 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
   const int m = blockIdx.x * 64 + wave * 16 + col;
   // folded BN coefficients of the workgroup's 64 channels (see epilogue.h)
   __shared__ float sCoef[4][64];
-  {
-    const bool fold = p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2;
-    if (threadIdx.x < 64) {
-      const float sc = p.scale[G * 64 + threadIdx.x] * p.enc_scale;
-      const float bi = p.bias[G * 64 + threadIdx.x];
-      sCoef[0][threadIdx.x] = fold ? sc * p.np.rtau : sc;
-      sCoef[1][threadIdx.x] = fold ? bi * p.np.rtau : bi;
-      sCoef[2][threadIdx.x] = sc;
-      sCoef[3][threadIdx.x] = bi;
-    }
-    __syncthreads();
-  }
+  load_coeffs(p, G, sCoef);
   const bool mvalid = m < p.M;
   int b = 0, oh = 0, ow = 0;
   if (mvalid) {
@@ -144,6 +149,154 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
                                         p.h_trace, p.x_trace, p.sew);
 }
 
+// ---- small-M variant: split-K over the waves of a workgroup --------------------------------
+// For layers with few output positions (the flat layout: one row per image), the direct
+// kernel's grid is a handful of workgroups, each walking the whole reduction alone.  Here
+// a workgroup of kSmallWaves waves owns 16 positions x 64 channels x all T; wave s
+// accumulates the reduction chunks q = s, s + kSmallWaves, ... (the next chunk's operands
+// are loaded before the current one is multiplied), the partial accumulators are summed
+// in LDS in wave order (deterministic), and wave 0 runs the epilogue.  Spike-bit input,
+// 1x1 geometry (the flat view), any T of the direct kernel.  Operands are loaded two
+// chunks ahead; the cross-wave sum takes up to four timesteps per LDS round.
+constexpr int kSmallWaves = 8;
+
+template <int T, int PLANES>
+struct SmallOperands {
+  half8_t av[PLANES][4];
+  uint32_t ix[4];
+  uint2 bw[T];
+};
+
+template <int T, int OUT_ENC, int PLANES, int MODE>
+__global__ __launch_bounds__(64 * kSmallWaves) void fused_smallm_kernel(FusedParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+  const int G = blockIdx.y;
+  const int m = blockIdx.x * 16 + col;
+  constexpr int TR = T < 4 ? T : 4;  // timesteps per reduction round
+  __shared__ float sCoef[4][64];
+  __shared__ float4_t red[kSmallWaves][TR][4][64];
+  const bool mvalid = m < p.M;
+  // Everything the epilogue reads from memory is requested now, next to the first operand
+  // loads, instead of after the reduction: BN vectors (to LDS before the first barrier)
+  // and, in wave 0, the SEW residual words.
+  float csc = 0.f, cbi = 0.f;
+  if (threadIdx.x < 64) {
+    const int c = (G * 64) % p.bn_period + threadIdx.x;
+    csc = p.scale[c];
+    cbi = p.bias[c];
+  }
+  SewRes<T> res;
+  if (wave == 0) load_sew_res<T>(p.sew, p.M, m, p.F, G * 64 + g * 16, mvalid, res);
+
+  float4_t acc[T][4];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) acc[t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nq = p.nq;
+  const int rowbytes = p.C >> 3;  // bytes of one position's input (the whole flattened image)
+  const uint8_t* src = p.in + (size_t)(mvalid ? m : 0) * rowbytes;
+  const size_t tstride = (size_t)p.in_t_stride * rowbytes;
+  const half8_t* wv = p.wvals + (size_t)G * nq * PLANES * 4 * 64 + lane;
+  const uint32_t* wm = p.wmeta + (size_t)G * nq * 4 * 64 + lane;
+  const uint32_t sel = 0x0c0c0000u | ((uint32_t)(4 + g) << 8) | (uint32_t)g;
+
+  auto load = [&](int q, SmallOperands<T, PLANES>& o) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+#pragma unroll
+      for (int pl = 0; pl < PLANES; ++pl) o.av[pl][a] = wv[((size_t)(q * PLANES + pl) * 4 + a) * 64];
+      o.ix[a] = wm[((size_t)q * 4 + a) * 64];
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      o.bw[t] = mvalid ? *reinterpret_cast<const uint2*>(src + t * tstride + q * 8) : uint2{0u, 0u};
+  };
+  constexpr int S = kSmallWaves;
+  constexpr bool DEEP = T * PLANES <= 4;  // two chunks ahead where the registers allow, else one
+  SmallOperands<T, PLANES> cur, n1, n2;
+  if (wave < nq) load(wave, cur);
+  if (DEEP && wave + S < nq) load(wave + S, n1);
+  for (int q = wave; q < nq; q += S) {
+    if (DEEP) {
+      if (q + 2 * S < nq) load(q + 2 * S, n2);
+    } else if (q + S < nq) {
+      load(q + S, n1);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const half16_t bf = expand_bits16(__builtin_amdgcn_perm(cur.bw[t].y, cur.bw[t].x, sel));
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int pl = 0; pl < PLANES; ++pl)
+          acc[t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(cur.av[pl][a], bf, acc[t][a], cur.ix[a], 0, 0);
+    }
+    cur = n1;
+    if (DEEP) n1 = n2;
+  }
+
+  if (threadIdx.x < 64) {
+    const bool fold = p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2;
+    const float sc = csc * p.enc_scale;
+    sCoef[0][threadIdx.x] = fold ? sc * p.np.rtau : sc;
+    sCoef[1][threadIdx.x] = fold ? cbi * p.np.rtau : cbi;
+    sCoef[2][threadIdx.x] = sc;
+    sCoef[3][threadIdx.x] = cbi;
+  }
+  // deterministic cross-wave sum (wave order), TR timesteps per round
+#pragma unroll
+  for (int t0 = 0; t0 < T; t0 += TR) {
+#pragma unroll
+    for (int u = 0; u < TR; ++u)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) red[wave][u][a][lane] = acc[t0 + u][a];
+    __syncthreads();
+    for (int i = threadIdx.x; i < TR * 4 * 64; i += 64 * S) {
+      const int u = i >> 8, a = (i >> 6) & 3, l = i & 63;
+      float4_t sum = red[0][u][a][l];
+#pragma unroll
+      for (int w = 1; w < S; ++w) sum += red[w][u][a][l];
+      red[0][u][a][l] = sum;
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int u = 0; u < TR; ++u)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) acc[t0 + u][a] = red[0][u][a][lane];
+    }
+    if (t0 + TR < T) __syncthreads();
+  }
+  if (wave != 0) return;
+  const EpiCoeffs cf{&sCoef[0][g * 16], &sCoef[1][g * 16], &sCoef[2][g * 16], &sCoef[3][g * 16]};
+  lif_epilogue<T, OUT_ENC, MODE>(acc, mvalid, m, p.M, p.F, G * 64 + g * 16, p.np, cf, p.state, p.out, p.h_trace,
+                                 p.x_trace, p.sew, &res);
+}
+
+template <int T>
+static hipError_t launch_smallm(const FusedParams& p, int out_enc, int planes, int mode, hipStream_t s) {
+  const dim3 grid((unsigned)((p.M + 15) / 16), (unsigned)(p.F / 64));
+  const dim3 block(64 * kSmallWaves);
+#define SENGINE_SMALLM_CASE(OE, PL, MD)                  \
+  if (out_enc == OE && planes == PL && mode == MD) {     \
+    hipLaunchKernelGGL((fused_smallm_kernel<T, OE, PL, MD>), grid, block, 0, s, p); \
+    return hipGetLastError();                            \
+  }
+  SENGINE_SMALLM_CASE(SENGINE_ENC_BITS, 1, EPI_LIF_HARD)
+  SENGINE_SMALLM_CASE(SENGINE_ENC_BITS, 1, EPI_IF_HARD)
+  SENGINE_SMALLM_CASE(SENGINE_ENC_BITS, 1, EPI_GENERIC)
+  SENGINE_SMALLM_CASE(SENGINE_ENC_BITS, 2, EPI_GENERIC)
+  SENGINE_SMALLM_CASE(SENGINE_ENC_F16, 1, EPI_GENERIC)
+  SENGINE_SMALLM_CASE(SENGINE_ENC_F16, 2, EPI_GENERIC)
+#undef SENGINE_SMALLM_CASE
+  return hipErrorInvalidValue;
+}
+
 template <int T, int IN_ENC, int OUT_ENC, int PLANES>
 static hipError_t launch_fused_t(const FusedParams& p, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL((fused_sparse_conv_bn_lif_kernel<T, IN_ENC, OUT_ENC, PLANES>), grid, dim3(256), 0, s, p);
@@ -187,10 +340,13 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
     return set_error(-2, "fused_sparse_conv_bn_lif: out_enc must be BITS or F16");
   if (geo.M > (1ll << 30)) return set_error(-2, "fused_sparse_conv_bn_lif: B*OH*OW too large");
 
-  // Bit inputs: tile kernel for 3x3 / stride 1 / pad 1 and 1x1 / pad 0, else the LDS-staged
+  // Small outputs run in the flat layout (their weight blob is built that way): the split-K
+  // small-M kernel for bit inputs, the direct kernel on the flat view otherwise.  Other bit
+  // inputs: tile kernel for 3x3 / stride 1 / pad 1 and 1x1 / pad 0, else the LDS-staged
   // kernel (its per-thread tap mask holds up to 64 taps), else the direct-gather kernel below.
   const int choice = fused_kernel_choice();
-  if (d->in_enc == SENGINE_ENC_BITS && choice != 1) {
+  const bool flat = flat_layout(d, geo);
+  if (!flat && d->in_enc == SENGINE_ENC_BITS && choice != 1) {
     const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace, sew};
     if (choice == 0 && tile_eligible(d)) return (int)launch_fused_bits_tile(d, geo, args, stream);
     if (d->KH * d->KW <= 64) return (int)launch_fused_bits_lds(d, geo, args, stream);
@@ -215,8 +371,32 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
   p.enc_scale = d->in_enc == SENGINE_ENC_BITS ? 1.0f / kBitSpikeValue : 1.0f;
   p.sew = sew;
+  p.sew.pix_ch = d->C_out;
+  p.bn_period = d->C_out;
+  if (flat) {  // one position per image: a 1x1 conv over the flattened image
+    p.C = d->H * d->W * d->C_in;
+    p.F = geo.OH * geo.OW * d->C_out;
+    p.H = p.W = p.OH = p.OW = 1;
+    p.KW = 1;
+    p.SH = p.SW = p.DH = p.DW = 1;
+    p.PH = p.PW = 0;
+    p.M = d->B;
+    p.nq = p.C / 64;
+    p.in_t_stride = d->B;
+    if (d->in_enc == SENGINE_ENC_BITS && choice != 1) {
+      // fast epilogue modes for the common case (one weight plane, bit output)
+      int mode = epilogue_mode(p.np, h_trace != nullptr || x_trace != nullptr);
+      if (d->weight_planes != 1 || d->out_enc != SENGINE_ENC_BITS) mode = EPI_GENERIC;
+      switch (d->T) {
+        case 1: return (int)launch_smallm<1>(p, d->out_enc, d->weight_planes, mode, stream);
+        case 2: return (int)launch_smallm<2>(p, d->out_enc, d->weight_planes, mode, stream);
+        case 4: return (int)launch_smallm<4>(p, d->out_enc, d->weight_planes, mode, stream);
+        default: return (int)launch_smallm<8>(p, d->out_enc, d->weight_planes, mode, stream);
+      }
+    }
+  }
 
-  dim3 grid((unsigned)((geo.M + 63) / 64), (unsigned)(d->C_out / 64));
+  dim3 grid((unsigned)((p.M + 63) / 64), (unsigned)(p.F / 64));
   hipError_t e;
   switch (d->T) {
     case 1: e = launch_fused_enc<1>(p, d->in_enc, d->out_enc, d->weight_planes, grid, stream); break;
@@ -233,7 +413,7 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
                                                     void* spikes, float* h_trace, float* x_trace,
                                                     hipStream_t stream) {
   return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace,
-                     SewAdd{nullptr, 0, 0}, stream);
+                     SewAdd{nullptr, 0, 0, 0}, stream);
 }
 
 extern "C" int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_desc* d, const void* data,
@@ -248,5 +428,5 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_d
     return set_error(-2, "fused_sparse_conv_bn_lif_add: need 1 <= residual_planes <= out_planes <= 3");
   if (d->C_out % 32 != 0) return set_error(-2, "fused_sparse_conv_bn_lif_add: C_out % 32 != 0");
   return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, out, nullptr, nullptr,
-                     SewAdd{static_cast<const uint8_t*>(residual), residual_planes, out_planes}, stream);
+                     SewAdd{static_cast<const uint8_t*>(residual), residual_planes, out_planes, d->C_out}, stream);
 }

@@ -19,6 +19,20 @@ int set_error(int code, const char* msg);
 // constraints of the 2:4 fused path (C_in % 64), otherwise the dense fallback's (C_in % 32).
 int check_desc(const sengine_conv_lif_desc* d, Geometry* geo, bool sparse);
 
+// Small-output ("flat") layout.  A convolution with at most kFlatMaxPixels output pixels
+// per image, on an input not much larger than its kernel window, runs as one GEMM per image: rows = images (B per timestep), reduction over
+// the whole input image in NHWC order (K_flat = H*W*C_in), columns = (output pixel,
+// C_out) (N_flat = OH*OW*C_out), with the conv weights placed at the taps each output
+// pixel sees and zeros elsewhere.  Input, output, membrane and trace memory are the
+// ordinary NHWC tensors (same bytes).  The sparse blob of such a layer is built in this
+// layout (sparse_blob_bytes / compress_2_4 use the same predicate), independent of the
+// activation encoding.
+constexpr int kFlatMaxPixels = 16;
+constexpr int64_t kFlatMaxK = 16384;
+constexpr int64_t kFlatMaxEntries = 1ll << 26;  // N_flat * K_flat
+constexpr int64_t kFlatMaxWaste = 4;             // H*W <= 4*KH*KW
+bool flat_layout(const sengine_conv_lif_desc* d, const Geometry& geo);
+
 // fp32 neuron parameters with the rounding of the reference's python scalars:
 // decay = float(1.0 - 1.0/tau) computed in double (models/neurons.py:124).
 NeuronParams make_neuron_params(int neuron, int hard_reset, float tau, float vth, float vreset);

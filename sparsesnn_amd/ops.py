@@ -150,7 +150,8 @@ def compress_2_4(s: ConvSpec, weight: torch.Tensor, layout: int = WLAYOUT_OIHW, 
     values = torch.empty(vb.value // 2, dtype=torch.int16, device=dev)
     meta = torch.empty(mb.value // 4, dtype=torch.int32, device=dev)
     n_groups = lib.sengine_amd_num_groups(ctypes.byref(d))
-    viol = torch.empty(n_groups, dtype=torch.int32, device=dev)
+    # zeroed: in the flat (small-output) layout taps that never touch the image are not visited
+    viol = torch.zeros(n_groups, dtype=torch.int32, device=dev)
     check(lib.sengine_amd_compress_2_4(ctypes.byref(d), _ptr(weight), _weight_enc(weight), layout,
                                        _ptr(values), _ptr(meta), _ptr(viol), _stream(dev)), "compress_2_4")
     if check_pattern:
@@ -306,6 +307,40 @@ def stem_conv_bn(s: ConvSpec, x: torch.Tensor, weight: torch.Tensor, bn_scale: t
     return out
 
 
+def stem_conv_bn_lif_pool(s: ConvSpec, x: torch.Tensor, weight_hwio: torch.Tensor, bn_scale: torch.Tensor,
+                          bn_bias: torch.Tensor, pool_k: int = 3, pool_stride: int = 2, pool_pad: int = 1,
+                          pooled: Optional[torch.Tensor] = None, spikes: Optional[torch.Tensor] = None):
+    """Stem conv + folded BN, the neuron of `s` over the output repeated s.T times, and
+    MaxPool2d(pool_k, pool_stride, pool_pad) of the spikes, in one launch.  Returns
+    (pooled, spikes): int32 spike-bit tensors (s.T*s.B, POH, POW, C_out/32) and, if a
+    `spikes` buffer is given, the stem spikes (s.T*s.B, OH, OW, C_out/32) (else None)."""
+    lib = _lib.load()
+    for t, n in ((x, "x"), (weight_hwio, "weight_hwio"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    _require_numel(x, s.B * s.C_in * s.H * s.W, torch.float32, "x")
+    _require_numel(weight_hwio, s.C_out * s.C_in * s.KH * s.KW, torch.float32, "weight_hwio")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    OH = (s.H + 2 * s.padding - s.KH) // s.stride + 1
+    OW = (s.W + 2 * s.padding - s.KW) // s.stride + 1
+    POH = (OH + 2 * pool_pad - pool_k) // pool_stride + 1
+    POW = (OW + 2 * pool_pad - pool_k) // pool_stride + 1
+    if pooled is None:
+        pooled = torch.empty(s.T * s.B, POH, POW, s.C_out // 32, dtype=torch.int32, device=x.device)
+    else:
+        _require_cuda(pooled, "pooled")
+        _require_numel(pooled, s.T * s.B * POH * POW * s.C_out // 32, torch.int32, "pooled")
+    if spikes is not None:
+        _require_cuda(spikes, "spikes")
+        _require_numel(spikes, s.T * s.B * OH * OW * s.C_out // 32, torch.int32, "spikes")
+    d = make_desc(s)
+    check(lib.sengine_amd_stem_conv_bn_lif_pool(ctypes.byref(d), _ptr(x), _ptr(weight_hwio), _ptr(bn_scale),
+                                                _ptr(bn_bias), int(pool_k), int(pool_stride), int(pool_pad),
+                                                _ptr(spikes) if spikes is not None else None, _ptr(pooled),
+                                                _stream(x.device)), "stem_conv_bn_lif_pool")
+    return pooled, spikes
+
+
 def multistep_neuron_repeat(x: torch.Tensor, T: int, neuron: str = "lif", tau: float = 2.0, v_threshold: float = 1.0,
                             v_reset: Optional[float] = 0.0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Neuron over T steps of the same input x (fp32, n % 32 == 0): spike bits int32 (T, n/32)."""
@@ -347,12 +382,12 @@ def maxpool_spikes(x: torch.Tensor, NT: int, H: int, W: int, C: int, k: int = 3,
 def sew_head(x: torch.Tensor, T: int, B: int, HW: int, C: int, planes: int, fc_weight: torch.Tensor,
              fc_bias: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Average pool + mean over T + Linear on `planes`-plane integer activations -> (B, N_out) fp32.
-    fc_weight: the transposed Linear weight, (C, N_out) contiguous."""
+    fc_weight: (N_out, C) contiguous, nn.Linear layout."""
     lib = _lib.load()
     for t, n in ((x, "x"), (fc_weight, "fc_weight"), (fc_bias, "fc_bias")):
         _require_cuda(t, n)
     _require_numel(x, T * B * HW * planes * C // 32, torch.int32, "x")
-    N_out = fc_weight.shape[1]
+    N_out = fc_weight.shape[0]
     _require_numel(fc_weight, N_out * C, torch.float32, "fc_weight")
     _require_numel(fc_bias, N_out, torch.float32, "fc_bias")
     if out is None:

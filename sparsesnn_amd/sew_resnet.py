@@ -20,6 +20,8 @@ residual add in its epilogue, and finally the pooled/time-averaged Linear head.
 """
 from __future__ import annotations
 
+import dataclasses
+
 from dataclasses import dataclass, field
 
 import torch
@@ -137,6 +139,15 @@ class SEWResNet18Engine:
         self.stem_out = torch.empty(batch, self.H1, self.W1, 64, dtype=torch.float32, device=self.dev)
         self.stem_spk = torch.empty(T * batch, self.H1, self.W1, 2, dtype=torch.int32, device=self.dev)
         self.pool_out = torch.empty(T * batch, self.H2, self.W2, 2, dtype=torch.int32, device=self.dev)
+        # stem + neuron + max-pool in one launch where one workgroup holds a whole image
+        self.stem_nspec = dataclasses.replace(self.stem_spec, T=T, neuron=neuron, hard_reset=v_reset is not None,
+                                              tau=tau, v_threshold=v_threshold,
+                                              v_reset=0.0 if v_reset is None else v_reset)
+        self.stem_fused = True
+        try:
+            self._run_stem_fused()
+        except SEngineError:
+            self.stem_fused = False
 
         # ---- blocks
         self.blocks: list[Block] = []
@@ -169,9 +180,9 @@ class SEWResNet18Engine:
                 self.blocks.append(blk)
                 inplanes, h, w, x_planes, x_max = planes, oh, ow, out_planes, out_max
         self.final_planes, self.final_hw, self.final_c = x_planes, h * w, inplanes
-        self.fc_w = p["fc.weight"].t().contiguous().to(self.dev)  # (C, N_out): coalesced head reads
+        self.fc_w = p["fc.weight"].contiguous().to(self.dev)
         self.fc_b = p["fc.bias"].contiguous().to(self.dev)
-        self.logits = torch.empty(batch, self.fc_w.shape[1], dtype=torch.float32, device=self.dev)
+        self.logits = torch.empty(batch, self.fc_w.shape[0], dtype=torch.float32, device=self.dev)
 
     # ------------------------------------------------------------------ build helpers
     def _fused(self, prefix, p, cin, cout, k, stride, pad, h, w, in_planes) -> FusedConv:
@@ -184,21 +195,8 @@ class SEWResNet18Engine:
             raise SEngineError(f"{wkey}: not 2:4 sparse along C_in (prune it, or run it on the dense fallback)")
         sc, bi = fold_batchnorm(p[bn + ".weight"], p[bn + ".bias"], p[bn + ".running_mean"], p[bn + ".running_var"])
         wx = expand_planes(w_, in_planes) if in_planes > 1 else w_
-        oh, ow = (h + 2 * pad - k) // stride + 1, (w + 2 * pad - k) // stride + 1
+        # (convs with <= 16 output pixels run in the library's flat small-output layout)
         geo = dict(C_in=cin * in_planes, H=h, W=w, KH=k, KW=k, stride=stride, padding=pad)
-        if k > 1 and oh == 1 and ow == 1:
-            # One output pixel per image (the last stage on small inputs): the conv is a 1x1
-            # conv over the whole image flattened into channels, NHWC order (pixel, plane, c),
-            # with the weights of the taps that land inside the image and zeros elsewhere.
-            # Same memory, no padded taps multiplied.
-            flat = torch.zeros(cout, h, w, wx.shape[1])
-            for ih in range(h):
-                for iw in range(w):
-                    kh, kw = ih + pad, iw + pad
-                    if kh < k and kw < k:
-                        flat[:, ih, iw, :] = wx[:, :, kh, kw]
-            wx = flat.reshape(cout, h * w * wx.shape[1], 1, 1)
-            geo = dict(C_in=h * w * cin * in_planes, H=1, W=1, KH=1, KW=1, stride=1, padding=0)
         spec = ConvSpec(T=self.T, B=self.B, C_out=cout, neuron=self.neuron, hard_reset=self.vreset is not None,
                         tau=self.tau, v_threshold=self.vth, v_reset=0.0 if self.vreset is None else self.vreset,
                         weight_planes=self.planes_w, **geo)
@@ -209,7 +207,14 @@ class SEWResNet18Engine:
         return FusedConv(prefix, spec, values, meta, sc.to(self.dev), bi.to(self.dev), in_planes)
 
     # ------------------------------------------------------------------ execution
+    def _run_stem_fused(self):
+        ops.stem_conv_bn_lif_pool(self.stem_nspec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias, 3, 2, 1,
+                                  pooled=self.pool_out, spikes=self.stem_spk)
+
     def run_stem(self):
+        if self.stem_fused:
+            self._run_stem_fused()
+            return
         ops.stem_conv_bn(self.stem_spec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias, out=self.stem_out,
                          layout=ops.WLAYOUT_HWIO)
         ops.multistep_neuron_repeat(self.stem_out, self.T, self.neuron, self.tau, self.vth, self.vreset,

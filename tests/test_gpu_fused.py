@@ -184,3 +184,53 @@ def test_tile_channel_blocking(dev, gpw, k, stride, H, W, C_in, C_out, B):
         assert rep2.ok, str(rep2)
     finally:
         del os.environ["SENGINE_AMD_TILE_GPW"]
+
+
+# ---- flat small-output layout: <= 16 output pixels per image run as one GEMM per image
+FLAT_CASES = [(2, 2, 3, 1, 1, 256, 256, 5, 4), (4, 4, 3, 2, 1, 128, 256, 3, 4), (6, 6, 3, 2, 1, 64, 128, 2, 2),
+              (4, 4, 3, 1, 1, 128, 128, 3, 8), (2, 2, 3, 2, 1, 256, 512, 4, 1), (2, 2, 1, 2, 0, 64, 128, 3, 4),
+              (5, 3, 3, 2, 1, 64, 64, 2, 4)]
+
+
+@pytest.mark.parametrize("kernel", ["auto", "direct"])
+@pytest.mark.parametrize("H,W,k,stride,pad,C_in,C_out,B,T", FLAT_CASES)
+def test_flat_layout_against_oracle(dev, kernel, H, W, k, stride, pad, C_in, C_out, B, T):
+    """Small outputs (flat layout): the split-K small-M kernel ('auto') and the direct kernel
+    on the flat view, with traces, against the oracle."""
+    ops.set_fused_kernel(kernel)
+    try:
+        case = ref.make_layer_case(60 + H + k + C_in // 64, T=T, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
+                                   stride=stride, padding=pad, fp16_weights=True, p_spike=0.3)
+        rep, x_err, r, _ = run_case(dev, case)
+        print(rep, x_err, float(r.spikes.mean()))
+        assert rep.ok, str(rep)
+        assert x_err < 1e-4
+        assert float(r.spikes.mean()) > 0.001
+    finally:
+        ops.set_fused_kernel("auto")
+
+
+@pytest.mark.parametrize("in_enc,out_enc,planes", [(ops.ENC_BITS, ops.ENC_F16, 1), (ops.ENC_F16, ops.ENC_BITS, 1),
+                                                   (ops.ENC_F16, ops.ENC_F16, 2), (ops.ENC_BITS, ops.ENC_BITS, 2)])
+def test_flat_layout_encodings_and_state(dev, in_enc, out_enc, planes):
+    case = ref.make_layer_case(71, T=4, B=3, C_in=128, C_out=128, H=4, W=4, k=3, stride=1, padding=1,
+                               fp16_weights=(planes == 1), p_spike=0.3)
+    g = torch.Generator().manual_seed(6)
+    v0 = torch.rand((3, 128, 4, 4), generator=g) * 0.9
+    rep, x_err, r, v_fin = run_case(dev, case, planes=planes, in_enc=in_enc, out_enc=out_enc, v0=v0)
+    assert rep.ok, str(rep)
+    assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("H,W,k,stride,pad", [(2, 2, 3, 1, 1), (6, 6, 3, 2, 1), (2, 2, 1, 2, 0), (3, 5, 3, 2, 1)])
+def test_flat_compressor_matches_numpy(dev, H, W, k, stride, pad):
+    """The compressor emits the flat blob for small outputs: byte-identical to the numpy
+    restatement applied to oracle.packing.flat_weight."""
+    g = torch.Generator().manual_seed(H * W + k)
+    w = ref.prune_conv_2_4(torch.randn((128, 64, k, k), generator=g) * 0.05).half().float()
+    spec = ops.ConvSpec(T=4, B=2, C_in=64, H=H, W=W, C_out=128, KH=k, KW=k, stride=stride, padding=pad)
+    values, meta, viol = ops.compress_2_4(spec, w.to(dev))
+    ev, em, _ = pk.compress_2_4(pk.flat_weight(w.numpy(), H, W, stride, pad), 1)
+    assert np.array_equal(values.cpu().numpy().view(np.uint16), ev.reshape(-1))
+    assert np.array_equal(meta.cpu().numpy().view(np.uint32), em.reshape(-1))
+    assert int(viol.sum()) == 0

@@ -39,6 +39,39 @@ def test_stem_conv_bn_matches_fp32_conv(dev, layout):
     assert torch.allclose(got, exp, rtol=1e-5, atol=1e-5), float((got - exp).abs().max())
 
 
+@pytest.mark.parametrize("neuron,v_reset,T,B", [("lif", 0.0, 4, 3), ("if", 0.0, 4, 2), ("lif", None, 2, 2),
+                                                ("if", None, 5, 1)])
+def test_stem_lif_pool_fused_matches_separate(dev, neuron, v_reset, T, B):
+    """One-launch stem + neuron + max-pool against the three separate entry points (the
+    separate path is checked against the oracle above): bit-identical spikes and pool."""
+    import dataclasses
+    p = sr.make_params(3, bn_random=True)
+    x = sr.make_images(4, B).to(dev)
+    spec = ops.ConvSpec(T=1, B=B, C_in=3, H=32, W=32, C_out=64, KH=7, KW=7, stride=2, padding=3)
+    nspec = dataclasses.replace(spec, T=T, neuron=neuron, hard_reset=v_reset is not None, tau=2.0,
+                                v_threshold=1.0, v_reset=0.0 if v_reset is None else v_reset)
+    sc, bi = ref.fold_batchnorm(p["bn1.weight"], p["bn1.bias"], p["bn1.running_mean"], p["bn1.running_var"])
+    sc, bi = torch.from_numpy(sc).to(dev), torch.from_numpy(bi).to(dev)
+    w = p["conv1.weight"].permute(2, 3, 1, 0).contiguous().to(dev)
+    stem = ops.stem_conv_bn(spec, x, w, sc, bi, layout=ops.WLAYOUT_HWIO)
+    spk = ops.multistep_neuron_repeat(stem.view(-1), T, neuron, 2.0, 1.0, v_reset)
+    pool = ops.maxpool_spikes(spk, T * B, 16, 16, 64, 3, 2, 1)
+    spk_f = torch.empty(T * B, 16, 16, 2, dtype=torch.int32, device=dev)
+    pool_f, _ = ops.stem_conv_bn_lif_pool(nspec, x, w, sc, bi, 3, 2, 1, spikes=spk_f)
+    torch.cuda.synchronize()
+    assert torch.equal(spk_f.view(-1).cpu(), spk.view(-1).cpu())
+    assert torch.equal(pool_f.view(-1).cpu(), pool.view(-1).cpu())
+    assert int(spk.view(torch.int32).ne(0).sum()) > 0  # the case spikes
+
+
+def test_stem_lif_pool_rejects_large_images(dev):
+    spec = ops.ConvSpec(T=4, B=1, C_in=3, H=64, W=64, C_out=64, KH=7, KW=7, stride=2, padding=3)
+    z = torch.zeros(1, 3, 64, 64, device=dev)
+    with pytest.raises(ops.SEngineError):
+        ops.stem_conv_bn_lif_pool(spec, z, torch.zeros(7, 7, 3, 64, device=dev), torch.ones(64, device=dev),
+                                  torch.zeros(64, device=dev))
+
+
 @pytest.mark.parametrize("neuron,v_reset", [("lif", 0.0), ("if", 0.0), ("lif", None)])
 def test_repeat_neuron(dev, neuron, v_reset):
     g = torch.Generator().manual_seed(4)
@@ -66,15 +99,15 @@ def test_maxpool_spikes(dev, H, W, C):
     assert np.array_equal(got, exp.view(2, 3, C, OH, OW).numpy())
 
 
-@pytest.mark.parametrize("planes,HW", [(2, 1), (1, 4), (3, 2)])
-def test_sew_head(dev, planes, HW):
+@pytest.mark.parametrize("planes,HW,C,N_out", [(2, 1, 64, 10), (1, 4, 64, 10), (3, 2, 96, 37), (2, 1, 512, 100)])
+def test_sew_head(dev, planes, HW, C, N_out):
     rng = np.random.default_rng(planes)
-    T, B, C = 4, 3, 64
+    T, B = 4, 3
     a = rng.integers(0, 1 << planes, size=(T, B, C, HW, 1))
     bits = torch.from_numpy(pk.seq_to_planes(a, planes).view(np.int32)).to(dev)
-    w = torch.randn(10, C) * 0.1
-    b = torch.randn(10) * 0.1
-    y = ops.sew_head(bits, T, B, HW, C, planes, w.t().contiguous().to(dev), b.to(dev)).cpu()
+    w = torch.randn(N_out, C) * 0.1
+    b = torch.randn(N_out) * 0.1
+    y = ops.sew_head(bits, T, B, HW, C, planes, w.to(dev), b.to(dev)).cpu()
     feat = torch.from_numpy(a.astype(np.float32)).flatten(3).mean(3).mean(0)
     assert torch.allclose(y, feat @ w.T + b, atol=1e-5)
 
@@ -132,7 +165,7 @@ def test_engine_blocks_teacher_forced(dev, sew_case):
         eng.run_block(i, x=xd)
         torch.cuda.synchronize()
         pre = blk.name
-        s = blk.stride  # the block's conv stride (the engine may run a conv in a reduced form)
+        s = blk.stride
         bn1 = sr._bn(p, pre + ".conv1.module.1")
         r1 = ref.fused_layer(torch.from_numpy(xin), p[pre + ".conv1.module.0.weight"], bn1, s, 1, 1, "lif", 2.0, 1.0,
                              0.0)

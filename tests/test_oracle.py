@@ -266,3 +266,19 @@ def test_golden_cfg0_reproduced_by_oracle():
     kept = z["w"][z["w"] != 0]
     assert kept.size == z["w"].size // 2
     assert math.isclose(float(np.sqrt(np.mean(kept ** 2))), (2 / 576) ** 0.5 * 1.3, rel_tol=0.15)
+
+
+@pytest.mark.parametrize("H,W,k,stride,pad,dil", [(2, 2, 3, 1, 1, 1), (4, 4, 3, 2, 1, 1), (8, 8, 3, 2, 1, 1),
+                                                 (4, 3, 1, 2, 0, 1), (1, 1, 3, 1, 1, 1), (5, 5, 3, 2, 2, 2)])
+def test_flat_weight_is_the_conv(H, W, k, stride, pad, dil):
+    """The flat small-output layout against torch's conv2d: NHWC-flattened images times the
+    flat matrix equal the NHWC conv output."""
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(H * 10 + k)
+    C_in, C_out, B = 8, 12, 3
+    x = torch.randn(B, C_in, H, W, generator=g, dtype=torch.float64)
+    w = torch.randn(C_out, C_in, k, k, generator=g, dtype=torch.float64)
+    y = F.conv2d(x, w, None, stride, pad, dil)  # (B, C_out, OH, OW)
+    flat = torch.from_numpy(pk.flat_weight(w.numpy(), H, W, stride, pad, dil))[:, :, 0, 0]
+    got = x.permute(0, 2, 3, 1).reshape(B, -1) @ flat.T
+    assert torch.allclose(got, y.permute(0, 2, 3, 1).reshape(B, -1), atol=1e-12)
