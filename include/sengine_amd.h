@@ -51,7 +51,11 @@ enum {
 };
 
 /* Neuron models (sengine/ir.py:44-48 NeuronType, models/neurons.py). */
-enum { SENGINE_NEURON_LIF = 0, SENGINE_NEURON_IF = 1 };
+/* LIF: h = v*(1 - 1/tau) + x/tau (models/neurons.py:121-146); IF: h = v + x;
+ * MS: h = v*decay + x with decay carried in the descriptor's `tau` field -- the MS-ResNet
+ * neuron mem = mem*decay*(1 - spike) + x (models/msresnet.py:28-56) with hard_reset = 1,
+ * v_reset = 0.  All fire when h >= v_threshold. */
+enum { SENGINE_NEURON_LIF = 0, SENGINE_NEURON_IF = 1, SENGINE_NEURON_MS = 2 };
 
 /* Weight tensor layouts accepted by the compressors. */
 enum {
@@ -71,9 +75,9 @@ typedef struct sengine_conv_lif_desc {
   int32_t stride_h, stride_w;
   int32_t pad_h, pad_w;
   int32_t dil_h, dil_w;
-  int32_t neuron;               /* SENGINE_NEURON_LIF / SENGINE_NEURON_IF */
+  int32_t neuron;               /* SENGINE_NEURON_LIF / _IF / _MS */
   int32_t hard_reset;           /* 1: v <- v_reset after a spike; 0: v <- v - v_threshold */
-  float tau, v_threshold, v_reset;
+  float tau, v_threshold, v_reset; /* tau: LIF time constant; MS: the decay factor */
   int32_t in_enc;               /* SENGINE_ENC_BITS or SENGINE_ENC_F16 */
   int32_t out_enc;              /* SENGINE_ENC_BITS or SENGINE_ENC_F16 */
   int32_t weight_planes;        /* 1: fp16 weights; 2: fp16 hi + fp16 lo (fp32-faithful) */
@@ -164,6 +168,19 @@ int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_desc* d, con
                                              const float* bn_scale, const float* bn_bias, const void* residual,
                                              int32_t residual_planes, void* out, int32_t out_planes,
                                              hipStream_t stream);
+
+/*
+ * Membrane-shortcut epilogue (MS-ResNet, models/msresnet.py:107-112,164-167; the reference
+ * engine's Add+LIF fusion, sengine/kernels/add_lif_fused.py): y = BN(conv(data)) +
+ * residual, stored as fp32 NHWC real_out (T*B, OH, OW, C_out) -- the block output that
+ * carries the shortcut stream -- and the neuron of d run over y (V0 = state or 0), its
+ * spikes stored in `spikes` (d->out_enc).  residual: fp32 (T*B, OH, OW, C_out), or NULL
+ * for y = BN(conv).  No traces; any kernel / geometry of sengine_amd_fused_sparse_conv_bn_lif.
+ */
+int sengine_amd_fused_sparse_conv_bn_add_neuron(const sengine_conv_lif_desc* d, const void* data,
+                                                const void* blob_values, const void* blob_meta, float* state,
+                                                const float* bn_scale, const float* bn_bias, const float* residual,
+                                                float* real_out, void* spikes, hipStream_t stream);
 
 /*
  * Dense stem convolution on images + folded BN (the reference runs it through cuDNN,

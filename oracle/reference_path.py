@@ -163,6 +163,29 @@ def multistep_if(x_seq: torch.Tensor, v_threshold=1.0, v_reset=0.0, v0=None):
     return torch.stack(spikes, 0), torch.stack(hs, 0), v
 
 
+def ms_neuron(x_seq: torch.Tensor, decay=0.25, thresh=0.5, v0=None):
+    """MSNeuron.forward (models/msresnet.py:28-56): per t, mem = mem * decay * (1 - spike) + x[t]
+    then spike = heaviside(mem - thresh, 'gate') = (mem - thresh).ge(0) (models/neurons.py:52-59).
+    mem starts at 0 (or v0).  Returns (spikes, mem per t, mem * (1 - last spike))."""
+    mem = torch.zeros_like(x_seq[0]) if v0 is None else v0.clone()
+    spike = torch.zeros_like(x_seq[0])
+    spikes, hs = [], []
+    for t in range(x_seq.shape[0]):
+        mem = mem * decay * (1.0 - spike) + x_seq[t]
+        hs.append(mem)
+        spike = (mem - thresh).ge(0.0).to(x_seq.dtype)
+        spikes.append(spike)
+    return torch.stack(spikes, 0), torch.stack(hs, 0), mem * (1.0 - spike)
+
+
+def _neuron(x, neuron, tau, v_threshold, v_reset, v0):
+    if neuron == "lif":
+        return multistep_lif(x, tau, v_threshold, v_reset, v0)
+    if neuron == "ms":  # tau carries the decay, as in the C ABI
+        return ms_neuron(x, tau, v_threshold, v0)
+    return multistep_if(x, v_threshold, v_reset, v0)
+
+
 @dataclass
 class LayerResult:
     spikes: torch.Tensor   # (T, B, C_out, OH, OW) {0,1} fp32
@@ -176,11 +199,21 @@ def fused_layer(x_seq, w, bn: BNParams, stride=1, padding=1, dilation=1, neuron=
     """The reference PyTorch path of one fused node: Conv -> BN -> multi-step neuron.
     x_seq (T, B, C_in, H, W) fp32; w (C_out, C_in, KH, KW) fp32 (already 2:4 pruned)."""
     x = conv_bn_seq(x_seq, w, bn, stride, padding, dilation)
-    if neuron == "lif":
-        s, h, v = multistep_lif(x, tau, v_threshold, v_reset, v0)
-    else:
-        s, h, v = multistep_if(x, v_threshold, v_reset, v0)
+    s, h, v = _neuron(x, neuron, tau, v_threshold, v_reset, v0)
     return LayerResult(s, h, x, v)
+
+
+def shortcut_layer(x_seq, w, bn: BNParams, residual, stride=1, padding=1, neuron="ms", tau=0.25,
+                   v_threshold=0.5, v_reset=0.0, v0=None) -> LayerResult:
+    """MS-ResNet's membrane shortcut around a conv: y = TDBN(conv(spikes)) + residual
+    (BasicBlock18.forward, models/msresnet.py:107-112; TDBNContainer :58-80 is Conv2d on the
+    flattened (T*B) batch then a per-channel eval BatchNorm), then the next neuron on y
+    (the following block's sn1, :108).  Returns the neuron's result with x = y."""
+    y = conv_bn_seq(x_seq, w, bn, stride, padding)
+    if residual is not None:
+        y = y + residual
+    s, h, v = _neuron(y, neuron, tau, v_threshold, v_reset, v0)
+    return LayerResult(s, h, y, v)
 
 
 # --------------------------------------------------------------------------------------

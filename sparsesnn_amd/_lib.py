@@ -11,7 +11,7 @@ import threading
 from .build import LIB_PATH
 
 ENC_BITS, ENC_F16, ENC_F32 = 0, 1, 2
-NEURON_LIF, NEURON_IF = 0, 1
+NEURON_LIF, NEURON_IF, NEURON_MS = 0, 1, 2
 WLAYOUT_OIHW, WLAYOUT_HWIO = 0, 1
 
 
@@ -52,6 +52,7 @@ SIGNATURES = {
     "sengine_amd_fused_sparse_conv_bn_lif_add": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32,
                                                                 _P]),
     "sengine_amd_stem_conv_bn": (ctypes.c_int, [_DP, _P, _P, _I32, _P, _P, _P, _P]),
+    "sengine_amd_fused_sparse_conv_bn_add_neuron": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sengine_amd_stem_conv_bn_lif_pool": (ctypes.c_int, [_DP, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P]),
     "sengine_amd_multistep_neuron_repeat": (ctypes.c_int, [_I32, _I64, _I32, _I32, _F, _F, _F, _P, _P, _P]),
     "sengine_amd_maxpool_spikes": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P]),

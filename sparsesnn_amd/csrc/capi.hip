@@ -29,9 +29,7 @@ int check_desc(const sengine_conv_lif_desc* d, Geometry* geo, bool sparse) {
   if (!sparse && d->C_in % 32 != 0) return set_error(-2, "dense path requires C_in % 32 == 0");
   if (d->C_out % 64 != 0) return set_error(-2, "C_out % 64 == 0 required");
   if (d->weight_planes != 1 && d->weight_planes != 2) return set_error(-2, "weight_planes must be 1 or 2");
-  if (d->neuron != SENGINE_NEURON_LIF && d->neuron != SENGINE_NEURON_IF)
-    return set_error(-2, "neuron must be LIF or IF");
-  if (d->neuron == SENGINE_NEURON_LIF && !(d->tau > 0.f)) return set_error(-2, "LIF tau must be > 0");
+  if (const char* why = neuron_invalid(d->neuron, d->tau)) return set_error(-2, why);
   const int64_t pixels = (int64_t)d->T * d->B * d->H * d->W;
   if (pixels * d->C_in > (1ll << 40)) return set_error(-2, "input too large");
   geo->OH = OH;
@@ -61,7 +59,32 @@ int fused_kernel_choice() {
   return g_kernel_choice;
 }
 
+const char* neuron_invalid(int neuron, float tau) {
+  if (neuron != SENGINE_NEURON_LIF && neuron != SENGINE_NEURON_IF && neuron != SENGINE_NEURON_MS)
+    return "neuron must be LIF, IF or MS";
+  if (neuron == SENGINE_NEURON_LIF && !(tau > 0.f)) return "LIF tau must be > 0";
+  if (neuron == SENGINE_NEURON_MS && !(tau >= 0.f && tau <= 1.f)) return "MS decay (tau field) must be in [0, 1]";
+  return nullptr;
+}
+
 NeuronParams make_neuron_params(int neuron, int hard_reset, float tau, float vth, float vreset) {
+  if (neuron == SENGINE_NEURON_MS) {
+    // h = v*decay + x is the LIF recurrence with x/tau = x (tau 1) and the given decay:
+    // fma(v, decay, x) when v*decay is exact (decay a power of two or zero), else the
+    // separately rounded product and sum, like torch's mem * decay + x.
+    NeuronParams np;
+    np.neuron = SENGINE_NEURON_LIF;
+    np.hard_reset = hard_reset;
+    np.tau = 1.0f;
+    np.vth = vth;
+    np.vreset = vreset;
+    np.decay = tau;
+    np.rtau = 1.0f;
+    int e;
+    const double dm = frexp((double)tau, &e);
+    np.pow2 = (tau == 0.0f || dm == 0.5) ? 1 : 0;
+    return np;
+  }
   NeuronParams np;
   np.neuron = neuron;
   np.hard_reset = hard_reset;

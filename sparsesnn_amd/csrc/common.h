@@ -91,6 +91,10 @@ struct SewAdd {
   int res_planes;  // planes of the residual (1..3)
   int out_planes;  // planes written (>= res_planes; the caller sizes it so no carry is lost)
   int pix_ch;      // channels per output pixel: planes interleave per pixel, (pixel, plane, c)
+  // Membrane-shortcut form (MS-ResNet): y = BN output + real_res (when given) is stored to
+  // real_out (fp32, the layout of the traces) and the neuron runs on y.
+  const float* real_res;
+  float* real_out;
 };
 
 // One charge step: returns the charged membrane h given the previous membrane v and

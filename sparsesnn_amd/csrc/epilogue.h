@@ -210,16 +210,40 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
         fire_hard(h, np.vth, vreset, v[j], word);
       }
     } else {
+      float rr[16];
+      const bool real = sa.real_out != nullptr && valid;
+      if (real) {
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) {
+          const float4_t r4 = sa.real_res ? *reinterpret_cast<const float4_t*>(sa.real_res + row + j)
+                                          : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rr[j + e] = r4[e];
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const float accv = acc[t][j >> 2][j & 3];
-        const float xin = __builtin_fmaf(accv, fsc[j], fbi[j]);
+        float xin = __builtin_fmaf(accv, fsc[j], fbi[j]);
+        if (real) {
+          // y = BN output + residual, rounded once as torch's out + sc; the neuron takes y
+          // (times 1/tau when that is folded: an exact power-of-two scaling)
+          const float xraw = fold ? __builtin_fmaf(accv, cf.sc[j], cf.bi[j]) : xin;
+          const float y = sa.real_res ? __fadd_rn(xraw, rr[j]) : xraw;
+          rr[j] = y;
+          xin = fold ? y * np.rtau : y;
+        }
         const float h = neuron_charge(np, v[j], xin);
         const bool spike = h >= np.vth;
         v[j] = neuron_reset(np, h, spike);
         if (h_trace && valid) h_trace[row + j] = h;
         if (x_trace && valid) x_trace[row + j] = fold ? __builtin_fmaf(accv, cf.sc[j], cf.bi[j]) : xin;
         word |= (uint32_t)spike << j;
+      }
+      if (real) {
+#pragma unroll
+        for (int j = 0; j < 16; j += 4)
+          *reinterpret_cast<float4_t*>(sa.real_out + row + j) = float4_t{rr[j], rr[j + 1], rr[j + 2], rr[j + 3]};
       }
     }
     if (!valid) continue;

@@ -227,9 +227,7 @@ extern "C" int sengine_amd_multistep_neuron(int32_t T, int64_t n, int32_t neuron
                                             int32_t out_enc, void* spikes, float* h_trace, hipStream_t stream) {
   if (T < 1 || n < 1) return set_error(-2, "multistep_neuron: T and n must be >= 1");
   if (!x || !spikes) return set_error(-1, "multistep_neuron: null pointer");
-  if (neuron != SENGINE_NEURON_LIF && neuron != SENGINE_NEURON_IF)
-    return set_error(-2, "multistep_neuron: neuron must be LIF or IF");
-  if (neuron == SENGINE_NEURON_LIF && !(tau > 0.f)) return set_error(-2, "multistep_neuron: tau must be > 0");
+  if (const char* why = neuron_invalid(neuron, tau)) return set_error(-2, why);
   if (out_enc == SENGINE_ENC_BITS && n % 32 != 0) return set_error(-2, "multistep_neuron: bit output needs n % 32 == 0");
   if (out_enc != SENGINE_ENC_BITS && out_enc != SENGINE_ENC_F16)
     return set_error(-2, "multistep_neuron: out_enc must be BITS or F16");

@@ -385,7 +385,7 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
     p.in_t_stride = d->B;
     if (d->in_enc == SENGINE_ENC_BITS && choice != 1) {
       // fast epilogue modes for the common case (one weight plane, bit output)
-      int mode = epilogue_mode(p.np, h_trace != nullptr || x_trace != nullptr);
+      int mode = epilogue_mode(p.np, h_trace != nullptr || x_trace != nullptr || sew.real_out != nullptr);
       if (d->weight_planes != 1 || d->out_enc != SENGINE_ENC_BITS) mode = EPI_GENERIC;
       switch (d->T) {
         case 1: return (int)launch_smallm<1>(p, d->out_enc, d->weight_planes, mode, stream);
@@ -413,7 +413,7 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
                                                     void* spikes, float* h_trace, float* x_trace,
                                                     hipStream_t stream) {
   return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace,
-                     SewAdd{nullptr, 0, 0, 0}, stream);
+                     SewAdd{nullptr, 0, 0, 0, nullptr, nullptr}, stream);
 }
 
 extern "C" int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_desc* d, const void* data,
@@ -428,5 +428,18 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_d
     return set_error(-2, "fused_sparse_conv_bn_lif_add: need 1 <= residual_planes <= out_planes <= 3");
   if (d->C_out % 32 != 0) return set_error(-2, "fused_sparse_conv_bn_lif_add: C_out % 32 != 0");
   return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, out, nullptr, nullptr,
-                     SewAdd{static_cast<const uint8_t*>(residual), residual_planes, out_planes, d->C_out}, stream);
+                     SewAdd{static_cast<const uint8_t*>(residual), residual_planes, out_planes, d->C_out, nullptr,
+                            nullptr},
+                     stream);
+}
+
+extern "C" int sengine_amd_fused_sparse_conv_bn_add_neuron(const sengine_conv_lif_desc* d, const void* data,
+                                                           const void* blob_values, const void* blob_meta,
+                                                           float* state, const float* bn_scale, const float* bn_bias,
+                                                           const float* residual, float* real_out, void* spikes,
+                                                           hipStream_t stream) {
+  if (!d) return set_error(-1, "fused_sparse_conv_bn_add_neuron: null descriptor");
+  if (!real_out) return set_error(-1, "fused_sparse_conv_bn_add_neuron: null real_out");
+  return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, nullptr, nullptr,
+                     SewAdd{nullptr, 0, 0, 0, residual, real_out}, stream);
 }

@@ -354,7 +354,7 @@ hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry&
   p.sew = a.sew;
   const int pt = choose_pt(d->T);
   const int gpw = choose_gpw(d->T, pt, geo.M, d->C_out);
-  const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr);
+  const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr || a.sew.real_out != nullptr);
   const int pl = d->weight_planes, oe = d->out_enc;
 #define SENGINE_LDS_T(TT)                                                                      \
   case TT:                                                                                     \

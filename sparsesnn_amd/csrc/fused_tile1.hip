@@ -71,7 +71,7 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
   p.enc_scale = 1.0f / kBitSpikeValue;
   p.sew = a.sew;
-  const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr);
+  const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr || a.sew.real_out != nullptr);
   const bool k3 = d->KH == 3;
 
   int shape = 0;

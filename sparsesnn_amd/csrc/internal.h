@@ -33,6 +33,9 @@ constexpr int64_t kFlatMaxEntries = 1ll << 26;  // N_flat * K_flat
 constexpr int64_t kFlatMaxWaste = 4;             // H*W <= 4*KH*KW
 bool flat_layout(const sengine_conv_lif_desc* d, const Geometry& geo);
 
+// Null if (neuron, tau) is a valid neuron description, else the reason.
+const char* neuron_invalid(int neuron, float tau);
+
 // fp32 neuron parameters with the rounding of the reference's python scalars:
 // decay = float(1.0 - 1.0/tau) computed in double (models/neurons.py:124).
 NeuronParams make_neuron_params(int neuron, int hard_reset, float tau, float vth, float vreset);

@@ -390,9 +390,7 @@ extern "C" int sengine_amd_stem_conv_bn_lif_pool(const sengine_conv_lif_desc* d,
       d->dil_w != 1)
     return set_error(-2, "stem_conv_bn_lif_pool: invalid shape fields (C_out % 32 == 0, dilation 1)");
   if (d->T < 1 || d->T > kStemMaxT) return set_error(-2, "stem_conv_bn_lif_pool: 1 <= T <= 16");
-  if (d->neuron != SENGINE_NEURON_LIF && d->neuron != SENGINE_NEURON_IF)
-    return set_error(-2, "stem_conv_bn_lif_pool: neuron must be LIF or IF");
-  if (d->neuron == SENGINE_NEURON_LIF && !(d->tau > 0.f)) return set_error(-2, "stem_conv_bn_lif_pool: tau <= 0");
+  if (const char* why = neuron_invalid(d->neuron, d->tau)) return set_error(-2, why);
   if (pool_k < 1 || pool_stride < 1 || pool_pad < 0 || 2 * pool_pad > pool_k)
     return set_error(-2, "stem_conv_bn_lif_pool: pool needs k >= 1, stride >= 1, 0 <= pad <= k/2");
   StemParams p{};
@@ -427,9 +425,7 @@ extern "C" int sengine_amd_multistep_neuron_repeat(int32_t T, int64_t n, int32_t
                                                    uint32_t* spikes, hipStream_t stream) {
   if (T < 1 || n < 1) return set_error(-2, "multistep_neuron_repeat: T and n must be >= 1");
   if (!x || !spikes) return set_error(-1, "multistep_neuron_repeat: null pointer");
-  if (neuron != SENGINE_NEURON_LIF && neuron != SENGINE_NEURON_IF)
-    return set_error(-2, "multistep_neuron_repeat: neuron must be LIF or IF");
-  if (neuron == SENGINE_NEURON_LIF && !(tau > 0.f)) return set_error(-2, "multistep_neuron_repeat: tau must be > 0");
+  if (const char* why = neuron_invalid(neuron, tau)) return set_error(-2, why);
   if (n % 32 != 0) return set_error(-2, "multistep_neuron_repeat: n % 32 != 0");
   RepeatNeuronParams p{x, spikes, n, T, make_neuron_params(neuron, hard_reset, tau, v_threshold, v_reset)};
   hipLaunchKernelGGL(repeat_neuron_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p);

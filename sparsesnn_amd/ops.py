@@ -14,14 +14,15 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import (ENC_BITS, ENC_F16, ENC_F32, NEURON_IF, NEURON_LIF, WLAYOUT_HWIO, WLAYOUT_OIHW,
+from ._lib import (ENC_BITS, ENC_F16, ENC_F32, NEURON_IF, NEURON_LIF, NEURON_MS, WLAYOUT_HWIO, WLAYOUT_OIHW,
                    ConvLifDesc, SEngineError, check)
 
 __all__ = [
     "ConvSpec", "make_desc", "geometry", "set_fused_kernel", "compress_2_4", "pack_dense_weights", "pack_spikes",
     "unpack_spikes", "fused_sparse_conv_bn_lif", "fused_sparse_conv_bn_lif_add", "stem_conv_bn",
     "multistep_neuron_repeat", "maxpool_spikes", "sew_head", "dense_conv_bn", "multistep_neuron", "SEngineError",
-    "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
+    "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "NEURON_MS", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
+    "neuron_code", "fused_sparse_conv_bn_add_neuron",
 ]
 
 
@@ -65,7 +66,7 @@ class ConvSpec:
     stride: int = 1
     padding: int = 1
     dilation: int = 1
-    neuron: str = "lif"          # "lif" | "if"
+    neuron: str = "lif"          # "lif" | "if" | "ms" (MS-ResNet neuron: `tau` holds its decay)
     hard_reset: bool = True
     tau: float = 2.0
     v_threshold: float = 1.0
@@ -78,14 +79,22 @@ class ConvSpec:
         return make_desc(self)
 
 
+_NEURON_CODES = {"lif": NEURON_LIF, "if": NEURON_IF, "ms": NEURON_MS}
+
+
+def neuron_code(name: str) -> int:
+    """C-ABI neuron kind for 'lif' | 'if' | 'ms'."""
+    if name not in _NEURON_CODES:
+        raise ValueError(f"neuron must be 'lif', 'if' or 'ms', got {name!r}")
+    return _NEURON_CODES[name]
+
+
 def make_desc(s: ConvSpec) -> ConvLifDesc:
-    if s.neuron not in ("lif", "if"):
-        raise ValueError(f"neuron must be 'lif' or 'if', got {s.neuron!r}")
     return ConvLifDesc(
         T=s.T, B=s.B, C_in=s.C_in, H=s.H, W=s.W, C_out=s.C_out, KH=s.KH, KW=s.KW,
         stride_h=s.stride, stride_w=s.stride, pad_h=s.padding, pad_w=s.padding,
         dil_h=s.dilation, dil_w=s.dilation,
-        neuron=NEURON_LIF if s.neuron == "lif" else NEURON_IF, hard_reset=int(bool(s.hard_reset)),
+        neuron=neuron_code(s.neuron), hard_reset=int(bool(s.hard_reset)),
         tau=float(s.tau), v_threshold=float(s.v_threshold), v_reset=float(s.v_reset),
         in_enc=s.in_enc, out_enc=s.out_enc, weight_planes=s.weight_planes)
 
@@ -283,6 +292,52 @@ def fused_sparse_conv_bn_lif_add(s: ConvSpec, data: torch.Tensor, values: torch.
     return out
 
 
+def fused_sparse_conv_bn_add_neuron(s: ConvSpec, data: torch.Tensor, values: torch.Tensor, meta: torch.Tensor,
+                                    bn_scale: torch.Tensor, bn_bias: torch.Tensor,
+                                    residual: Optional[torch.Tensor] = None, state: Optional[torch.Tensor] = None,
+                                    real_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+    """Membrane-shortcut form (MS-ResNet): y = BN(conv(data)) + residual (fp32 NHWC
+    (T*B, OH, OW, C_out), or none) and the neuron of `s` run over y.  Returns (y, spikes)."""
+    lib = _lib.load()
+    OH, OW, M, _ = geometry(s)
+    d = make_desc(s)
+    vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+    check(lib.sengine_amd_sparse_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)), "sparse_blob_bytes")
+    for t, n in ((data, "data"), (values, "values"), (meta, "meta"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    dev = data.device
+    dt, n_in = _enc_numel(s.in_enc, s.T * s.B * s.H * s.W * s.C_in)
+    _require_numel(data, n_in, dt, "data")
+    if values.numel() * values.element_size() != vb.value or meta.numel() * meta.element_size() != mb.value:
+        raise SEngineError("fused_sparse_conv_bn_add_neuron: weight blob does not match the descriptor")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    n_real = s.T * M * s.C_out
+    if residual is not None:
+        _require_cuda(residual, "residual")
+        _require_numel(residual, n_real, torch.float32, "residual")
+    if state is not None:
+        _require_cuda(state, "state")
+        _require_numel(state, M * s.C_out, torch.float32, "state")
+    if real_out is None:
+        real_out = torch.empty(s.T * s.B, OH, OW, s.C_out, dtype=torch.float32, device=dev)
+    else:
+        _require_cuda(real_out, "real_out")
+        _require_numel(real_out, n_real, torch.float32, "real_out")
+    odt, n_out = _enc_numel(s.out_enc, s.T * M * s.C_out)
+    if out is None:
+        last = s.C_out // 32 if s.out_enc == ENC_BITS else s.C_out
+        out = torch.empty(s.T * s.B, OH, OW, last, dtype=odt, device=dev)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, n_out, odt, "out")
+    rc = lib.sengine_amd_fused_sparse_conv_bn_add_neuron(
+        ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta), _ptr(state), _ptr(bn_scale), _ptr(bn_bias),
+        _ptr(residual), _ptr(real_out), _ptr(out), _stream(dev))
+    check(rc, "fused_sparse_conv_bn_add_neuron")
+    return real_out, out
+
+
 def stem_conv_bn(s: ConvSpec, x: torch.Tensor, weight: torch.Tensor, bn_scale: torch.Tensor, bn_bias: torch.Tensor,
                  out: Optional[torch.Tensor] = None, layout: int = WLAYOUT_OIHW) -> torch.Tensor:
     """Dense fp32 conv + folded BN on NCHW images (s.B images; s.T ignored) -> NHWC fp32.
@@ -355,7 +410,7 @@ def multistep_neuron_repeat(x: torch.Tensor, T: int, neuron: str = "lif", tau: f
         _require_cuda(out, "out")
         _require_numel(out, T * n // 32, torch.int32, "out")
     hard = v_reset is not None
-    check(lib.sengine_amd_multistep_neuron_repeat(int(T), int(n), NEURON_LIF if neuron == "lif" else NEURON_IF,
+    check(lib.sengine_amd_multistep_neuron_repeat(int(T), int(n), neuron_code(neuron),
                                                   int(hard), float(tau), float(v_threshold),
                                                   float(v_reset if hard else 0.0), _ptr(x), _ptr(out),
                                                   _stream(x.device)), "multistep_neuron_repeat")
@@ -446,7 +501,7 @@ def multistep_neuron(x: torch.Tensor, T: int, neuron: str = "lif", tau: float = 
     odt, n_out = _enc_numel(out_enc, T * n)
     out = torch.empty(n_out, dtype=odt, device=x.device)
     hard = v_reset is not None
-    check(lib.sengine_amd_multistep_neuron(T, n, NEURON_LIF if neuron == "lif" else NEURON_IF, int(hard), float(tau),
+    check(lib.sengine_amd_multistep_neuron(T, n, neuron_code(neuron), int(hard), float(tau),
                                            float(v_threshold), float(v_reset if hard else 0.0), _ptr(x), _ptr(state),
                                            out_enc, _ptr(out), _ptr(h_trace), _stream(x.device)), "multistep_neuron")
     return out

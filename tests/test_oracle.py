@@ -282,3 +282,33 @@ def test_flat_weight_is_the_conv(H, W, k, stride, pad, dil):
     flat = torch.from_numpy(pk.flat_weight(w.numpy(), H, W, stride, pad, dil))[:, :, 0, 0]
     got = x.permute(0, 2, 3, 1).reshape(B, -1) @ flat.T
     assert torch.allclose(got, y.permute(0, 2, 3, 1).reshape(B, -1), atol=1e-12)
+
+
+def test_ms_neuron_closed_forms():
+    """MSNeuron (decay 1/4, threshold 1/2) on constant inputs with exact binary fractions:
+    x = 3/8 approaches 1/2 from below and never fires; x = 1/2 fires at every step (each
+    spike zeroes the carried membrane); x = 7/16 charges to 35/64 >= 1/2 and fires every
+    other step; a negative input never fires and the membrane follows x * sum(decay^k)."""
+    T = 6
+    x = torch.tensor([0.375, 0.5, 0.4375, -0.25]).view(1, 4).repeat(T, 1)
+    s, h, _ = ref.ms_neuron(x, 0.25, 0.5)
+    assert s[:, 0].sum() == 0
+    assert torch.equal(s[:, 1], torch.ones(T))
+    assert torch.equal(s[:, 2], torch.tensor([0.0, 1, 0, 1, 0, 1]))
+    assert h[1, 2] == 0.546875 and h[2, 2] == 0.4375
+    geo = torch.tensor([sum(0.25 ** k for k in range(t + 1)) for t in range(T)])
+    assert torch.allclose(h[:, 0], 0.375 * geo) and torch.allclose(h[:, 3], -0.25 * geo)
+    assert s[:, 3].sum() == 0
+    # initial membrane: charged once by decay, then the input
+    s0, h0, _ = ref.ms_neuron(x[:, :1], 0.25, 0.5, v0=torch.tensor([1.0]))
+    assert h0[0, 0] == 0.625 and s0[0, 0] == 1 and h0[1, 0] == 0.375
+
+
+def test_shortcut_layer_composition():
+    """The membrane-shortcut layer is conv+BN, plus the residual, then the neuron."""
+    case = ref.make_layer_case(3, T=3, B=1, C_in=8, C_out=8, H=5, W=5, k=3)
+    res = torch.randn(3, 1, 8, 5, 5, generator=torch.Generator().manual_seed(1))
+    r = ref.shortcut_layer(case.x_seq, case.w, case.bn, res, 1, 1, "ms", 0.25, 0.5)
+    y = ref.conv_bn_seq(case.x_seq, case.w, case.bn, 1, 1) + res
+    assert torch.equal(r.x, y)
+    assert torch.equal(r.spikes, ref.ms_neuron(y, 0.25, 0.5)[0])
