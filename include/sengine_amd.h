@@ -183,6 +183,23 @@ int sengine_amd_fused_sparse_conv_bn_add_neuron(const sengine_conv_lif_desc* d, 
                                                 float* real_out, void* spikes, hipStream_t stream);
 
 /*
+ * Spiking self-attention (Spikformer SSA, models/spikformer.py:103-130): for every (t, b,
+ * head) x = (Q K^T * scale) V on binary spikes, then the neuron over T (the reference's
+ * attn_lif: LIF tau 2, V_th 0.5).  Every product and partial sum is an integer times
+ * `scale` (a power of two), exact in fp32 in any order; this library evaluates
+ * Q (K^T V) * scale, which is bit-identical and costs N*d^2 instead of N^2*d per head.
+ * q/k/v/out: spike bits (T*B, N, C), head h = channels [h*d, h*d + d), d = C/heads
+ * (d % 16 == 0, d <= 64, N <= 8192).  Two steps:
+ *   sengine_amd_ssa_kv:             kv (T*B, heads, d, d) int32 = K^T V   (caller's workspace)
+ *   sengine_amd_ssa_attend_neuron:  out = neuron over T of (Q kv * scale)
+ */
+int sengine_amd_ssa_kv(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, const uint32_t* k_bits,
+                       const uint32_t* v_bits, int32_t* kv, hipStream_t stream);
+int sengine_amd_ssa_attend_neuron(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, float scale,
+                                  int32_t neuron, int32_t hard_reset, float tau, float v_threshold, float v_reset,
+                                  const uint32_t* q_bits, const int32_t* kv, uint32_t* out_bits, hipStream_t stream);
+
+/*
  * Dense stem convolution on images + folded BN (the reference runs it through cuDNN,
  * sengine/csrc/cpp_executor.cu:306-347; models/sewresnet.py:140-141,199-200):
  * x NCHW fp32 (d->B images, d->C_in, d->H, d->W), weight fp32 in w_layout (HWIO reads

@@ -22,7 +22,7 @@ __all__ = [
     "unpack_spikes", "fused_sparse_conv_bn_lif", "fused_sparse_conv_bn_lif_add", "stem_conv_bn",
     "multistep_neuron_repeat", "maxpool_spikes", "sew_head", "dense_conv_bn", "multistep_neuron", "SEngineError",
     "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "NEURON_MS", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
-    "neuron_code", "fused_sparse_conv_bn_add_neuron",
+    "neuron_code", "fused_sparse_conv_bn_add_neuron", "spiking_self_attention",
 ]
 
 
@@ -336,6 +336,38 @@ def fused_sparse_conv_bn_add_neuron(s: ConvSpec, data: torch.Tensor, values: tor
         _ptr(residual), _ptr(real_out), _ptr(out), _stream(dev))
     check(rc, "fused_sparse_conv_bn_add_neuron")
     return real_out, out
+
+
+def spiking_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, T: int, B: int, N: int, C: int,
+                           heads: int, scale: float = 0.125, neuron: str = "lif", tau: float = 2.0,
+                           v_threshold: float = 0.5, v_reset: Optional[float] = 0.0,
+                           kv: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Spikformer SSA on spike bits: q, k, v int32 (T*B, N, C/32) -> the attention neuron's
+    spikes over T of (Q K^T * scale) V per head, int32 (T*B, N, C/32).  kv: optional
+    workspace int32 (T*B, heads, d, d) (K^T V per head)."""
+    lib = _lib.load()
+    n_bits = T * B * N * C // 32
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _require_cuda(t, name)
+        _require_numel(t, n_bits, torch.int32, name)
+    d = C // heads if heads else 0
+    if kv is None:
+        kv = torch.empty(T * B, heads, d, d, dtype=torch.int32, device=q.device)
+    else:
+        _require_cuda(kv, "kv")
+        _require_numel(kv, T * B * heads * d * d, torch.int32, "kv")
+    if out is None:
+        out = torch.empty(T * B, N, C // 32, dtype=torch.int32, device=q.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, n_bits, torch.int32, "out")
+    st = _stream(q.device)
+    check(lib.sengine_amd_ssa_kv(T, B, N, C, heads, _ptr(k), _ptr(v), _ptr(kv), st), "ssa_kv")
+    hard = v_reset is not None
+    check(lib.sengine_amd_ssa_attend_neuron(T, B, N, C, heads, float(scale), neuron_code(neuron), int(hard),
+                                            float(tau), float(v_threshold), float(v_reset if hard else 0.0),
+                                            _ptr(q), _ptr(kv), _ptr(out), st), "ssa_attend_neuron")
+    return out
 
 
 def stem_conv_bn(s: ConvSpec, x: torch.Tensor, weight: torch.Tensor, bn_scale: torch.Tensor, bn_bias: torch.Tensor,
