@@ -189,7 +189,8 @@ int sengine_amd_fused_sparse_conv_bn_add_neuron(const sengine_conv_lif_desc* d, 
  * `scale` (a power of two), exact in fp32 in any order; this library evaluates
  * Q (K^T V) * scale, which is bit-identical and costs N*d^2 instead of N^2*d per head.
  * q/k/v/out: spike bits (T*B, N, C), head h = channels [h*d, h*d + d), d = C/heads
- * (d % 16 == 0, d <= 64, N <= 8192).  Two steps:
+ * (d % 16 == 0, d <= 64, N <= 8192, 16*d*ceil(N/64) + 4*d*d <= 65536 bytes of token masks and
+ * sums, T in {1, 2, 4, 8}).  Two steps:
  *   sengine_amd_ssa_kv:             kv (T*B, heads, d, d) int32 = K^T V   (caller's workspace)
  *   sengine_amd_ssa_attend_neuron:  out = neuron over T of (Q kv * scale)
  */

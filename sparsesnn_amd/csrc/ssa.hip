@@ -6,21 +6,24 @@
 // this build evaluates x = Q (K^T V) * scale: K^T V is d x d, the work drops from
 // N^2 d to N d^2 per head, and the result is bit-identical.
 //
-//   ssa_kv_kernel:     KV[t, b, h] = K^T V (int32 d x d).  A workgroup per (t*B + b, h):
-//                      each wave turns 64 tokens' head slices into per-channel 64-token
-//                      masks with ballots (bit transposition into LDS), then each
-//                      thread sums popcount(K_i & V_j) over the token masks.
+//   ssa_kv_kernel:     KV[t, b, h] = K^T V (int32 d x d).  A workgroup of 16 waves per
+//                      (t*B + b, h): each wave turns 64 tokens' head slices into
+//                      per-channel 64-token masks with ballots (bit transposition into
+//                      LDS), then threads sum popcount(K_i & V_j) over the token masks.
 //   ssa_attend_kernel: X = Q KV on MFMA (v_mfma_f32_16x16x32_f16: A = KV^T as two exact
-//                      6-bit fp16 pieces, B = Q expanded from bits), the neuron over T in
+//                      6-bit fp16 pieces pre-scaled by a power of two, B = Q expanded
+//                      from bits, one fp32 accumulator), the neuron over T in
 //                      registers, 16 output channels of a token assembled across lanes
 //                      and stored as one u16.
 #include "common.h"
+#include "epilogue.h"
 #include "internal.h"
 
 namespace sengine {
 
 constexpr int kSsaMaxN = 8192;   // tokens (the KV kernel keeps 2 x d x N/64 token masks in LDS)
 constexpr int kSsaMaxD = 64;
+constexpr size_t kSsaMaxLds = 163840;  // attend kernel: KV pieces of every t and the staged Q slices
 
 struct SsaParams {
   const uint32_t* q;
@@ -29,7 +32,7 @@ struct SsaParams {
   int32_t* kv;     // (T*B, H, d, d)
   uint16_t* out;   // spike bits (T*B, N, C) viewed as u16 words
   int T, B, N, C, H, d;
-  float xscale;    // scale / 2 (the MFMA sees spikes as 2.0)
+  float xscale;    // scale / 2 (the MFMA sees spikes as 2.0), times 1/tau on the fast path
   NeuronParams np;
 };
 
@@ -42,128 +45,202 @@ __device__ __forceinline__ uint64_t head_slice(const uint32_t* row, int words, i
   return d == 64 ? v : (v & ((1ull << d) - 1));
 }
 
-__global__ __launch_bounds__(256) void ssa_kv_kernel(SsaParams p) {
-  extern __shared__ uint64_t masks[];  // K masks [d][G], then V masks [d][G]
+constexpr int kSsaKvWaves = 16;
+
+template <int D>
+__global__ __launch_bounds__(64 * kSsaKvWaves) void ssa_kv_kernel(SsaParams p) {
+  extern __shared__ uint64_t masks[];  // K masks [G][D], then V masks [G][D], then KV sums
   const int G = (p.N + 63) >> 6;
   uint64_t* Km = masks;
-  uint64_t* Vm = masks + (size_t)p.d * G;
+  uint64_t* Vm = masks + (size_t)D * G;
+  uint32_t* sum = reinterpret_cast<uint32_t*>(masks + (size_t)2 * D * G);  // [D][D]
+  for (int idx = threadIdx.x; idx < D * D; idx += blockDim.x) sum[idx] = 0u;
   const int tb = blockIdx.x / p.H;
   const int h = blockIdx.x - tb * p.H;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int words = p.C >> 5;
-  for (int g = wave; g < G; g += 4) {
+  // this lane's token slices, loaded one token group ahead of the ballots
+  auto load = [&](int g, uint64_t& ks, uint64_t& vs) {
     const int n = (g << 6) + lane;
-    uint64_t ks = 0, vs = 0;
-    if (n < p.N) {
+    ks = vs = 0;
+    if (g < G && n < p.N) {
       const size_t row = ((size_t)tb * p.N + n) * words;
-      ks = head_slice(p.k + row, words, h * p.d, p.d);
-      vs = head_slice(p.v + row, words, h * p.d, p.d);
+      ks = head_slice(p.k + row, words, h * D, D);
+      vs = head_slice(p.v + row, words, h * D, D);
     }
-    for (int i = 0; i < p.d; ++i) {
-      const uint64_t mk = __ballot((ks >> i) & 1ull);
-      const uint64_t mv = __ballot((vs >> i) & 1ull);
+  };
+  uint64_t ksn, vsn;
+  load(wave, ksn, vsn);
+  for (int g = wave; g < G; g += kSsaKvWaves) {
+    const uint32_t k0 = (uint32_t)ksn, k1 = (uint32_t)(ksn >> 32);
+    const uint32_t v0 = (uint32_t)vsn, v1 = (uint32_t)(vsn >> 32);
+    load(g + kSsaKvWaves, ksn, vsn);
+    uint64_t* kd = Km + (size_t)g * D;
+    uint64_t* vd = Vm + (size_t)g * D;
+#pragma unroll
+    for (int i = 0; i < D; ++i) {  // compile-time bit masks: one test and one ballot per bit
+      const uint64_t mk = __ballot(((i < 32 ? k0 : k1) >> (i & 31)) & 1u);
+      const uint64_t mv = __ballot(((i < 32 ? v0 : v1) >> (i & 31)) & 1u);
       if (lane == 0) {
-        Km[(size_t)i * G + g] = mk;
-        Vm[(size_t)i * G + g] = mv;
+        kd[i] = mk;
+        vd[i] = mv;
       }
     }
   }
   __syncthreads();
-  // work item = (i, 16 consecutive j): K_i masks read once per token group
-  const int jchunks = p.d >> 4;
-  int32_t* kv = p.kv + (size_t)blockIdx.x * p.d * p.d;
-  for (int item = threadIdx.x; item < p.d * jchunks; item += blockDim.x) {
-    const int i = item / jchunks;
-    const int j0 = (item - i * jchunks) << 4;
+  // work item = (i, 16 consecutive j, token-group residue r): K_i masks read once per
+  // token group; the residues' partial counts meet in LDS by integer atomics (exact, order-free)
+  constexpr int JC = D / 16;
+  constexpr int R = kSsaKvWaves * 64 / (D * JC) > 0 ? kSsaKvWaves * 64 / (D * JC) : 1;
+  for (int item = threadIdx.x; item < D * JC * R; item += blockDim.x) {
+    const int r = item / (D * JC);
+    const int ij = item - r * (D * JC);
+    const int i = ij / JC;
+    const int j0 = (ij - i * JC) << 4;
     uint32_t acc[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) acc[u] = 0;
-    for (int g = 0; g < G; ++g) {
-      const uint64_t ki = Km[(size_t)i * G + g];
+    for (int g = r; g < G; g += R) {
+      const uint64_t ki = Km[(size_t)g * D + i];
+      const uint64_t* vj = Vm + (size_t)g * D + j0;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) acc[u] += (uint32_t)__popcll(ki & Vm[(size_t)(j0 + u) * G + g]);
+      for (int u = 0; u < 16; ++u) acc[u] += (uint32_t)__popcll(ki & vj[u]);
     }
 #pragma unroll
-    for (int u = 0; u < 16; ++u) kv[i * p.d + j0 + u] = (int32_t)acc[u];
+    for (int u = 0; u < 16; ++u) atomicAdd(&sum[i * D + j0 + u], acc[u]);
   }
+  __syncthreads();
+  int32_t* kv = p.kv + (size_t)blockIdx.x * D * D;
+  for (int idx = threadIdx.x; idx < D * D; idx += blockDim.x) kv[idx] = (int32_t)sum[idx];
 }
 
-// Workgroup = (b, h) x 64 tokens (4 waves x 16); T outer loop with the membrane in
-// registers.  MFMA roles: D[j][token] = sum_i KV^T[j][i] * Q^T[i][token].
-__global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p) {
-  // [piece][j][i/8]: i padded to 64 fp16 plus 8 so the 16 rows a lane group reads sit in
-  // different banks
-  __shared__ half8_t skv[2][kSsaMaxD][9];
+// Workgroup = (b, h, one of `splits` token ranges): KV of every t is staged once in LDS
+// (fp16 hi/lo 6-bit pieces, exact, transposed to [j][i]); each wave then walks 16-token
+// tiles, t inner, membrane in registers.  MFMA roles: D[j][token] = sum_i KV^T[j][i] *
+// Q^T[i][token].
+constexpr int kSsaRow = 72;  // fp16 per staged KV row: i padded to 64 plus 8 (bank spread)
+
+template <int D, int T, int MODE>
+__global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits) {
+  extern __shared__ half8_t skv[];  // [t][piece][j][kSsaRow / 8]
+  constexpr int JT = D / 16;        // j tiles of 16
+  constexpr int KS = (D + 31) / 32; // k steps of 32 channels
+  constexpr int RV = kSsaRow / 8;   // half8 per row
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4;
   const int c = lane & 15;
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x / splits;
+  const int split = blockIdx.x - bh * splits;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
-  const int n = blockIdx.y * 64 + wave * 16 + c;  // this lane's token (MFMA column)
-  const bool nvalid = n < p.N;
   const int words = p.C >> 5;
-  const int jt_n = p.d >> 4;       // j tiles of 16
-  const int ks_n = (p.d + 31) >> 5;  // k steps of 32 channels
-  float v[4][4];                   // membrane per (j tile, row e)
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[jt][e] = 0.f;
   const bool fold = p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2;
 
-  for (int t = 0; t < p.T; ++t) {
-    const int tb = t * p.B + b;
-    // stage KV[tb, h] as fp16 hi/lo 6-bit pieces (exact), transposed to [j][i]
-    __syncthreads();
-    const int32_t* kv = p.kv + ((size_t)tb * p.H + h) * p.d * p.d;
-    _Float16* s = reinterpret_cast<_Float16*>(&skv[0][0][0]);
-    for (int idx = threadIdx.x; idx < p.d * 64; idx += blockDim.x) {
-      const int j = idx >> 6, i = idx & 63;
-      const int32_t x = i < p.d ? kv[i * p.d + j] : 0;
-      s[(0 * kSsaMaxD + j) * 72 + i] = (_Float16)(x & 63);
-      s[(1 * kSsaMaxD + j) * 72 + i] = (_Float16)(x >> 6);
+  // stage: a wave per (t, i) row, lanes over j (coalesced reads), transposed fp16 pieces
+  _Float16* s = reinterpret_cast<_Float16*>(skv);
+  for (int ti = wave; ti < T * 64; ti += 4) {
+    const int t = ti >> 6, i = ti & 63;
+    if (lane < D) {
+      // pieces pre-scaled by xscale (a power of two): lo * xs and hi * 64 * xs stay exact in
+      // fp16, and both MFMAs accumulate x itself into one fp32 accumulator
+      const int32_t x = i < D ? p.kv[((size_t)(t * p.B + b) * p.H + h) * D * D + i * D + lane] : 0;
+      s[((size_t)(t * 2 + 0) * D + lane) * kSsaRow + i] = (_Float16)((float)(x & 63) * p.xscale);
+      s[((size_t)(t * 2 + 1) * D + lane) * kSsaRow + i] = (_Float16)((float)((x >> 6) << 6) * p.xscale);
     }
-    __syncthreads();
-    const uint64_t qs = nvalid ? head_slice(p.q + ((size_t)tb * p.N + n) * words, words, h * p.d, p.d) : 0ull;
-    float4_t lo[4], hi[4];
+  }
+  __syncthreads();
+
+  const int tiles = (p.N + 15) >> 4;
+  const int per = (tiles + splits - 1) / splits;
+  const int tile0 = split * per;
+  const int tile_end = min(tiles, tile0 + per);
+  // Every Q slice of the workgroup's tokens is staged in LDS before the first output store:
+  // the vector-memory counter also counts stores, so a load waited for after stores would
+  // wait for those stores too.
+  uint64_t* sq = reinterpret_cast<uint64_t*>(skv + (size_t)T * 2 * D * RV);  // [t][token]
+  const int ntok = (tile_end - tile0) * 16;
+  for (int idx = threadIdx.x; idx < T * ntok; idx += blockDim.x) {
+    const int t = idx / ntok, k = idx - (idx / ntok) * ntok;
+    const int n = tile0 * 16 + k;
+    sq[idx] = n < p.N ? head_slice(p.q + ((size_t)(t * p.B + b) * p.N + n) * words, words, h * D, D) : 0ull;
+  }
+  __syncthreads();
+  for (int tile = tile0 + wave; tile < tile_end; tile += 4) {
+    uint64_t qcur[T];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) lo[jt] = hi[jt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < T; ++t) qcur[t] = sq[t * ntok + (tile - tile0) * 16 + c];
+    const int n = tile * 16 + c;  // this lane's token (MFMA column)
+    const bool nvalid = n < p.N;
+    float v[JT][4];  // membrane per (j tile, row e)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (ks >= ks_n) break;
-      const half8_t bq = expand_bits8((uint32_t)(qs >> (32 * ks + 8 * g)) & 0xffu);
+    for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        if (jt >= jt_n) break;
-        const half8_t a0 = skv[0][jt * 16 + c][ks * 4 + g];
-        const half8_t a1 = skv[1][jt * 16 + c][ks * 4 + g];
-        lo[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bq, lo[jt], 0, 0, 0);
-        hi[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bq, hi[jt], 0, 0, 0);
+      for (int e = 0; e < 4; ++e) v[jt][e] = 0.f;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const half8_t* st = skv + (size_t)t * 2 * D * RV;
+      float4_t acc[JT];
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) acc[jt] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const half8_t bq = expand_bits8((uint32_t)(qcur[t] >> (32 * ks + 8 * g)) & 0xffu);
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt) {
+          const half8_t a0 = st[(size_t)(jt * 16 + c) * RV + ks * 4 + g];
+          const half8_t a1 = st[(size_t)(D + jt * 16 + c) * RV + ks * 4 + g];
+          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bq, acc[jt], 0, 0, 0);
+          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bq, acc[jt], 0, 0, 0);
+        }
       }
-    }
-    // neuron on x[token][j = 16 jt + 4 g + e]; 16 spikes of a token gathered from 4 lanes
+      // neuron on x[token][j = 16 jt + 4 g + e]; 16 spikes of a token gathered from 4 lanes
+      uint32_t word[JT];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      if (jt >= jt_n) break;
-      uint32_t nib = 0;
+      for (int jt = 0; jt < JT; ++jt) {
+        uint32_t nib = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x = __builtin_fmaf(hi[jt][e], 64.f, lo[jt][e]) * p.xscale;  // exact integers x 2^-k
-        const float xf = fold ? x * p.np.rtau : x;
-        const float hh = neuron_charge(p.np, v[jt][e], xf);
-        const bool spike = hh >= p.np.vth;
-        v[jt][e] = neuron_reset(p.np, hh, spike);
-        nib |= (uint32_t)spike << e;
+        for (int e = 0; e < 4; ++e) {
+          const float x = acc[jt][e];  // the attention output (times 1/tau on the fast path), exact
+          if (MODE == EPI_LIF_HARD) {
+            const float hh = __builtin_fmaf(v[jt][e], p.np.decay, x);  // v*decay exact: one rounding
+            const bool spike = hh >= p.np.vth;
+            v[jt][e] = spike ? p.np.vreset : hh;
+            nib |= (uint32_t)spike << e;
+          } else {
+            const float xf = fold ? x * p.np.rtau : x;
+            const float hh = neuron_charge(p.np, v[jt][e], xf);
+            const bool spike = hh >= p.np.vth;
+            v[jt][e] = neuron_reset(p.np, hh, spike);
+            nib |= (uint32_t)spike << e;
+          }
+        }
+        const uint32_t n1 = __shfl(nib, c + 16, 64), n2 = __shfl(nib, c + 32, 64), n3 = __shfl(nib, c + 48, 64);
+        word[jt] = nib | (n1 << 4) | (n2 << 8) | (n3 << 12);
       }
-      const uint32_t n1 = __shfl(nib, c + 16, 64), n2 = __shfl(nib, c + 32, 64), n3 = __shfl(nib, c + 48, 64);
       if (g == 0 && nvalid) {
-        const uint32_t word = nib | (n1 << 4) | (n2 << 8) | (n3 << 12);
-        p.out[(((size_t)tb * p.N + n) * p.C + h * p.d + jt * 16) >> 4] = (uint16_t)word;
+        uint16_t* o = p.out + (((size_t)(t * p.B + b) * p.N + n) * p.C + h * D) / 16;
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt) o[jt] = (uint16_t)word[jt];
       }
     }
+  }
+}
+
+template <int D, int T>
+static void* attend_fn_t(bool fast) {
+  return fast ? reinterpret_cast<void*>(&ssa_attend_kernel<D, T, EPI_LIF_HARD>)
+              : reinterpret_cast<void*>(&ssa_attend_kernel<D, T, EPI_GENERIC>);
+}
+
+template <int D>
+static void* attend_fn(int T, bool fast) {
+  switch (T) {
+    case 1: return attend_fn_t<D, 1>(fast);
+    case 2: return attend_fn_t<D, 2>(fast);
+    case 4: return attend_fn_t<D, 4>(fast);
+    default: return attend_fn_t<D, 8>(fast);
   }
 }
 
@@ -189,9 +266,15 @@ extern "C" int sengine_amd_ssa_kv(int32_t T, int32_t B, int32_t N, int32_t C, in
   SsaParams p{};
   p.k = k_bits; p.v = v_bits; p.kv = kv;
   p.T = T; p.B = B; p.N = N; p.C = C; p.H = heads; p.d = C / heads;
-  const size_t lds = 2 * (size_t)p.d * ((N + 63) / 64) * sizeof(uint64_t);
-  if (lds > 65536) return set_error(-2, "ssa_kv: (C/heads) * ceil(N/64) must be <= 4096 (token masks in LDS)");
-  hipLaunchKernelGGL(ssa_kv_kernel, dim3((unsigned)(T * B * heads)), dim3(256), lds, stream, p);
+  const size_t lds = 2 * (size_t)p.d * ((N + 63) / 64) * sizeof(uint64_t) + (size_t)p.d * p.d * sizeof(uint32_t);
+  if (lds > 65536) return set_error(-2, "ssa_kv: (C/heads) * ceil(N/64) too large for the token masks in LDS");
+  const dim3 grid((unsigned)(T * B * heads)), block(64 * kSsaKvWaves);
+  switch (p.d) {
+    case 16: hipLaunchKernelGGL(ssa_kv_kernel<16>, grid, block, lds, stream, p); break;
+    case 32: hipLaunchKernelGGL(ssa_kv_kernel<32>, grid, block, lds, stream, p); break;
+    case 48: hipLaunchKernelGGL(ssa_kv_kernel<48>, grid, block, lds, stream, p); break;
+    default: hipLaunchKernelGGL(ssa_kv_kernel<64>, grid, block, lds, stream, p); break;
+  }
   return (int)hipGetLastError();
 }
 
@@ -202,6 +285,7 @@ extern "C" int sengine_amd_ssa_attend_neuron(int32_t T, int32_t B, int32_t N, in
   if (const char* why = ssa_check(T, B, N, C, heads)) return set_error(-2, why);
   if (!q_bits || !kv || !out_bits) return set_error(-1, "ssa_attend_neuron: null pointer");
   if (const char* why = neuron_invalid(neuron, tau)) return set_error(-2, why);
+  if (T != 1 && T != 2 && T != 4 && T != 8) return set_error(-2, "ssa_attend_neuron: T must be 1, 2, 4 or 8");
   int e;
   if (!(scale > 0.f) || frexpf(scale, &e) != 0.5f)
     return set_error(-2, "ssa_attend_neuron: scale must be a power of two (exact attention arithmetic)");
@@ -210,7 +294,22 @@ extern "C" int sengine_amd_ssa_attend_neuron(int32_t T, int32_t B, int32_t N, in
   p.T = T; p.B = B; p.N = N; p.C = C; p.H = heads; p.d = C / heads;
   p.xscale = scale * 0.5f;
   p.np = make_neuron_params(neuron, hard_reset, tau, v_threshold, v_reset);
-  hipLaunchKernelGGL(ssa_attend_kernel, dim3((unsigned)(B * heads), (unsigned)((N + 63) / 64)), dim3(256), 0, stream,
-                     p);
-  return (int)hipGetLastError();
+  // token ranges per (b, head): enough workgroups for every CU several times over
+  const int tiles = (N + 15) / 16;
+  const int splits = std::max(1, std::min((tiles + 3) / 4, (2048 + B * heads - 1) / (B * heads)));
+  const int per = (tiles + splits - 1) / splits;
+  const size_t lds = (size_t)T * 2 * p.d * kSsaRow * sizeof(_Float16) + (size_t)T * per * 16 * sizeof(uint64_t);
+  if (lds > kSsaMaxLds)
+    return set_error(-2, "ssa_attend_neuron: T * (C/heads) and the token range too large for LDS");
+  // fast path: LIF with an exact power-of-two 1/tau and decay, hard reset (the reference's attn_lif)
+  const bool fast = epilogue_mode(p.np, false) == EPI_LIF_HARD;
+  void* fn = p.d == 16 ? attend_fn<16>(T, fast) : p.d == 32 ? attend_fn<32>(T, fast)
+                                                 : p.d == 48 ? attend_fn<48>(T, fast) : attend_fn<64>(T, fast);
+  if (fast) p.xscale *= p.np.rtau;  // exact: both powers of two
+  if (lds > 65536) {  // opt in to more than 64 KB of dynamic LDS (a host-side attribute)
+    const hipError_t e2 = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSsaMaxLds);
+    if (e2 != hipSuccess) return (int)e2;
+  }
+  void* args[] = {&p, const_cast<int*>(&splits)};
+  return (int)hipLaunchKernel(fn, dim3((unsigned)(B * heads * splits)), dim3(256), args, lds, stream);
 }
