@@ -105,7 +105,17 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
   if (d->T == 4 && d->C_out % 128 == 0 && (fg == 1 || fg == 2)) gpw = fg;
   if ((int64_t)p.ntiles * (d->C_out / (64 * gpw)) > 0x7fffffff) return hipErrorInvalidValue;
 
-  if (k3) return launch_tile3(p, d->T, shape, gpw, d->out_enc, mode, stream);
+  // Split the reduction over two wave sets when the grid gives at most one workgroup per
+  // CU (deep layers: few, long workgroups, one wave per SIMD); with more workgroups the
+  // doubled LDS footprint costs more than it gains (measured).  SENGINE_AMD_TILE_KSPLIT
+  // =1|2 overrides.
+  int ksplit = 1;
+  if (k3 && d->T == 4 && gpw == 1 && p.nchunk % 2 == 0) {
+    ksplit = (int64_t)p.ntiles * (d->C_out / 64) <= 256 ? 2 : 1;
+    const int fk = env_int_now("SENGINE_AMD_TILE_KSPLIT", 0);
+    if (fk == 1 || fk == 2) ksplit = fk;
+  }
+  if (k3) return launch_tile3(p, d->T, shape, gpw, ksplit, d->out_enc, mode, stream);
   return launch_tile1(p, d->T, gpw, d->out_enc, mode, stream);
 }
 

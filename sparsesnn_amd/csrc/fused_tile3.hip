@@ -4,13 +4,19 @@
 namespace sengine {
 
 // shape: 0 = 8x8 tiles (8-row blocks), 1 = 14x4 (8-row blocks), 2 = 7x7 (7-row blocks).
-hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int oe, int mode, hipStream_t s) {
+hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int ksplit, int oe, int mode,
+                        hipStream_t s) {
   switch (T) {
     case 1:
       return launch_tile<1, 3, 8, 8, 8, 1>(p, oe, mode, s);
     case 2:
       return launch_tile<2, 3, 8, 8, 8, 1>(p, oe, mode, s);
     case 4:
+      if (ksplit == 2) {
+        if (shape == 1) return launch_tile<4, 3, 14, 4, 8, 1, 2>(p, oe, mode, s);
+        if (shape == 2) return launch_tile<4, 3, 7, 7, 7, 1, 2>(p, oe, mode, s);
+        return launch_tile<4, 3, 8, 8, 8, 1, 2>(p, oe, mode, s);
+      }
       if (shape == 1)
         return gpw == 2 ? launch_tile<4, 3, 14, 4, 8, 2>(p, oe, mode, s) : launch_tile<4, 3, 14, 4, 8, 1>(p, oe, mode, s);
       if (shape == 2)

@@ -93,21 +93,26 @@ __device__ __forceinline__ void expand_word64(uint2 w, u32x4_t (&pc)[8]) {
   }
 }
 
-template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE>
-__global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR))
-__attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(TileParams p) {
+// KSP = 2 splits the reduction inside the workgroup: a second set of waves covers the same
+// positions and channels over the odd reduction chunks (its own LDS buffer), and its
+// accumulators are added to the first set's in LDS, in a fixed order, before the
+// epilogue.  Twice the waves per tile for layers whose grid leaves SIMDs with one wave.
+template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP>
+__global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR * KSP))
+__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : 2))) void fused_tile_kernel(TileParams p) {
   using Gm = TileGeom<KS, TR, TC, GR>;
   constexpr int NPIX = Gm::NPIX;
-  constexpr int NTHR = Gm::NTHR;
+  constexpr int NTHR = Gm::NTHR;  // threads of one set
   constexpr int NTAP = Gm::NTAP;
   constexpr int NBUF = Gm::NBUF;
   constexpr int NCH = 64 * GPW;
   constexpr int UNITS = T * NPIX;                 // (t, pixel) spike words per chunk
   constexpr int UPT = (UNITS + NTHR - 1) / NTHR;  // per thread
-  __shared__ uint2 sB[NBUF][T * 16 * NPIX];
+  __shared__ uint2 sB[NBUF * KSP][T * 16 * NPIX];
   __shared__ float sCoef[4][NCH];
 
-  const int tid = threadIdx.x;
+  const int set = KSP == 1 ? 0 : (int)threadIdx.x / NTHR;
+  const int tid = (int)threadIdx.x - set * NTHR;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int g = lane >> 4;
@@ -129,7 +134,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(Ti
   }
 
   const bool fold = MODE == EPI_LIF_HARD || (MODE == EPI_GENERIC && p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2);
-  if (tid < NCH) {
+  if (set == 0 && tid < NCH) {
     const float sc = p.scale[G0 * 64 + tid] * p.enc_scale;  // exact: enc_scale is a power of two
     const float bi = p.bias[G0 * 64 + tid];
     sCoef[0][tid] = fold ? sc * p.np.rtau : sc;             // exact: rtau is a power of two
@@ -212,7 +217,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(Ti
   // LDS byte address of this lane's tap-(0,0) half-piece g (half 0) in buffer 0; the four
   // 8-byte reads of a fragment are at compile-time offsets from it.
   const uint32_t lds0 =
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint2*)&sB[0][0] + (uint32_t)bbase * 8u;
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint2*)&sB[set * NBUF][0] + (uint32_t)bbase * 8u;
   const size_t wgroup = (size_t)p.nq * 4 * 64;
   const u32x4_t* wv = p.wvals + (size_t)G0 * wgroup + lane;
   const uint32_t* wm = p.wmeta + (size_t)G0 * wgroup + lane;
@@ -226,8 +231,8 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(Ti
       for (int a = 0; a < 4; ++a) acc[gg][t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   uint2 stg[UPT];
-  load_units(stg, 0);
-  store_units(0, stg);
+  load_units(stg, set);
+  store_units(set * NBUF, stg);
   __syncthreads();
 
   // A operands of (chunk c, tap) -> registers
@@ -244,16 +249,16 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(Ti
 
   u32x4_t av[GPW][4];
   uint32_t ix[GPW][4];
-  load_a(0, 0, av, ix);
-  for (int c = 0; c < p.nchunk; ++c) {
-    const bool more = c + 1 < p.nchunk;
-    const int buf = NBUF == 2 ? (c & 1) : 0;
-    if (more) load_units(stg, c + 1);
+  load_a(set, 0, av, ix);
+  for (int c = set; c < p.nchunk; c += KSP) {  // host: nchunk % KSP == 0 (sets stay in step)
+    const bool more = c + KSP < p.nchunk;
+    const int buf = NBUF == 2 ? ((c / KSP) & 1) : 0;
+    if (more) load_units(stg, c + KSP);
     // B fragments: four ds_read_b64 per (tap, t), issued one step ahead of their SMFMACs
     // and waited for with an explicit lgkmcnt (the loop issues no other LDS operation).
     // Written as asm so the compiler neither fuses them into 16-byte or paired reads nor
     // hoists them further (both measured slower / register-starved).
-    const uint32_t lbase = lds0 + (uint32_t)buf * (uint32_t)(T * 16 * NPIX * 8);
+    const uint32_t lbase = lds0 + (uint32_t)buf * (uint32_t)(T * 16 * NPIX * 8);  // within this set's buffers
     uint2 fr[2][4];
     auto issue = [&](int step, uint2 (&f)[4]) {
       const int tp = step / T, t = step - (step / T) * T;
@@ -270,7 +275,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(Ti
       u32x4_t avn[GPW][4];
       uint32_t ixn[GPW][4];
       if (tap + 1 < NTAP) load_a(c, tap + 1, avn, ixn);
-      else if (more) load_a(c + 1, 0, avn, ixn);
+      else if (more) load_a(c + KSP, 0, avn, ixn);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int step = tap * T + t;
@@ -304,9 +309,31 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 ? 3 : 2))) void fused_tile_kernel(Ti
     }
     if (more) {
       if (NBUF == 1) __syncthreads();  // every wave is done reading the single buffer
-      store_units(NBUF == 2 ? (buf ^ 1) : 0, stg);
+      store_units(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), stg);
       __syncthreads();
     }
+  }
+
+  if (KSP == 2) {  // set 1's accumulators join set 0's through the (now free) LDS buffers
+    static_assert(KSP == 1 || sizeof(sB) >= (size_t)NTHR * GPW * T * 4 * sizeof(float4_t), "LDS too small");
+    float4_t* red = reinterpret_cast<float4_t*>(&sB[0][0]);
+    __syncthreads();
+    if (set == 1) {
+#pragma unroll
+      for (int gg = 0; gg < GPW; ++gg)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int a = 0; a < 4; ++a) red[((gg * T + t) * 4 + a) * NTHR + tid] = acc[gg][t][a];
+    }
+    __syncthreads();
+    if (set == 1) return;
+#pragma unroll
+    for (int gg = 0; gg < GPW; ++gg)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) acc[gg][t][a] += red[((gg * T + t) * 4 + a) * NTHR + tid];
   }
 
 #pragma unroll
@@ -323,29 +350,31 @@ struct TileShape {
   int KS, TR, TC, GR;
 };
 
-template <int T, int KS, int TR, int TC, int GR, int GPW>
+template <int T, int KS, int TR, int TC, int GR, int GPW, int KSP = 1>
 hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s) {
-  constexpr int NTHR = TileGeom<KS, TR, TC, GR>::NTHR;
+  constexpr int NTHR = TileGeom<KS, TR, TC, GR>::NTHR * KSP;
   const dim3 grid((unsigned)(p.ntiles * (p.F / (64 * GPW))));
   if (out_enc == SENGINE_ENC_BITS) {
     if (mode == EPI_LIF_HARD)
-      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_LIF_HARD>), grid,
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_LIF_HARD, KSP>), grid,
                          dim3(NTHR), 0, s, p);
     else if (mode == EPI_IF_HARD)
-      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_IF_HARD>), grid,
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_IF_HARD, KSP>), grid,
                          dim3(NTHR), 0, s, p);
     else
-      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_GENERIC>), grid,
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_GENERIC, KSP>), grid,
                          dim3(NTHR), 0, s, p);
   } else {
-    hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16, EPI_GENERIC>), grid, dim3(NTHR),
-                       0, s, p);
+    hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16, EPI_GENERIC, KSP>), grid,
+                       dim3(NTHR), 0, s, p);
   }
   return hipGetLastError();
 }
 
-// Launchers compiled in fused_tile3.hip (KS = 3) and fused_tile1.hip (KS = 1).
-hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int out_enc, int mode, hipStream_t s);
+// Launchers compiled in fused_tile3.hip (KS = 3) and fused_tile1.hip (KS = 1).  ksplit: 1
+// or 2 (3x3, T = 4, one channel group per wave, nchunk even).
+hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int ksplit, int out_enc, int mode,
+                        hipStream_t s);
 hipError_t launch_tile1(const TileParams& p, int T, int gpw, int out_enc, int mode, hipStream_t s);
 
 }  // namespace sengine

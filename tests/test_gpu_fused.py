@@ -186,6 +186,31 @@ def test_tile_channel_blocking(dev, gpw, k, stride, H, W, C_in, C_out, B):
         del os.environ["SENGINE_AMD_TILE_GPW"]
 
 
+@pytest.mark.parametrize("ksplit", ["1", "2"])
+@pytest.mark.parametrize("shape", ["0", "1", "2"])
+@pytest.mark.parametrize("H,W,C_in,C_out,B", [(7, 7, 256, 128, 3), (13, 11, 128, 64, 2), (9, 16, 512, 64, 1)])
+def test_tile_reduction_split(dev, ksplit, shape, H, W, C_in, C_out, B):
+    """3x3 halo tiles with the reduction split over two wave sets (SENGINE_AMD_TILE_KSPLIT),
+    each tile shape, LIF (fast epilogue) and IF with state (generic epilogue), against the oracle."""
+    import os
+    os.environ["SENGINE_AMD_TILE_KSPLIT"] = ksplit
+    os.environ["SENGINE_AMD_TILE_SHAPE"] = shape
+    try:
+        case = ref.make_layer_case(110 + H + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
+                                   fp16_weights=True, p_spike=0.2)
+        rep, x_err, _, _ = run_case(dev, case)
+        assert rep.ok, str(rep)
+        assert x_err < 1e-4
+        g = torch.Generator().manual_seed(3)
+        v0 = torch.rand((B, C_out, H, W), generator=g) * 0.4
+        rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0)
+        assert rep2.ok, str(rep2)
+        assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
+    finally:
+        del os.environ["SENGINE_AMD_TILE_KSPLIT"]
+        del os.environ["SENGINE_AMD_TILE_SHAPE"]
+
+
 # ---- flat small-output layout: <= 16 output pixels per image run as one GEMM per image
 FLAT_CASES = [(2, 2, 3, 1, 1, 256, 256, 5, 4), (4, 4, 3, 2, 1, 128, 256, 3, 4), (6, 6, 3, 2, 1, 64, 128, 2, 2),
               (4, 4, 3, 1, 1, 128, 128, 3, 8), (2, 2, 3, 2, 1, 256, 512, 4, 1), (2, 2, 1, 2, 0, 64, 128, 3, 4),
