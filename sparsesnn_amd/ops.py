@@ -182,7 +182,7 @@ def pack_dense_weights(s: ConvSpec, weight: torch.Tensor, layout: int = WLAYOUT_
     return values
 
 
-def pack_spikes(x: torch.Tensor) -> torch.Tensor:
+def pack_spikes(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Dense (..., C) fp16/fp32 -> spike bits int32 (..., C/32) (value != 0 -> 1)."""
     lib = _lib.load()
     _require_cuda(x, "x")
@@ -193,12 +193,16 @@ def pack_spikes(x: torch.Tensor) -> torch.Tensor:
     if enc is None:
         raise SEngineError("pack_spikes: x must be fp16 or fp32")
     n_pos = x.numel() // C
-    out = torch.empty(*x.shape[:-1], C // 32, dtype=torch.int32, device=x.device)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], C // 32, dtype=torch.int32, device=x.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, n_pos * (C // 32), torch.int32, "out")
     check(lib.sengine_amd_pack_spikes(_ptr(x), enc, n_pos, C, _ptr(out), _stream(x.device)), "pack_spikes")
     return out
 
 
-def unpack_spikes(bits: torch.Tensor, C: int, dtype=torch.float16) -> torch.Tensor:
+def unpack_spikes(bits: torch.Tensor, C: int, dtype=torch.float16, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     lib = _lib.load()
     _require_cuda(bits, "bits")
     if C % 32 or bits.shape[-1] != C // 32 or bits.dtype != torch.int32:
@@ -207,7 +211,11 @@ def unpack_spikes(bits: torch.Tensor, C: int, dtype=torch.float16) -> torch.Tens
     if enc is None:
         raise SEngineError("unpack_spikes: dtype must be fp16 or fp32")
     n_pos = bits.numel() // (C // 32)
-    out = torch.empty(*bits.shape[:-1], C, dtype=dtype, device=bits.device)
+    if out is None:
+        out = torch.empty(*bits.shape[:-1], C, dtype=dtype, device=bits.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, n_pos * C, dtype, "out")
     check(lib.sengine_amd_unpack_spikes(_ptr(bits), n_pos, C, _ptr(out), enc, _stream(bits.device)), "unpack_spikes")
     return out
 
@@ -515,7 +523,7 @@ def dense_conv_bn(s: ConvSpec, data: torch.Tensor, values: torch.Tensor, bn_scal
 
 def multistep_neuron(x: torch.Tensor, T: int, neuron: str = "lif", tau: float = 2.0, v_threshold: float = 1.0,
                      v_reset: Optional[float] = 0.0, state: Optional[torch.Tensor] = None, out_enc: int = ENC_BITS,
-                     h_trace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     h_trace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Standalone multi-step LIF/IF over T on x (T, ...) fp32 (n = x.numel()/T per step).
     v_reset=None selects soft reset (models/neurons.py:135-137).  Returns spikes as bits
     int32 (T, n/32) or fp16 (T, n)."""
@@ -531,7 +539,11 @@ def multistep_neuron(x: torch.Tensor, T: int, neuron: str = "lif", tau: float = 
         _require_cuda(h_trace, "h_trace")
         _require_numel(h_trace, T * n, torch.float32, "h_trace")
     odt, n_out = _enc_numel(out_enc, T * n)
-    out = torch.empty(n_out, dtype=odt, device=x.device)
+    if out is None:
+        out = torch.empty(n_out, dtype=odt, device=x.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, n_out, odt, "out")
     hard = v_reset is not None
     check(lib.sengine_amd_multistep_neuron(T, n, neuron_code(neuron), int(hard), float(tau),
                                            float(v_threshold), float(v_reset if hard else 0.0), _ptr(x), _ptr(state),
