@@ -91,11 +91,15 @@ const char* sengine_amd_last_error(void);
 
 /*
  * Kernel selection for sengine_amd_fused_sparse_conv_bn_lif with spike-bit input:
- * 0 = automatic (the default: tile kernel for 3x3 / stride 1 / pad 1 and 1x1 / pad 0 with
- * one weight plane and T <= 4, else the LDS-staged kernel), 1 = direct-gather kernel (the kernel fp16
- * inputs always use), 2 = LDS-staged kernel.  Process-wide; the environment variable
- * SENGINE_AMD_FUSED_KERNEL=direct|lds sets 1|2 at load time.  Every choice computes the
- * same operator (the tests hold each one to the same oracle).
+ * 0 = automatic (the default: a split-K small-M kernel when the output has fewer than 128
+ * units of 64 positions x 64 channels, else the tile kernel for 3x3 / stride 1 / pad 1 and
+ * 1x1 / pad 0 with one weight plane and T <= 4, else the LDS-staged kernel), 1 =
+ * direct-gather kernel (the kernel fp16 inputs always use), 2 = LDS-staged kernel, 3 =
+ * tile kernel where eligible (never small-M).  Convs in the flat small-output layout (at
+ * most 16 output pixels, an input at most 2x the kernel window and a flat matrix of at most
+ * 4x the conv's weight entries) use its kernels for every choice.  Process-wide; the
+ * environment variable SENGINE_AMD_FUSED_KERNEL=direct|lds|tile sets 1|2|3 at load time.
+ * Every choice computes the same operator (the tests hold each one to the same oracle).
  */
 int sengine_amd_set_fused_kernel(int32_t choice);
 

@@ -46,7 +46,9 @@ bool flat_layout(const sengine_conv_lif_desc* d, const Geometry& geo) {
   // the flat matrix multiplies H*W / (KH*KW) times the conv's own work (taps outside the
   // window are zeros): allowed up to kFlatMaxWaste
   const bool cheap = (int64_t)d->H * d->W <= kFlatMaxWaste * d->KH * d->KW;
-  return npix <= kFlatMaxPixels && kf <= kFlatMaxK && nf * kf <= kFlatMaxEntries && cheap;
+  // ... and holds OH*OW*H*W / (KH*KW) times the conv's weight entries, all read every call
+  const bool compact = npix * d->H * d->W <= kFlatMaxInflate * d->KH * d->KW;
+  return npix <= kFlatMaxPixels && kf <= kFlatMaxK && nf * kf <= kFlatMaxEntries && cheap && compact;
 }
 
 static int g_kernel_choice = -1;
@@ -54,7 +56,11 @@ static int g_kernel_choice = -1;
 int fused_kernel_choice() {
   if (g_kernel_choice < 0) {
     const char* e = getenv("SENGINE_AMD_FUSED_KERNEL");
-    g_kernel_choice = !e ? 0 : strcmp(e, "direct") == 0 ? 1 : strcmp(e, "lds") == 0 ? 2 : 0;
+    g_kernel_choice = !e                         ? 0
+                      : strcmp(e, "direct") == 0 ? 1
+                      : strcmp(e, "lds") == 0    ? 2
+                      : strcmp(e, "tile") == 0   ? 3
+                                                 : 0;
   }
   return g_kernel_choice;
 }
@@ -122,8 +128,8 @@ extern "C" int sengine_amd_version(void) { return 100; }
 extern "C" const char* sengine_amd_last_error(void) { return g_last_error; }
 
 extern "C" int sengine_amd_set_fused_kernel(int32_t choice) {
-  if (choice < 0 || choice > 2)
-    return set_error(-2, "set_fused_kernel: choice must be 0 (auto), 1 (direct) or 2 (lds)");
+  if (choice < 0 || choice > 3)
+    return set_error(-2, "set_fused_kernel: choice must be 0 (auto), 1 (direct), 2 (lds) or 3 (tile)");
   g_kernel_choice = choice;
   return 0;
 }

@@ -150,15 +150,16 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
 }
 
 // ---- small-M variant: split-K over the waves of a workgroup --------------------------------
-// For layers with few output positions (the flat layout: one row per image), the direct
-// kernel's grid is a handful of workgroups, each walking the whole reduction alone.  Here
-// a workgroup of kSmallWaves waves owns 16 positions x 64 channels x all T; wave s
-// accumulates the reduction chunks q = s, s + kSmallWaves, ... (the next chunk's operands
-// are loaded before the current one is multiplied), the partial accumulators are summed
-// in LDS in wave order (deterministic), and wave 0 runs the epilogue.  Spike-bit input,
-// 1x1 geometry (the flat view), any T of the direct kernel.  Operands are loaded two
-// chunks ahead; the cross-wave sum takes up to four timesteps per LDS round.
+// For layers with few output positions (the flat layout, or small images at small batch),
+// 64-position workgroups give a handful of workgroups, each walking the whole reduction
+// alone.  Here a workgroup of kSmallWaves waves owns 16 positions x 64 channels x all T;
+// wave s accumulates the reduction chunks q = s, s + kSmallWaves, ... (implicit im2col as
+// the direct kernel, any geometry), the partial accumulators are summed in LDS in wave
+// order (deterministic), and wave 0 runs the epilogue.  Spike-bit input, any T of the
+// direct kernel.  Operands are loaded two chunks ahead; the cross-wave sum takes up to
+// four timesteps per LDS round.
 constexpr int kSmallWaves = 8;
+constexpr int64_t kSmallMaxUnits = 128;  // outputs below 128 (64 positions x 64 channels) units
 
 template <int T, int PLANES>
 struct SmallOperands {
@@ -198,9 +199,19 @@ __global__ __launch_bounds__(64 * kSmallWaves) void fused_smallm_kernel(FusedPar
     for (int a = 0; a < 4; ++a) acc[t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nq = p.nq;
-  const int rowbytes = p.C >> 3;  // bytes of one position's input (the whole flattened image)
-  const uint8_t* src = p.in + (size_t)(mvalid ? m : 0) * rowbytes;
-  const size_t tstride = (size_t)p.in_t_stride * rowbytes;
+  // implicit im2col, as the direct kernel: chunk q = (tap, 64 input channels); the lane's
+  // spike word is the tap-shifted input pixel of its position (zero outside the image)
+  int b = 0, oh = 0, ow = 0;
+  if (mvalid) {
+    const int ohw = p.OH * p.OW;
+    b = m / ohw;
+    const int r = m - b * ohw;
+    oh = r / p.OW;
+    ow = r - oh * p.OW;
+  }
+  const int cbytes = p.C >> 3;
+  const int chunks_per_tap = p.C >> 6;
+  const size_t tstride = (size_t)p.in_t_stride * cbytes;
   const half8_t* wv = p.wvals + (size_t)G * nq * PLANES * 4 * 64 + lane;
   const uint32_t* wm = p.wmeta + (size_t)G * nq * 4 * 64 + lane;
   const uint32_t sel = 0x0c0c0000u | ((uint32_t)(4 + g) << 8) | (uint32_t)g;
@@ -212,9 +223,16 @@ __global__ __launch_bounds__(64 * kSmallWaves) void fused_smallm_kernel(FusedPar
       for (int pl = 0; pl < PLANES; ++pl) o.av[pl][a] = wv[((size_t)(q * PLANES + pl) * 4 + a) * 64];
       o.ix[a] = wm[((size_t)q * 4 + a) * 64];
     }
+    const int tap = q / chunks_per_tap;
+    const int c0 = q - tap * chunks_per_tap;
+    const int kr = tap / p.KW;
+    const int ih = oh * p.SH - p.PH + kr * p.DH;
+    const int iw = ow * p.SW - p.PW + (tap - kr * p.KW) * p.DW;
+    const bool ok = mvalid && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
+    const uint8_t* src = p.in + (((size_t)b * p.H + (ok ? ih : 0)) * p.W + (ok ? iw : 0)) * cbytes + c0 * 8;
 #pragma unroll
     for (int t = 0; t < T; ++t)
-      o.bw[t] = mvalid ? *reinterpret_cast<const uint2*>(src + t * tstride + q * 8) : uint2{0u, 0u};
+      o.bw[t] = ok ? *reinterpret_cast<const uint2*>(src + t * tstride) : uint2{0u, 0u};
   };
   constexpr int S = kSmallWaves;
   constexpr bool DEEP = T * PLANES <= 4;  // two chunks ahead where the registers allow, else one
@@ -346,9 +364,12 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
   // kernel (its per-thread tap mask holds up to 64 taps), else the direct-gather kernel below.
   const int choice = fused_kernel_choice();
   const bool flat = flat_layout(d, geo);
-  if (!flat && d->in_enc == SENGINE_ENC_BITS && choice != 1) {
+  // few 64-position x 64-channel work units: split the reduction inside workgroups instead
+  const bool small = d->in_enc == SENGINE_ENC_BITS && choice == 0 &&
+                     ((geo.M + 63) / 64) * (int64_t)(d->C_out / 64) < kSmallMaxUnits;
+  if (!flat && !small && d->in_enc == SENGINE_ENC_BITS && choice != 1) {
     const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace, sew};
-    if (choice == 0 && tile_eligible(d)) return (int)launch_fused_bits_tile(d, geo, args, stream);
+    if ((choice == 0 || choice == 3) && tile_eligible(d)) return (int)launch_fused_bits_tile(d, geo, args, stream);
     if (d->KH * d->KW <= 64) return (int)launch_fused_bits_lds(d, geo, args, stream);
   }
 
@@ -383,7 +404,9 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
     p.M = d->B;
     p.nq = p.C / 64;
     p.in_t_stride = d->B;
-    if (d->in_enc == SENGINE_ENC_BITS && choice != 1) {
+  }
+  if ((flat || small) && d->in_enc == SENGINE_ENC_BITS && choice != 1) {
+    {
       // fast epilogue modes for the common case (one weight plane, bit output)
       int mode = epilogue_mode(p.np, h_trace != nullptr || x_trace != nullptr || sew.real_out != nullptr);
       if (d->weight_planes != 1 || d->out_enc != SENGINE_ENC_BITS) mode = EPI_GENERIC;

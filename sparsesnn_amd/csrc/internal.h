@@ -30,7 +30,8 @@ int check_desc(const sengine_conv_lif_desc* d, Geometry* geo, bool sparse);
 constexpr int kFlatMaxPixels = 16;
 constexpr int64_t kFlatMaxK = 16384;
 constexpr int64_t kFlatMaxEntries = 1ll << 26;  // N_flat * K_flat
-constexpr int64_t kFlatMaxWaste = 4;             // H*W <= 4*KH*KW
+constexpr int64_t kFlatMaxWaste = 2;             // H*W <= 2*KH*KW (MACs vs the conv's)
+constexpr int64_t kFlatMaxInflate = 4;           // OH*OW*H*W <= 4*KH*KW (weight entries vs the conv's)
 bool flat_layout(const sengine_conv_lif_desc* d, const Geometry& geo);
 
 // Null if (neuron, tau) is a valid neuron description, else the reason.
@@ -64,9 +65,12 @@ bool tile_eligible(const sengine_conv_lif_desc* d);
 hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
                                   hipStream_t stream);
 
-// Kernel selection for the fused op with spike-bit input: 0 = automatic (tile kernel where
-// eligible, else the LDS-staged kernel), 1 = always the direct-gather kernel, 2 = always
-// the LDS-staged kernel.  Read once from SENGINE_AMD_FUSED_KERNEL ("auto" | "direct" | "lds").
+// Kernel selection for the fused op with spike-bit input: 0 = automatic (the split-K
+// small-M kernel for small outputs, else the tile kernel where eligible, else the
+// LDS-staged kernel), 1 = always the direct-gather kernel, 2 = the LDS-staged kernel,
+// 3 = the tile kernel where eligible (never small-M).  The flat small-output layout
+// always takes the small-M kernel (direct for 1).  Read once from
+// SENGINE_AMD_FUSED_KERNEL ("auto" | "direct" | "lds" | "tile").
 int fused_kernel_choice();
 
 }  // namespace sengine

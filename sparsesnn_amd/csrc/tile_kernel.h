@@ -99,7 +99,7 @@ __device__ __forceinline__ void expand_word64(uint2 w, u32x4_t (&pc)[8]) {
 // epilogue.  Twice the waves per tile for layers whose grid leaves SIMDs with one wave.
 template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP>
 __global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR * KSP))
-__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : 2))) void fused_tile_kernel(TileParams p) {
+__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
   using Gm = TileGeom<KS, TR, TC, GR>;
   constexpr int NPIX = Gm::NPIX;
   constexpr int NTHR = Gm::NTHR;  // threads of one set

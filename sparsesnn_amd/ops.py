@@ -100,10 +100,12 @@ def make_desc(s: ConvSpec) -> ConvLifDesc:
 
 
 def set_fused_kernel(choice: str) -> None:
-    """Kernel for spike-bit inputs: 'auto' (halo-tiled kernel for 3x3 / stride 1 / pad 1, else
-    the LDS-staged kernel), 'direct' (direct-gather kernel) or 'lds' (LDS-staged kernel)."""
+    """Kernel for spike-bit inputs: 'auto' (split-K small-M kernel for small outputs, else the
+    halo-tiled kernel where eligible, else the LDS-staged kernel), 'direct' (direct-gather
+    kernel), 'lds' (LDS-staged kernel) or 'tile' (halo-tiled kernel where eligible)."""
     lib = _lib.load()
-    check(lib.sengine_amd_set_fused_kernel({"auto": 0, "direct": 1, "lds": 2}[choice]), "set_fused_kernel")
+    check(lib.sengine_amd_set_fused_kernel({"auto": 0, "direct": 1, "lds": 2, "tile": 3}[choice]),
+          "set_fused_kernel")
 
 
 def geometry(s: ConvSpec):

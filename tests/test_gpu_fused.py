@@ -117,7 +117,7 @@ def test_hwio_layout(dev):
     assert rep.ok, str(rep)
 
 
-@pytest.mark.parametrize("kernel", ["direct", "lds", "auto"])
+@pytest.mark.parametrize("kernel", ["direct", "lds", "auto", "tile"])
 @pytest.mark.parametrize("k,stride,pad,B,C_in,C_out,H,W", [(3, 1, 1, 5, 64, 128, 13, 11), (3, 2, 1, 3, 128, 64, 15, 9),
                                                            (1, 1, 0, 2, 256, 192, 7, 7), (1, 2, 0, 2, 64, 64, 9, 10)])
 def test_bit_kernels_agree_and_match_oracle(dev, kernel, k, stride, pad, B, C_in, C_out, H, W):
@@ -142,6 +142,7 @@ def test_halo_tiles_against_oracle(dev, tile, H, W, C_in, C_out, B):
     leave ragged tiles, one to three input-channel chunks and several output-channel groups."""
     import os
     os.environ["SENGINE_AMD_TILE_SHAPE"] = tile
+    ops.set_fused_kernel("tile")  # small test shapes would otherwise take the small-M kernel
     try:
         case = ref.make_layer_case(60 + H + W + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
                                    fp16_weights=True)
@@ -151,6 +152,7 @@ def test_halo_tiles_against_oracle(dev, tile, H, W, C_in, C_out, B):
         rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=None, out_enc=ops.ENC_F16)
         assert rep2.ok, str(rep2)
     finally:
+        ops.set_fused_kernel("auto")
         del os.environ["SENGINE_AMD_TILE_SHAPE"]
 
 
@@ -161,7 +163,11 @@ def test_halo_short_sequences_and_state(dev, T, neuron, v_reset):
                                p_spike=0.3)
     g = torch.Generator().manual_seed(9)
     v0 = torch.rand((2, 64, 9, 10), generator=g) * 0.5
-    rep, _, r, v_fin = run_case(dev, case, neuron=neuron, v_reset=v_reset, v_th=0.6, v0=v0)
+    ops.set_fused_kernel("tile")  # small test shapes would otherwise take the small-M kernel
+    try:
+        rep, _, r, v_fin = run_case(dev, case, neuron=neuron, v_reset=v_reset, v_th=0.6, v0=v0)
+    finally:
+        ops.set_fused_kernel("auto")
     assert rep.ok, str(rep)
     assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
 
@@ -174,6 +180,7 @@ def test_tile_channel_blocking(dev, gpw, k, stride, H, W, C_in, C_out, B):
     3x3 halo tiles and flat 1x1 tiles (stride 1 and 2), against the oracle."""
     import os
     os.environ["SENGINE_AMD_TILE_GPW"] = gpw
+    ops.set_fused_kernel("tile")  # small test shapes would otherwise take the small-M kernel
     try:
         case = ref.make_layer_case(80 + k + stride + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
                                    stride=stride, padding=k // 2, fp16_weights=True)
@@ -183,6 +190,7 @@ def test_tile_channel_blocking(dev, gpw, k, stride, H, W, C_in, C_out, B):
         rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0)
         assert rep2.ok, str(rep2)
     finally:
+        ops.set_fused_kernel("auto")
         del os.environ["SENGINE_AMD_TILE_GPW"]
 
 
@@ -195,6 +203,7 @@ def test_tile_reduction_split(dev, ksplit, shape, H, W, C_in, C_out, B):
     import os
     os.environ["SENGINE_AMD_TILE_KSPLIT"] = ksplit
     os.environ["SENGINE_AMD_TILE_SHAPE"] = shape
+    ops.set_fused_kernel("tile")  # small test shapes would otherwise take the small-M kernel
     try:
         case = ref.make_layer_case(110 + H + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
                                    fp16_weights=True, p_spike=0.2)
@@ -207,21 +216,26 @@ def test_tile_reduction_split(dev, ksplit, shape, H, W, C_in, C_out, B):
         assert rep2.ok, str(rep2)
         assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
     finally:
+        ops.set_fused_kernel("auto")
         del os.environ["SENGINE_AMD_TILE_KSPLIT"]
         del os.environ["SENGINE_AMD_TILE_SHAPE"]
 
 
 # ---- flat small-output layout: <= 16 output pixels per image run as one GEMM per image
-FLAT_CASES = [(2, 2, 3, 1, 1, 256, 256, 5, 4), (4, 4, 3, 2, 1, 128, 256, 3, 4), (6, 6, 3, 2, 1, 64, 128, 2, 2),
-              (4, 4, 3, 1, 1, 128, 128, 3, 8), (2, 2, 3, 2, 1, 256, 512, 4, 1), (2, 2, 1, 2, 0, 64, 128, 3, 4),
-              (5, 3, 3, 2, 1, 64, 64, 2, 4)]
+# flat: (2,2,3,1,1) (3,3,3,2,1) (2,3,3,1,1) (2,2,3,2,1) (1,2,1,2,0) (3,2,3,2,1); the rest
+# have small outputs on inputs over 2x the kernel window or whose flat matrix would hold over
+# 4x the conv's weights, so they take the small-M kernel on the ordinary layout
+FLAT_CASES = [(2, 2, 3, 1, 1, 256, 256, 5, 4), (3, 3, 3, 2, 1, 64, 128, 2, 4), (2, 3, 3, 1, 1, 128, 128, 3, 8),
+              (2, 2, 3, 2, 1, 256, 512, 4, 1), (1, 2, 1, 2, 0, 64, 128, 3, 4), (3, 2, 3, 2, 1, 64, 64, 2, 4),
+              (4, 4, 3, 2, 1, 128, 256, 3, 4), (4, 4, 3, 1, 1, 128, 128, 3, 8),
+              (6, 6, 3, 2, 1, 64, 128, 2, 2), (2, 2, 1, 2, 0, 64, 128, 3, 4), (5, 3, 3, 2, 1, 64, 64, 2, 4)]
 
 
 @pytest.mark.parametrize("kernel", ["auto", "direct"])
 @pytest.mark.parametrize("H,W,k,stride,pad,C_in,C_out,B,T", FLAT_CASES)
 def test_flat_layout_against_oracle(dev, kernel, H, W, k, stride, pad, C_in, C_out, B, T):
-    """Small outputs (flat layout): the split-K small-M kernel ('auto') and the direct kernel
-    on the flat view, with traces, against the oracle."""
+    """Small outputs (flat layout where it applies): the split-K small-M kernel ('auto') and
+    the direct kernel, with traces, against the oracle."""
     ops.set_fused_kernel(kernel)
     try:
         case = ref.make_layer_case(60 + H + k + C_in // 64, T=T, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
@@ -237,25 +251,34 @@ def test_flat_layout_against_oracle(dev, kernel, H, W, k, stride, pad, C_in, C_o
 
 @pytest.mark.parametrize("in_enc,out_enc,planes", [(ops.ENC_BITS, ops.ENC_F16, 1), (ops.ENC_F16, ops.ENC_BITS, 1),
                                                    (ops.ENC_F16, ops.ENC_F16, 2), (ops.ENC_BITS, ops.ENC_BITS, 2)])
-def test_flat_layout_encodings_and_state(dev, in_enc, out_enc, planes):
-    case = ref.make_layer_case(71, T=4, B=3, C_in=128, C_out=128, H=4, W=4, k=3, stride=1, padding=1,
+@pytest.mark.parametrize("H", [2, 4])
+def test_flat_layout_encodings_and_state(dev, in_enc, out_enc, planes, H):
+    """Encodings, two weight planes and a carried membrane on a flat layer (2x2) and on a
+    small non-flat one (4x4)."""
+    case = ref.make_layer_case(71 + H, T=4, B=3, C_in=128, C_out=128, H=H, W=H, k=3, stride=1, padding=1,
                                fp16_weights=(planes == 1), p_spike=0.3)
     g = torch.Generator().manual_seed(6)
-    v0 = torch.rand((3, 128, 4, 4), generator=g) * 0.9
+    v0 = torch.rand((3, 128, H, H), generator=g) * 0.9
     rep, x_err, r, v_fin = run_case(dev, case, planes=planes, in_enc=in_enc, out_enc=out_enc, v0=v0)
     assert rep.ok, str(rep)
     assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
 
 
-@pytest.mark.parametrize("H,W,k,stride,pad", [(2, 2, 3, 1, 1), (6, 6, 3, 2, 1), (2, 2, 1, 2, 0), (3, 5, 3, 2, 1)])
-def test_flat_compressor_matches_numpy(dev, H, W, k, stride, pad):
-    """The compressor emits the flat blob for small outputs: byte-identical to the numpy
-    restatement applied to oracle.packing.flat_weight."""
+@pytest.mark.parametrize("H,W,k,stride,pad,flat", [(2, 2, 3, 1, 1, True), (3, 3, 3, 2, 1, True),
+                                                    (1, 2, 1, 2, 0, True), (3, 2, 3, 2, 1, True),
+                                                    (4, 4, 3, 1, 1, False), (6, 6, 3, 2, 1, False),
+                                                    (3, 4, 3, 2, 1, False), (2, 2, 1, 2, 0, False)])
+def test_flat_compressor_matches_numpy(dev, H, W, k, stride, pad, flat):
+    """The compressor emits the flat blob for small outputs whose flat matrix stays within 4x
+    the conv's weight entries and whose input is at most 2x the kernel window: byte-identical
+    to the numpy restatement applied to oracle.packing.flat_weight; other small outputs keep
+    the ordinary layout."""
     g = torch.Generator().manual_seed(H * W + k)
     w = ref.prune_conv_2_4(torch.randn((128, 64, k, k), generator=g) * 0.05).half().float()
     spec = ops.ConvSpec(T=4, B=2, C_in=64, H=H, W=W, C_out=128, KH=k, KW=k, stride=stride, padding=pad)
     values, meta, viol = ops.compress_2_4(spec, w.to(dev))
-    ev, em, _ = pk.compress_2_4(pk.flat_weight(w.numpy(), H, W, stride, pad), 1)
+    wl = pk.flat_weight(w.numpy(), H, W, stride, pad) if flat else w.numpy()
+    ev, em, _ = pk.compress_2_4(wl, 1)
     assert np.array_equal(values.cpu().numpy().view(np.uint16), ev.reshape(-1))
     assert np.array_equal(meta.cpu().numpy().view(np.uint32), em.reshape(-1))
     assert int(viol.sum()) == 0

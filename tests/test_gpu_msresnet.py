@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 DECAY, THRESH = 0.25, 0.5  # models/msresnet.py:20-21
 
 
-@pytest.mark.parametrize("kernel", ["auto", "lds", "direct"])
+@pytest.mark.parametrize("kernel", ["auto", "lds", "direct", "tile"])
 @pytest.mark.parametrize("k,stride,H,C_in,C_out", [(3, 1, 12, 64, 64), (3, 2, 11, 128, 64), (1, 1, 9, 256, 128),
                                                    (3, 1, 2, 128, 128)])
 def test_ms_neuron_in_fused_kernels(dev, kernel, k, stride, H, C_in, C_out):
@@ -71,7 +71,7 @@ def _shortcut_case(dev, seed, T, B, C_in, C_out, H, k, stride, neuron, tau, v_th
     return s_gpu, y_gpu, r
 
 
-@pytest.mark.parametrize("kernel", ["auto", "direct"])
+@pytest.mark.parametrize("kernel", ["auto", "direct", "tile"])
 @pytest.mark.parametrize("neuron,tau,v_th", [("ms", DECAY, THRESH), ("lif", 2.0, 1.0), ("ms", 0.3, THRESH)])
 @pytest.mark.parametrize("k,stride,H,C_in,C_out", [(3, 1, 10, 64, 64), (3, 2, 9, 64, 128), (1, 1, 7, 128, 64),
                                                    (3, 1, 2, 128, 128)])
