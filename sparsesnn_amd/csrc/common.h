@@ -25,6 +25,10 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
 
+// Fourth dword of a raw buffer resource on gfx9 parts (untyped 32-bit data, no swizzle):
+// loads through it are bounds-checked against num_records bytes and return 0 beyond.
+constexpr int kBufferDword3 = 0x00020000;
+
 // Spike value fed to the matrix cores for a set bit: fp16 2.0 (0x4000) is a single
 // set bit, so expansion is one shift + one mask per register.  The factor 2 is exact
 // and folded into the epilogue scale.

@@ -28,11 +28,17 @@
 //    HBM).  GPW = 2 halves the B bytes per SMFMAC (each fragment feeds 8 SMFMACs).
 //  * A operands (2:4 values + metadata) come from global memory (L2-resident, shared by
 //    every workgroup of a channel group), one tap ahead of their use.
-//  * LDS layout: 8-byte half-pieces [t][half h][piece i][pixel]; piece i holds channels
-//    8i..8i+7 (half h: 8i+4h..8i+4h+3), so a lane group's 16 lanes read 16 distinct
-//    half-pieces (conflict-free), staging writes are consecutive, and a fragment is four
-//    8-byte reads (measured cheaper for the SIMD than two 16-byte reads; the halves of a
-//    piece are kept more than 2 KB apart so they are not merged into one 16-byte access).
+//  * LDS layout: 8-byte half-pieces; half-piece q = 8h + i (piece i holds channels
+//    8i..8i+7, half h channels 8i+4h..8i+4h+3) of pixel px at timestep t sits at entry
+//    t*(16*NPIX + PAD) + (q >> 1)*NPIX + (q & 1)*(8*NPIX + PAD) + px: even and odd q in
+//    two regions, the odd one PAD entries further on.  Staging writes are consecutive and
+//    a fragment is four 8-byte reads (measured cheaper for the SIMD than two 16-byte
+//    reads).  The LDS has 64 four-byte banks and serves a ds_read_b64 32 lanes at a time,
+//    i.e. lane groups g, g+1 that read half-pieces q, q+1 of the same pixels; PAD (per tile
+//    shape, found by enumerating the banks of every fragment read of the shape) puts the two
+//    groups on disjoint banks, and lanes outside the tile read the address of a lane inside
+//    it (same address: broadcast).  Without the shift the same reads measured 1.45x the
+//    LDS cycles.
 //  * Workgroup ids are remapped so each XCD (own L2) runs a contiguous range of
 //    (channel block, tile) ids: an XCD touches few channel blocks' weights.
 #pragma once
@@ -72,6 +78,9 @@ struct TileGeom {
   static constexpr int NTHR = 64 * NWAVE;
   static constexpr int NTAP = KS * KS;
   static constexpr int NBUF = KS == 3 ? 1 : 2;
+  // odd half-piece region shift (entries) that makes every fragment read conflict-free
+  static constexpr int PAD = (KS == 3 && TR == 7 && TC == 7) ? 8 : 16;
+  static constexpr int TS = 16 * NPIX + PAD;  // entries per timestep
 };
 
 // Consecutive hardware workgroup ids go round-robin over the 8 XCDs; give XCD x the
@@ -108,10 +117,14 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
   constexpr int NCH = 64 * GPW;
   constexpr int UNITS = T * NPIX;                 // (t, pixel) spike words per chunk
   constexpr int UPT = (UNITS + NTHR - 1) / NTHR;  // per thread
-  __shared__ uint2 sB[NBUF * KSP][T * 16 * NPIX];
+  constexpr int PAD = Gm::PAD;
+  constexpr int TS = Gm::TS;
+  constexpr int BUFE = T * TS;  // entries per buffer
+  __shared__ uint2 sB[NBUF * KSP][BUFE];
   __shared__ float sCoef[4][NCH];
 
-  const int set = KSP == 1 ? 0 : (int)threadIdx.x / NTHR;
+  // wave-uniform (NTHR is a multiple of 64): keeps the reduction-chunk loop in scalar registers
+  const int set = KSP == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x / NTHR);
   const int tid = (int)threadIdx.x - set * NTHR;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -170,7 +183,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
       iw = (r - oh * p.OW) * p.S;
     }
     goff[j] = inb ? (((t * p.B + ib) * p.H + ih) * p.W + iw) * cbytes : -1;
-    soff[j] = t * 16 * NPIX + px;
+    soff[j] = t * TS + px;
   }
   auto load_units = [&](uint2 (&v)[UPT], int c) {
 #pragma unroll
@@ -185,8 +198,10 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
         expand_word64(v[j], pc);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          sB[buf][soff[j] + i * NPIX] = uint2{pc[i][0], pc[i][1]};
-          sB[buf][soff[j] + (8 + i) * NPIX] = uint2{pc[i][2], pc[i][3]};
+          // half-piece i, and 8 + i (the piece's other half) 4*NPIX entries on
+          const int q = (i >> 1) * NPIX + (i & 1) * (8 * NPIX + PAD);
+          sB[buf][soff[j] + q] = uint2{pc[i][0], pc[i][1]};
+          sB[buf][soff[j] + q + 4 * NPIX] = uint2{pc[i][2], pc[i][3]};
         }
       }
     }
@@ -201,16 +216,17 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
     const int pr_ = rb * GR + r_in;
     const int pc0 = (wave - rb * Gm::NCP) * 2 + (col & 1);
     const bool pin = r_in < GR && pr_ < TR && pc0 < TC;
-    const int pr = pin ? pr_ : 0;
-    const int pc = pin ? pc0 : 0;
+    // a lane outside the tile reads the pixels of a lane inside it (row rb*GR, its column)
+    const int pr = pin ? pr_ : rb * GR;
+    const int pc = pin ? pc0 : (pc0 < TC ? pc0 : 0);
     const int oh = oh0 + pr, ow = ow0 + pc;
     valid = pin && oh < p.OH && ow < p.OW;
-    bbase = g * NPIX + pr * Gm::HC + pc;  // piece g of halo pixel (pr, pc) = tap (0, 0)
+    bbase = (g >> 1) * NPIX + (g & 1) * (8 * NPIX + PAD) + pr * Gm::HC + pc;  // half-piece g, halo pixel (pr, pc)
     m = valid ? (b * p.OH + oh) * p.OW + ow : 0;
   } else {
     const int pos = wave * 16 + col;
     valid = m0 + pos < p.M;
-    bbase = g * NPIX + pos;
+    bbase = (g >> 1) * NPIX + (g & 1) * (8 * NPIX + PAD) + pos;
     m = valid ? m0 + pos : 0;
   }
 
@@ -218,9 +234,28 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
   // 8-byte reads of a fragment are at compile-time offsets from it.
   const uint32_t lds0 =
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint2*)&sB[set * NBUF][0] + (uint32_t)bbase * 8u;
+  // A operands through buffer resources: the (chunk, tap, group) offset is wave-uniform and
+  // goes in the scalar offset, this lane's byte offset is one fixed VGPR and the tile index
+  // an immediate, so a load costs no vector address arithmetic.
   const size_t wgroup = (size_t)p.nq * 4 * 64;
-  const u32x4_t* wv = p.wvals + (size_t)G0 * wgroup + lane;
-  const uint32_t* wm = p.wmeta + (size_t)G0 * wgroup + lane;
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u32x4_t*>(p.wvals + (size_t)G0 * wgroup), 0, (int)(GPW * wgroup * sizeof(u32x4_t)), kBufferDword3);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(p.wmeta + (size_t)G0 * wgroup), 0, (int)(GPW * wgroup * sizeof(uint32_t)), kBufferDword3);
+  const int lv = lane * (int)sizeof(u32x4_t), lm = lane * 4;
+  auto load_a = [&](int c, int tap, u32x4_t (&av)[GPW][4], uint32_t (&ix)[GPW][4]) {
+    const int q = (tap * p.nchunk + c) * 4 * 64;
+#pragma unroll
+    for (int gg = 0; gg < GPW; ++gg)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int e = gg * (int)wgroup + q;  // entry offset, uniform
+        av[gg][a] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, lv + a * 64 * (int)sizeof(u32x4_t),
+                                                           e * (int)sizeof(u32x4_t), 0));
+        ix[gg][a] = __builtin_amdgcn_raw_buffer_load_b32(rm, lm + a * 64 * 4, e * 4, 0);
+      }
+  };
 
   float4_t acc[GPW][T][4];
 #pragma unroll
@@ -230,26 +265,14 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
 #pragma unroll
       for (int a = 0; a < 4; ++a) acc[gg][t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
 
+  // the first A operands go out before the first staging loads: their latencies overlap
+  u32x4_t av[GPW][4];
+  uint32_t ix[GPW][4];
+  load_a(set, 0, av, ix);
   uint2 stg[UPT];
   load_units(stg, set);
   store_units(set * NBUF, stg);
   __syncthreads();
-
-  // A operands of (chunk c, tap) -> registers
-  auto load_a = [&](int c, int tap, u32x4_t (&av)[GPW][4], uint32_t (&ix)[GPW][4]) {
-    const size_t q = (size_t)(tap * p.nchunk + c) * 4 * 64;
-#pragma unroll
-    for (int gg = 0; gg < GPW; ++gg)
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        av[gg][a] = wv[gg * wgroup + q + a * 64];
-        ix[gg][a] = wm[gg * wgroup + q + a * 64];
-      }
-  };
-
-  u32x4_t av[GPW][4];
-  uint32_t ix[GPW][4];
-  load_a(set, 0, av, ix);
   for (int c = set; c < p.nchunk; c += KSP) {  // host: nchunk % KSP == 0 (sets stay in step)
     const bool more = c + KSP < p.nchunk;
     const int buf = NBUF == 2 ? ((c / KSP) & 1) : 0;
@@ -258,16 +281,17 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
     // and waited for with an explicit lgkmcnt (the loop issues no other LDS operation).
     // Written as asm so the compiler neither fuses them into 16-byte or paired reads nor
     // hoists them further (both measured slower / register-starved).
-    const uint32_t lbase = lds0 + (uint32_t)buf * (uint32_t)(T * 16 * NPIX * 8);  // within this set's buffers
+    const uint32_t lbase = lds0 + (uint32_t)buf * (uint32_t)(BUFE * 8);  // within this set's buffers
     uint2 fr[2][4];
     auto issue = [&](int step, uint2 (&f)[4]) {
       const int tp = step / T, t = step - (step / T) * T;
       const int toff = KS == 3 ? (tp / 3) * Gm::HC + (tp % 3) : 0;
-      const int o = (t * 16 * NPIX + toff) * 8;
+      const int o = (t * TS + toff) * 8;
+      // half-pieces g, 8 + g, 4 + g, 12 + g: +0, +4, +2, +6 NPIX from this lane's base
       asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[0]) : "v"(lbase), "i"(o));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[1]) : "v"(lbase), "i"(o + 8 * NPIX * 8));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[2]) : "v"(lbase), "i"(o + 4 * NPIX * 8));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[3]) : "v"(lbase), "i"(o + 12 * NPIX * 8));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[1]) : "v"(lbase), "i"(o + 4 * NPIX * 8));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[2]) : "v"(lbase), "i"(o + 2 * NPIX * 8));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[3]) : "v"(lbase), "i"(o + 6 * NPIX * 8));
     };
     issue(0, fr[0]);
 #pragma unroll
