@@ -115,7 +115,16 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
     const int fk = env_int_now("SENGINE_AMD_TILE_KSPLIT", 0);
     if (fk == 1 || fk == 2) ksplit = fk;
   }
-  if (k3) return launch_tile3(p, d->T, shape, gpw, ksplit, d->out_enc, mode, stream);
+  // Two-deep operand prefetch where the grid leaves at most two workgroups per CU (two waves
+  // per SIMD: registers to spare, SMFMAC issue waiting on latency).  SENGINE_AMD_TILE_PF=1|2
+  // overrides.
+  int pf = 1;
+  if (k3 && d->T == 4 && gpw == 1) {
+    pf = (int64_t)p.ntiles * (d->C_out / 64) <= 512 ? 2 : 1;
+    const int fp = env_int_now("SENGINE_AMD_TILE_PF", 0);
+    if (fp == 1 || fp == 2) pf = fp;
+  }
+  if (k3) return launch_tile3(p, d->T, shape, gpw, ksplit, pf, d->out_enc, mode, stream);
   return launch_tile1(p, d->T, gpw, d->out_enc, mode, stream);
 }
 

@@ -4,7 +4,9 @@
 namespace sengine {
 
 // shape: 0 = 8x8 tiles (8-row blocks), 1 = 14x4 (8-row blocks), 2 = 7x7 (7-row blocks).
-hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int ksplit, int oe, int mode,
+// pf: prefetch depth (1, or 2 for grids of at most two workgroups per CU; T = 4, one
+// channel group per wave).
+hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int ksplit, int pf, int oe, int mode,
                         hipStream_t s) {
   switch (T) {
     case 1:
@@ -14,14 +16,23 @@ hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int kspl
     case 4:
       if (ksplit == 2) {
         if (shape == 1) return launch_tile<4, 3, 14, 4, 8, 1, 2>(p, oe, mode, s);
-        if (shape == 2) return launch_tile<4, 3, 7, 7, 7, 1, 2>(p, oe, mode, s);
+        if (shape == 2)
+          return pf == 2 ? launch_tile<4, 3, 7, 7, 7, 1, 2, 2>(p, oe, mode, s)
+                         : launch_tile<4, 3, 7, 7, 7, 1, 2>(p, oe, mode, s);
         return launch_tile<4, 3, 8, 8, 8, 1, 2>(p, oe, mode, s);
       }
-      if (shape == 1)
-        return gpw == 2 ? launch_tile<4, 3, 14, 4, 8, 2>(p, oe, mode, s) : launch_tile<4, 3, 14, 4, 8, 1>(p, oe, mode, s);
-      if (shape == 2)
-        return gpw == 2 ? launch_tile<4, 3, 7, 7, 7, 2>(p, oe, mode, s) : launch_tile<4, 3, 7, 7, 7, 1>(p, oe, mode, s);
-      return gpw == 2 ? launch_tile<4, 3, 8, 8, 8, 2>(p, oe, mode, s) : launch_tile<4, 3, 8, 8, 8, 1>(p, oe, mode, s);
+      if (shape == 1) {
+        if (gpw == 2) return launch_tile<4, 3, 14, 4, 8, 2>(p, oe, mode, s);
+        return pf == 2 ? launch_tile<4, 3, 14, 4, 8, 1, 1, 2>(p, oe, mode, s)
+                       : launch_tile<4, 3, 14, 4, 8, 1>(p, oe, mode, s);
+      }
+      if (shape == 2) {
+        if (gpw == 2) return launch_tile<4, 3, 7, 7, 7, 2>(p, oe, mode, s);
+        return pf == 2 ? launch_tile<4, 3, 7, 7, 7, 1, 1, 2>(p, oe, mode, s)
+                       : launch_tile<4, 3, 7, 7, 7, 1>(p, oe, mode, s);
+      }
+      if (gpw == 2) return launch_tile<4, 3, 8, 8, 8, 2>(p, oe, mode, s);
+      return pf == 2 ? launch_tile<4, 3, 8, 8, 8, 1, 1, 2>(p, oe, mode, s) : launch_tile<4, 3, 8, 8, 8, 1>(p, oe, mode, s);
     default:
       return hipErrorInvalidValue;
   }

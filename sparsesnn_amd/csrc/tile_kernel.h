@@ -106,10 +106,18 @@ __device__ __forceinline__ void expand_word64(uint2 w, u32x4_t (&pc)[8]) {
 // positions and channels over the odd reduction chunks (its own LDS buffer), and its
 // accumulators are added to the first set's in LDS, in a fixed order, before the
 // epilogue.  Twice the waves per tile for layers whose grid leaves SIMDs with one wave.
-template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP>
+//
+// PF = 2 (3x3 only) prefetches A operands two taps and B fragments two (tap, t) steps
+// ahead instead of one: for grids of at most two workgroups per CU, whose waves (two per
+// SIMD) have the registers for it and whose SMFMAC issue otherwise waits on L2 and LDS
+// latency.
+template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP, int PF = 1>
 __global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR * KSP))
-__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
+__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 ? 3 : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
   using Gm = TileGeom<KS, TR, TC, GR>;
+  static_assert(PF == 1 || (PF == 2 && KS == 3), "two-deep prefetch needs the unrolled 9-tap loop");
+  constexpr int NA = PF + 1;  // A operand sets in flight (ring over taps; 9 % 3 == 0)
+  constexpr int NB = PF + 1;  // B fragment sets in flight (ring over (tap, t) steps)
   constexpr int NPIX = Gm::NPIX;
   constexpr int NTHR = Gm::NTHR;  // threads of one set
   constexpr int NTAP = Gm::NTAP;
@@ -266,9 +274,10 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
       for (int a = 0; a < 4; ++a) acc[gg][t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   // the first A operands go out before the first staging loads: their latencies overlap
-  u32x4_t av[GPW][4];
-  uint32_t ix[GPW][4];
-  load_a(set, 0, av, ix);
+  u32x4_t av[NA][GPW][4];
+  uint32_t ix[NA][GPW][4];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) load_a(set, i, av[i], ix[i]);
   uint2 stg[UPT];
   load_units(stg, set);
   store_units(set * NBUF, stg);
@@ -277,12 +286,13 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
     const bool more = c + KSP < p.nchunk;
     const int buf = NBUF == 2 ? ((c / KSP) & 1) : 0;
     if (more) load_units(stg, c + KSP);
-    // B fragments: four ds_read_b64 per (tap, t), issued one step ahead of their SMFMACs
+    // B fragments: four ds_read_b64 per (tap, t), issued PF steps ahead of their SMFMACs
     // and waited for with an explicit lgkmcnt (the loop issues no other LDS operation).
     // Written as asm so the compiler neither fuses them into 16-byte or paired reads nor
     // hoists them further (both measured slower / register-starved).
     const uint32_t lbase = lds0 + (uint32_t)buf * (uint32_t)(BUFE * 8);  // within this set's buffers
-    uint2 fr[2][4];
+    constexpr int NSTEP = NTAP * T;
+    uint2 fr[NB][4];
     auto issue = [&](int step, uint2 (&f)[4]) {
       const int tp = step / T, t = step - (step / T) * T;
       const int toff = KS == 3 ? (tp / 3) * Gm::HC + (tp % 3) : 0;
@@ -293,21 +303,28 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
       asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[2]) : "v"(lbase), "i"(o + 2 * NPIX * 8));
       asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(f[3]) : "v"(lbase), "i"(o + 6 * NPIX * 8));
     };
-    issue(0, fr[0]);
+#pragma unroll
+    for (int i = 0; i < PF; ++i) issue(i, fr[i]);
 #pragma unroll
     for (int tap = 0; tap < NTAP; ++tap) {
-      u32x4_t avn[GPW][4];
-      uint32_t ixn[GPW][4];
-      if (tap + 1 < NTAP) load_a(c, tap + 1, avn, ixn);
-      else if (more) load_a(c + KSP, 0, avn, ixn);
+      // A operands PF taps ahead (crossing into the next chunk: they do not depend on LDS)
+      const int ra = PF == 1 ? 0 : tap % NA;            // ring slot in use (PF = 2)
+      const int rn = PF == 1 ? 1 : (tap + PF) % NA;     // ring slot being filled
+      if (tap + PF < NTAP) load_a(c, tap + PF, av[rn], ix[rn]);
+      else if (more) load_a(c + KSP, tap + PF - NTAP, av[rn], ix[rn]);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int step = tap * T + t;
-        uint2(&f)[4] = fr[step & 1];
+        uint2(&f)[4] = fr[step % NB];
         // The wait names the fragment registers as operands, so every use of them is
         // ordered after it.
-        if (step + 1 < NTAP * T) {
-          issue(step + 1, fr[(step + 1) & 1]);
+        if (step + PF < NSTEP) {
+          issue(step + PF, fr[(step + PF) % NB]);
+          if (PF == 2)
+            asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) :: "memory");
+          else
+            asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) :: "memory");
+        } else if (PF == 2 && step + 1 < NSTEP) {
           asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) :: "memory");
         } else {
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) :: "memory");
@@ -318,16 +335,16 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 ? 3 : (GPW == 2 && KS ==
         for (int gg = 0; gg < GPW; ++gg)
 #pragma unroll
           for (int a = 0; a < 4; ++a)
-            acc[gg][t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(half8_t, av[gg][a]), bf,
-                                                                     acc[gg][t][a], (int)ix[gg][a], 0, 0);
+            acc[gg][t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(half8_t, av[ra][gg][a]), bf,
+                                                                     acc[gg][t][a], (int)ix[ra][gg][a], 0, 0);
       }
-      if (tap + 1 < NTAP || more) {
+      if (PF == 1 && (tap + 1 < NTAP || more)) {
 #pragma unroll
         for (int gg = 0; gg < GPW; ++gg)
 #pragma unroll
           for (int a = 0; a < 4; ++a) {
-            av[gg][a] = avn[gg][a];
-            ix[gg][a] = ixn[gg][a];
+            av[0][gg][a] = av[1][gg][a];
+            ix[0][gg][a] = ix[1][gg][a];
           }
       }
     }
@@ -374,22 +391,22 @@ struct TileShape {
   int KS, TR, TC, GR;
 };
 
-template <int T, int KS, int TR, int TC, int GR, int GPW, int KSP = 1>
+template <int T, int KS, int TR, int TC, int GR, int GPW, int KSP = 1, int PF = 1>
 hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s) {
   constexpr int NTHR = TileGeom<KS, TR, TC, GR>::NTHR * KSP;
   const dim3 grid((unsigned)(p.ntiles * (p.F / (64 * GPW))));
   if (out_enc == SENGINE_ENC_BITS) {
     if (mode == EPI_LIF_HARD)
-      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_LIF_HARD, KSP>), grid,
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_LIF_HARD, KSP, PF>), grid,
                          dim3(NTHR), 0, s, p);
     else if (mode == EPI_IF_HARD)
-      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_IF_HARD, KSP>), grid,
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_IF_HARD, KSP, PF>), grid,
                          dim3(NTHR), 0, s, p);
     else
-      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_GENERIC, KSP>), grid,
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_GENERIC, KSP, PF>), grid,
                          dim3(NTHR), 0, s, p);
   } else {
-    hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16, EPI_GENERIC, KSP>), grid,
+    hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16, EPI_GENERIC, KSP, PF>), grid,
                        dim3(NTHR), 0, s, p);
   }
   return hipGetLastError();
@@ -397,7 +414,7 @@ hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s
 
 // Launchers compiled in fused_tile3.hip (KS = 3) and fused_tile1.hip (KS = 1).  ksplit: 1
 // or 2 (3x3, T = 4, one channel group per wave, nchunk even).
-hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int ksplit, int out_enc, int mode,
+hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int ksplit, int pf, int out_enc, int mode,
                         hipStream_t s);
 hipError_t launch_tile1(const TileParams& p, int T, int gpw, int out_enc, int mode, hipStream_t s);
 

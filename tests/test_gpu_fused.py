@@ -221,6 +221,37 @@ def test_tile_reduction_split(dev, ksplit, shape, H, W, C_in, C_out, B):
         del os.environ["SENGINE_AMD_TILE_SHAPE"]
 
 
+@pytest.mark.parametrize("pf", ["1", "2"])
+@pytest.mark.parametrize("ksplit,shape", [("1", "0"), ("1", "1"), ("1", "2"), ("2", "2")])
+@pytest.mark.parametrize("H,W,C_in,C_out,B", [(7, 7, 256, 128, 3), (13, 11, 192, 64, 2), (14, 14, 128, 128, 1)])
+def test_tile_prefetch_depth(dev, pf, ksplit, shape, H, W, C_in, C_out, B):
+    """3x3 halo tiles with one- and two-deep operand prefetch (SENGINE_AMD_TILE_PF): A operands
+    fetched across the 64-channel chunk boundary, B fragments two steps ahead; odd and even
+    chunk counts, ragged tiles, LIF fast epilogue and IF with state, against the oracle."""
+    import os
+    if ksplit == "2" and (C_in // 64) % 2:
+        pytest.skip("the reduction split needs an even number of 64-channel chunks")
+    os.environ["SENGINE_AMD_TILE_PF"] = pf
+    os.environ["SENGINE_AMD_TILE_KSPLIT"] = ksplit
+    os.environ["SENGINE_AMD_TILE_SHAPE"] = shape
+    ops.set_fused_kernel("tile")  # small test shapes would otherwise take the small-M kernel
+    try:
+        case = ref.make_layer_case(130 + H + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
+                                   fp16_weights=True, p_spike=0.2)
+        rep, x_err, _, _ = run_case(dev, case)
+        assert rep.ok, str(rep)
+        assert x_err < 1e-4
+        g = torch.Generator().manual_seed(4)
+        v0 = torch.rand((B, C_out, H, W), generator=g) * 0.4
+        rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0)
+        assert rep2.ok, str(rep2)
+        assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
+    finally:
+        ops.set_fused_kernel("auto")
+        for k in ("SENGINE_AMD_TILE_PF", "SENGINE_AMD_TILE_KSPLIT", "SENGINE_AMD_TILE_SHAPE"):
+            del os.environ[k]
+
+
 # ---- flat small-output layout: <= 16 output pixels per image run as one GEMM per image
 # flat: (2,2,3,1,1) (3,3,3,2,1) (2,3,3,1,1) (2,2,3,2,1) (1,2,1,2,0) (3,2,3,2,1); the rest
 # have small outputs on inputs over 2x the kernel window or whose flat matrix would hold over
