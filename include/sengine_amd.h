@@ -187,6 +187,21 @@ int sengine_amd_fused_sparse_conv_bn_add_neuron(const sengine_conv_lif_desc* d, 
                                                 float* real_out, void* spikes, hipStream_t stream);
 
 /*
+ * Real-valued shortcut of an MS-ResNet block (BasicBlock18.shortcut: TDBNContainer(Conv2d
+ * 1x1 / stride s, BatchNorm3d), models/msresnet.py:113-118, applied at :111 to the block's
+ * real-valued input, not to spikes): out = conv1x1(x) * bn_scale + bn_bias in fp32.
+ * x: fp32 NHWC (in_T*B, H, W, C_in); out: fp32 NHWC (T*B, OH, OW, C_out).  in_T = 1 takes
+ * one timestep of input (the stem output, which the reference repeats over T before the
+ * first block, :146-150) and stores each output value T times; in_T = d->T maps timestep
+ * to timestep.  weight: OIHW (C_out, C_in, 1, 1) or HWIO (1, 1, C_in, C_out) fp32 (dense:
+ * a 2:4-pruned weight runs with its zeros).  Needs KH = KW = 1, pad 0, equal strides,
+ * C_in % 16 == 0, C_out % 64 == 0.
+ */
+int sengine_amd_real_conv_bn(const sengine_conv_lif_desc* d, const float* x, int32_t in_T, const float* weight,
+                             int32_t w_layout, const float* bn_scale, const float* bn_bias, float* out,
+                             hipStream_t stream);
+
+/*
  * Spiking self-attention (Spikformer SSA, models/spikformer.py:103-130): for every (t, b,
  * head) x = (Q K^T * scale) V on binary spikes, then the neuron over T (the reference's
  * attn_lif: LIF tau 2, V_th 0.5).  Every product and partial sum is an integer times

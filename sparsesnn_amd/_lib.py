@@ -53,6 +53,7 @@ SIGNATURES = {
                                                                 _P]),
     "sengine_amd_stem_conv_bn": (ctypes.c_int, [_DP, _P, _P, _I32, _P, _P, _P, _P]),
     "sengine_amd_fused_sparse_conv_bn_add_neuron": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "sengine_amd_real_conv_bn": (ctypes.c_int, [_DP, _P, _I32, _P, _I32, _P, _P, _P, _P]),
     "sengine_amd_ssa_kv": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
     "sengine_amd_ssa_attend_neuron": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _F, _I32, _I32, _F, _F, _F,
                                                      _P, _P, _P, _P]),

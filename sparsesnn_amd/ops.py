@@ -348,6 +348,33 @@ def fused_sparse_conv_bn_add_neuron(s: ConvSpec, data: torch.Tensor, values: tor
     return real_out, out
 
 
+def real_conv_bn(s: ConvSpec, x: torch.Tensor, weight: torch.Tensor, bn_scale: torch.Tensor, bn_bias: torch.Tensor,
+                 in_T: Optional[int] = None, out: Optional[torch.Tensor] = None,
+                 layout: int = WLAYOUT_OIHW) -> torch.Tensor:
+    """MS-ResNet shortcut: fp32 1x1 conv (stride s.stride) + folded BN on the real-valued
+    NHWC input x (in_T*s.B, H, W, C_in) -> fp32 NHWC (s.T*s.B, OH, OW, C_out).  in_T = 1
+    (one timestep of input, e.g. the stem output) stores every output value s.T times;
+    default in_T = s.T.  weight: OIHW (C_out, C_in, 1, 1) or HWIO (1, 1, C_in, C_out)."""
+    lib = _lib.load()
+    in_T = s.T if in_T is None else in_T
+    for t, n in ((x, "x"), (weight, "weight"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    _require_numel(x, in_T * s.B * s.H * s.W * s.C_in, torch.float32, "x")
+    _require_numel(weight, s.C_out * s.C_in, torch.float32, "weight")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    OH, OW = (s.H - 1) // s.stride + 1, (s.W - 1) // s.stride + 1
+    if out is None:
+        out = torch.empty(s.T * s.B, OH, OW, s.C_out, dtype=torch.float32, device=x.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, s.T * s.B * OH * OW * s.C_out, torch.float32, "out")
+    d = make_desc(s)
+    check(lib.sengine_amd_real_conv_bn(ctypes.byref(d), _ptr(x), int(in_T), _ptr(weight), int(layout),
+                                       _ptr(bn_scale), _ptr(bn_bias), _ptr(out), _stream(x.device)), "real_conv_bn")
+    return out
+
+
 def spiking_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, T: int, B: int, N: int, C: int,
                            heads: int, scale: float = 0.125, neuron: str = "lif", tau: float = 2.0,
                            v_threshold: float = 0.5, v_reset: Optional[float] = 0.0,
