@@ -264,8 +264,10 @@ int sengine_amd_maxpool_spikes(int32_t NT, int32_t H, int32_t W, int32_t C, int3
 
 /*
  * Head: AdaptiveAvgPool2d(1) per timestep, mean over T, Linear (models/sewresnet.py:152-153,
- * 208-210).  in: integer activations as `planes` bit planes, (T*B, HW) positions x planes*C
- * bits; fc_weight (N_out, C) fp32 (nn.Linear layout), fc_bias (N_out); out (B, N_out) fp32.
+ * 208-210; the same values as MS-ResNet's mean over T then pool, models/msresnet.py:155-160).
+ * in: integer activations as `planes` bit planes, (T*B, HW) positions x planes*C bits;
+ * fc_weight (N_out, C) fp32 (nn.Linear layout), fc_bias (N_out); out (B, N_out) fp32.
+ * C % 32 == 0, 1 <= planes <= 3, planes * C <= 8192.
  */
 int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t planes, const uint32_t* in,
                          const float* fc_weight, const float* fc_bias, int32_t N_out, float* out,

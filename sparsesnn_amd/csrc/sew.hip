@@ -271,12 +271,16 @@ __global__ __launch_bounds__(256) void maxpool_bits_kernel(PoolParams p) {
 }
 
 // ---- head: global average pool per timestep, mean over T, Linear ------------------------
-// (models/sewresnet.py:208-210).  in: integer activations as `planes` bit planes, NHWC with
-// planes*C channels, (T*B, HW) positions.  Workgroup (image, group of HEAD_OPW*4 outputs):
-// the pooled features are exact integer sums scaled once into LDS; each wave then owns
-// HEAD_OPW outputs, its lanes split the reduction over C (coalesced reads of the Linear
-// weight rows) and a cross-lane sum finishes each output.
-constexpr int HEAD_OPW = 4;  // outputs per wave
+// (models/sewresnet.py:208-210; models/msresnet.py:155-160).  in: integer activations as
+// `planes` bit planes, NHWC with planes*C channels, (T*B, HW) positions.  Workgroup (image,
+// slice of the outputs): the per-channel sums are exact integers, counted once per
+// workgroup -- thread (word column wi, position slice) walks its slice of the T*HW positions
+// with coalesced word reads and keeps 32 bit counters in registers, then adds them into LDS
+// -- and scaled once into fp32 features; each wave then owns HEAD_OPW outputs at a time
+// (looping over the workgroup's slice of the outputs), its lanes split the reduction over C
+// (coalesced reads of the Linear weight rows) and a cross-lane sum finishes each output.
+constexpr int HEAD_OPW = 4;        // outputs per wave and pass
+constexpr int HEAD_MAX_PC = 8192;  // planes * C held as integer counters in LDS
 struct HeadParams {
   const uint32_t* in;
   const float* w;  // (N_out, C) fp32, nn.Linear layout
@@ -292,51 +296,64 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 __global__ __launch_bounds__(256) void sew_head_kernel(HeadParams p) {
-  extern __shared__ float feat[];  // C
+  __shared__ int cnt[HEAD_MAX_PC];
+  __shared__ float feat[HEAD_MAX_PC];
   const int bimg = blockIdx.x;
   const int words = p.planes * p.C / 32;
-  const int nsrc = p.T * p.HW * p.planes;  // (t, s, plane) words holding one channel's bits
+  const int npos = p.T * p.HW;  // (t, s) positions of this image
+  for (int i = threadIdx.x; i < p.planes * p.C; i += blockDim.x) cnt[i] = 0;
+  __syncthreads();
+  const int per = words < (int)blockDim.x ? words : (int)blockDim.x;  // word columns per pass
+  const int nslice = (int)blockDim.x / per;
+  const int slice = (int)threadIdx.x / per;
+  for (int wbase = 0; wbase < words; wbase += per) {
+    const int wi = wbase + (int)threadIdx.x % per;
+    if (slice >= nslice || wi >= words) continue;
+    uint32_t c32[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) c32[j] = 0;
+    for (int q = slice; q < npos; q += nslice) {
+      const int t = q / p.HW;
+      const uint32_t w = p.in[((int64_t)(t * p.B + bimg) * p.HW + (q - t * p.HW)) * words + wi];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) c32[j] += (w >> j) & 1u;
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      if (c32[j]) atomicAdd(&cnt[wi * 32 + j], (int)c32[j]);
+  }
+  __syncthreads();
+  // channel c of plane pl is bit (pl*C + c) of a position's words
   for (int c = threadIdx.x; c < p.C; c += blockDim.x) {
     int sum = 0;
-    // groups of 8 words loaded before any is used (the loop's loads are independent)
-    for (int i0 = 0; i0 < nsrc; i0 += 8) {
-      uint32_t wv[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = min(i0 + u, nsrc - 1);
-        const int pl = i % p.planes;
-        const int ts = i / p.planes;  // t * HW + s
-        const int t = ts / p.HW;
-        wv[u] = p.in[((int64_t)(t * p.B + bimg) * p.HW + (ts - t * p.HW)) * words + ((pl * p.C + c) >> 5)];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (i0 + u < nsrc) sum += (int)((wv[u] >> (c & 31)) & 1u) << ((i0 + u) % p.planes);
-    }
-    // mean over HW then over T, as the reference: both are exact for the integer sums here
+    for (int pl = 0; pl < p.planes; ++pl) sum += cnt[pl * p.C + c] << pl;
+    // mean over HW then over T: both exact or one rounding for the integer sums here
     feat[c] = ((float)sum / (float)p.HW) / (float)p.T;
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  const int o0 = (blockIdx.y * 4 + (threadIdx.x >> 6)) * HEAD_OPW;
-  float acc[HEAD_OPW];
-  const float* wrow[HEAD_OPW];
+  const int nwave_out = (int)(blockDim.x >> 6) * HEAD_OPW;  // outputs per pass of the workgroup
+  for (int base = blockIdx.y * nwave_out; base < p.N_out; base += gridDim.y * nwave_out) {
+    const int o0 = base + (int)(threadIdx.x >> 6) * HEAD_OPW;
+    float acc[HEAD_OPW];
+    const float* wrow[HEAD_OPW];
 #pragma unroll
-  for (int j = 0; j < HEAD_OPW; ++j) {
-    acc[j] = 0.f;
-    wrow[j] = p.w + (int64_t)min(o0 + j, p.N_out - 1) * p.C;  // rows past N_out: computed, not stored
-  }
-  // branch-free body, so the unrolled iterations' loads are all in flight together
+    for (int j = 0; j < HEAD_OPW; ++j) {
+      acc[j] = 0.f;
+      wrow[j] = p.w + (int64_t)min(o0 + j, p.N_out - 1) * p.C;  // rows past N_out: computed, not stored
+    }
+    // branch-free body, so the unrolled iterations' loads are all in flight together
 #pragma unroll 8
-  for (int c = lane; c < p.C; c += 64) {
-    const float f = feat[c];
+    for (int c = lane; c < p.C; c += 64) {
+      const float f = feat[c];
 #pragma unroll
-    for (int j = 0; j < HEAD_OPW; ++j) acc[j] = __builtin_fmaf(f, wrow[j][c], acc[j]);
-  }
+      for (int j = 0; j < HEAD_OPW; ++j) acc[j] = __builtin_fmaf(f, wrow[j][c], acc[j]);
+    }
 #pragma unroll
-  for (int j = 0; j < HEAD_OPW; ++j) {
-    const float v = wave_sum(acc[j]);
-    if (lane == 0 && o0 + j < p.N_out) p.out[(int64_t)bimg * p.N_out + o0 + j] = v + p.b[o0 + j];
+    for (int j = 0; j < HEAD_OPW; ++j) {
+      const float v = wave_sum(acc[j]);
+      if (lane == 0 && o0 + j < p.N_out) p.out[(int64_t)bimg * p.N_out + o0 + j] = v + p.b[o0 + j];
+    }
   }
 }
 
@@ -448,10 +465,13 @@ extern "C" int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C,
                                     const uint32_t* in, const float* fc_weight, const float* fc_bias, int32_t N_out,
                                     float* out, hipStream_t stream) {
   if (!in || !fc_weight || !fc_bias || !out) return set_error(-1, "sew_head: null pointer");
-  if (T < 1 || B < 1 || HW < 1 || C < 32 || C % 32 != 0 || planes < 1 || planes > 3 || N_out < 1 || C > 8192)
-    return set_error(-2, "sew_head: invalid shape (C % 32 == 0, C <= 8192, 1 <= planes <= 3)");
+  if (T < 1 || B < 1 || HW < 1 || C < 32 || C % 32 != 0 || planes < 1 || planes > 3 || N_out < 1 ||
+      (int64_t)planes * C > HEAD_MAX_PC)
+    return set_error(-2, "sew_head: invalid shape (C % 32 == 0, 1 <= planes <= 3, planes * C <= 8192)");
   HeadParams p{in, fc_weight, fc_bias, out, T, B, HW, C, planes, N_out};
-  const unsigned ogroups = (unsigned)((N_out + 4 * HEAD_OPW - 1) / (4 * HEAD_OPW));
-  hipLaunchKernelGGL(sew_head_kernel, dim3((unsigned)B, ogroups), dim3(256), (size_t)C * sizeof(float), stream, p);
+  // a few output slices per image, so that about 512 workgroups share the chip
+  const int passes = (N_out + 4 * HEAD_OPW - 1) / (4 * HEAD_OPW);
+  const int slices = std::max(1, std::min(passes, (512 + B - 1) / B));
+  hipLaunchKernelGGL(sew_head_kernel, dim3((unsigned)B, (unsigned)slices), dim3(256), 0, stream, p);
   return (int)hipGetLastError();
 }

@@ -99,7 +99,8 @@ def test_maxpool_spikes(dev, H, W, C):
     assert np.array_equal(got, exp.view(2, 3, C, OH, OW).numpy())
 
 
-@pytest.mark.parametrize("planes,HW,C,N_out", [(2, 1, 64, 10), (1, 4, 64, 10), (3, 2, 96, 37), (2, 1, 512, 100)])
+@pytest.mark.parametrize("planes,HW,C,N_out", [(2, 1, 64, 10), (1, 4, 64, 10), (3, 2, 96, 37), (2, 1, 512, 100),
+                                              (1, 49, 512, 1000), (3, 9, 2720, 7), (1, 3, 8192, 65)])
 def test_sew_head(dev, planes, HW, C, N_out):
     rng = np.random.default_rng(planes)
     T, B = 4, 3
