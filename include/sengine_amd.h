@@ -161,8 +161,9 @@ int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const v
  * Integer-valued activations are stored as bit planes interleaved per position: a tensor
  * with P planes is an NHWC spike-bit tensor with P*C channels, channel p*C + c holding bit p
  * of channel c's value.  residual: (T*B, OH, OW) positions x residual_planes*C_out bits;
- * out: out_planes*C_out bits per position; 1 <= residual_planes <= out_planes <= 3 and the
- * caller chooses out_planes so that spike + residual fits (SEW-ResNet-18: 2 planes).
+ * out: out_planes*C_out bits per position; 1 <= residual_planes <= out_planes <= 5 and the
+ * caller chooses out_planes so that spike + residual fits (SEW-ResNet-18: up to 3 planes;
+ * Spikformer's residual stream: up to 5).
  * A conv whose input is such a P-plane tensor is an ordinary spike-bit conv with C_in =
  * P*C and weights [W, 2W, 4W, ...] along the input channels (sparsesnn_amd.sparsity).
  * Requires out_enc = BITS; state may be NULL; no traces.
@@ -267,7 +268,7 @@ int sengine_amd_maxpool_spikes(int32_t NT, int32_t H, int32_t W, int32_t C, int3
  * 208-210; the same values as MS-ResNet's mean over T then pool, models/msresnet.py:155-160).
  * in: integer activations as `planes` bit planes, (T*B, HW) positions x planes*C bits;
  * fc_weight (N_out, C) fp32 (nn.Linear layout), fc_bias (N_out); out (B, N_out) fp32.
- * C % 32 == 0, 1 <= planes <= 3, planes * C <= 8192.
+ * C % 32 == 0, 1 <= planes <= 5, planes * C <= 8192.
  */
 int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t planes, const uint32_t* in,
                          const float* fc_weight, const float* fc_bias, int32_t N_out, float* out,

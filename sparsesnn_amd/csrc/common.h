@@ -84,6 +84,8 @@ struct NeuronParams {
   float vth, vreset;
 };
 
+constexpr int kMaxPlanes = 5;  // bit planes of an integer activation: values up to 31 (Spikformer's residual stream)
+
 // SEW 'ADD' connection fused into a fused layer's output (models/sewresnet.py:58-59; the
 // reference's conv2d_bn_if_add_t4_kernel, sengine/kernels/conv2d_bn_if_t4.py:813-911):
 // out = spike + residual, integer-valued.  Integer activations are stored as bit planes

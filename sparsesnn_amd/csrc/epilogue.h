@@ -54,9 +54,12 @@ struct EpiCoeffs {
 // stores by themselves, so loading them inside the loop costs one memory latency per t.
 // Channel cob of a row is channel c of output pixel `pix` (one pixel per row unless the
 // layer runs in the flat small-output layout); the planes of a pixel sit together.
+constexpr int kResWords = (kMaxPlanes + 1) / 2;  // two 16-bit plane words per register
+
+// r[t][k]: plane 2k in the low and plane 2k + 1 in the high 16 bits.
 template <int T>
 struct SewRes {
-  uint32_t r[T][3];
+  uint32_t r[T][kResWords];
 };
 
 template <int T>
@@ -70,17 +73,19 @@ __device__ __forceinline__ void load_sew_res(const SewAdd& sa, int M, int m, int
     const size_t rbase =
         ((size_t)t * M + m) * sa.res_planes * F + (size_t)pix * sa.res_planes * sa.pix_ch + c;
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
-      o.r[t][pl] = (valid && pl < sa.res_planes)
-                       ? *reinterpret_cast<const uint16_t*>(sa.res + ((rbase + (size_t)pl * sa.pix_ch) >> 3))
-                       : 0u;
+    for (int k = 0; k < kResWords; ++k) o.r[t][k] = 0u;
+#pragma unroll
+    for (int pl = 0; pl < kMaxPlanes; ++pl)
+      if (valid && pl < sa.res_planes)
+        o.r[t][pl >> 1] |= (uint32_t)*reinterpret_cast<const uint16_t*>(sa.res + ((rbase + (size_t)pl * sa.pix_ch) >> 3))
+                           << (16 * (pl & 1));
   }
 }
 
 // Store the 16 spike bits of (position row_pos = t*M + m, channels cob..cob+15), plus the
-// residual r (its planes) when the SEW add is fused.
+// residual r (its planes, packed as in SewRes) when the SEW add is fused.
 __device__ __forceinline__ void store_spike_word(uint32_t word, size_t row_pos, int F, int cob, uint8_t* out,
-                                                 const SewAdd& sa, const uint32_t (&r)[3]) {
+                                                 const SewAdd& sa, const uint32_t (&r)[kResWords]) {
   if (sa.res == nullptr) {
     *reinterpret_cast<uint16_t*>(out + ((row_pos * F + cob) >> 3)) = (uint16_t)word;
     return;
@@ -90,10 +95,11 @@ __device__ __forceinline__ void store_spike_word(uint32_t word, size_t row_pos, 
   const size_t obase = row_pos * (size_t)sa.out_planes * F + (size_t)pix * sa.out_planes * sa.pix_ch + c;
   uint32_t carry = word;
 #pragma unroll
-  for (int pl = 0; pl < 3; ++pl) {
+  for (int pl = 0; pl < kMaxPlanes; ++pl) {
     if (pl >= sa.out_planes) break;
-    *reinterpret_cast<uint16_t*>(out + ((obase + (size_t)pl * sa.pix_ch) >> 3)) = (uint16_t)(r[pl] ^ carry);
-    carry &= r[pl];
+    const uint32_t rp = (r[pl >> 1] >> (16 * (pl & 1))) & 0xffffu;
+    *reinterpret_cast<uint16_t*>(out + ((obase + (size_t)pl * sa.pix_ch) >> 3)) = (uint16_t)(rp ^ carry);
+    carry &= rp;
   }
 }
 

@@ -465,9 +465,9 @@ extern "C" int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C,
                                     const uint32_t* in, const float* fc_weight, const float* fc_bias, int32_t N_out,
                                     float* out, hipStream_t stream) {
   if (!in || !fc_weight || !fc_bias || !out) return set_error(-1, "sew_head: null pointer");
-  if (T < 1 || B < 1 || HW < 1 || C < 32 || C % 32 != 0 || planes < 1 || planes > 3 || N_out < 1 ||
+  if (T < 1 || B < 1 || HW < 1 || C < 32 || C % 32 != 0 || planes < 1 || planes > kMaxPlanes || N_out < 1 ||
       (int64_t)planes * C > HEAD_MAX_PC)
-    return set_error(-2, "sew_head: invalid shape (C % 32 == 0, 1 <= planes <= 3, planes * C <= 8192)");
+    return set_error(-2, "sew_head: invalid shape (C % 32 == 0, 1 <= planes <= 5, planes * C <= 8192)");
   HeadParams p{in, fc_weight, fc_bias, out, T, B, HW, C, planes, N_out};
   // a few output slices per image, so that about 512 workgroups share the chip
   const int passes = (N_out + 4 * HEAD_OPW - 1) / (4 * HEAD_OPW);

@@ -1,0 +1,273 @@
+"""Spikformer inference on the fused kernels, replayed as one hipGraph.
+
+The reference model is models/spikformer.py: SPS patch splitting (:153-209), Blocks of
+spiking self-attention and MLP with residual adds (:59-150), mean over tokens and T and a
+Linear head (:273-288).  SpikformerEngine maps it onto this library:
+
+* SPS: the first conv (C_in = 3, dense) runs once on the B images (the reference repeats the
+  image over T before it, :283-285, so the T copies are equal) through
+  sengine_amd_stem_conv_bn, its LIF over the repeated output through
+  sengine_amd_multistep_neuron_repeat; the other four convs are fused 2:4 Conv+BN+LIF
+  launches on spike bits, with spike max-pools after the third and fourth, and the
+  relative-position conv's spikes added to the max-pooled features in its epilogue (an
+  integer activation of 2 bit planes).  Channel counts that are not multiples of 64
+  (embed/8 = 48, embed/4 = 96 for embed 384) are padded with zero weights and a zero BN
+  affine: the padded channels never fire (V_th > 0) and multiply zero weights downstream;
+* blocks: the token stream x (T*B, N tokens, embed) is integer-valued (the residual adds of
+  spikes, :148-149) and stored as bit planes; q, k, v (Linear + BN1d + LIF, :103-125) are
+  fused 1x1 convs over the token grid with plane-expanded weights and the Linear bias
+  folded into the BN affine; SSA runs as the two-kernel Q (K^T V) path with the attention
+  LIF (V_th 0.5); proj and MLP fc2 add their spikes to the stream in their epilogues;
+* head: mean over tokens and T of the integer stream and the Linear (sengine_amd_sew_head).
+
+Every buffer is allocated once; the launch sequence is captured into one hipGraph.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+from .ops import ConvSpec, SEngineError
+from .sparsity import expand_planes, fold_batchnorm, validate_2_4_pattern
+
+ATTN_VTH = 0.5  # attn_lif threshold, models/spikformer.py:96
+
+
+def _pad64(c: int) -> int:
+    return (c + 63) // 64 * 64
+
+
+def _planes(max_value: int) -> int:
+    return max(1, int(max_value).bit_length())
+
+
+@dataclass
+class Fused:
+    spec: ConvSpec
+    values: torch.Tensor
+    meta: torch.Tensor
+    scale: torch.Tensor
+    bias: torch.Tensor
+
+
+@dataclass
+class SBlock:
+    name: str
+    planes_in: int
+    planes_mid: int
+    planes_out: int
+    q: Fused
+    k: Fused
+    v: Fused
+    proj: Fused
+    fc1: Fused
+    fc2: Fused
+    bufs: dict
+
+
+class SpikformerEngine:
+    """Static-shape Spikformer forward for `batch` images of in_hw pixels (embed channels,
+    `heads` heads, `depth` blocks, MLP ratio `mlp_ratio`)."""
+
+    def __init__(self, params: dict, batch: int, T: int = 4, embed: int = 384, heads: int = 8, depth: int = 8,
+                 mlp_ratio: int = 4, in_hw=(224, 224), in_channels: int = 3, device="cuda"):
+        if embed % 64 or embed % heads:
+            raise SEngineError("embed must be a multiple of 64 and of heads")
+        H, W = in_hw
+        if H % 4 or W % 4:
+            raise SEngineError("image sides must be multiples of 4 (two stride-2 max-pools)")
+        self.dev = torch.device(device)
+        self.B, self.T, self.embed, self.heads, self.depth = batch, T, embed, heads, depth
+        self.in_shape = (batch, in_channels, H, W)
+        p = {k: v.detach().float().cpu() for k, v in params.items()}
+        self.graph = None
+        TB = T * batch
+        i32 = dict(dtype=torch.int32, device=self.dev)
+
+        # ---- SPS
+        c8, c4, c2 = embed // 8, embed // 4, embed // 2
+        P8, P4 = _pad64(c8), _pad64(c4)
+        w0 = p["patch_embed.proj_conv.weight"]
+        if tuple(w0.shape) != (c8, in_channels, 3, 3):
+            raise SEngineError(f"patch_embed.proj_conv.weight: expected {(c8, in_channels, 3, 3)}")
+        w0p = torch.zeros(P8, in_channels, 3, 3)
+        w0p[:c8] = w0
+        sc, bi = self._bn(p, "patch_embed.proj_bn", pad_to=P8)
+        self.stem_spec = ConvSpec(T=1, B=batch, C_in=in_channels, H=H, W=W, C_out=P8, KH=3, KW=3, stride=1,
+                                  padding=1)
+        self.stem_w = w0p.permute(2, 3, 1, 0).contiguous().to(self.dev)  # HWIO
+        self.stem_scale, self.stem_bias = sc.to(self.dev), bi.to(self.dev)
+        self.x_buf = torch.zeros(self.in_shape, dtype=torch.float32, device=self.dev)
+        self.stem_out = torch.empty(batch, H, W, P8, dtype=torch.float32, device=self.dev)
+        self.s0 = torch.empty(TB, H, W, P8 // 32, **i32)
+        self.c1 = self._conv(p, "proj_conv1", c8, c4, P8, P4, H, W)
+        self.s1 = torch.empty(TB, H, W, P4 // 32, **i32)
+        self.c2 = self._conv(p, "proj_conv2", c4, c2, P4, c2, H, W)
+        self.s2 = torch.empty(TB, H, W, c2 // 32, **i32)
+        self.H2, self.W2 = (H - 1) // 2 + 1, (W - 1) // 2 + 1
+        self.p2 = torch.empty(TB, self.H2, self.W2, c2 // 32, **i32)
+        self.c3 = self._conv(p, "proj_conv3", c2, embed, c2, embed, self.H2, self.W2)
+        self.s3 = torch.empty(TB, self.H2, self.W2, embed // 32, **i32)
+        self.H4, self.W4 = (self.H2 - 1) // 2 + 1, (self.W2 - 1) // 2 + 1
+        self.p3 = torch.empty(TB, self.H4, self.W4, embed // 32, **i32)
+        self.rpe = self._conv(p, "rpe_conv", embed, embed, embed, embed, self.H4, self.W4)
+        self.N = self.H4 * self.W4
+        maxv = 2  # rpe spike + max-pooled feature spike
+        self.x0 = torch.empty(TB, self.N, _planes(maxv) * embed // 32, **i32)
+
+        # ---- blocks
+        hidden = embed * mlp_ratio
+        self.blocks: list[SBlock] = []
+        for i in range(depth):
+            pre = f"block.{i}"
+            P0, P1, P2 = _planes(maxv), _planes(maxv + 1), _planes(maxv + 2)
+            if P2 > 5:
+                raise SEngineError("the residual stream needs more than 5 bit planes (depth too large)")
+            blk = SBlock(pre, P0, P1, P2,
+                         q=self._linear(p, pre + ".attn.q", embed, embed, P0),
+                         k=self._linear(p, pre + ".attn.k", embed, embed, P0),
+                         v=self._linear(p, pre + ".attn.v", embed, embed, P0),
+                         proj=self._linear(p, pre + ".attn.proj", embed, embed, 1),
+                         fc1=self._linear(p, pre + ".mlp.fc1", embed, hidden, P1),
+                         fc2=self._linear(p, pre + ".mlp.fc2", hidden, embed, 1),
+                         bufs={})
+            d = embed // heads
+            for n in ("q", "k", "v", "a"):
+                blk.bufs[n] = torch.empty(TB, self.N, embed // 32, **i32)
+            blk.bufs["kv"] = torch.empty(TB, heads, d, d, **i32)
+            blk.bufs["x1"] = torch.empty(TB, self.N, P1 * embed // 32, **i32)
+            blk.bufs["h"] = torch.empty(TB, self.N, hidden // 32, **i32)
+            blk.bufs["x2"] = torch.empty(TB, self.N, P2 * embed // 32, **i32)
+            self.blocks.append(blk)
+            maxv += 2
+        self.final_planes = self.blocks[-1].planes_out if self.blocks else _planes(2)
+        self.head_w = p["head.weight"].contiguous().to(self.dev)
+        self.head_b = p["head.bias"].contiguous().to(self.dev)
+        self.logits = torch.empty(batch, self.head_w.shape[0], dtype=torch.float32, device=self.dev)
+
+    # ------------------------------------------------------------------ build helpers
+    @staticmethod
+    def _bn(p, name, conv_bias=None, pad_to=None):
+        sc, bi = fold_batchnorm(p[name + ".weight"], p[name + ".bias"], p[name + ".running_mean"],
+                                p[name + ".running_var"], 1e-5, conv_bias)
+        if pad_to is not None and pad_to > sc.numel():  # padded channels: zero affine, never fire
+            sc = torch.cat([sc, torch.zeros(pad_to - sc.numel())])
+            bi = torch.cat([bi, torch.zeros(pad_to - bi.numel())])
+        return sc, bi
+
+    def _spec(self, cin, cout, k, h, w, pad) -> ConvSpec:
+        return ConvSpec(T=self.T, B=self.B, C_in=cin, H=h, W=w, C_out=cout, KH=k, KW=k, stride=1, padding=pad,
+                        neuron="lif", hard_reset=True, tau=2.0, v_threshold=1.0, v_reset=0.0)
+
+    def _prepare(self, spec: ConvSpec, w4: torch.Tensor, sc, bi) -> Fused:
+        values, meta, _ = ops.compress_2_4(spec, w4.contiguous().to(self.dev).half())
+        return Fused(spec, values, meta, sc.to(self.dev), bi.to(self.dev))
+
+    def _conv(self, p, name, cin, cout, cin_p, cout_p, h, w) -> Fused:
+        wk = f"patch_embed.{name}.weight"
+        w_ = p[wk]
+        if tuple(w_.shape) != (cout, cin, 3, 3):
+            raise SEngineError(f"{wk}: expected shape {(cout, cin, 3, 3)}, got {tuple(w_.shape)}")
+        if not validate_2_4_pattern(w_):
+            raise SEngineError(f"{wk}: not 2:4 sparse along C_in")
+        wp = torch.zeros(cout_p, cin_p, 3, 3)
+        wp[:cout, :cin] = w_
+        sc, bi = self._bn(p, f"patch_embed.{name.replace('conv', 'bn')}", pad_to=cout_p)
+        return self._prepare(self._spec(cin_p, cout_p, 3, h, w, 1), wp, sc, bi)
+
+    def _linear(self, p, name, cin, cout, planes) -> Fused:
+        wk = name + "_linear.weight"
+        w_ = p[wk]
+        if tuple(w_.shape) != (cout, cin):
+            raise SEngineError(f"{wk}: expected shape {(cout, cin)}, got {tuple(w_.shape)}")
+        w4 = w_[:, :, None, None]
+        if not validate_2_4_pattern(w4):
+            raise SEngineError(f"{wk}: not 2:4 sparse along its input")
+        sc, bi = self._bn(p, name + "_bn", conv_bias=p[name + "_linear.bias"])
+        wx = expand_planes(w4, planes) if planes > 1 else w4
+        # tokens as a (T*B, N, 1) grid of pixels: a Linear is a 1x1 conv
+        return self._prepare(self._spec(cin * planes, cout, 1, self.N, 1, 0), wx, sc, bi)
+
+    # ------------------------------------------------------------------ execution
+    def _fused(self, f: Fused, data, out):
+        ops.fused_sparse_conv_bn_lif(f.spec, data.view(-1), f.values, f.meta, f.scale, f.bias, out=out)
+
+    def _fused_add(self, f: Fused, data, residual, res_planes, out, out_planes):
+        ops.fused_sparse_conv_bn_lif_add(f.spec, data.view(-1), f.values, f.meta, f.scale, f.bias, residual,
+                                         res_planes, out_planes, out=out)
+
+    def run_sps(self):
+        ops.stem_conv_bn(self.stem_spec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias, out=self.stem_out,
+                         layout=ops.WLAYOUT_HWIO)
+        ops.multistep_neuron_repeat(self.stem_out, self.T, "lif", 2.0, 1.0, 0.0, out=self.s0.view(self.T, -1))
+        self._fused(self.c1, self.s0, self.s1)
+        self._fused(self.c2, self.s1, self.s2)
+        H, W = self.stem_spec.H, self.stem_spec.W
+        TB = self.T * self.B
+        ops.maxpool_spikes(self.s2, TB, H, W, self.embed // 2, 3, 2, 1, out=self.p2)
+        self._fused(self.c3, self.p2, self.s3)
+        ops.maxpool_spikes(self.s3, TB, self.H2, self.W2, self.embed, 3, 2, 1, out=self.p3)
+        self._fused_add(self.rpe, self.p3, self.p3, 1, self.x0, _planes(2))
+
+    def block_input(self, i: int):
+        """(token stream, its planes) entering block i."""
+        if i == 0:
+            return self.x0, _planes(2)
+        prev = self.blocks[i - 1]
+        return prev.bufs["x2"], prev.planes_out
+
+    def run_block(self, i: int, x: torch.Tensor | None = None):
+        blk = self.blocks[i]
+        if x is None:
+            x, _ = self.block_input(i)
+        b = blk.bufs
+        self._fused(blk.q, x, b["q"])
+        self._fused(blk.k, x, b["k"])
+        self._fused(blk.v, x, b["v"])
+        ops.spiking_self_attention(b["q"], b["k"], b["v"], self.T, self.B, self.N, self.embed, self.heads,
+                                   v_threshold=ATTN_VTH, kv=b["kv"], out=b["a"])
+        self._fused_add(blk.proj, b["a"], x, blk.planes_in, b["x1"], blk.planes_mid)
+        self._fused(blk.fc1, b["x1"], b["h"])
+        self._fused_add(blk.fc2, b["h"], b["x1"], blk.planes_mid, b["x2"], blk.planes_out)
+
+    def run_head(self):
+        x, planes = self.block_input(len(self.blocks))
+        ops.sew_head(x, self.T, self.B, self.N, self.embed, planes, self.head_w, self.head_b, out=self.logits)
+
+    def _run_all(self):
+        self.run_sps()
+        for i in range(len(self.blocks)):
+            self.run_block(i)
+        self.run_head()
+
+    @property
+    def launches(self) -> int:
+        return 8 + 8 * len(self.blocks) + 1
+
+    def capture(self):
+        """Capture the whole forward into a hipGraph (replayed by forward())."""
+        s = torch.cuda.Stream(self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s):
+            self._run_all()  # warm-up on a side stream (no allocation happens in _run_all)
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._run_all()
+        self.graph = g
+        return g
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """Logits (B, num_classes) for images x (B, C, H, W) fp32; returns the engine's
+        output buffer (overwritten by the next call)."""
+        if tuple(x.shape) != self.in_shape:
+            raise SEngineError(f"expected input {self.in_shape}, got {tuple(x.shape)}")
+        self.x_buf.copy_(x)
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._run_all()
+        return self.logits

@@ -143,6 +143,39 @@ def test_fused_add_with_bit_plane_inputs(dev, k, stride, in_planes, res_planes, 
     assert rep.ok, str(rep)
 
 
+@pytest.mark.parametrize("kernel", ["auto", "tile", "direct"])
+@pytest.mark.parametrize("res_planes,out_planes,k,H", [(3, 4, 3, 9), (4, 5, 1, 11), (5, 5, 3, 2), (4, 4, 1, 3)])
+def test_fused_add_up_to_five_planes(dev, kernel, res_planes, out_planes, k, H):
+    """The residual add into 4 and 5 bit planes (integer streams up to 31, Spikformer's
+    residual after 8 blocks), every spike-bit kernel family (small outputs take the flat /
+    small-M kernels under 'auto'), carries through all planes checked exactly."""
+    T, B, C_in, C_out = 4, 2, 128, 64
+    case = ref.make_layer_case(90 + res_planes + k + H, T=T, B=B, C_in=C_in, C_out=C_out, H=H, W=H, k=k,
+                               padding=k // 2, fp16_weights=True, p_spike=0.3)
+    rng = np.random.default_rng(res_planes + H)
+    hi = (1 << res_planes) - (1 if out_planes > res_planes else 2)  # spike + residual fits out_planes
+    res = rng.integers(0, hi + 1, size=(T, B, C_out, H, H))
+    res[0, 0, :, 0, 0] = hi  # the longest carry chain
+    spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=H, C_out=C_out, KH=k, KW=k, padding=k // 2)
+    values, meta, _ = ops.compress_2_4(spec, case.w.half().to(dev))
+    sc, bi = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
+    data = torch.from_numpy(pk.seq_to_nhwc_bits(case.x_seq.numpy()).view(np.int32)).to(dev)
+    resd = torch.from_numpy(pk.seq_to_planes(res, res_planes).view(np.int32)).to(dev)
+    ops.set_fused_kernel(kernel)
+    try:
+        out = ops.fused_sparse_conv_bn_lif_add(spec, data, values, meta, torch.from_numpy(sc).to(dev),
+                                               torch.from_numpy(bi).to(dev), resd, res_planes, out_planes)
+    finally:
+        ops.set_fused_kernel("auto")
+    got = _bits_to_seq(out, T, B, C_out, H, H, planes=out_planes)
+    r = ref.fused_layer(case.x_seq, case.w, case.bn, 1, k // 2, 1, "lif", 2.0, 1.0, 0.0)
+    spikes_gpu = got - res
+    assert set(np.unique(spikes_gpu)) <= {0.0, 1.0}
+    rep = compare(spikes_gpu, None, r.spikes.numpy(), r.h.numpy(), 1.0)
+    assert rep.ok, str(rep)
+    assert float(r.spikes.sum()) > 0
+
+
 @pytest.fixture(scope="module")
 def sew_case():
     p = sr.make_params(11, bn_random=True, fp16_weights=True)

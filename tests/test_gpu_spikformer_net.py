@@ -1,0 +1,184 @@
+"""GPU parity of Spikformer as a whole network: the SPS stages, every block
+teacher-forced on the oracle's own token stream, the whole forward from one hipGraph replay
+against the oracle's logits, and the config-4 shape (224x224, embed 384, 8 heads, 8 blocks)
+with SPS and the first block checked on one image."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import packing as pk
+from oracle import reference_path as ref
+from oracle import spikformer as sf
+from sparsesnn_amd.spikformer import SpikformerEngine
+from tests.parity import compare
+
+pytestmark = pytest.mark.gpu
+
+
+def _img_bits(bits, T, B, C, H, W, c_real=None):
+    """(T*B, H, W, C/32) bits -> (T, B, C, H, W) float; keep the first c_real channels."""
+    a = pk.unpack_bits(bits.cpu().numpy().view(np.uint32).reshape(-1, C // 32), C)
+    a = np.ascontiguousarray(a.reshape(T, B, H, W, C).transpose(0, 1, 4, 2, 3))
+    return torch.from_numpy(a[:, :, :c_real] if c_real else a)
+
+
+def _tok_bits(bits, T, B, N, C):
+    """(T*B, N, C/32) bits -> (T, B, N, C) float."""
+    a = pk.unpack_bits(bits.cpu().numpy().view(np.uint32).reshape(-1, C // 32), C)
+    return torch.from_numpy(a.reshape(T, B, N, C))
+
+
+def _tok_planes(bits, planes, T, B, N, C):
+    """(T*B, N, planes*C/32) -> integer (T, B, N, C) float."""
+    a = pk.planes_to_seq(bits.cpu().numpy().view(np.uint32).reshape(-1, planes * C // 32), planes, T, B, C, N, 1)
+    return torch.from_numpy(a[..., 0].transpose(0, 1, 3, 2).copy())
+
+
+def _planes_of(x, planes, dev):
+    """integer tokens (T, B, N, C) -> device bit planes (T*B, N, planes*C/32)."""
+    T, B, N, C = x.shape
+    seq = x.permute(0, 1, 3, 2).unsqueeze(-1).numpy()  # (T, B, C, N, 1)
+    return torch.from_numpy(pk.seq_to_planes(seq, planes).view(np.int32)).to(dev)
+
+
+def _stage(p, name, x_seq):
+    bn = sf.bn_of(p, f"patch_embed.{name.replace('conv', 'bn')}")
+    return ref.fused_layer(x_seq, p[f"patch_embed.{name}.weight"], bn, 1, 1, 1, "lif", 2.0, 1.0, 0.0)
+
+
+def _pool(x):
+    T = x.shape[0]
+    y = F.max_pool2d(x.flatten(0, 1), 3, 2, 1)
+    return y.view(T, -1, *y.shape[1:])
+
+
+def _check_sps(eng, p, x_img, T, B, embed):
+    """Each SPS stage of the engine against the oracle stage run on the engine's own input."""
+    H, W = eng.stem_spec.H, eng.stem_spec.W
+    c8, c4, c2 = embed // 8, embed // 4, embed // 2
+    P8, P4 = eng.stem_spec.C_out, eng.c1.spec.C_out
+    r0 = _stage(p, "proj_conv", x_img.float().unsqueeze(0).repeat(T, 1, 1, 1, 1))
+    s0 = _img_bits(eng.s0, T, B, P8, H, W)
+    assert float(s0[:, :, c8:].abs().sum()) == 0  # padded channels never fire
+    rep = compare(s0[:, :, :c8].numpy(), None, r0.spikes.numpy(), r0.h.numpy(), 1.0)
+    assert rep.ok, f"proj_conv {rep}"
+    r1 = _stage(p, "proj_conv1", s0[:, :, :c8])
+    s1 = _img_bits(eng.s1, T, B, P4, H, W)
+    assert float(s1[:, :, c4:].abs().sum()) == 0
+    rep = compare(s1[:, :, :c4].numpy(), None, r1.spikes.numpy(), r1.h.numpy(), 1.0)
+    assert rep.ok, f"proj_conv1 {rep}"
+    r2 = _stage(p, "proj_conv2", s1[:, :, :c4])
+    s2 = _img_bits(eng.s2, T, B, c2, H, W)
+    rep = compare(s2.numpy(), None, r2.spikes.numpy(), r2.h.numpy(), 1.0)
+    assert rep.ok, f"proj_conv2 {rep}"
+    p2 = _img_bits(eng.p2, T, B, c2, eng.H2, eng.W2)
+    assert torch.equal(p2, _pool(s2))
+    r3 = _stage(p, "proj_conv3", p2)
+    s3 = _img_bits(eng.s3, T, B, embed, eng.H2, eng.W2)
+    rep = compare(s3.numpy(), None, r3.spikes.numpy(), r3.h.numpy(), 1.0)
+    assert rep.ok, f"proj_conv3 {rep}"
+    p3 = _img_bits(eng.p3, T, B, embed, eng.H4, eng.W4)
+    assert torch.equal(p3, _pool(s3))
+    rr = _stage(p, "rpe_conv", p3)
+    x0 = _tok_planes(eng.x0, 2, T, B, eng.N, embed)
+    srpe = x0 - p3.flatten(-2).transpose(-1, -2)
+    assert set(np.unique(srpe.numpy())) <= {0.0, 1.0}
+    rep = compare(srpe.transpose(-1, -2).reshape(rr.spikes.shape).numpy(), None, rr.spikes.numpy(), rr.h.numpy(),
+                  1.0)
+    assert rep.ok, f"rpe_conv {rep}"
+    return [float(r.spikes.mean()) for r in (r0, r1, r2, r3, rr)]
+
+
+def _check_block(dev, eng, p, i, x, T, B, heads):
+    """Block i on the oracle token stream x (T, B, N, C): q/k/v and fc1 spikes under the
+    parity rule on the engine's own inputs, SSA bit-exact on the engine's q/k/v, the two
+    residual adds exact.  Returns the oracle block output."""
+    blk = eng.blocks[i]
+    N, C = x.shape[2], x.shape[3]
+    pre = blk.name
+    eng.run_block(i, x=_planes_of(x, blk.planes_in, dev))
+    torch.cuda.synchronize()
+    b = blk.bufs
+
+    def lin(name, inp, got, v_th=1.0):
+        s, h, _ = sf.linear_bn_lif(inp, p[f"{pre}.{name}_linear.weight"], p[f"{pre}.{name}_linear.bias"],
+                                   sf.bn_of(p, f"{pre}.{name}_bn"), 2.0, v_th)
+        rep = compare(got.numpy(), None, s.numpy(), h.numpy(), v_th)
+        assert rep.ok, f"{pre}.{name} {rep}"
+        return s
+
+    q = _tok_bits(b["q"], T, B, N, C)
+    k = _tok_bits(b["k"], T, B, N, C)
+    v = _tok_bits(b["v"], T, B, N, C)
+    for name, got in (("attn.q", q), ("attn.k", k), ("attn.v", v)):
+        lin(name, x, got)
+    a_ref = sf.ssa(q, k, v, heads)[0]
+    a = _tok_bits(b["a"], T, B, N, C)
+    assert torch.equal(a, a_ref), f"{pre} ssa"
+    x1 = _tok_planes(b["x1"], blk.planes_mid, T, B, N, C)
+    sp = x1 - x
+    assert set(np.unique(sp.numpy())) <= {0.0, 1.0}
+    lin("attn.proj", a, sp)
+    h = _tok_bits(b["h"], T, B, N, C * 4)
+    lin("mlp.fc1", x1, h)
+    x2 = _tok_planes(b["x2"], blk.planes_out, T, B, N, C)
+    s2 = x2 - x1
+    assert set(np.unique(s2.numpy())) <= {0.0, 1.0}
+    lin("mlp.fc2", h, s2)
+    return float(a_ref.mean())
+
+
+@pytest.fixture(scope="module")
+def sf_case():
+    p = sf.make_params(31, embed=128, depth=4, num_classes=10)
+    x = torch.randn(2, 3, 32, 32, generator=torch.Generator().manual_seed(32))
+    logits, xs = sf.forward(p, x, T=4, heads=2, depth=4, keep=True)
+    return p, x, logits, xs
+
+
+def test_engine_sps_and_blocks_teacher_forced(dev, sf_case):
+    p, x, _, xs = sf_case
+    eng = SpikformerEngine(p, batch=2, T=4, embed=128, heads=2, depth=4, in_hw=(32, 32), device=dev)
+    eng.forward(x.to(dev))
+    torch.cuda.synchronize()
+    rates = _check_sps(eng, p, x, 4, 2, 128)
+    assert all(0.005 < r < 0.9 for r in rates), rates
+    for i in range(4):
+        ra = _check_block(dev, eng, p, i, xs[i], 4, 2, 2)
+        assert 0.005 < ra < 0.95
+
+
+def test_engine_end_to_end_graph(dev, sf_case):
+    p, x, logits, xs = sf_case
+    eng = SpikformerEngine(p, batch=2, T=4, embed=128, heads=2, depth=4, in_hw=(32, 32), device=dev)
+    eager = eng.forward(x.to(dev)).clone()
+    eng.capture()
+    for _ in range(3):
+        y = eng.forward(x.to(dev))
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+    final = _tok_planes(eng.blocks[-1].bufs["x2"], eng.final_planes, 4, 2, eng.N, 128)
+    assert float((final != xs[-1]).float().mean()) <= 1e-3
+    err = float((eager.cpu() - logits).abs().max())
+    assert err < 5e-2, err
+    assert eng.launches == 8 + 8 * 4 + 1
+
+
+def test_engine_cfg4_shape_one_image(dev):
+    """BASELINE config 4's shape on one image: 3x224x224 pixels ~N(0,1), T=4, embed 384,
+    8 heads, MLP ratio 4, 8 blocks (3,136 tokens), 1000 classes; the SPS stages and the
+    first block teacher-forced against the oracle, graph replays equal to the eager run."""
+    p = sf.make_params(41, embed=384, depth=8, num_classes=1000)
+    x = torch.randn(1, 3, 224, 224, generator=torch.Generator().manual_seed(42))
+    eng = SpikformerEngine(p, batch=1, T=4, embed=384, heads=8, depth=8, in_hw=(224, 224), device=dev)
+    assert eng.N == 3136 and eng.final_planes == 5
+    eager = eng.forward(x.to(dev)).clone()
+    eng.capture()
+    y = eng.forward(x.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(y, eager)
+    rates = _check_sps(eng, p, x, 4, 1, 384)
+    assert all(0.005 < r < 0.9 for r in rates), rates
+    x0 = _tok_planes(eng.x0, 2, 4, 1, eng.N, 384)  # the engine's own (parity-checked) SPS output
+    _check_block(dev, eng, p, 0, x0, 4, 1, 8)
