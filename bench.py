@@ -206,6 +206,67 @@ def cpu_e2e(params, x, budget_s=6.0, min_runs=2):
     return statistics.median(ts), len(ts), torch.get_num_threads()
 
 
+CFG34_BATCH, CFG34_HW, CFG34_CLASSES = 32, 224, 1000
+
+
+def bench_graph_engine(eng, x, warmup: int, iters: int) -> float:
+    """Seconds per batch of a captured engine: HIP events around `iters` hipGraph replays."""
+    import torch
+    eng.forward(x)
+    eng.capture()
+    for _ in range(warmup):
+        eng.forward(x)
+    torch.cuda.synchronize(x.device)
+    stream = torch.cuda.current_stream(x.device)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    eng.x_buf.copy_(x)
+    a.record(stream)
+    for _ in range(iters):
+        eng.graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize(x.device)
+    return a.elapsed_time(b) * 1e-3 / iters
+
+
+def bench_msresnet34(dev, warmup: int, iters: int):
+    """MS-ResNet-34 (membrane shortcut, LIF tau 2 / V_th 1, 2:4 convs but the
+    stem, reference initialisation), 3x224x224 pixels ~N(0,1), T=4, batch 32, 1000 classes."""
+    import torch
+    from sparsesnn_amd.ms_resnet import MSResNetEngine, random_params
+    params = random_params(2025, 34, CFG34_CLASSES)
+    eng = MSResNetEngine(params, batch=CFG34_BATCH, T=T_STEPS, depth=34, neuron="lif", in_hw=(CFG34_HW, CFG34_HW),
+                         device=dev)
+    x = torch.randn((CFG34_BATCH, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(8))
+    s = bench_graph_engine(eng, x.to(dev), warmup, iters)
+    return dict(params=params, x=x, batch_s=s, launches=eng.launches)
+
+
+def bench_spikformer(dev, warmup: int, iters: int):
+    """Spikformer, 8 blocks, embed 384, 8 heads, MLP ratio 4, SPS stem on
+    3x224x224 pixels ~N(0,1) (3,136 tokens), T=4, batch 32, 1000 classes, the stem convs after
+    the first and every block Linear 2:4 with fused BN+LIF, the model's own initialisation."""
+    import torch
+    from sparsesnn_amd.spikformer import SpikformerEngine, random_params
+    params = random_params(2026, embed=384, depth=8, num_classes=CFG34_CLASSES)
+    eng = SpikformerEngine(params, batch=CFG34_BATCH, T=T_STEPS, embed=384, heads=8, depth=8,
+                           in_hw=(CFG34_HW, CFG34_HW), device=dev)
+    x = torch.randn((CFG34_BATCH, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(9))
+    s = bench_graph_engine(eng, x.to(dev), warmup, iters)
+    return dict(params=params, x=x, batch_s=s, launches=eng.launches)
+
+
+def cpu_sample(fn, budget_s: float, min_runs: int = 1):
+    """Median seconds of fn() (the oracle on the host cores) over runs until budget_s."""
+    import torch
+    with torch.no_grad():
+        ts = []
+        while len(ts) < min_runs or sum(ts) < budget_s:
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), len(ts), torch.get_num_threads()
+
+
 def copy_calibration(dev, nbytes=256 << 20, reps=3):
     """A plain device-to-device copy of known size, launched `reps` times, so that rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters can be scaled to bytes (each launch reads and writes
@@ -229,7 +290,11 @@ def main():
     ap.add_argument("--json-out", default="")
     ap.add_argument("--no-e2e", action="store_true", help="skip the SEW-ResNet-18 end-to-end measurement")
     ap.add_argument("--e2e-only", action="store_true",
-                    help="only the SEW-ResNet-18 end-to-end measurement (prints its JSON object; for profiling)")
+                    help="only one end-to-end measurement (--e2e-model; prints its JSON object; for profiling)")
+    ap.add_argument("--e2e-model", default="sew18", choices=("sew18", "msresnet34", "spikformer"),
+                    help="network of --e2e-only: BASELINE config 2, 3 or 4")
+    ap.add_argument("--no-e2e-extra", action="store_true",
+                    help="skip the config-3 (MS-ResNet-34) and config-4 (Spikformer) end-to-end measurements")
     ap.add_argument("--profile-pass", action="store_true",
                     help="counter-collection pass for rocprofv3 --pmc: eager launches only (no graph, no "
                          "JSON line), followed by the copy-calibration kernel")
@@ -245,9 +310,14 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     if args.e2e_only:
-        e2e = bench_e2e(dev, warmup=args.warmup, iters=args.steps)
-        print(json.dumps({"metric": "images/sec", "value": round(E2E_BATCH / e2e["batch_s"], 1),
-                          "ms_per_batch": round(e2e["batch_s"] * 1e3, 4), "batch": E2E_BATCH, "timesteps": T_STEPS,
+        if args.e2e_model == "sew18":
+            e2e, batch = bench_e2e(dev, warmup=args.warmup, iters=args.steps), E2E_BATCH
+        elif args.e2e_model == "msresnet34":
+            e2e, batch = bench_msresnet34(dev, warmup=args.warmup, iters=args.steps), CFG34_BATCH
+        else:
+            e2e, batch = bench_spikformer(dev, warmup=args.warmup, iters=args.steps), CFG34_BATCH
+        print(json.dumps({"metric": "images/sec", "model": args.e2e_model, "value": round(batch / e2e["batch_s"], 1),
+                          "ms_per_batch": round(e2e["batch_s"] * 1e3, 4), "batch": batch, "timesteps": T_STEPS,
                           "replays": args.steps, "warmup": args.warmup}))
         return
     work = build_workloads(dev, T_STEPS, BATCH)
@@ -379,6 +449,39 @@ def main():
                                                                        f"median of {runs} batches",
                                              "ms_per_batch": round(cs * 1e3, 2)}
             result["e2e"]["speedup_vs_cpu"] = round(cs / e2e["batch_s"], 1)
+    if not args.no_e2e and not args.no_e2e_extra:
+        import torch
+        m = bench_msresnet34(dev, warmup=5, iters=max(20, args.steps))
+        result["e2e_cfg3"] = {
+            "metric": "images/sec", "model": "MS-ResNet-34 (membrane shortcut, LIF tau=2 V_th=1, 2:4 convs except the stem)",
+            "value": round(CFG34_BATCH / m["batch_s"], 1), "batch": CFG34_BATCH, "timesteps": T_STEPS,
+            "input": f"3x{CFG34_HW}x{CFG34_HW} ~N(0,1)", "ms_per_batch": round(m["batch_s"] * 1e3, 4),
+            "launches_per_batch": m["launches"], "step": "one hipGraph replay per batch",
+            "data": "synthetic images, reference random init (models/msresnet.py)"}
+        del m["x"]
+        torch.cuda.empty_cache()
+        f = bench_spikformer(dev, warmup=2, iters=10)
+        result["e2e_cfg4"] = {
+            "metric": "images/sec", "model": "Spikformer-8-384 (8 heads, MLP x4, 3136 tokens, 2:4 Linears/convs, fused BN+LIF)",
+            "value": round(CFG34_BATCH / f["batch_s"], 1), "batch": CFG34_BATCH, "timesteps": T_STEPS,
+            "input": f"3x{CFG34_HW}x{CFG34_HW} ~N(0,1)", "ms_per_batch": round(f["batch_s"] * 1e3, 4),
+            "launches_per_batch": f["launches"], "step": "one hipGraph replay per batch",
+            "data": "synthetic images, the model's own random init (models/spikformer.py:238-245)"}
+        if not args.no_cpu_baseline:  # the oracle networks on the host cores (CPU baseline leg only)
+            from oracle import ms_resnet as msr
+            from oracle import spikformer as sfo
+            x1 = torch.randn((1, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(10))
+            cs, runs, thr = cpu_sample(lambda: msr.forward(m["params"], x1, T=T_STEPS, depth=34, kind="lif", tau=2.0,
+                                                           v_threshold=1.0), budget_s=4.0)
+            result["e2e_cfg3"]["cpu_baseline"] = {"value": round(1.0 / cs, 3), "unit": "images/sec", "cores": thr,
+                                                  "kind": "port", "sample": f"one image (batch 1), median of {runs} "
+                                                                            "forwards", "s_per_image": round(cs, 3)}
+            result["e2e_cfg3"]["speedup_vs_cpu"] = round(result["e2e_cfg3"]["value"] * cs, 1)
+            cs, runs, thr = cpu_sample(lambda: sfo.forward(f["params"], x1, T=T_STEPS, heads=8, depth=8), budget_s=0.0)
+            result["e2e_cfg4"]["cpu_baseline"] = {"value": round(1.0 / cs, 3), "unit": "images/sec", "cores": thr,
+                                                  "kind": "port", "sample": "one image (batch 1), one forward",
+                                                  "s_per_image": round(cs, 3)}
+            result["e2e_cfg4"]["speedup_vs_cpu"] = round(result["e2e_cfg4"]["value"] * cs, 1)
     line = json.dumps(result)
     print(line)
     if args.json_out:

@@ -43,6 +43,42 @@ def _planes(max_value: int) -> int:
     return max(1, int(max_value).bit_length())
 
 
+def random_params(seed: int = 0, embed: int = 384, depth: int = 8, mlp_ratio: int = 4, num_classes: int = 1000,
+                  in_channels: int = 3) -> dict:
+    """Random Spikformer parameters with the reference's state_dict names and the model's own
+    initialisation (models/spikformer.py:238-245: Linear weights N(0, 0.02) clamped to +-0.04,
+    biases 0; Conv2d U(+-1/sqrt(fan_in)) and BatchNorm defaults), every conv after the first
+    (C_in = 3) and every block Linear 2:4-pruned along its input and rounded to fp16
+    (BASELINE config 4)."""
+    import math
+    from .sparsity import prune_conv_2_4
+    g = torch.Generator().manual_seed(seed)
+    p = {}
+
+    def bn(name, c):
+        p[name + ".weight"], p[name + ".bias"] = torch.ones(c), torch.zeros(c)
+        p[name + ".running_mean"], p[name + ".running_var"] = torch.zeros(c), torch.ones(c)
+
+    chans = [("proj_conv", in_channels, embed // 8), ("proj_conv1", embed // 8, embed // 4),
+             ("proj_conv2", embed // 4, embed // 2), ("proj_conv3", embed // 2, embed), ("rpe_conv", embed, embed)]
+    for name, cin, cout in chans:
+        b = 1.0 / math.sqrt(cin * 9)
+        w = (torch.rand((cout, cin, 3, 3), generator=g) * 2 - 1) * b
+        p[f"patch_embed.{name}.weight"] = w if name == "proj_conv" else prune_conv_2_4(w).half().float()
+        bn(f"patch_embed.{name.replace('conv', 'bn')}", cout)
+    hidden = embed * mlp_ratio
+    for i in range(depth):
+        for lin, cin, cout in (("attn.q", embed, embed), ("attn.k", embed, embed), ("attn.v", embed, embed),
+                               ("attn.proj", embed, embed), ("mlp.fc1", embed, hidden), ("mlp.fc2", hidden, embed)):
+            w = (torch.randn((cout, cin, 1, 1), generator=g) * 0.02).clamp_(-0.04, 0.04)
+            p[f"block.{i}.{lin}_linear.weight"] = prune_conv_2_4(w).half().float()[:, :, 0, 0]
+            p[f"block.{i}.{lin}_linear.bias"] = torch.zeros(cout)
+            bn(f"block.{i}.{lin}_bn", cout)
+    p["head.weight"] = (torch.randn((num_classes, embed), generator=g) * 0.02).clamp_(-0.04, 0.04)
+    p["head.bias"] = torch.zeros(num_classes)
+    return p
+
+
 @dataclass
 class Fused:
     spec: ConvSpec
