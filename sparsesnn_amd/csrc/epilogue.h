@@ -180,16 +180,6 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
   else load_sew_res<T>(sa, M, m, F, cob, valid, res);
   float fsc[16], fbi[16], v[16];
   const bool fold = MODE == EPI_LIF_HARD || (MODE == EPI_GENERIC && np.neuron == SENGINE_NEURON_LIF && np.pow2);
-#pragma unroll
-  for (int j = 0; j < 16; j += 4) {
-    const float4_t s4 = *reinterpret_cast<const float4_t*>(cf.fsc + j);
-    const float4_t b4 = *reinterpret_cast<const float4_t*>(cf.fbi + j);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      fsc[j + e] = s4[e];
-      fbi[j + e] = b4[e];
-    }
-  }
   float* st = state ? state + (size_t)m * F + cob : nullptr;
   const bool has_state = st != nullptr;
 #pragma unroll
@@ -200,6 +190,83 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
     for (int e = 0; e < 4; ++e) v[j + e] = v4[e];
   }
   const float vreset = np.vreset;
+  if (MODE == EPI_GENERIC && sa.real_out != nullptr) {  // uniform branch
+    // Membrane-shortcut form (no traces): y = BN(acc) + residual is stored and the neuron
+    // runs on y.  All T residual rows of the lane's channels (of 4 of them for T > 4) are
+    // loaded before any is used: the stores of y could alias them, so loads issued per t
+    // would each wait out one memory latency.
+    constexpr int RCH = T <= 4 ? 16 : 4;  // channels whose T residual rows are loaded together
+    uint32_t words[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) words[t] = 0;
+#pragma unroll
+    for (int hf = 0; hf < 16 / RCH; ++hf) {
+      float4_t rr[T][RCH / 4];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const size_t row = ((size_t)t * M + m) * F + cob + RCH * hf;
+#pragma unroll
+        for (int q = 0; q < RCH / 4; ++q)
+          rr[t][q] = (valid && sa.real_res) ? *reinterpret_cast<const float4_t*>(sa.real_res + row + 4 * q)
+                                            : float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int jj = 0; jj < RCH; ++jj) {
+          const int j = RCH * hf + jj;
+          const float accv = acc[t][j >> 2][j & 3];
+          // y = BN output + residual, rounded once as torch's out + sc; the neuron takes y
+          // (times 1/tau when that is folded: an exact power-of-two scaling)
+          const float xraw = __builtin_fmaf(accv, cf.sc[j], cf.bi[j]);  // unfolded BN (LDS coefficients)
+          const float y = sa.real_res ? __fadd_rn(xraw, rr[t][jj >> 2][jj & 3]) : xraw;
+          rr[t][jj >> 2][jj & 3] = y;
+          const float h = neuron_charge(np, v[j], fold ? y * np.rtau : y);
+          const bool spike = h >= np.vth;
+          v[j] = neuron_reset(np, h, spike);
+          words[t] |= (uint32_t)spike << j;
+        }
+        if (valid) {
+          const size_t row = ((size_t)t * M + m) * F + cob + RCH * hf;
+#pragma unroll
+          for (int q = 0; q < RCH / 4; ++q) *reinterpret_cast<float4_t*>(sa.real_out + row + 4 * q) = rr[t][q];
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (!valid) continue;
+      if (OUT_ENC == SENGINE_ENC_BITS) {
+        store_spike_word(words[t], (size_t)t * M + m, F, cob, out, sa, res.r[t]);
+      } else {
+        half8_t o0, o1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          o0[j] = (words[t] >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+          o1[j] = (words[t] >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+        }
+        half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(out) + ((size_t)t * M + m) * F + cob);
+        dst[0] = o0;
+        dst[1] = o1;
+      }
+    }
+    if (has_state && valid) {
+#pragma unroll
+      for (int j = 0; j < 16; j += 4)
+        *reinterpret_cast<float4_t*>(st + j) = float4_t{v[j], v[j + 1], v[j + 2], v[j + 3]};
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j += 4) {
+    const float4_t s4 = *reinterpret_cast<const float4_t*>(cf.fsc + j);
+    const float4_t b4 = *reinterpret_cast<const float4_t*>(cf.fbi + j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      fsc[j + e] = s4[e];
+      fbi[j + e] = b4[e];
+    }
+  }
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     uint32_t word = 0;

@@ -107,13 +107,16 @@ __device__ __forceinline__ void expand_word64(uint2 w, u32x4_t (&pc)[8]) {
 // accumulators are added to the first set's in LDS, in a fixed order, before the
 // epilogue.  Twice the waves per tile for layers whose grid leaves SIMDs with one wave.
 //
+// The generic epilogue (any neuron, traces, the membrane-shortcut form) is allowed two waves
+// per SIMD: its fp32 residual rows are loaded for all T at once.
+//
 // PF = 2 (3x3 only) prefetches A operands two taps and B fragments two (tap, t) steps
 // ahead instead of one: for grids of at most two workgroups per CU, whose waves (two per
 // SIMD) have the registers for it and whose SMFMAC issue otherwise waits on L2 and LDS
 // latency.
 template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP, int PF = 1>
 __global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR * KSP))
-__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 ? 3 : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
+__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EPI_GENERIC ? 3 : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
   using Gm = TileGeom<KS, TR, TC, GR>;
   static_assert(PF == 1 || (PF == 2 && KS == 3), "two-deep prefetch needs the unrolled 9-tap loop");
   constexpr int NA = PF + 1;  // A operand sets in flight (ring over taps; 9 % 3 == 0)
