@@ -237,13 +237,28 @@ int sengine_amd_stem_conv_bn(const sengine_conv_lif_desc* d, const float* x, con
  * MaxPool2d(pool_k, pool_stride, pool_pad) of the spikes.  pooled: (T, B, POH, POW) x
  * C_out bits; spikes (optional, may be NULL): the stem spikes (T, B, OH, OW) x C_out bits.
  * Bit-identical to the three separate entry points.  Needs C_out % 32 == 0, T <= 16,
- * OH*OW <= 256 and the image's staged input rows and weights within LDS (a 3x32x32 image
- * with a 7x7/2 stem fits); returns -2 otherwise.
+ * OH*OW <= 256 and the image's staged input rows within LDS (a 3x32x32 image with a 7x7/2
+ * stem fits); returns -2 otherwise.
  */
 int sengine_amd_stem_conv_bn_lif_pool(const sengine_conv_lif_desc* d, const float* x, const float* weight,
                                       const float* bn_scale, const float* bn_bias, int32_t pool_k,
                                       int32_t pool_stride, int32_t pool_pad, uint32_t* spikes, uint32_t* pooled,
                                       hipStream_t stream);
+
+/*
+ * The stem and the neuron over its output repeated T times in one launch (MS-ResNet:
+ * models/msresnet.py:135-138 conv1, :146-150 the image repeated over T, :119-120 the first
+ * block's sn1 on that output and its shortcut on the same real-valued output): conv +
+ * folded BN as sengine_amd_stem_conv_bn (HWIO weights) into out (optional, may be NULL: NHWC
+ * fp32 (B, OH, OW, C_out)), and the neuron of d (V0 = 0) on it repeated over d->T into
+ * spikes (T, B, OH, OW) x C_out bits, the layout of sengine_amd_multistep_neuron_repeat on
+ * that out.  Bit-identical to those two entry points.  Needs C_out % 32 == 0 and the input
+ * rows of 256 consecutive output pixels within LDS (3 channels of 224-wide images with a
+ * 7x7/2 or 3x3/1 stem fit); returns -2 otherwise.
+ */
+int sengine_amd_stem_conv_bn_neuron(const sengine_conv_lif_desc* d, const float* x, const float* weight,
+                                    const float* bn_scale, const float* bn_bias, float* out, uint32_t* spikes,
+                                    hipStream_t stream);
 
 /*
  * Multi-step neuron on an input repeated at every timestep (the stem output,

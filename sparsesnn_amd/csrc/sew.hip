@@ -11,10 +11,9 @@ namespace sengine {
 // x: NCHW fp32 images (N, C_in, H, W) (the reference feeds the raw 4-D batch to conv1,
 // models/sewresnet.py:199); w: OIHW or HWIO fp32; out: NHWC fp32 (N, OH, OW, C_out);
 // accumulation in (c_in, kh, kw) order in fp32 like the reference's CPU conv.
-// Fast path (HWIO, kernel <= 64 taps, C_in*KH*KW*C_out <= 16K floats): the workgroup stages
-// all weights in LDS once; each thread computes 16 output channels of one pixel, so every
-// input value it loads feeds 16 FMAs and the weight reads are LDS broadcasts.  Generic
-// path: one output value per thread.
+// Fast path (HWIO, C_out % 16 == 0, the input rows of 256 output pixels fit in LDS): each
+// thread computes 8 or 16 output channels of one pixel from LDS-staged input, with the
+// weights in SGPRs.  Generic path: one output value per thread.
 struct StemParams {
   const float* x;
   const float* w;
@@ -22,29 +21,75 @@ struct StemParams {
   const float* bias;
   float* out;
   int N, C, H, W, F, KH, KW, SH, SW, PH, PW, OH, OW;
-  // fused neuron + max-pool (stem_conv_bn_lds_kernel<KW, true>)
+  // fused neuron (+ max-pool): stem_conv_bn_lds_kernel<KW, kStemPool / kStemSpikes, CPT>
   uint16_t* spikes;  // (T, N, OH, OW) x F bits, or null
   uint16_t* pooled;  // (T, N, POH, POW) x F bits
   int T, PK, PS, PP, POH, POW;
   NeuronParams np;
 };
 
-constexpr int kStemPix = 256;        // output pixels (of one image) per workgroup, one per thread
-constexpr int kStemLdsInput = 12288; // staged, zero-padded input floats
-constexpr int kStemLdsW = 4096;      // staged weights of the workgroup's 16 channels
+constexpr int kStemPix = 256;        // output pixels (of one image) per workgroup
+constexpr int kStemLdsInput = 12288; // staged, zero-padded input floats (at most)
+constexpr int kStemMaxT = 16;        // fused variant: spike words of all T kept in LDS for the pool
+constexpr int kStemRows = 6;         // row-wise staging: rows per wave whose loads are in flight together
+constexpr int kStemFlat = 16;        // flat staging: floats in flight per thread of a 256-thread workgroup
+constexpr int kStemTouchTaps = 160;  // weight taps (64-byte lines) prefetched into the scalar cache
+
+// Exact n / d for 0 <= n < 2^16 and 1 <= d < 2^16 by a multiply-high with m = ceil(2^32 / d):
+// with e = m*d - 2^32 < d, n*m / 2^32 = n/d + n*e / (d * 2^32) and n*e < 2^32, so the
+// fraction added never carries past the next integer.
+struct StemDiv {
+  uint32_t m, d;
+  __device__ explicit StemDiv(uint32_t d_) : m(d_ > 1 ? (uint32_t)(0xffffffffull / d_ + 1) : 0u), d(d_) {}
+  __device__ uint32_t operator()(uint32_t n) const { return d > 1 ? __umulhi(n, m) : n; }
+};
+
+typedef const float4_t __attribute__((address_space(4)))* StemWPtr;
+
+// Brings the scalar-cache lines at base + off[i] bytes (wave-uniform) in: eight scalar loads
+// issued back to back, then one wait, so the eight misses overlap.  Loads only; the loaded
+// words are discarded.  The outputs are early-clobber: a load may land while later loads of
+// the block still read their base and offset registers.
+__device__ inline void stem_touch8(const float* base, const int (&off)[8]) {
+  uint32_t d0, d1, d2, d3, d4, d5, d6, d7;
+  asm volatile(
+      "s_load_dword %0, %8, %9\n\t"
+      "s_load_dword %1, %8, %10\n\t"
+      "s_load_dword %2, %8, %11\n\t"
+      "s_load_dword %3, %8, %12\n\t"
+      "s_load_dword %4, %8, %13\n\t"
+      "s_load_dword %5, %8, %14\n\t"
+      "s_load_dword %6, %8, %15\n\t"
+      "s_load_dword %7, %8, %16\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7)
+      : "s"(base), "s"(off[0]), "s"(off[1]), "s"(off[2]), "s"(off[3]), "s"(off[4]), "s"(off[5]), "s"(off[6]),
+        "s"(off[7]));
+}
 
 // Workgroup = (image n, block of kStemPix output pixels in (oh, ow) order, 16-channel group
-// fg); thread = one output pixel x 16 channels.  The workgroup stages the input rows the
-// block reads, with the padding as zeros, and its 16 channels' HWIO weights in LDS; the tap
-// loop then has no bounds checks, the weight reads are LDS broadcasts, and with KW_ known
-// at compile time a whole tap row's reads are issued before its FMAs.
-constexpr int kStemMaxT = 16;  // fused variant: spike words of all T kept in LDS for the pool
+// fg); thread = one output pixel x CPT channels (CPT = 8: two threads per pixel, waves
+// 0-3 channels 0-7 of the group and waves 4-7 channels 8-15, so a small grid still has two
+// waves per SIMD).  The workgroup stages the input rows the block reads, with the padding
+// as zeros, in dynamic LDS sized to the block; the tap loop then has no bounds checks.  The
+// weights of a wave's channels are the same for all its lanes, so they are read from global
+// memory at wave-uniform addresses (constant address space: scalar loads into SGPRs, which
+// the FMAs take as operands) -- read from LDS, every 16 FMAs would need a 1 KB wave-wide
+// float4 broadcast read, which kept the tap loop LDS-bound.
+// What the LDS stem kernel does after the convolution.
+enum StemMode : int {
+  kStemOut = 0,    // folded BN -> fp32 NHWC out
+  kStemPool = 1,   // folded BN -> neuron over T repeats -> spike max-pool (whole image per workgroup)
+  kStemSpikes = 2  // folded BN -> fp32 out (if p.out) and neuron over T repeats -> spike bits
+};
 
-template <int KW_, bool FUSE>
-__global__ __launch_bounds__(256) void stem_conv_bn_lds_kernel(StemParams p) {
-  __shared__ float sx[kStemLdsInput];
-  __shared__ float4 sw4[kStemLdsW / 4];
-  __shared__ uint16_t sspk[FUSE ? kStemMaxT * kStemPix : 1];
+template <int KW_, int MODE, int CPT>
+__global__ __launch_bounds__(kStemPix * 16 / CPT) void stem_conv_bn_lds_kernel(StemParams p) {
+  static_assert(CPT == 16 || CPT == 8, "8 or 16 channels per thread");
+  constexpr int NT = kStemPix * 16 / CPT;
+  constexpr int NW = NT / 64;
+  constexpr int FLAT = kStemFlat * 256 / NT;  // flat staging: loads per thread in flight
+  extern __shared__ float sx[];  // staged input (row = c * nrows + r, then column); fused: spike words after it
   const int KW = KW_ > 0 ? KW_ : p.KW;
   const int fgroups = p.F / 16;
   const int pblocks = (p.OH * p.OW + kStemPix - 1) / kStemPix;
@@ -57,68 +102,118 @@ __global__ __launch_bounds__(256) void stem_conv_bn_lds_kernel(StemParams p) {
   const int ih0 = oh_first * p.SH - p.PH;
   const int nrows = (oh_last - oh_first) * p.SH + p.KH;
   const int WP = p.W + 2 * p.PW;  // padded row
-  // weights: tap-major (kh, kw, c), 16 channels of group fg each, as 4 float4
-  const int ntap = p.KH * KW * p.C;
-  for (int i = threadIdx.x; i < ntap * 4; i += blockDim.x)
-    sw4[i] = *reinterpret_cast<const float4*>(p.w + (int64_t)(i >> 2) * p.F + fg * 16 + (i & 3) * 4);
-  const int nx = p.C * nrows * WP;
-  for (int i0 = threadIdx.x; i0 < nx; i0 += 8 * blockDim.x) {
-    float v[8];
+  const int nrow_st = p.C * nrows;
+  const int nx = nrow_st * WP;
+  const float* xn = p.x + (int64_t)n * p.C * p.H * p.W;
+  // Weight prefetch: the tap loop's scalar loads come one (c, kh) row at a time, each row
+  // waited for before its FMAs, so a workgroup that finds the scalar cache cold (small
+  // grids: one workgroup per CU) would pay one L2/HBM round trip per row.  Wave w first
+  // touches the 64-byte lines of taps w, w + NW, ... with scalar loads issued eight at a
+  // time, one round trip per eight lines.
+  {
+    const int last = p.KH * KW * p.C - 1;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const float* wl = p.w + fg * 16;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = i0 + u * blockDim.x;
-      const int c = i / (nrows * WP);
-      const int rem = i - c * (nrows * WP);
-      const int rr = rem / WP;
-      const int ih = ih0 + rr;
-      const int iw = rem - rr * WP - p.PW;
-      v[u] = (i < nx && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W)
-                 ? p.x[(((int64_t)n * p.C + c) * p.H + ih) * p.W + iw]
-                 : 0.f;
+    for (int i0 = 0; i0 < (kStemTouchTaps + NW - 1) / NW; i0 += 8) {
+      int off[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) off[i] = min(wv + NW * (i0 + i), last) * p.F * (int)sizeof(float);
+      stem_touch8(wl, off);
     }
+  }
+  if (WP >= 128) {
+    // Row-wise: wave w copies staged rows w, w + NW, ..., lane l columns l, l + 64, ...; the
+    // loads of kStemRows rows x 4 column chunks are issued before any of them is stored.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    for (int col0 = 0; col0 < WP; col0 += 4 * 64)
+      for (int row0 = wave; row0 < nrow_st; row0 += NW * kStemRows) {
+        float v[kStemRows][4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (i0 + u * blockDim.x < nx) sx[i0 + u * blockDim.x] = v[u];
+        for (int u = 0; u < kStemRows; ++u) {
+          const int row = row0 + NW * u;
+          const int c = row / nrows;
+          const int ih = ih0 + row - c * nrows;
+          const bool row_ok = row < nrow_st && ih >= 0 && ih < p.H;
+          const float* xr = xn + ((int64_t)c * p.H + ih) * p.W;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int iw = col0 + 64 * j + lane - p.PW;
+            v[u][j] = row_ok && iw >= 0 && iw < p.W ? xr[iw] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kStemRows; ++u) {
+          const int row = row0 + NW * u;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int col = col0 + 64 * j + lane;
+            if (row < nrow_st && col < WP) sx[row * WP + col] = v[u][j];
+          }
+        }
+      }
+  } else {
+    // Flat (narrow rows): thread i copies staged floats i, i + NT, ..., FLAT loads in flight.
+    const StemDiv by_wp(WP), by_rows(nrows);
+    for (int i0 = threadIdx.x; i0 < nx; i0 += FLAT * NT) {
+      float v[FLAT];
+#pragma unroll
+      for (int u = 0; u < FLAT; ++u) {
+        const int i = i0 + u * NT;
+        const int row = (int)by_wp((uint32_t)i);
+        const int c = (int)by_rows((uint32_t)row);
+        const int ih = ih0 + row - c * nrows;
+        const int iw = i - row * WP - p.PW;
+        v[u] = i < nx && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W ? xn[((int64_t)c * p.H + ih) * p.W + iw] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < FLAT; ++u)
+        if (i0 + u * NT < nx) sx[i0 + u * NT] = v[u];
+    }
   }
   __syncthreads();
-  const int pix_ = pix0 + threadIdx.x;
+  const int part = CPT == 16 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kStemPix));
+  const int tpix = (int)(threadIdx.x % kStemPix);
+  const int pix_ = pix0 + tpix;
   const bool valid = pix_ < p.OH * p.OW;
-  if (!FUSE && !valid) return;
-  const int pix = valid ? pix_ : pix0;  // the fused variant keeps every thread for its barrier
+  if (MODE != kStemPool && !valid) return;
+  const int pix = valid ? pix_ : pix0;  // the pooling variant keeps every thread for its barriers
   const int oh = pix / p.OW;
   const int ow = pix - oh * p.OW;
   const float* xb = &sx[(oh - oh_first) * p.SH * WP + ow * p.SW];
-  float acc[16];
+  float acc[CPT];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+  for (int j = 0; j < CPT; ++j) acc[j] = 0.f;
+  // HWIO weights: tap (kh, kw, c) of channel f at ((kh*KW + kw)*C + c)*F + f
+  const int ch0 = fg * 16 + part * CPT;
+  const StemWPtr wg = (StemWPtr)(p.w + ch0);
+  const int wtap = p.F / 4;  // float4 stride between consecutive (kh, kw, c) taps
   for (int c = 0; c < p.C; ++c)
     for (int kh = 0; kh < p.KH; ++kh) {
       const float* xr = xb + (c * nrows + kh) * WP;
-      const float4* wr = sw4 + ((kh * KW) * p.C + c) * 4;
-      float xv[KW_ > 0 ? KW_ : 1];
-      float4 wv[KW_ > 0 ? KW_ : 1][4];
+      const StemWPtr wr = wg + ((kh * KW) * p.C + c) * wtap;
       if (KW_ > 0) {
+        float xv[KW_ > 0 ? KW_ : 1];
+#pragma unroll
+        for (int kw = 0; kw < (KW_ > 0 ? KW_ : 1); ++kw) xv[kw] = xr[kw];
 #pragma unroll
         for (int kw = 0; kw < (KW_ > 0 ? KW_ : 1); ++kw) {
-          xv[kw] = xr[kw];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) wv[kw][q] = wr[kw * p.C * 4 + q];
-        }
-#pragma unroll
-        for (int kw = 0; kw < (KW_ > 0 ? KW_ : 1); ++kw)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc[4 * q + 0] = __builtin_fmaf(xv[kw], wv[kw][q].x, acc[4 * q + 0]);
-            acc[4 * q + 1] = __builtin_fmaf(xv[kw], wv[kw][q].y, acc[4 * q + 1]);
-            acc[4 * q + 2] = __builtin_fmaf(xv[kw], wv[kw][q].z, acc[4 * q + 2]);
-            acc[4 * q + 3] = __builtin_fmaf(xv[kw], wv[kw][q].w, acc[4 * q + 3]);
+          for (int q = 0; q < CPT / 4; ++q) {
+            const float4_t w1 = wr[kw * p.C * wtap + q];
+            acc[4 * q + 0] = __builtin_fmaf(xv[kw], w1.x, acc[4 * q + 0]);
+            acc[4 * q + 1] = __builtin_fmaf(xv[kw], w1.y, acc[4 * q + 1]);
+            acc[4 * q + 2] = __builtin_fmaf(xv[kw], w1.z, acc[4 * q + 2]);
+            acc[4 * q + 3] = __builtin_fmaf(xv[kw], w1.w, acc[4 * q + 3]);
           }
+        }
       } else {
         for (int kw = 0; kw < KW; ++kw) {
           const float x1 = xr[kw];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float4 w1 = wr[kw * p.C * 4 + q];
+          for (int q = 0; q < CPT / 4; ++q) {
+            const float4_t w1 = wr[kw * p.C * wtap + q];
             acc[4 * q + 0] = __builtin_fmaf(x1, w1.x, acc[4 * q + 0]);
             acc[4 * q + 1] = __builtin_fmaf(x1, w1.y, acc[4 * q + 1]);
             acc[4 * q + 2] = __builtin_fmaf(x1, w1.z, acc[4 * q + 2]);
@@ -127,44 +222,90 @@ __global__ __launch_bounds__(256) void stem_conv_bn_lds_kernel(StemParams p) {
         }
       }
     }
-  const float* sc = p.scale + fg * 16;
-  const float* bi = p.bias + fg * 16;
-  if (!FUSE) {
-    float* o = p.out + (((int64_t)n * p.OH + oh) * p.OW + ow) * p.F + fg * 16;
+  const float* sc = p.scale + ch0;
+  const float* bi = p.bias + ch0;
+  if (MODE == kStemOut) {
+    float* o = p.out + (((int64_t)n * p.OH + oh) * p.OW + ow) * p.F + ch0;
 #pragma unroll
-    for (int j = 0; j < 16; j += 4)
+    for (int j = 0; j < CPT; j += 4)
       *reinterpret_cast<float4*>(o + j) =
           float4{__builtin_fmaf(acc[j], sc[j], bi[j]), __builtin_fmaf(acc[j + 1], sc[j + 1], bi[j + 1]),
                  __builtin_fmaf(acc[j + 2], sc[j + 2], bi[j + 2]), __builtin_fmaf(acc[j + 3], sc[j + 3], bi[j + 3])};
     return;
   }
-  // The neuron on the stem output repeated over T (models/sewresnet.py:201-202), the same
-  // arithmetic as repeat_neuron_kernel: 16 spike bits per t for this pixel.
-  float xf[16], v[16];
+  if (MODE == kStemSpikes) {
+    // The stem output (stored as by kStemOut when p.out is set) and the neuron over it
+    // repeated T times with the arithmetic of repeat_neuron_kernel; the CPT spike bits of
+    // (t, pixel) form 16-bit word fg of the pixel's F/16 words.
+    float xo[CPT];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < CPT; ++j) xo[j] = __builtin_fmaf(acc[j], sc[j], bi[j]);
+    const int64_t opix = ((int64_t)n * p.OH + oh) * p.OW + ow;
+    if (p.out) {
+      float* o = p.out + opix * p.F + ch0;
+#pragma unroll
+      for (int j = 0; j < CPT; j += 4)
+        *reinterpret_cast<float4*>(o + j) = float4{xo[j], xo[j + 1], xo[j + 2], xo[j + 3]};
+    }
+    float v[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      if (p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2) xo[j] *= p.np.rtau;  // exact
+      v[j] = 0.f;
+    }
+    const int64_t tstride = (int64_t)p.N * p.OH * p.OW * (p.F / 16);
+    uint16_t* so = p.spikes + opix * (p.F / 16) + ch0 / 16;
+    for (int t = 0; t < p.T; ++t) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        const float h = neuron_charge(p.np, v[j], xo[j]);
+        const bool spike = h >= p.np.vth;
+        v[j] = neuron_reset(p.np, h, spike);
+        word |= (uint32_t)spike << j;
+      }
+      so[t * tstride] = (uint16_t)word;
+    }
+    return;
+  }
+  // The neuron on the stem output repeated over T (models/sewresnet.py:201-202), the same
+  // arithmetic as repeat_neuron_kernel: CPT spike bits per t for this pixel, into the
+  // 16-bit word of (t, pixel) after the staged input (bits 0-7 from part 0, 8-15 from part 1).
+  uint16_t* sspk = reinterpret_cast<uint16_t*>(sx + ((nx + 3) & ~3));
+  float xf[CPT], v[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
     const float x = __builtin_fmaf(acc[j], sc[j], bi[j]);
     xf[j] = (p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2) ? x * p.np.rtau : x;  // exact
     v[j] = 0.f;
   }
-  const int npix = p.OH * p.OW;
-  const int fw = p.F / 16;  // 16-bit spike words per pixel
+  __syncthreads();  // every thread is done reading the staged input before spikes land next to it
   for (int t = 0; t < p.T; ++t) {
     uint32_t word = 0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < CPT; ++j) {
       const float h = neuron_charge(p.np, v[j], xf[j]);
       const bool spike = h >= p.np.vth;
       v[j] = neuron_reset(p.np, h, spike);
       word |= (uint32_t)spike << j;
     }
-    sspk[t * kStemPix + threadIdx.x] = (uint16_t)word;
-    if (p.spikes && valid) p.spikes[((int64_t)(t * p.N + n) * npix + pix) * fw + fg] = (uint16_t)word;
+    if (CPT == 16)
+      sspk[t * kStemPix + tpix] = (uint16_t)word;
+    else
+      reinterpret_cast<uint8_t*>(sspk)[(t * kStemPix + tpix) * 2 + part] = (uint8_t)word;
   }
   __syncthreads();
+  const int npix = p.OH * p.OW;
+  const int fw = p.F / 16;  // 16-bit spike words per pixel
+  if (p.spikes)
+    for (int i = threadIdx.x; i < p.T * npix; i += NT) {
+      const int t = i / npix;
+      const int q = i - t * npix;
+      p.spikes[((int64_t)(t * p.N + n) * npix + q) * fw + fg] = sspk[t * kStemPix + q];
+    }
   // max-pool of the spikes (models/sewresnet.py:143,203): OR over the in-image taps
   const int npool = p.POH * p.POW;
-  for (int i = threadIdx.x; i < p.T * npool; i += blockDim.x) {
+  for (int i = threadIdx.x; i < p.T * npool; i += NT) {
     const int t = i / npool;
     const int q = i - t * npool;
     const int ph = q / p.POW;
@@ -383,16 +524,64 @@ extern "C" int sengine_amd_stem_conv_bn(const sengine_conv_lif_desc* d, const fl
   const int64_t max_orows = std::min<int64_t>(p.OH, (kStemPix + p.OW - 1) / p.OW + 1);
   const int64_t staged = (int64_t)p.C * ((max_orows - 1) * p.SH + p.KH) * (p.W + 2 * p.PW);
   if (w_layout == SENGINE_WLAYOUT_HWIO && p.F % 16 == 0 && staged <= kStemLdsInput &&
-      (int64_t)p.KH * p.KW * p.C * 16 <= kStemLdsW) {
+      reinterpret_cast<uintptr_t>(weight) % 16 == 0) {
     const int64_t blocks = (int64_t)p.N * ((p.OH * p.OW + kStemPix - 1) / kStemPix) * (p.F / 16);
+    const size_t lds = (size_t)staged * sizeof(float);
     if (p.KW == 7)
-      hipLaunchKernelGGL((stem_conv_bn_lds_kernel<7, false>), dim3((unsigned)blocks), dim3(kStemPix), 0, stream, p);
+      hipLaunchKernelGGL((stem_conv_bn_lds_kernel<7, kStemOut, 16>), dim3((unsigned)blocks), dim3(kStemPix), lds,
+                         stream, p);
+    else if (p.KW == 3)
+      hipLaunchKernelGGL((stem_conv_bn_lds_kernel<3, kStemOut, 16>), dim3((unsigned)blocks), dim3(kStemPix), lds,
+                         stream, p);
     else
-      hipLaunchKernelGGL((stem_conv_bn_lds_kernel<0, false>), dim3((unsigned)blocks), dim3(kStemPix), 0, stream, p);
+      hipLaunchKernelGGL((stem_conv_bn_lds_kernel<0, kStemOut, 16>), dim3((unsigned)blocks), dim3(kStemPix), lds,
+                         stream, p);
   } else if (w_layout == SENGINE_WLAYOUT_HWIO)
     hipLaunchKernelGGL(stem_conv_bn_kernel<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL(stem_conv_bn_kernel<0>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sengine_amd_stem_conv_bn_neuron(const sengine_conv_lif_desc* d, const float* x, const float* weight,
+                                               const float* bn_scale, const float* bn_bias, float* out,
+                                               uint32_t* spikes, hipStream_t stream) {
+  if (!d || !x || !weight || !bn_scale || !bn_bias || !spikes)
+    return set_error(-1, "stem_conv_bn_neuron: null pointer");
+  if (d->B < 1 || d->C_in < 1 || d->H < 1 || d->W < 1 || d->C_out < 32 || d->C_out % 32 != 0 || d->KH < 1 ||
+      d->KW < 1 || d->stride_h < 1 || d->stride_w < 1 || d->pad_h < 0 || d->pad_w < 0 || d->dil_h != 1 ||
+      d->dil_w != 1)
+    return set_error(-2, "stem_conv_bn_neuron: invalid shape fields (C_out % 32 == 0, dilation 1)");
+  if (d->T < 1) return set_error(-2, "stem_conv_bn_neuron: T >= 1");
+  if (const char* why = neuron_invalid(d->neuron, d->tau)) return set_error(-2, why);
+  if (reinterpret_cast<uintptr_t>(weight) % 16 != 0)
+    return set_error(-2, "stem_conv_bn_neuron: weight must be 16-byte aligned");
+  StemParams p{};
+  p.x = x; p.w = weight; p.scale = bn_scale; p.bias = bn_bias; p.out = out;
+  p.N = d->B; p.C = d->C_in; p.H = d->H; p.W = d->W; p.F = d->C_out; p.KH = d->KH; p.KW = d->KW;
+  p.SH = d->stride_h; p.SW = d->stride_w; p.PH = d->pad_h; p.PW = d->pad_w;
+  p.OH = (d->H + 2 * d->pad_h - d->KH) / d->stride_h + 1;
+  p.OW = (d->W + 2 * d->pad_w - d->KW) / d->stride_w + 1;
+  if (p.OH < 1 || p.OW < 1) return set_error(-2, "stem_conv_bn_neuron: empty output");
+  const int64_t max_orows = std::min<int64_t>(p.OH, (kStemPix + p.OW - 1) / p.OW + 1);
+  const int64_t staged = (int64_t)p.C * ((max_orows - 1) * p.SH + p.KH) * (p.W + 2 * p.PW);
+  if (staged > kStemLdsInput)
+    return set_error(-2, "stem_conv_bn_neuron: the input rows of 256 output pixels do not fit in LDS; use "
+                         "stem_conv_bn + multistep_neuron_repeat");
+  p.spikes = reinterpret_cast<uint16_t*>(spikes);
+  p.T = d->T;
+  p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
+  const int64_t blocks = (int64_t)p.N * ((p.OH * p.OW + kStemPix - 1) / kStemPix) * (p.F / 16);
+  const size_t lds = (size_t)staged * sizeof(float);
+  if (p.KW == 7)
+    hipLaunchKernelGGL((stem_conv_bn_lds_kernel<7, kStemSpikes, 16>), dim3((unsigned)blocks), dim3(kStemPix), lds,
+                       stream, p);
+  else if (p.KW == 3)
+    hipLaunchKernelGGL((stem_conv_bn_lds_kernel<3, kStemSpikes, 16>), dim3((unsigned)blocks), dim3(kStemPix), lds,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((stem_conv_bn_lds_kernel<0, kStemSpikes, 16>), dim3((unsigned)blocks), dim3(kStemPix), lds,
+                       stream, p);
   return (int)hipGetLastError();
 }
 
@@ -422,18 +611,22 @@ extern "C" int sengine_amd_stem_conv_bn_lif_pool(const sengine_conv_lif_desc* d,
   if (p.POH < 1 || p.POW < 1) return set_error(-2, "stem_conv_bn_lif_pool: empty pooled output");
   // one workgroup holds a whole image's stem output for its 16 channels
   const int64_t staged = (int64_t)p.C * ((p.OH - 1) * p.SH + p.KH) * (p.W + 2 * p.PW);
-  if ((int64_t)p.OH * p.OW > kStemPix || staged > kStemLdsInput || (int64_t)p.KH * p.KW * p.C * 16 > kStemLdsW)
+  if ((int64_t)p.OH * p.OW > kStemPix || staged > kStemLdsInput)
     return set_error(-2, "stem_conv_bn_lif_pool: image too large for the fused stem (OH*OW <= 256 and the "
-                         "staged input / weights must fit in LDS); use stem_conv_bn + neuron + max-pool");
+                         "staged input must fit in LDS); use stem_conv_bn + neuron + max-pool");
+  if (reinterpret_cast<uintptr_t>(weight) % 16 != 0)
+    return set_error(-2, "stem_conv_bn_lif_pool: weight must be 16-byte aligned");
   p.spikes = reinterpret_cast<uint16_t*>(spikes);
   p.pooled = reinterpret_cast<uint16_t*>(pooled);
   p.T = d->T; p.PK = pool_k; p.PS = pool_stride; p.PP = pool_pad;
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
   const unsigned blocks = (unsigned)(p.N * (p.F / 16));
+  // staged input (padded to 4 floats) + T x kStemPix 16-bit spike words
+  const size_t lds = (size_t)((staged + 3) & ~3) * sizeof(float) + (size_t)p.T * kStemPix * sizeof(uint16_t);
   if (p.KW == 7)
-    hipLaunchKernelGGL((stem_conv_bn_lds_kernel<7, true>), dim3(blocks), dim3(kStemPix), 0, stream, p);
+    hipLaunchKernelGGL((stem_conv_bn_lds_kernel<7, kStemPool, 8>), dim3(blocks), dim3(2 * kStemPix), lds, stream, p);
   else
-    hipLaunchKernelGGL((stem_conv_bn_lds_kernel<0, true>), dim3(blocks), dim3(kStemPix), 0, stream, p);
+    hipLaunchKernelGGL((stem_conv_bn_lds_kernel<0, kStemPool, 8>), dim3(blocks), dim3(2 * kStemPix), lds, stream, p);
   return (int)hipGetLastError();
 }
 

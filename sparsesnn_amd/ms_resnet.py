@@ -6,11 +6,10 @@ real-valued stream: a block's input x is the previous block's `out + shortcut`, 
 fires its own neuron on it (sn1), and the shortcut adds x (or a 1x1 TDBN conv of x) back
 after conv_bn2.  MSResNetEngine maps that onto this library:
 
-* stem: dense fp32 conv 7x7/2 + folded BN on the B images (sengine_amd_stem_conv_bn); the
+* stem + first block's sn1: dense fp32 conv 7x7/2 + folded BN on the B images and the neuron
+  over that output repeated T times, one launch (sengine_amd_stem_conv_bn_neuron); the
   reference repeats the image over T before conv1 (:146-150), so the T copies are equal and
-  the stem runs once;
-* first block's sn1: the neuron over the stem output repeated T times
-  (sengine_amd_multistep_neuron_repeat);
+  the stem runs once, its fp32 output kept for block 0's shortcut;
 * per block: conv_bn1 + sn2 as one fused 2:4 Conv+BN+neuron launch (spike bits in and out);
   conv_bn2 + BN + shortcut add as the membrane-shortcut epilogue
   (sengine_amd_fused_sparse_conv_bn_add_neuron), which stores the block output y (fp32, the
@@ -26,6 +25,7 @@ time; the launch sequence is captured into one hipGraph.
 """
 from __future__ import annotations
 
+import dataclasses
 import math
 from dataclasses import dataclass
 
@@ -143,6 +143,9 @@ class MSResNetEngine:
         self.x_buf = torch.zeros(self.in_shape, dtype=torch.float32, device=self.dev)
         self.stem_out = torch.empty(batch, h, w, 64, dtype=torch.float32, device=self.dev)
         self.stem_spk = torch.empty(T * batch, h, w, 2, dtype=torch.int32, device=self.dev)
+        # conv1 + the first block's sn1 over its output repeated T times, in one launch
+        self.stem_nspec = dataclasses.replace(self.stem_spec, T=T, neuron=neuron, hard_reset=True, tau=self.tau,
+                                              v_threshold=self.vth, v_reset=0.0)
 
         TB = T * batch
         self.blocks: list[MSBlock] = []
@@ -197,10 +200,8 @@ class MSResNetEngine:
 
     # ------------------------------------------------------------------ execution
     def run_stem(self):
-        ops.stem_conv_bn(self.stem_spec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias, out=self.stem_out,
-                         layout=ops.WLAYOUT_HWIO)
-        ops.multistep_neuron_repeat(self.stem_out, self.T, self.neuron, self.tau, self.vth, 0.0,
-                                    out=self.stem_spk.view(self.T, -1))
+        ops.stem_conv_bn_neuron(self.stem_nspec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias,
+                                out=self.stem_out, spikes=self.stem_spk)
 
     def block_input(self, i: int):
         """(real-valued input, its spikes, timesteps of the real input) of block i."""
@@ -239,7 +240,7 @@ class MSResNetEngine:
 
     @property
     def launches(self) -> int:
-        return 2 + sum(3 if b.sc_spec is not None else 2 for b in self.blocks) + 1
+        return 1 + sum(3 if b.sc_spec is not None else 2 for b in self.blocks) + 1
 
     def capture(self):
         """Capture the whole forward into a hipGraph (replayed by forward())."""

@@ -22,7 +22,7 @@ __all__ = [
     "unpack_spikes", "fused_sparse_conv_bn_lif", "fused_sparse_conv_bn_lif_add", "stem_conv_bn",
     "multistep_neuron_repeat", "maxpool_spikes", "sew_head", "dense_conv_bn", "multistep_neuron", "SEngineError",
     "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "NEURON_MS", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
-    "neuron_code", "fused_sparse_conv_bn_add_neuron", "spiking_self_attention",
+    "neuron_code", "fused_sparse_conv_bn_add_neuron", "spiking_self_attention", "stem_conv_bn_neuron",
 ]
 
 
@@ -463,6 +463,39 @@ def stem_conv_bn_lif_pool(s: ConvSpec, x: torch.Tensor, weight_hwio: torch.Tenso
                                                 _ptr(spikes) if spikes is not None else None, _ptr(pooled),
                                                 _stream(x.device)), "stem_conv_bn_lif_pool")
     return pooled, spikes
+
+
+def stem_conv_bn_neuron(s: ConvSpec, x: torch.Tensor, weight_hwio: torch.Tensor, bn_scale: torch.Tensor,
+                        bn_bias: torch.Tensor, out: Optional[torch.Tensor] = None, spikes: Optional[torch.Tensor] = None,
+                        want_out: bool = True):
+    """Stem conv + folded BN (NHWC fp32 `out`, skipped when want_out is False and no `out`
+    is given) and the neuron of `s` over that output repeated s.T times (spike bits int32
+    (s.T*s.B, OH, OW, C_out/32), the layout of multistep_neuron_repeat on `out`), in one
+    launch.  Returns (out or None, spikes)."""
+    lib = _lib.load()
+    for t, n in ((x, "x"), (weight_hwio, "weight_hwio"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    _require_numel(x, s.B * s.C_in * s.H * s.W, torch.float32, "x")
+    _require_numel(weight_hwio, s.C_out * s.C_in * s.KH * s.KW, torch.float32, "weight_hwio")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    OH = (s.H + 2 * s.padding - s.KH) // s.stride + 1
+    OW = (s.W + 2 * s.padding - s.KW) // s.stride + 1
+    if out is None and want_out:
+        out = torch.empty(s.B, OH, OW, s.C_out, dtype=torch.float32, device=x.device)
+    elif out is not None:
+        _require_cuda(out, "out")
+        _require_numel(out, s.B * OH * OW * s.C_out, torch.float32, "out")
+    if spikes is None:
+        spikes = torch.empty(s.T * s.B, OH, OW, s.C_out // 32, dtype=torch.int32, device=x.device)
+    else:
+        _require_cuda(spikes, "spikes")
+        _require_numel(spikes, s.T * s.B * OH * OW * s.C_out // 32, torch.int32, "spikes")
+    d = make_desc(s)
+    check(lib.sengine_amd_stem_conv_bn_neuron(ctypes.byref(d), _ptr(x), _ptr(weight_hwio), _ptr(bn_scale),
+                                              _ptr(bn_bias), _ptr(out) if out is not None else None, _ptr(spikes),
+                                              _stream(x.device)), "stem_conv_bn_neuron")
+    return out, spikes
 
 
 def multistep_neuron_repeat(x: torch.Tensor, T: int, neuron: str = "lif", tau: float = 2.0, v_threshold: float = 1.0,

@@ -139,7 +139,7 @@ def test_engine_cfg3_shape_one_image(dev):
     x = torch.randn(1, 3, 224, 224, generator=torch.Generator().manual_seed(22))
     logits, xs = ms.forward(p, x, T=4, depth=34, kind="lif", tau=2.0, v_threshold=1.0, keep=True)
     eng = MSResNetEngine(p, batch=1, T=4, depth=34, neuron="lif", in_hw=(224, 224), device=dev)
-    assert eng.launches == 2 + 16 * 2 + 4 + 1
+    assert eng.launches == 1 + 16 * 2 + 4 + 1
     eager = eng.forward(x.to(dev)).clone()
     eng.capture()
     y = eng.forward(x.to(dev))

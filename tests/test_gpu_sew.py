@@ -39,6 +39,59 @@ def test_stem_conv_bn_matches_fp32_conv(dev, layout):
     assert torch.allclose(got, exp, rtol=1e-5, atol=1e-5), float((got - exp).abs().max())
 
 
+@pytest.mark.parametrize("B,C,H,W,F,K,S,P", [
+    (2, 3, 224, 224, 64, 7, 2, 3),   # ImageNet 7x7/2 stem (MS-ResNet, SEW-ResNet at 224)
+    (1, 3, 224, 224, 48, 3, 1, 1),   # Spikformer SPS proj_conv: 3x3/1, three 16-channel groups
+    (2, 2, 40, 300, 32, 5, 1, 2),    # padded row wider than 256: two column passes of the staging
+    (3, 4, 17, 23, 16, 3, 2, 0),     # odd sizes, no padding
+    (1, 1, 9, 9, 16, 1, 1, 0),       # 1x1 taps, runtime-KW variant
+])
+def test_stem_conv_bn_shapes(dev, B, C, H, W, F, K, S, P):
+    """The LDS stem kernel (HWIO weights) over stem shapes of the three networks and
+    edge geometries, against an fp32 conv + folded BN on the CPU."""
+    g = torch.Generator().manual_seed(B * 1000 + C * 100 + K)
+    x = torch.randn(B, C, H, W, generator=g)
+    w = torch.randn(F, C, K, K, generator=g) / (C * K * K) ** 0.5
+    sc = torch.rand(F, generator=g) + 0.5
+    bi = torch.randn(F, generator=g) * 0.1
+    spec = ops.ConvSpec(T=1, B=B, C_in=C, H=H, W=W, C_out=F, KH=K, KW=K, stride=S, padding=P)
+    out = ops.stem_conv_bn(spec, x.to(dev), w.permute(2, 3, 1, 0).contiguous().to(dev), sc.to(dev), bi.to(dev),
+                           layout=ops.WLAYOUT_HWIO)
+    exp = F_conv(x, w, S, P) * sc[:, None, None] + bi[:, None, None]
+    got = out.cpu().permute(0, 3, 1, 2)
+    assert got.shape == exp.shape
+    assert torch.allclose(got, exp, rtol=1e-5, atol=2e-5), float((got - exp).abs().max())
+
+
+def F_conv(x, w, stride, padding):
+    return F.conv2d(x.double(), w.double(), None, stride, padding).float()
+
+
+@pytest.mark.parametrize("K,S,P,pk_,ps,pp", [(3, 1, 1, 3, 2, 1), (5, 2, 2, 2, 2, 0)])
+def test_stem_lif_pool_fused_runtime_kw(dev, K, S, P, pk_, ps, pp):
+    """Fused stem + LIF + max-pool with a tap width other than 7 (runtime-KW variant)
+    against the separate entry points: bit-identical spikes and pool."""
+    import dataclasses
+    B, C, H, W, F_, T = 2, 3, 16, 16, 32, 4
+    g = torch.Generator().manual_seed(K * 10 + S)
+    x = torch.rand(B, C, H, W, generator=g).to(dev)
+    w = (torch.randn(K, K, C, F_, generator=g) * 1.5 / (C * K * K) ** 0.5).to(dev)
+    sc = (torch.rand(F_, generator=g) + 0.5).to(dev)
+    bi = (torch.randn(F_, generator=g) * 0.3 + 0.5).to(dev)
+    spec = ops.ConvSpec(T=1, B=B, C_in=C, H=H, W=W, C_out=F_, KH=K, KW=K, stride=S, padding=P)
+    OH = (H + 2 * P - K) // S + 1
+    nspec = dataclasses.replace(spec, T=T, neuron="lif", hard_reset=True, tau=2.0, v_threshold=1.0, v_reset=0.0)
+    stem = ops.stem_conv_bn(spec, x, w, sc, bi, layout=ops.WLAYOUT_HWIO)
+    spk = ops.multistep_neuron_repeat(stem.view(-1), T, "lif", 2.0, 1.0, 0.0)
+    pool = ops.maxpool_spikes(spk, T * B, OH, OH, F_, pk_, ps, pp)
+    spk_f = torch.empty(T * B, OH, OH, F_ // 32, dtype=torch.int32, device=dev)
+    pool_f, _ = ops.stem_conv_bn_lif_pool(nspec, x, w, sc, bi, pk_, ps, pp, spikes=spk_f)
+    torch.cuda.synchronize()
+    assert torch.equal(spk_f.view(-1).cpu(), spk.view(-1).cpu())
+    assert torch.equal(pool_f.view(-1).cpu(), pool.view(-1).cpu())
+    assert int(spk.view(torch.int32).ne(0).sum()) > 0
+
+
 @pytest.mark.parametrize("neuron,v_reset,T,B", [("lif", 0.0, 4, 3), ("if", 0.0, 4, 2), ("lif", None, 2, 2),
                                                 ("if", None, 5, 1)])
 def test_stem_lif_pool_fused_matches_separate(dev, neuron, v_reset, T, B):
@@ -61,6 +114,36 @@ def test_stem_lif_pool_fused_matches_separate(dev, neuron, v_reset, T, B):
     torch.cuda.synchronize()
     assert torch.equal(spk_f.view(-1).cpu(), spk.view(-1).cpu())
     assert torch.equal(pool_f.view(-1).cpu(), pool.view(-1).cpu())
+    assert int(spk.view(torch.int32).ne(0).sum()) > 0  # the case spikes
+
+
+@pytest.mark.parametrize("B,H,F,K,S,P,neuron,T,v_reset", [
+    (2, 224, 64, 7, 2, 3, "ms", 4, 0.0),    # MS-ResNet-34 stem + first sn1
+    (1, 64, 64, 7, 2, 3, "lif", 3, None),   # soft reset, odd T
+    (2, 40, 32, 3, 1, 1, "if", 5, 0.0),     # 3x3/1, one 32-channel word
+])
+def test_stem_conv_bn_neuron_matches_separate(dev, B, H, F, K, S, P, neuron, T, v_reset):
+    """One-launch stem + neuron over the repeated output against stem_conv_bn followed by
+    multistep_neuron_repeat: the fp32 output and the spike bits bit-identical, also with
+    the fp32 output not requested."""
+    import dataclasses
+    g = torch.Generator().manual_seed(H + F + K)
+    x = torch.rand(B, 3, H, H, generator=g).to(dev)
+    w = (torch.randn(K, K, 3, F, generator=g) * 2.0 / (3 * K * K) ** 0.5).to(dev)
+    sc = (torch.rand(F, generator=g) + 0.5).to(dev)
+    bi = (torch.randn(F, generator=g) * 0.3).to(dev)
+    spec = ops.ConvSpec(T=1, B=B, C_in=3, H=H, W=H, C_out=F, KH=K, KW=K, stride=S, padding=P)
+    tau, vth = (0.25, 0.5) if neuron == "ms" else (2.0, 1.0)
+    nspec = dataclasses.replace(spec, T=T, neuron=neuron, hard_reset=v_reset is not None, tau=tau, v_threshold=vth,
+                                v_reset=0.0 if v_reset is None else v_reset)
+    ref_out = ops.stem_conv_bn(spec, x, w, sc, bi, layout=ops.WLAYOUT_HWIO)
+    ref_spk = ops.multistep_neuron_repeat(ref_out.view(-1), T, neuron, tau, vth, v_reset)
+    out, spk = ops.stem_conv_bn_neuron(nspec, x, w, sc, bi)
+    _, spk2 = ops.stem_conv_bn_neuron(nspec, x, w, sc, bi, want_out=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), ref_out.cpu())
+    assert torch.equal(spk.view(-1).cpu(), ref_spk.view(-1).cpu())
+    assert torch.equal(spk2.view(-1).cpu(), ref_spk.view(-1).cpu())
     assert int(spk.view(torch.int32).ne(0).sum()) > 0  # the case spikes
 
 
