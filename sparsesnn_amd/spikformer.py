@@ -5,9 +5,9 @@ spiking self-attention and MLP with residual adds (:59-150), mean over tokens an
 Linear head (:273-288).  SpikformerEngine maps it onto this library:
 
 * SPS: the first conv (C_in = 3, dense) runs once on the B images (the reference repeats the
-  image over T before it, :283-285, so the T copies are equal) through
-  sengine_amd_stem_conv_bn, its LIF over the repeated output through
-  sengine_amd_multistep_neuron_repeat; the other four convs are fused 2:4 Conv+BN+LIF
+  image over T before it, :283-285, so the T copies are equal), in the same launch as its
+  LIF over the repeated output (sengine_amd_stem_conv_bn_neuron, the fp32 conv output not
+  stored); the other four convs are fused 2:4 Conv+BN+LIF
   launches on spike bits, with spike max-pools after the third and fourth, and the
   relative-position conv's spikes added to the max-pooled features in its epilogue (an
   integer activation of 2 bit planes).  Channel counts that are not multiples of 64
@@ -24,6 +24,7 @@ Every buffer is allocated once; the launch sequence is captured into one hipGrap
 """
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass
 
 import torch
@@ -136,7 +137,10 @@ class SpikformerEngine:
         self.stem_w = w0p.permute(2, 3, 1, 0).contiguous().to(self.dev)  # HWIO
         self.stem_scale, self.stem_bias = sc.to(self.dev), bi.to(self.dev)
         self.x_buf = torch.zeros(self.in_shape, dtype=torch.float32, device=self.dev)
-        self.stem_out = torch.empty(batch, H, W, P8, dtype=torch.float32, device=self.dev)
+        # the stem's LIF over its output repeated T times runs in the stem launch; the fp32
+        # output itself is not stored
+        self.stem_nspec = dataclasses.replace(self.stem_spec, T=T, neuron="lif", hard_reset=True, tau=2.0,
+                                              v_threshold=1.0, v_reset=0.0)
         self.s0 = torch.empty(TB, H, W, P8 // 32, **i32)
         self.c1 = self._conv(p, "proj_conv1", c8, c4, P8, P4, H, W)
         self.s1 = torch.empty(TB, H, W, P4 // 32, **i32)
@@ -235,9 +239,8 @@ class SpikformerEngine:
                                          res_planes, out_planes, out=out)
 
     def run_sps(self):
-        ops.stem_conv_bn(self.stem_spec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias, out=self.stem_out,
-                         layout=ops.WLAYOUT_HWIO)
-        ops.multistep_neuron_repeat(self.stem_out, self.T, "lif", 2.0, 1.0, 0.0, out=self.s0.view(self.T, -1))
+        ops.stem_conv_bn_neuron(self.stem_nspec, self.x_buf, self.stem_w, self.stem_scale, self.stem_bias,
+                                want_out=False, spikes=self.s0)
         self._fused(self.c1, self.s0, self.s1)
         self._fused(self.c2, self.s1, self.s2)
         H, W = self.stem_spec.H, self.stem_spec.W
@@ -280,7 +283,7 @@ class SpikformerEngine:
 
     @property
     def launches(self) -> int:
-        return 8 + 8 * len(self.blocks) + 1
+        return 7 + 8 * len(self.blocks) + 1
 
     def capture(self):
         """Capture the whole forward into a hipGraph (replayed by forward())."""

@@ -162,7 +162,7 @@ def test_engine_end_to_end_graph(dev, sf_case):
     assert float((final != xs[-1]).float().mean()) <= 1e-3
     err = float((eager.cpu() - logits).abs().max())
     assert err < 5e-2, err
-    assert eng.launches == 8 + 8 * 4 + 1
+    assert eng.launches == 7 + 8 * 4 + 1
 
 
 def test_engine_cfg4_shape_one_image(dev):
