@@ -416,7 +416,7 @@ __global__ __launch_bounds__(256) void maxpool_bits_kernel(PoolParams p) {
 // `planes` bit planes, NHWC with planes*C channels, (T*B, HW) positions.  Workgroup (image,
 // slice of the outputs): the per-channel sums are exact integers, counted once per
 // workgroup -- thread (word column wi, position slice) walks its slice of the T*HW positions
-// with coalesced word reads and keeps 32 bit counters in registers, then adds them into LDS
+// with coalesced word reads and counts in SWAR lanes and registers, then adds into LDS
 // -- and scaled once into fp32 features; each wave then owns HEAD_OPW outputs at a time
 // (looping over the workgroup's slice of the outputs), its lanes split the reduction over C
 // (coalesced reads of the Linear weight rows) and a cross-lane sum finishes each output.
@@ -436,28 +436,71 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void sew_head_kernel(HeadParams p) {
+template <int NT>
+__global__ __launch_bounds__(NT) void sew_head_kernel(HeadParams p) {
   __shared__ int cnt[HEAD_MAX_PC];
   __shared__ float feat[HEAD_MAX_PC];
   const int bimg = blockIdx.x;
   const int words = p.planes * p.C / 32;
   const int npos = p.T * p.HW;  // (t, s) positions of this image
-  for (int i = threadIdx.x; i < p.planes * p.C; i += blockDim.x) cnt[i] = 0;
+  for (int i = threadIdx.x; i < p.planes * p.C; i += NT) cnt[i] = 0;
   __syncthreads();
-  const int per = words < (int)blockDim.x ? words : (int)blockDim.x;  // word columns per pass
-  const int nslice = (int)blockDim.x / per;
+  const int per = words < NT ? words : NT;  // word columns per pass
+  const int nslice = NT / per;
   const int slice = (int)threadIdx.x / per;
+  // Bit counting in SWAR lanes: nibble n of a / b / c / d counts channel 4n / 4n+1 / 4n+2 /
+  // 4n+3 of the word column (3 VALU per word and lane set, flushed every 15 words before a
+  // nibble can overflow), their even / odd nibbles go into byte counters (flushed every
+  // 17 x 15 = 255 words), and those into 32 integer counters: ~12 VALU per word instead of
+  // two per bit.  Exact.
   for (int wbase = 0; wbase < words; wbase += per) {
     const int wi = wbase + (int)threadIdx.x % per;
     if (slice >= nslice || wi >= words) continue;
     uint32_t c32[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j) c32[j] = 0;
-    for (int q = slice; q < npos; q += nslice) {
-      const int t = q / p.HW;
-      const uint32_t w = p.in[((int64_t)(t * p.B + bimg) * p.HW + (q - t * p.HW)) * words + wi];
+    const uint32_t* src = p.in + (int64_t)bimg * p.HW * words + wi;
+    // position q = t*HW + s of this image sits at ((t*B + bimg)*HW + s) * words: walked
+    // incrementally (no division per word)
+    int sp = slice % p.HW;
+    int64_t off = ((int64_t)(slice / p.HW) * p.B * p.HW + sp) * words;
+    const int64_t step = (int64_t)nslice * words, tjump = (int64_t)(p.B - 1) * p.HW * words;
+    int left = (npos - slice + nslice - 1) / nslice;  // positions this thread reads
+    while (left > 0) {
+      uint32_t by[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+      for (int r = 0; r < 17 && left > 0; ++r) {
+        uint32_t w[15];
 #pragma unroll
-      for (int j = 0; j < 32; ++j) c32[j] += (w >> j) & 1u;
+        for (int k = 0; k < 15; ++k) {
+          w[k] = k < left ? src[off] : 0u;
+          sp += nslice;
+          off += step;
+          while (sp >= p.HW) {
+            sp -= p.HW;
+            off += tjump;
+          }
+        }
+        left -= 15;
+        uint32_t a = 0, b = 0, c = 0, d = 0;
+#pragma unroll
+        for (int k = 0; k < 15; ++k) {
+          a += w[k] & 0x11111111u;
+          b += (w[k] >> 1) & 0x11111111u;
+          c += (w[k] >> 2) & 0x11111111u;
+          d += (w[k] >> 3) & 0x11111111u;
+        }
+        by[0] += a & 0x0f0f0f0fu; by[1] += (a >> 4) & 0x0f0f0f0fu;
+        by[2] += b & 0x0f0f0f0fu; by[3] += (b >> 4) & 0x0f0f0f0fu;
+        by[4] += c & 0x0f0f0f0fu; by[5] += (c >> 4) & 0x0f0f0f0fu;
+        by[6] += d & 0x0f0f0f0fu; by[7] += (d >> 4) & 0x0f0f0f0fu;
+      }
+      // byte m of by[2l + h] counts channel 8m + 4h + l
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int m = 0; m < 4; ++m) c32[8 * m + 4 * h + l] += (by[2 * l + h] >> (8 * m)) & 0xffu;
     }
 #pragma unroll
     for (int j = 0; j < 32; ++j)
@@ -465,7 +508,7 @@ __global__ __launch_bounds__(256) void sew_head_kernel(HeadParams p) {
   }
   __syncthreads();
   // channel c of plane pl is bit (pl*C + c) of a position's words
-  for (int c = threadIdx.x; c < p.C; c += blockDim.x) {
+  for (int c = threadIdx.x; c < p.C; c += NT) {
     int sum = 0;
     for (int pl = 0; pl < p.planes; ++pl) sum += cnt[pl * p.C + c] << pl;
     // mean over HW then over T: both exact or one rounding for the integer sums here
@@ -473,7 +516,7 @@ __global__ __launch_bounds__(256) void sew_head_kernel(HeadParams p) {
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  const int nwave_out = (int)(blockDim.x >> 6) * HEAD_OPW;  // outputs per pass of the workgroup
+  const int nwave_out = (NT >> 6) * HEAD_OPW;  // outputs per pass of the workgroup
   for (int base = blockIdx.y * nwave_out; base < p.N_out; base += gridDim.y * nwave_out) {
     const int o0 = base + (int)(threadIdx.x >> 6) * HEAD_OPW;
     float acc[HEAD_OPW];
@@ -662,9 +705,16 @@ extern "C" int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C,
       (int64_t)planes * C > HEAD_MAX_PC)
     return set_error(-2, "sew_head: invalid shape (C % 32 == 0, 1 <= planes <= 5, planes * C <= 8192)");
   HeadParams p{in, fc_weight, fc_bias, out, T, B, HW, C, planes, N_out};
-  // a few output slices per image, so that about 512 workgroups share the chip
-  const int passes = (N_out + 4 * HEAD_OPW - 1) / (4 * HEAD_OPW);
-  const int slices = std::max(1, std::min(passes, (512 + B - 1) / B));
-  hipLaunchKernelGGL(sew_head_kernel, dim3((unsigned)B, (unsigned)slices), dim3(256), 0, stream, p);
+  const int64_t words_per_image = (int64_t)T * HW * planes * C / 32;
+  if (words_per_image >= 16384) {
+    // counting dominates (token grids): one 1024-thread workgroup per image counts once
+    hipLaunchKernelGGL(sew_head_kernel<1024>, dim3((unsigned)B, 1u), dim3(1024), 0, stream, p);
+  } else {
+    // a few output slices per image (each counts its image again), so that about 512
+    // workgroups share the chip
+    const int passes = (N_out + 4 * HEAD_OPW - 1) / (4 * HEAD_OPW);
+    const int slices = std::max(1, std::min(passes, (512 + B - 1) / B));
+    hipLaunchKernelGGL(sew_head_kernel<256>, dim3((unsigned)B, (unsigned)slices), dim3(256), 0, stream, p);
+  }
   return (int)hipGetLastError();
 }

@@ -182,18 +182,23 @@ def test_maxpool_spikes(dev, H, W, C):
     assert np.array_equal(got, exp.view(2, 3, C, OH, OW).numpy())
 
 
-@pytest.mark.parametrize("planes,HW,C,N_out", [(2, 1, 64, 10), (1, 4, 64, 10), (3, 2, 96, 37), (2, 1, 512, 100),
-                                              (1, 49, 512, 1000), (3, 9, 2720, 7), (1, 3, 8192, 65)])
-def test_sew_head(dev, planes, HW, C, N_out):
-    rng = np.random.default_rng(planes)
-    T, B = 4, 3
+@pytest.mark.parametrize("planes,HW,C,N_out,T", [
+    (2, 1, 64, 10, 4), (1, 4, 64, 10, 4), (3, 2, 96, 37, 4), (2, 1, 512, 100, 4), (1, 49, 512, 1000, 4),
+    (3, 9, 2720, 7, 4), (1, 3, 8192, 65, 4),
+    # counting-heavy grids (one 1024-thread workgroup per image): Spikformer's token grid,
+    # a position stride above HW (T=64, HW=1), a ragged one
+    (5, 3136, 384, 1000, 4), (4, 1, 2048, 10, 64), (3, 700, 224, 5, 4)])
+def test_sew_head(dev, planes, HW, C, N_out, T):
+    rng = np.random.default_rng(planes + HW)
+    B = 3
     a = rng.integers(0, 1 << planes, size=(T, B, C, HW, 1))
     bits = torch.from_numpy(pk.seq_to_planes(a, planes).view(np.int32)).to(dev)
     w = torch.randn(N_out, C) * 0.1
     b = torch.randn(N_out) * 0.1
     y = ops.sew_head(bits, T, B, HW, C, planes, w.to(dev), b.to(dev)).cpu()
-    feat = torch.from_numpy(a.astype(np.float32)).flatten(3).mean(3).mean(0)
-    assert torch.allclose(y, feat @ w.T + b, atol=1e-5)
+    feat = torch.from_numpy(a.astype(np.float64)).flatten(3).mean(3).mean(0)
+    exp = (feat @ w.T.double() + b.double()).float()
+    assert torch.allclose(y, exp, rtol=1e-5, atol=1e-5), float((y - exp).abs().max())
 
 
 @pytest.mark.parametrize("k,stride,in_planes,res_planes,C_in,C_out,H", [(3, 1, 2, 2, 64, 64, 9), (3, 1, 1, 1, 128, 64, 8),
