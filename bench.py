@@ -187,9 +187,7 @@ def bench_e2e(dev, warmup: int, iters: int):
     b.record(stream)
     torch.cuda.synchronize(dev)
     s = a.elapsed_time(b) * 1e-3 / iters
-    stem_launches = 1 if eng.stem_fused else 3
-    return dict(params=params, x=x.cpu(), batch_s=s,
-                launches=stem_launches + sum(3 if blk.downsample is not None else 2 for blk in eng.blocks) + 1)
+    return dict(params=params, x=x.cpu(), batch_s=s, launches=eng.launches)
 
 
 def cpu_e2e(params, x, budget_s=6.0, min_runs=2):

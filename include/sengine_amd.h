@@ -155,6 +155,21 @@ int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const v
                                          hipStream_t stream);
 
 /*
+ * Two fused Conv + BN + neuron nodes that read the same input `data` -- a residual block's
+ * conv1 and its 1x1 downsample (models/sewresnet.py:50-66: conv1 -> bn1 -> sn1 and
+ * downsample(x) on the same x) -- with the results of sengine_amd_fused_sparse_conv_bn_lif
+ * (d0, data, values0, meta0, NULL, scale0, bias0, spikes0, NULL, NULL) followed by the same
+ * for d1 (bit-identical).  Both descriptors must share T, B, C_in, H, W and in_enc.  When both
+ * convs run on the split-K small-output kernel with the same epilogue, it is one launch (a
+ * launch each otherwise).  No state or traces.
+ */
+int sengine_amd_fused_sparse_conv_bn_lif_pair(const sengine_conv_lif_desc* d0, const sengine_conv_lif_desc* d1,
+                                              const void* data, const void* values0, const void* meta0,
+                                              const float* bn_scale0, const float* bn_bias0, void* spikes0,
+                                              const void* values1, const void* meta1, const float* bn_scale1,
+                                              const float* bn_bias1, void* spikes1, hipStream_t stream);
+
+/*
  * Fused Conv + BN + neuron with the SEW 'ADD' residual connection in the epilogue:
  * out = spike + residual (models/sewresnet.py:58-59; replaces conv2d_bn_if_add_t4_kernel,
  * sengine/kernels/conv2d_bn_if_t4.py:813-911, whose output is fp16 spike + residual).

@@ -168,14 +168,14 @@ struct SmallOperands {
   uint2 bw[T];
 };
 
+// Workgroup (bx, G): positions bx*16 .. bx*16+15, output channels G*64 .. G*64+63.
 template <int T, int OUT_ENC, int PLANES, int MODE>
-__global__ __launch_bounds__(64 * kSmallWaves) void fused_smallm_kernel(FusedParams p) {
+__device__ __forceinline__ void smallm_body(const FusedParams& p, const int bx, const int G) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4;
   const int col = lane & 15;
-  const int G = blockIdx.y;
-  const int m = blockIdx.x * 16 + col;
+  const int m = bx * 16 + col;
   constexpr int TR = T < 4 ? T : 4;  // timesteps per reduction round
   __shared__ float sCoef[4][64];
   __shared__ float4_t red[kSmallWaves][TR][4][64];
@@ -296,6 +296,22 @@ __global__ __launch_bounds__(64 * kSmallWaves) void fused_smallm_kernel(FusedPar
                                  p.x_trace, p.sew, &res);
 }
 
+template <int T, int OUT_ENC, int PLANES, int MODE>
+__global__ __launch_bounds__(64 * kSmallWaves) void fused_smallm_kernel(FusedParams p) {
+  smallm_body<T, OUT_ENC, PLANES, MODE>(p, (int)blockIdx.x, (int)blockIdx.y);
+}
+
+// Two convs that read the same input (a residual block's conv1 and its downsample) in one
+// grid: channel groups y < g0 are p0's, the rest p1's; position tiles past a conv's M exit.
+// Each workgroup runs exactly the code of the single-conv kernel.
+template <int T, int OUT_ENC, int PLANES, int MODE>
+__global__ __launch_bounds__(64 * kSmallWaves) void fused_smallm_pair_kernel(FusedParams p0, FusedParams p1, int g0) {
+  const bool second = (int)blockIdx.y >= g0;
+  const FusedParams& p = second ? p1 : p0;
+  if ((int)blockIdx.x * 16 >= p.M) return;
+  smallm_body<T, OUT_ENC, PLANES, MODE>(p, (int)blockIdx.x, second ? (int)blockIdx.y - g0 : (int)blockIdx.y);
+}
+
 template <int T>
 static hipError_t launch_smallm(const FusedParams& p, int out_enc, int planes, int mode, hipStream_t s) {
   const dim3 grid((unsigned)((p.M + 15) / 16), (unsigned)(p.F / 64));
@@ -312,6 +328,25 @@ static hipError_t launch_smallm(const FusedParams& p, int out_enc, int planes, i
   SENGINE_SMALLM_CASE(SENGINE_ENC_F16, 1, EPI_GENERIC)
   SENGINE_SMALLM_CASE(SENGINE_ENC_F16, 2, EPI_GENERIC)
 #undef SENGINE_SMALLM_CASE
+  return hipErrorInvalidValue;
+}
+
+template <int T>
+static hipError_t launch_smallm_pair(const FusedParams& p0, const FusedParams& p1, int out_enc, int planes, int mode,
+                                     hipStream_t s) {
+  const int g0 = p0.F / 64;
+  const dim3 grid((unsigned)((std::max(p0.M, p1.M) + 15) / 16), (unsigned)(g0 + p1.F / 64));
+  const dim3 block(64 * kSmallWaves);
+#define SENGINE_SMALLM_PAIR_CASE(OE, PL, MD)                                        \
+  if (out_enc == OE && planes == PL && mode == MD) {                               \
+    hipLaunchKernelGGL((fused_smallm_pair_kernel<T, OE, PL, MD>), grid, block, 0, s, p0, p1, g0); \
+    return hipGetLastError();                                                      \
+  }
+  SENGINE_SMALLM_PAIR_CASE(SENGINE_ENC_BITS, 1, EPI_LIF_HARD)
+  SENGINE_SMALLM_PAIR_CASE(SENGINE_ENC_BITS, 1, EPI_IF_HARD)
+  SENGINE_SMALLM_PAIR_CASE(SENGINE_ENC_BITS, 1, EPI_GENERIC)
+  SENGINE_SMALLM_PAIR_CASE(SENGINE_ENC_BITS, 2, EPI_GENERIC)
+#undef SENGINE_SMALLM_PAIR_CASE
   return hipErrorInvalidValue;
 }
 
@@ -342,10 +377,25 @@ static hipError_t launch_fused_enc(const FusedParams& p, int in_enc, int out_enc
 
 using namespace sengine;
 
-static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const void* blob_values,
-                       const void* blob_meta, float* state, const float* bn_scale, const float* bn_bias, void* spikes,
-                       float* h_trace, float* x_trace, const SewAdd& sew, hipStream_t stream) {
+// Where fused_entry sends a descriptor.
+enum FusedRoute { kRouteTiled, kRouteSmall, kRouteDirect };
+
+struct FusedPlan {
   Geometry geo;
+  FusedRoute route;
+  FusedParams p;  // kRouteSmall / kRouteDirect
+  int mode;       // kRouteSmall: epilogue mode
+};
+
+// Checks a descriptor and its pointers and picks the kernel.  Small outputs run in the flat
+// layout (their weight blob is built that way): the split-K small-M kernel for bit inputs,
+// the direct kernel on the flat view otherwise.  Other bit inputs: tile kernel for 3x3 /
+// stride 1 / pad 1 and 1x1 / pad 0, else the LDS-staged kernel (its per-thread tap mask holds
+// up to 64 taps), else the direct-gather kernel.
+static int plan_fused(const sengine_conv_lif_desc* d, const void* data, const void* blob_values,
+                      const void* blob_meta, float* state, const float* bn_scale, const float* bn_bias, void* spikes,
+                      float* h_trace, float* x_trace, const SewAdd& sew, FusedPlan& plan) {
+  Geometry& geo = plan.geo;
   int rc = check_desc(d, &geo, /*sparse=*/true);
   if (rc) return rc;
   if (!data || !blob_values || !blob_meta || !bn_scale || !bn_bias || !spikes)
@@ -358,22 +408,18 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
     return set_error(-2, "fused_sparse_conv_bn_lif: out_enc must be BITS or F16");
   if (geo.M > (1ll << 30)) return set_error(-2, "fused_sparse_conv_bn_lif: B*OH*OW too large");
 
-  // Small outputs run in the flat layout (their weight blob is built that way): the split-K
-  // small-M kernel for bit inputs, the direct kernel on the flat view otherwise.  Other bit
-  // inputs: tile kernel for 3x3 / stride 1 / pad 1 and 1x1 / pad 0, else the LDS-staged
-  // kernel (its per-thread tap mask holds up to 64 taps), else the direct-gather kernel below.
   const int choice = fused_kernel_choice();
   const bool flat = flat_layout(d, geo);
   // few 64-position x 64-channel work units: split the reduction inside workgroups instead
   const bool small = d->in_enc == SENGINE_ENC_BITS && choice == 0 &&
                      ((geo.M + 63) / 64) * (int64_t)(d->C_out / 64) < kSmallMaxUnits;
-  if (!flat && !small && d->in_enc == SENGINE_ENC_BITS && choice != 1) {
-    const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace, sew};
-    if ((choice == 0 || choice == 3) && tile_eligible(d)) return (int)launch_fused_bits_tile(d, geo, args, stream);
-    if (d->KH * d->KW <= 64) return (int)launch_fused_bits_lds(d, geo, args, stream);
+  if (!flat && !small && d->in_enc == SENGINE_ENC_BITS && choice != 1 &&
+      (((choice == 0 || choice == 3) && tile_eligible(d)) || d->KH * d->KW <= 64)) {
+    plan.route = kRouteTiled;
+    return 0;
   }
 
-  FusedParams p;
+  FusedParams& p = plan.p;
   p.in = static_cast<const uint8_t*>(data);
   p.wvals = static_cast<const half8_t*>(blob_values);
   p.wmeta = static_cast<const uint32_t*>(blob_meta);
@@ -406,19 +452,38 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
     p.in_t_stride = d->B;
   }
   if ((flat || small) && d->in_enc == SENGINE_ENC_BITS && choice != 1) {
-    {
-      // fast epilogue modes for the common case (one weight plane, bit output)
-      int mode = epilogue_mode(p.np, h_trace != nullptr || x_trace != nullptr || sew.real_out != nullptr);
-      if (d->weight_planes != 1 || d->out_enc != SENGINE_ENC_BITS) mode = EPI_GENERIC;
-      switch (d->T) {
-        case 1: return (int)launch_smallm<1>(p, d->out_enc, d->weight_planes, mode, stream);
-        case 2: return (int)launch_smallm<2>(p, d->out_enc, d->weight_planes, mode, stream);
-        case 4: return (int)launch_smallm<4>(p, d->out_enc, d->weight_planes, mode, stream);
-        default: return (int)launch_smallm<8>(p, d->out_enc, d->weight_planes, mode, stream);
-      }
+    plan.route = kRouteSmall;
+    // fast epilogue modes for the common case (one weight plane, bit output)
+    plan.mode = epilogue_mode(p.np, h_trace != nullptr || x_trace != nullptr || sew.real_out != nullptr);
+    if (d->weight_planes != 1 || d->out_enc != SENGINE_ENC_BITS) plan.mode = EPI_GENERIC;
+  } else {
+    plan.route = kRouteDirect;
+  }
+  return 0;
+}
+
+static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const void* blob_values,
+                       const void* blob_meta, float* state, const float* bn_scale, const float* bn_bias, void* spikes,
+                       float* h_trace, float* x_trace, const SewAdd& sew, hipStream_t stream) {
+  FusedPlan plan;
+  const int rc = plan_fused(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace, sew,
+                            plan);
+  if (rc) return rc;
+  if (plan.route == kRouteTiled) {
+    const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace, sew};
+    const int choice = fused_kernel_choice();
+    if ((choice == 0 || choice == 3) && tile_eligible(d)) return (int)launch_fused_bits_tile(d, plan.geo, args, stream);
+    return (int)launch_fused_bits_lds(d, plan.geo, args, stream);
+  }
+  const FusedParams& p = plan.p;
+  if (plan.route == kRouteSmall) {
+    switch (d->T) {
+      case 1: return (int)launch_smallm<1>(p, d->out_enc, d->weight_planes, plan.mode, stream);
+      case 2: return (int)launch_smallm<2>(p, d->out_enc, d->weight_planes, plan.mode, stream);
+      case 4: return (int)launch_smallm<4>(p, d->out_enc, d->weight_planes, plan.mode, stream);
+      default: return (int)launch_smallm<8>(p, d->out_enc, d->weight_planes, plan.mode, stream);
     }
   }
-
   dim3 grid((unsigned)((p.M + 63) / 64), (unsigned)(p.F / 64));
   hipError_t e;
   switch (d->T) {
@@ -437,6 +502,38 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
                                                     hipStream_t stream) {
   return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace,
                      SewAdd{nullptr, 0, 0, 0, nullptr, nullptr}, stream);
+}
+
+extern "C" int sengine_amd_fused_sparse_conv_bn_lif_pair(const sengine_conv_lif_desc* d0,
+                                                         const sengine_conv_lif_desc* d1, const void* data,
+                                                         const void* values0, const void* meta0,
+                                                         const float* bn_scale0, const float* bn_bias0, void* spikes0,
+                                                         const void* values1, const void* meta1,
+                                                         const float* bn_scale1, const float* bn_bias1, void* spikes1,
+                                                         hipStream_t stream) {
+  if (!d0 || !d1) return set_error(-1, "fused_sparse_conv_bn_lif_pair: null descriptor");
+  if (d0->T != d1->T || d0->B != d1->B || d0->C_in != d1->C_in || d0->H != d1->H || d0->W != d1->W ||
+      d0->in_enc != d1->in_enc)
+    return set_error(-2, "fused_sparse_conv_bn_lif_pair: the two convs must read the same input (T, B, C_in, H, W, "
+                         "in_enc)");
+  const SewAdd none{nullptr, 0, 0, 0, nullptr, nullptr};
+  FusedPlan a, b;
+  int rc = plan_fused(d0, data, values0, meta0, nullptr, bn_scale0, bn_bias0, spikes0, nullptr, nullptr, none, a);
+  if (rc) return rc;
+  rc = plan_fused(d1, data, values1, meta1, nullptr, bn_scale1, bn_bias1, spikes1, nullptr, nullptr, none, b);
+  if (rc) return rc;
+  if (a.route == kRouteSmall && b.route == kRouteSmall && a.mode == b.mode && d0->out_enc == d1->out_enc &&
+      d0->weight_planes == d1->weight_planes) {
+    switch (d0->T) {
+      case 1: return (int)launch_smallm_pair<1>(a.p, b.p, d0->out_enc, d0->weight_planes, a.mode, stream);
+      case 2: return (int)launch_smallm_pair<2>(a.p, b.p, d0->out_enc, d0->weight_planes, a.mode, stream);
+      case 4: return (int)launch_smallm_pair<4>(a.p, b.p, d0->out_enc, d0->weight_planes, a.mode, stream);
+      default: return (int)launch_smallm_pair<8>(a.p, b.p, d0->out_enc, d0->weight_planes, a.mode, stream);
+    }
+  }
+  rc = fused_entry(d0, data, values0, meta0, nullptr, bn_scale0, bn_bias0, spikes0, nullptr, nullptr, none, stream);
+  if (rc) return rc;
+  return fused_entry(d1, data, values1, meta1, nullptr, bn_scale1, bn_bias1, spikes1, nullptr, nullptr, none, stream);
 }
 
 extern "C" int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_desc* d, const void* data,

@@ -23,6 +23,7 @@ __all__ = [
     "multistep_neuron_repeat", "maxpool_spikes", "sew_head", "dense_conv_bn", "multistep_neuron", "SEngineError",
     "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "NEURON_MS", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
     "neuron_code", "fused_sparse_conv_bn_add_neuron", "spiking_self_attention", "stem_conv_bn_neuron",
+    "fused_sparse_conv_bn_lif_pair",
 ]
 
 
@@ -261,6 +262,52 @@ def fused_sparse_conv_bn_lif(s: ConvSpec, data: torch.Tensor, values: torch.Tens
         _ptr(out), _ptr(h_trace), _ptr(x_trace), _stream(dev))
     check(rc, "fused_sparse_conv_bn_lif")
     return out
+
+
+def fused_sparse_conv_bn_lif_pair(s0: ConvSpec, s1: ConvSpec, data: torch.Tensor, values0: torch.Tensor,
+                                  meta0: torch.Tensor, bn_scale0: torch.Tensor, bn_bias0: torch.Tensor,
+                                  values1: torch.Tensor, meta1: torch.Tensor, bn_scale1: torch.Tensor,
+                                  bn_bias1: torch.Tensor, out0: Optional[torch.Tensor] = None,
+                                  out1: Optional[torch.Tensor] = None):
+    """Two fused 2:4 Conv + BN + neuron nodes on the same input (a block's conv1 and its
+    downsample), one launch where both run on the small-output kernel.  Returns (out0, out1),
+    each as fused_sparse_conv_bn_lif would."""
+    lib = _lib.load()
+    for s in (s0, s1):
+        if (s.T, s.B, s.C_in, s.H, s.W, s.in_enc) != (s0.T, s0.B, s0.C_in, s0.H, s0.W, s0.in_enc):
+            raise SEngineError("fused_sparse_conv_bn_lif_pair: the two convs must read the same input")
+    dev = data.device
+    dt, n_in = _enc_numel(s0.in_enc, s0.T * s0.B * s0.H * s0.W * s0.C_in)
+    _require_cuda(data, "data")
+    _require_numel(data, n_in, dt, "data")
+    outs = []
+    for s, values, meta, sc, bi, out, tag in ((s0, values0, meta0, bn_scale0, bn_bias0, out0, "0"),
+                                               (s1, values1, meta1, bn_scale1, bn_bias1, out1, "1")):
+        OH, OW, M, _ = geometry(s)
+        d = make_desc(s)
+        vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib.sengine_amd_sparse_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)),
+              "sparse_blob_bytes")
+        for t, n in ((values, "values"), (meta, "meta"), (sc, "bn_scale"), (bi, "bn_bias")):
+            _require_cuda(t, n + tag)
+        if values.numel() * values.element_size() != vb.value or meta.numel() * meta.element_size() != mb.value:
+            raise SEngineError(f"fused_sparse_conv_bn_lif_pair: weight blob {tag} does not match its descriptor")
+        _require_numel(sc, s.C_out, torch.float32, "bn_scale" + tag)
+        _require_numel(bi, s.C_out, torch.float32, "bn_bias" + tag)
+        odt, n_out = _enc_numel(s.out_enc, s.T * M * s.C_out)
+        if out is None:
+            last = s.C_out // 32 if s.out_enc == ENC_BITS else s.C_out
+            out = torch.empty(s.T * s.B, OH, OW, last, dtype=odt, device=dev)
+        else:
+            _require_cuda(out, "out" + tag)
+            _require_numel(out, n_out, odt, "out" + tag)
+        outs.append(out)
+    d0, d1 = make_desc(s0), make_desc(s1)
+    check(lib.sengine_amd_fused_sparse_conv_bn_lif_pair(
+        ctypes.byref(d0), ctypes.byref(d1), _ptr(data), _ptr(values0), _ptr(meta0), _ptr(bn_scale0), _ptr(bn_bias0),
+        _ptr(outs[0]), _ptr(values1), _ptr(meta1), _ptr(bn_scale1), _ptr(bn_bias1), _ptr(outs[1]), _stream(dev)),
+        "fused_sparse_conv_bn_lif_pair")
+    return outs[0], outs[1]
 
 
 def fused_sparse_conv_bn_lif_add(s: ConvSpec, data: torch.Tensor, values: torch.Tensor, meta: torch.Tensor,

@@ -228,11 +228,15 @@ class SEWResNet18Engine:
         blk = self.blocks[i]
         x = self.block_input(i) if x is None else x
         c1, c2, ds = blk.conv1, blk.conv2, blk.downsample
-        ops.fused_sparse_conv_bn_lif(c1.spec, x.view(-1), c1.values, c1.meta, c1.scale, c1.bias, out=blk.bufs["s1"])
         if ds is not None:
-            ops.fused_sparse_conv_bn_lif(ds.spec, x, ds.values, ds.meta, ds.scale, ds.bias, out=blk.bufs["ds"])
+            # conv1 and the downsample read the same x: one launch for both
+            ops.fused_sparse_conv_bn_lif_pair(c1.spec, ds.spec, x.view(-1), c1.values, c1.meta, c1.scale, c1.bias,
+                                              ds.values, ds.meta, ds.scale, ds.bias, out0=blk.bufs["s1"],
+                                              out1=blk.bufs["ds"])
             identity = blk.bufs["ds"]
         else:
+            ops.fused_sparse_conv_bn_lif(c1.spec, x.view(-1), c1.values, c1.meta, c1.scale, c1.bias,
+                                         out=blk.bufs["s1"])
             identity = x
         ops.fused_sparse_conv_bn_lif_add(c2.spec, blk.bufs["s1"].view(-1), c2.values, c2.meta, c2.scale, c2.bias,
                                          identity, blk.id_planes, blk.out_planes, out=blk.bufs["out"])
@@ -246,6 +250,22 @@ class SEWResNet18Engine:
         for i in range(len(self.blocks)):
             self.run_block(i)
         self.run_head()
+
+    @property
+    def launches(self) -> int:
+        """Kernel launches per forward: a block's conv1 and downsample share one launch when
+        both run on the library's small-output kernel (fewer than 128 units of 64 positions
+        x 64 channels)."""
+        def small(spec):
+            M = spec.B * ((spec.H + 2 * spec.padding - spec.KH) // spec.stride + 1) * \
+                ((spec.W + 2 * spec.padding - spec.KW) // spec.stride + 1)
+            return ((M + 63) // 64) * (spec.C_out // 64) < 128
+        n = (1 if self.stem_fused else 3) + 1
+        for blk in self.blocks:
+            n += 2
+            if blk.downsample is not None and not (small(blk.conv1.spec) and small(blk.downsample.spec)):
+                n += 1
+        return n
 
     def capture(self):
         """Capture the whole forward into a hipGraph (replayed by forward())."""
