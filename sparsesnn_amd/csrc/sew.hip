@@ -452,7 +452,7 @@ __global__ __launch_bounds__(NT) void sew_head_kernel(HeadParams p) {
   // 4n+3 of the word column (3 VALU per word and lane set, flushed every 15 words before a
   // nibble can overflow), their even / odd nibbles go into byte counters (flushed every
   // 17 x 15 = 255 words), and those into 32 integer counters: ~12 VALU per word instead of
-  // two per bit.  Exact.
+  // two per bit; the last < 15 positions of a thread are added bit by bit.  Exact.
   for (int wbase = 0; wbase < words; wbase += per) {
     const int wi = wbase + (int)threadIdx.x % per;
     if (slice >= nslice || wi >= words) continue;
@@ -466,19 +466,22 @@ __global__ __launch_bounds__(NT) void sew_head_kernel(HeadParams p) {
     int64_t off = ((int64_t)(slice / p.HW) * p.B * p.HW + sp) * words;
     const int64_t step = (int64_t)nslice * words, tjump = (int64_t)(p.B - 1) * p.HW * words;
     int left = (npos - slice + nslice - 1) / nslice;  // positions this thread reads
-    while (left > 0) {
+    auto advance = [&]() {
+      sp += nslice;
+      off += step;
+      while (sp >= p.HW) {
+        sp -= p.HW;
+        off += tjump;
+      }
+    };
+    while (left >= 15) {
       uint32_t by[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-      for (int r = 0; r < 17 && left > 0; ++r) {
+      for (int r = 0; r < 17 && left >= 15; ++r) {
         uint32_t w[15];
 #pragma unroll
         for (int k = 0; k < 15; ++k) {
-          w[k] = k < left ? src[off] : 0u;
-          sp += nslice;
-          off += step;
-          while (sp >= p.HW) {
-            sp -= p.HW;
-            off += tjump;
-          }
+          w[k] = src[off];
+          advance();
         }
         left -= 15;
         uint32_t a = 0, b = 0, c = 0, d = 0;
@@ -501,6 +504,13 @@ __global__ __launch_bounds__(NT) void sew_head_kernel(HeadParams p) {
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int m = 0; m < 4; ++m) c32[8 * m + 4 * h + l] += (by[2 * l + h] >> (8 * m)) & 0xffu;
+    }
+    // the last < 15 positions (all of them on small grids): one add per bit
+    for (; left > 0; --left) {
+      const uint32_t w = src[off];
+      advance();
+#pragma unroll
+      for (int j = 0; j < 32; ++j) c32[j] += (w >> j) & 1u;
     }
 #pragma unroll
     for (int j = 0; j < 32; ++j)
