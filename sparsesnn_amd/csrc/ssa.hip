@@ -8,8 +8,9 @@
 //
 //   ssa_kv_kernel:     KV[t, b, h] = K^T V (int32 d x d).  A workgroup of 16 waves per
 //                      (t*B + b, h): each wave turns 64 tokens' head slices into
-//                      per-channel 64-token masks with ballots (bit transposition into
-//                      LDS), then threads sum popcount(K_i & V_j) over the token masks.
+//                      per-channel 64-token masks with ballots (bit transposition; lane i
+//                      collects mask i, one wave-wide LDS store per group), then threads
+//                      sum popcount(K_i & V_j) over the token masks.
 //   ssa_attend_kernel: X = Q KV on MFMA (v_mfma_f32_16x16x32_f16: A = KV^T as two exact
 //                      6-bit fp16 pieces pre-scaled by a power of two, B = Q expanded
 //                      from bits, one fp32 accumulator), the neuron over T in
@@ -49,11 +50,14 @@ constexpr int kSsaKvWaves = 16;
 
 template <int D>
 __global__ __launch_bounds__(64 * kSsaKvWaves) void ssa_kv_kernel(SsaParams p) {
-  extern __shared__ uint64_t masks[];  // K masks [G][D], then V masks [G][D], then KV sums
+  // K masks [G][D], then V masks [G][VS] (mask j at j + j/32: a read of masks j0+u by lane
+  // groups j0 = 0, 16, 32, 48 hits four different bank pairs), then the KV sums
+  extern __shared__ uint64_t masks[];
+  constexpr int VS = D + 2;
   const int G = (p.N + 63) >> 6;
   uint64_t* Km = masks;
   uint64_t* Vm = masks + (size_t)D * G;
-  uint32_t* sum = reinterpret_cast<uint32_t*>(masks + (size_t)2 * D * G);  // [D][D]
+  uint32_t* sum = reinterpret_cast<uint32_t*>(masks + (size_t)(D + VS) * G);  // [D][D]
   for (int idx = threadIdx.x; idx < D * D; idx += blockDim.x) sum[idx] = 0u;
   const int tb = blockIdx.x / p.H;
   const int h = blockIdx.x - tb * p.H;
@@ -76,16 +80,23 @@ __global__ __launch_bounds__(64 * kSsaKvWaves) void ssa_kv_kernel(SsaParams p) {
     const uint32_t k0 = (uint32_t)ksn, k1 = (uint32_t)(ksn >> 32);
     const uint32_t v0 = (uint32_t)vsn, v1 = (uint32_t)(vsn >> 32);
     load(g + kSsaKvWaves, ksn, vsn);
-    uint64_t* kd = Km + (size_t)g * D;
-    uint64_t* vd = Vm + (size_t)g * D;
+    // compile-time bit masks: one test and one ballot per bit; lane i keeps mask i, so the
+    // group's masks go to LDS as two wave-wide stores instead of 2*D single-lane ones
+    int km0 = 0, km1 = 0, vm0 = 0, vm1 = 0;  // lane i: mask i (low, high word)
 #pragma unroll
-    for (int i = 0; i < D; ++i) {  // compile-time bit masks: one test and one ballot per bit
+    for (int i = 0; i < D; ++i) {
       const uint64_t mk = __ballot(((i < 32 ? k0 : k1) >> (i & 31)) & 1u);
       const uint64_t mv = __ballot(((i < 32 ? v0 : v1) >> (i & 31)) & 1u);
-      if (lane == 0) {
-        kd[i] = mk;
-        vd[i] = mv;
-      }
+      // the ballot's SGPRs come from a VALU compare: wait states before v_writelane reads
+      // them (the compiler's hazard recognizer does not look inside inline asm)
+      asm("s_nop 4\n\tv_writelane_b32 %0, %1, %2" : "+v"(km0) : "s"((uint32_t)mk), "i"(i));
+      asm("v_writelane_b32 %0, %1, %2" : "+v"(km1) : "s"((uint32_t)(mk >> 32)), "i"(i));
+      asm("s_nop 4\n\tv_writelane_b32 %0, %1, %2" : "+v"(vm0) : "s"((uint32_t)mv), "i"(i));
+      asm("v_writelane_b32 %0, %1, %2" : "+v"(vm1) : "s"((uint32_t)(mv >> 32)), "i"(i));
+    }
+    if (lane < D) {
+      Km[(size_t)g * D + lane] = ((uint64_t)(uint32_t)km1 << 32) | (uint32_t)km0;
+      Vm[(size_t)g * VS + lane + (lane >> 5)] = ((uint64_t)(uint32_t)vm1 << 32) | (uint32_t)vm0;
     }
   }
   __syncthreads();
@@ -103,7 +114,7 @@ __global__ __launch_bounds__(64 * kSsaKvWaves) void ssa_kv_kernel(SsaParams p) {
     for (int u = 0; u < 16; ++u) acc[u] = 0;
     for (int g = r; g < G; g += R) {
       const uint64_t ki = Km[(size_t)g * D + i];
-      const uint64_t* vj = Vm + (size_t)g * D + j0;
+      const uint64_t* vj = Vm + (size_t)g * VS + j0 + (j0 >> 5);  // j0 % 32 + 16 <= 32: one shift for all u
 #pragma unroll
       for (int u = 0; u < 16; ++u) acc[u] += (uint32_t)__popcll(ki & vj[u]);
     }
@@ -266,7 +277,7 @@ extern "C" int sengine_amd_ssa_kv(int32_t T, int32_t B, int32_t N, int32_t C, in
   SsaParams p{};
   p.k = k_bits; p.v = v_bits; p.kv = kv;
   p.T = T; p.B = B; p.N = N; p.C = C; p.H = heads; p.d = C / heads;
-  const size_t lds = 2 * (size_t)p.d * ((N + 63) / 64) * sizeof(uint64_t) + (size_t)p.d * p.d * sizeof(uint32_t);
+  const size_t lds = (2 * (size_t)p.d + 2) * ((N + 63) / 64) * sizeof(uint64_t) + (size_t)p.d * p.d * sizeof(uint32_t);
   if (lds > 65536) return set_error(-2, "ssa_kv: (C/heads) * ceil(N/64) too large for the token masks in LDS");
   const dim3 grid((unsigned)(T * B * heads)), block(64 * kSsaKvWaves);
   switch (p.d) {
