@@ -23,6 +23,7 @@ def _conv(dev, g, spec):
     (64, 256, 2, 512, "lif"),   # layer4.0: 1x1 output (flat layout)
     (8, 128, 7, 256, "if"),     # ragged position tiles, IF
     (32, 64, 56, 128, "lif"),   # large output: tile / LDS kernels, two launches
+    (3, 64, 5, 64, "lif"),      # ragged: 27 positions, a partial 16-position tile
 ])
 def test_pair_matches_two_single_calls(dev, B, C_in, H, C_out, neuron):
     g = torch.Generator().manual_seed(B + C_in + H)
