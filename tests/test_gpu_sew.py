@@ -63,6 +63,39 @@ def test_stem_conv_bn_shapes(dev, B, C, H, W, F, K, S, P):
     assert torch.allclose(got, exp, rtol=1e-5, atol=2e-5), float((got - exp).abs().max())
 
 
+@pytest.mark.parametrize("shift", [4, 2])
+def test_stem_weight_alignment(dev, shift):
+    """HWIO weights at a 16-byte (shift 4 floats) or 8-byte (shift 2) offset: the scalar-load
+    kernel takes the first, the per-output kernel the second; both match the conv.  The
+    fused entries need 16-byte aligned weights and say so."""
+    import dataclasses
+    g = torch.Generator().manual_seed(shift)
+    B, C, H, F_, K = 2, 3, 32, 64, 7
+    x = torch.randn(B, C, H, H, generator=g)
+    w = torch.randn(F_, C, K, K, generator=g) / (C * K * K) ** 0.5
+    sc = torch.rand(F_, generator=g) + 0.5
+    bi = torch.randn(F_, generator=g) * 0.1
+    n = K * K * C * F_
+    buf = torch.zeros(n + shift, device=dev)
+    buf[shift:] = w.permute(2, 3, 1, 0).reshape(-1).to(dev)
+    wv = buf[shift:]
+    spec = ops.ConvSpec(T=1, B=B, C_in=C, H=H, W=H, C_out=F_, KH=K, KW=K, stride=2, padding=3)
+    out = ops.stem_conv_bn(spec, x.to(dev), wv, sc.to(dev), bi.to(dev), layout=ops.WLAYOUT_HWIO)
+    exp = F_conv(x, w, 2, 3) * sc[:, None, None] + bi[:, None, None]
+    assert torch.allclose(out.cpu().permute(0, 3, 1, 2), exp, rtol=1e-5, atol=2e-5)
+    nspec = dataclasses.replace(spec, T=4, neuron="lif")
+    if shift % 4 == 0:
+        _, spk = ops.stem_conv_bn_neuron(nspec, x.to(dev), wv, sc.to(dev), bi.to(dev))
+        ref = ops.multistep_neuron_repeat(out.view(-1), 4, "lif", 2.0, 1.0, 0.0)
+        torch.cuda.synchronize()
+        assert torch.equal(spk.view(-1).cpu(), ref.view(-1).cpu())
+    else:
+        with pytest.raises(ops.SEngineError):
+            ops.stem_conv_bn_neuron(nspec, x.to(dev), wv, sc.to(dev), bi.to(dev))
+        with pytest.raises(ops.SEngineError):
+            ops.stem_conv_bn_lif_pool(nspec, x.to(dev), wv, sc.to(dev), bi.to(dev))
+
+
 def F_conv(x, w, stride, padding):
     return F.conv2d(x.double(), w.double(), None, stride, padding).float()
 
