@@ -155,6 +155,24 @@ int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const v
                                          hipStream_t stream);
 
 /*
+ * Names the kernel instance that sengine_amd_fused_sparse_conv_bn_lif (and its _add /
+ * _add_neuron forms) would launch for descriptor d, without launching anything: the
+ * route (tile / lds / smallm / direct) and its compile-time specialisation, e.g.
+ * "tile<T=4,KS=3,TR=7,TC=7,GR=7,GPW=1,KSP=2,PF=2,out=bits,epi=lif_hard> grid=256".
+ * flags: SENGINE_PLAN_* bits saying which optional buffers the call would pass (traces,
+ * state, a SEW residual, the membrane-shortcut output).  Honours the same environment
+ * switches and sengine_amd_set_fused_kernel choice as a launch.  Host-only (no GPU
+ * needed).  This build's own introspection: the reference's compiler records the chosen
+ * TileLang config on the node instead (sengine/build/tilelang_compiler.py:537,649).
+ * Returns 0, or a negative code when d is invalid or buf (len bytes) is too small.
+ */
+#define SENGINE_PLAN_TRACES 1
+#define SENGINE_PLAN_STATE 2
+#define SENGINE_PLAN_SEW_ADD 4
+#define SENGINE_PLAN_SHORTCUT 8
+int sengine_amd_fused_plan(const sengine_conv_lif_desc* d, int32_t flags, char* buf, size_t len);
+
+/*
  * Two fused Conv + BN + neuron nodes that read the same input `data` -- a residual block's
  * conv1 and its 1x1 downsample (models/sewresnet.py:50-66: conv1 -> bn1 -> sn1 and
  * downsample(x) on the same x) -- with the results of sengine_amd_fused_sparse_conv_bn_lif

@@ -26,6 +26,8 @@
 #include "epilogue.h"
 #include "internal.h"
 
+#include <stdio.h>
+
 namespace sengine {
 
 struct FusedParams {
@@ -493,6 +495,40 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
     default: e = launch_fused_enc<8>(p, d->in_enc, d->out_enc, d->weight_planes, grid, stream); break;
   }
   return (int)e;
+}
+
+extern "C" int sengine_amd_fused_plan(const sengine_conv_lif_desc* d, int32_t flags, char* buf, size_t len) {
+  if (!d || !buf || len == 0) return set_error(-1, "fused_plan: null descriptor or buffer");
+  const bool traces = flags & SENGINE_PLAN_TRACES;
+  const bool state = flags & SENGINE_PLAN_STATE;
+  const bool shortcut = flags & SENGINE_PLAN_SHORTCUT;
+  // never dereferenced: the plan only checks that the pointers are present
+  const void* nz = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+  float* fz = reinterpret_cast<float*>(static_cast<uintptr_t>(256));
+  const SewAdd sew{(flags & SENGINE_PLAN_SEW_ADD) ? static_cast<const uint8_t*>(nz) : nullptr, 1, 2, d->C_out,
+                   nullptr, shortcut ? fz : nullptr};
+  FusedPlan plan;
+  const int rc = plan_fused(d, nz, nz, nz, state ? fz : nullptr, fz, fz, fz, traces ? fz : nullptr,
+                            traces ? fz : nullptr, sew, plan);
+  if (rc) return rc;
+  static const char* const kEpi[] = {"generic", "lif_hard", "if_hard"};
+  const NeuronParams np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
+  const int mode = epilogue_mode(np, traces || shortcut);
+  int n;
+  if (plan.route == kRouteTiled) {
+    const int choice = fused_kernel_choice();
+    n = (choice == 0 || choice == 3) && tile_eligible(d) ? describe_tile(d, plan.geo, mode, buf, len)
+                                                         : describe_lds(d, plan.geo, mode, buf, len);
+  } else if (plan.route == kRouteSmall) {
+    n = snprintf(buf, len, "smallm<T=%d,planes=%d,out=%s,epi=%s,flat=%d>", d->T, d->weight_planes,
+                 d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16", kEpi[plan.mode], flat_layout(d, plan.geo) ? 1 : 0);
+  } else {
+    n = snprintf(buf, len, "direct<T=%d,in=%s,planes=%d,out=%s,flat=%d>", d->T,
+                 d->in_enc == SENGINE_ENC_BITS ? "bits" : "f16", d->weight_planes,
+                 d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16", flat_layout(d, plan.geo) ? 1 : 0);
+  }
+  if (n < 0 || (size_t)n >= len) return set_error(-2, "fused_plan: buffer too small");
+  return 0;
 }
 
 extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const void* data,

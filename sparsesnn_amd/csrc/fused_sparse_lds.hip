@@ -25,6 +25,8 @@
 #include "epilogue.h"
 #include "internal.h"
 
+#include <stdio.h>
+
 #include <stdlib.h>
 
 namespace sengine {
@@ -329,6 +331,16 @@ static int choose_gpw(int T, int pt, int64_t M, int F) {
   if (forced == 1 || forced == 2) return forced;
   const int64_t waves = ((M + 63) / 64) * (F / 128) * 4;
   return waves >= 1024 ? 2 : 1;
+}
+
+int describe_lds(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len) {
+  static const char* const kEpi[] = {"generic", "lif_hard", "if_hard"};
+  const int pt = choose_pt(d->T);
+  const int gpw = choose_gpw(d->T, pt, geo.M, d->C_out);
+  const bool fast = d->out_enc == SENGINE_ENC_BITS && (mode == EPI_LIF_HARD || mode == EPI_IF_HARD);
+  return snprintf(buf, len, "lds<T=%d,PT=%d,GPW=%d,planes=%d,out=%s,epi=%s>", d->T, d->T == 8 ? 1 : pt,
+                  d->T == 8 ? 1 : gpw, d->weight_planes, d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16",
+                  fast ? kEpi[mode] : "generic");
 }
 
 hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,

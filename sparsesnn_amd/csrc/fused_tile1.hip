@@ -2,6 +2,7 @@
 // stride), and the host-side choice between tile shapes and channel blocking.
 #include "tile_kernel.h"
 
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -51,8 +52,84 @@ bool tile_eligible(const sengine_conv_lif_desc* d) {
   return k3 || k1;
 }
 
+// The tile kernel instance for a descriptor: tile shape, channel groups per wave, reduction
+// split and prefetch depth (the launchers' template arguments) and the grid.  False when
+// the grid would not fit.
+bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice& c) {
+  c.k3 = d->KH == 3;
+  c.shape = 0;
+  if (c.k3) {
+    if (d->T == 4) {
+      const int forced = env_int_now("SENGINE_AMD_TILE_SHAPE", -1);  // tuning: 0, 1, 2
+      if (forced >= 0 && forced < 3) {
+        c.shape = forced;
+      } else {
+        double best = 0;
+        for (int i = 0; i < 3; ++i) {
+          const double cost = shape_cost(kShapes3[i], geo.OH, geo.OW);
+          if (i == 0 || cost < best) best = cost, c.shape = i;
+        }
+      }
+    }
+    const TileShape s = kShapes3[c.shape];
+    c.tiles_w = (geo.OW + s.TC - 1) / s.TC;
+    c.tiles_per_image = ((geo.OH + s.TR - 1) / s.TR) * c.tiles_w;
+    c.ntiles = d->B * c.tiles_per_image;
+  } else {
+    c.tiles_w = c.tiles_per_image = 0;
+    c.ntiles = (int)((geo.M + 63) / 64);
+  }
+
+  // Two 64-channel groups per wave halve the B bytes per SMFMAC but double the
+  // accumulators (2 waves per SIMD instead of 3) and halve the workgroup count; used when
+  // the grid still gives every CU two workgroups.  SENGINE_AMD_TILE_GPW=1|2 overrides.
+  c.gpw = (!c.k3 && d->T == 4 && d->C_out % 128 == 0 && (int64_t)c.ntiles * (d->C_out / 128) >= 512) ? 2 : 1;
+  const int fg = env_int_now("SENGINE_AMD_TILE_GPW", 0);
+  if (d->T == 4 && d->C_out % 128 == 0 && (fg == 1 || fg == 2)) c.gpw = fg;
+  if ((int64_t)c.ntiles * (d->C_out / (64 * c.gpw)) > 0x7fffffff) return false;
+
+  // Split the reduction over two wave sets when the grid gives at most one workgroup per
+  // CU (deep layers: few, long workgroups, one wave per SIMD); with more workgroups the
+  // doubled LDS footprint costs more than it gains (measured).  SENGINE_AMD_TILE_KSPLIT
+  // =1|2 overrides.
+  c.ksplit = 1;
+  if (c.k3 && d->T == 4 && c.gpw == 1 && (d->C_in / 64) % 2 == 0) {
+    c.ksplit = (int64_t)c.ntiles * (d->C_out / 64) <= 256 ? 2 : 1;
+    const int fk = env_int_now("SENGINE_AMD_TILE_KSPLIT", 0);
+    if (fk == 1 || fk == 2) c.ksplit = fk;
+  }
+  // Two-deep operand prefetch where the grid leaves at most two workgroups per CU (two waves
+  // per SIMD: registers to spare, SMFMAC issue waiting on latency).  SENGINE_AMD_TILE_PF=1|2
+  // overrides.
+  c.pf = 1;
+  if (c.k3 && d->T == 4 && c.gpw == 1) {
+    c.pf = (int64_t)c.ntiles * (d->C_out / 64) <= 512 ? 2 : 1;
+    const int fp = env_int_now("SENGINE_AMD_TILE_PF", 0);
+    if (fp == 1 || fp == 2) c.pf = fp;
+  }
+  return true;
+}
+
+int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len) {
+  TileChoice c;
+  if (!choose_tile(d, geo, c)) return snprintf(buf, len, "none (grid too large)");
+  static const char* const kEpi[] = {"generic", "lif_hard", "if_hard"};
+  const char* oe = d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16";
+  const char* epi = d->out_enc == SENGINE_ENC_BITS ? kEpi[mode] : "generic";
+  if (c.k3) {
+    const TileShape s = kShapes3[c.shape];
+    return snprintf(buf, len, "tile<T=%d,KS=3,TR=%d,TC=%d,GR=%d,GPW=%d,KSP=%d,PF=%d,out=%s,epi=%s> grid=%lld",
+                    d->T, s.TR, s.TC, s.GR, c.gpw, c.ksplit, c.pf, oe, epi,
+                    (long long)c.ntiles * (d->C_out / (64 * c.gpw)));
+  }
+  return snprintf(buf, len, "tile<T=%d,KS=1,GPW=%d,out=%s,epi=%s> grid=%lld", d->T, c.gpw, oe, epi,
+                  (long long)c.ntiles * (d->C_out / (64 * c.gpw)));
+}
+
 hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
                                   hipStream_t stream) {
+  TileChoice c;
+  if (!choose_tile(d, geo, c)) return hipErrorInvalidValue;
   TileParams p;
   p.in = static_cast<const uint8_t*>(a.data);
   p.wvals = static_cast<const u32x4_t*>(a.wvals);
@@ -71,61 +148,12 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
   p.enc_scale = 1.0f / kBitSpikeValue;
   p.sew = a.sew;
+  p.tiles_w = c.tiles_w;
+  p.tiles_per_image = c.tiles_per_image;
+  p.ntiles = c.ntiles;
   const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr || a.sew.real_out != nullptr);
-  const bool k3 = d->KH == 3;
-
-  int shape = 0;
-  if (k3) {
-    if (d->T == 4) {
-      const int forced = env_int_now("SENGINE_AMD_TILE_SHAPE", -1);  // tuning: 0, 1, 2
-      if (forced >= 0 && forced < 3) {
-        shape = forced;
-      } else {
-        double best = 0;
-        for (int i = 0; i < 3; ++i) {
-          const double c = shape_cost(kShapes3[i], geo.OH, geo.OW);
-          if (i == 0 || c < best) best = c, shape = i;
-        }
-      }
-    }
-    const TileShape s = kShapes3[shape];
-    p.tiles_w = (geo.OW + s.TC - 1) / s.TC;
-    p.tiles_per_image = ((geo.OH + s.TR - 1) / s.TR) * p.tiles_w;
-    p.ntiles = d->B * p.tiles_per_image;
-  } else {
-    p.tiles_w = p.tiles_per_image = 0;
-    p.ntiles = (int)((geo.M + 63) / 64);
-  }
-
-  // Two 64-channel groups per wave halve the B bytes per SMFMAC but double the
-  // accumulators (2 waves per SIMD instead of 3) and halve the workgroup count; used when
-  // the grid still gives every CU two workgroups.  SENGINE_AMD_TILE_GPW=1|2 overrides.
-  int gpw = (!k3 && d->T == 4 && d->C_out % 128 == 0 && (int64_t)p.ntiles * (d->C_out / 128) >= 512) ? 2 : 1;
-  const int fg = env_int_now("SENGINE_AMD_TILE_GPW", 0);
-  if (d->T == 4 && d->C_out % 128 == 0 && (fg == 1 || fg == 2)) gpw = fg;
-  if ((int64_t)p.ntiles * (d->C_out / (64 * gpw)) > 0x7fffffff) return hipErrorInvalidValue;
-
-  // Split the reduction over two wave sets when the grid gives at most one workgroup per
-  // CU (deep layers: few, long workgroups, one wave per SIMD); with more workgroups the
-  // doubled LDS footprint costs more than it gains (measured).  SENGINE_AMD_TILE_KSPLIT
-  // =1|2 overrides.
-  int ksplit = 1;
-  if (k3 && d->T == 4 && gpw == 1 && p.nchunk % 2 == 0) {
-    ksplit = (int64_t)p.ntiles * (d->C_out / 64) <= 256 ? 2 : 1;
-    const int fk = env_int_now("SENGINE_AMD_TILE_KSPLIT", 0);
-    if (fk == 1 || fk == 2) ksplit = fk;
-  }
-  // Two-deep operand prefetch where the grid leaves at most two workgroups per CU (two waves
-  // per SIMD: registers to spare, SMFMAC issue waiting on latency).  SENGINE_AMD_TILE_PF=1|2
-  // overrides.
-  int pf = 1;
-  if (k3 && d->T == 4 && gpw == 1) {
-    pf = (int64_t)p.ntiles * (d->C_out / 64) <= 512 ? 2 : 1;
-    const int fp = env_int_now("SENGINE_AMD_TILE_PF", 0);
-    if (fp == 1 || fp == 2) pf = fp;
-  }
-  if (k3) return launch_tile3(p, d->T, shape, gpw, ksplit, pf, d->out_enc, mode, stream);
-  return launch_tile1(p, d->T, gpw, d->out_enc, mode, stream);
+  if (c.k3) return launch_tile3(p, d->T, c.shape, c.gpw, c.ksplit, c.pf, d->out_enc, mode, stream);
+  return launch_tile1(p, d->T, c.gpw, d->out_enc, mode, stream);
 }
 
 }  // namespace sengine

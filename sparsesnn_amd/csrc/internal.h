@@ -65,6 +65,18 @@ bool tile_eligible(const sengine_conv_lif_desc* d);
 hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
                                   hipStream_t stream);
 
+// The tile kernel instance chosen for a descriptor (template arguments and grid).
+struct TileChoice {
+  bool k3;
+  int shape, gpw, ksplit, pf;
+  int tiles_w, tiles_per_image, ntiles;
+};
+bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice& c);
+
+// Human-readable names of the kernel instance a launch would run (snprintf semantics).
+int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len);
+int describe_lds(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len);
+
 // Kernel selection for the fused op with spike-bit input: 0 = automatic (the split-K
 // small-M kernel for small outputs, else the tile kernel where eligible, else the
 // LDS-staged kernel), 1 = always the direct-gather kernel, 2 = the LDS-staged kernel,

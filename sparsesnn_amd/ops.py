@@ -23,7 +23,7 @@ __all__ = [
     "multistep_neuron_repeat", "maxpool_spikes", "sew_head", "dense_conv_bn", "multistep_neuron", "SEngineError",
     "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "NEURON_MS", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
     "neuron_code", "fused_sparse_conv_bn_add_neuron", "spiking_self_attention", "stem_conv_bn_neuron",
-    "fused_sparse_conv_bn_lif_pair",
+    "fused_sparse_conv_bn_lif_pair", "fused_plan",
 ]
 
 
@@ -107,6 +107,22 @@ def set_fused_kernel(choice: str) -> None:
     lib = _lib.load()
     check(lib.sengine_amd_set_fused_kernel({"auto": 0, "direct": 1, "lds": 2, "tile": 3}[choice]),
           "set_fused_kernel")
+
+
+PLAN_TRACES, PLAN_STATE, PLAN_SEW_ADD, PLAN_SHORTCUT = 1, 2, 4, 8
+
+
+def fused_plan(s: ConvSpec, traces: bool = False, state: bool = False, sew_add: bool = False,
+               shortcut: bool = False) -> str:
+    """Name of the kernel instance a fused call with these optional buffers would launch
+    (route and compile-time specialisation); host-only, launches nothing."""
+    lib = _lib.load()
+    d = make_desc(s)
+    flags = ((PLAN_TRACES if traces else 0) | (PLAN_STATE if state else 0) | (PLAN_SEW_ADD if sew_add else 0)
+             | (PLAN_SHORTCUT if shortcut else 0))
+    buf = ctypes.create_string_buffer(256)
+    check(lib.sengine_amd_fused_plan(ctypes.byref(d), flags, buf, len(buf)), "fused_plan")
+    return buf.value.decode()
 
 
 def geometry(s: ConvSpec):

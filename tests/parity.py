@@ -1,11 +1,15 @@
 """Parity helpers shared by the GPU tests, smoke() and bench.py.
 
 Acceptance rule, applied per layer call:
-  * spikes bit-exact, except for at most floor(1e-4 * n_neuron_steps) mismatches, each of
-    which must have a reference membrane within 1e-3 of V_th;
+  * spikes bit-exact, except for at most floor(1e-4 * n_neuron_steps) mismatching
+    neuron-steps;
+  * a neuron's first mismatch (its spike history agreed with the reference up to the
+    previous step) must have a reference membrane within 1e-3 of V_th at that step.  Later
+    mismatches of the same neuron follow from that flip -- one side reset, the other did
+    not, so the two membrane trajectories differ from then on -- and are counted against
+    the budget above but not required to be near threshold;
   * charged membranes within 1e-3 * max(|v_ref|, V_th), compared wherever the spike
-    history of the neuron agrees with the reference up to the previous step (after an
-    allowed near-threshold flip the two trajectories legitimately diverge).
+    history of the neuron agrees with the reference up to the previous step.
 """
 from __future__ import annotations
 
@@ -22,10 +26,11 @@ MEMBRANE_RTOL = 1e-3
 @dataclass
 class ParityReport:
     n: int                 # neuron-steps compared
-    spike_mismatch: int
-    far_mismatch: int      # mismatches whose reference membrane is not near threshold
+    spike_mismatch: int    # all mismatching neuron-steps
+    far_mismatch: int      # first flips of a neuron whose reference membrane is not near threshold
     membrane_max_rel: float
     membrane_compared: int
+    flips: int = 0         # first mismatches (neurons whose history diverged)
 
     @property
     def ok(self) -> bool:
@@ -33,7 +38,8 @@ class ParityReport:
         return self.far_mismatch == 0 and self.spike_mismatch <= allowed and self.membrane_max_rel <= MEMBRANE_RTOL
 
     def __str__(self):
-        return (f"n={self.n} spike_mismatch={self.spike_mismatch} far={self.far_mismatch} "
+        return (f"n={self.n} spike_mismatch={self.spike_mismatch} (first flips {self.flips}, "
+                f"{self.spike_mismatch - self.flips} after a flip) far={self.far_mismatch} "
                 f"membrane_max_rel={self.membrane_max_rel:.3e} over {self.membrane_compared}")
 
 
@@ -42,20 +48,33 @@ def compare(spikes_gpu: np.ndarray, h_gpu, spikes_ref: np.ndarray, h_ref: np.nda
     s_g = spikes_gpu.astype(bool)
     s_r = spikes_ref.astype(bool)
     mism = s_g != s_r
-    near = np.abs(h_ref - v_th) <= NEAR_THRESHOLD
-    far = int(np.sum(mism & ~near))
-    rel, cnt = 0.0, 0
-    if h_gpu is not None:
-        # compare step t only where spike histories agree on steps < t
-        hist_ok = np.ones(s_g.shape[1:], bool)
-        for t in range(s_g.shape[0]):
+    rel, cnt, far, flips = 0.0, 0, 0, 0
+    hist_ok = np.ones(s_g.shape[1:], bool)  # spike histories agree on steps < t
+    for t in range(s_g.shape[0]):
+        first = mism[t] & hist_ok
+        if first.any():
+            flips += int(first.sum())
+            far += int(np.sum(np.abs(h_ref[t][first] - v_th) > NEAR_THRESHOLD))
+        if h_gpu is not None and hist_ok.any():
             sel = hist_ok
-            if sel.any():
-                err = np.abs(h_gpu[t][sel] - h_ref[t][sel]) / np.maximum(np.abs(h_ref[t][sel]), v_th)
-                rel = max(rel, float(err.max()))
-                cnt += int(sel.sum())
-            hist_ok = hist_ok & ~mism[t]
-    return ParityReport(int(s_g.size), int(mism.sum()), far, rel, cnt)
+            err = np.abs(h_gpu[t][sel] - h_ref[t][sel]) / np.maximum(np.abs(h_ref[t][sel]), v_th)
+            rel = max(rel, float(err.max()))
+            cnt += int(sel.sum())
+        hist_ok = hist_ok & ~mism[t]
+    return ParityReport(int(s_g.size), int(mism.sum()), far, rel, cnt, flips)
+
+
+def compare_final(v_gpu: np.ndarray, v_ref: np.ndarray, spikes_gpu: np.ndarray, spikes_ref: np.ndarray,
+                  v_th: float):
+    """Final membranes (after the last reset), compared where the neuron's whole spike history
+    agrees with the reference (an allowed near-threshold flip legitimately changes the
+    trajectory).  spikes_* (T, ...) and v_* (...) in the same element order.  Returns
+    (max relative error, neurons compared)."""
+    same = np.all(spikes_gpu.astype(bool) == spikes_ref.astype(bool), axis=0)
+    if not same.any():
+        return 0.0, 0
+    err = np.abs(v_gpu[same] - v_ref[same]) / np.maximum(np.abs(v_ref[same]), v_th)
+    return float(err.max()), int(same.sum())
 
 
 def nhwc_seq(x: torch.Tensor, T: int) -> np.ndarray:

@@ -17,7 +17,11 @@ pytestmark = pytest.mark.gpu
 
 
 def run_case(dev, case: ref.LayerCase, neuron="lif", tau=2.0, v_th=1.0, v_reset=0.0, planes=1,
-             in_enc=ops.ENC_BITS, out_enc=ops.ENC_BITS, v0=None, layout=ops.WLAYOUT_OIHW):
+             in_enc=ops.ENC_BITS, out_enc=ops.ENC_BITS, v0=None, layout=ops.WLAYOUT_OIHW, traces=True):
+    """One fused call against the oracle.  traces=True also records the per-step membrane and
+    BN output (which selects the generic epilogue); traces=False runs the call as an engine
+    does (the fast epilogue where the neuron allows it) and compares spikes and, with v0, the
+    final membrane.  Returns (report, BN-output error or None, oracle result, final state)."""
     T, B, C_in, H, W = case.x_seq.shape
     C_out, _, KH, KW = case.w.shape
     hard = v_reset is not None
@@ -38,8 +42,8 @@ def run_case(dev, case: ref.LayerCase, neuron="lif", tau=2.0, v_th=1.0, v_reset=
     state = None
     if v0 is not None:
         state = v0.permute(0, 2, 3, 1).reshape(M, C_out).contiguous().to(dev)
-    h_tr = torch.empty(T, M, C_out, dtype=torch.float32, device=dev)
-    x_tr = torch.empty(T, M, C_out, dtype=torch.float32, device=dev)
+    h_tr = torch.empty(T, M, C_out, dtype=torch.float32, device=dev) if traces else None
+    x_tr = torch.empty(T, M, C_out, dtype=torch.float32, device=dev) if traces else None
     out = ops.fused_sparse_conv_bn_lif(spec, data, values, meta, scale_d, bias_d, state=state,
                                        h_trace=h_tr, x_trace=x_tr)
     torch.cuda.synchronize()
@@ -49,10 +53,12 @@ def run_case(dev, case: ref.LayerCase, neuron="lif", tau=2.0, v_th=1.0, v_reset=
     else:
         s_gpu = out.float().cpu()
     r = ref.fused_layer(case.x_seq, case.w, case.bn, case.stride, case.padding, 1, neuron, tau, v_th, v_reset, v0)
-    h_gpu = nhwc_seq(h_tr.view(T * B, OH, OW, C_out), T)
+    h_gpu = nhwc_seq(h_tr.view(T * B, OH, OW, C_out), T) if traces else None
     rep = compare(nhwc_seq(s_gpu, T), h_gpu, r.spikes.numpy(), r.h.numpy(), v_th)
-    x_gpu = nhwc_seq(x_tr.view(T * B, OH, OW, C_out), T)
-    x_err = float(np.max(np.abs(x_gpu - r.x.numpy())))
+    x_err = None
+    if traces:
+        x_gpu = nhwc_seq(x_tr.view(T * B, OH, OW, C_out), T)
+        x_err = float(np.max(np.abs(x_gpu - r.x.numpy())))
     v_fin = None
     if state is not None:
         v_fin = state.view(B, OH, OW, C_out).permute(0, 3, 1, 2).cpu()
@@ -117,27 +123,29 @@ def test_hwio_layout(dev):
     assert rep.ok, str(rep)
 
 
+@pytest.mark.parametrize("traces", [True, False])
 @pytest.mark.parametrize("kernel", ["direct", "lds", "auto", "tile"])
 @pytest.mark.parametrize("k,stride,pad,B,C_in,C_out,H,W", [(3, 1, 1, 5, 64, 128, 13, 11), (3, 2, 1, 3, 128, 64, 15, 9),
                                                            (1, 1, 0, 2, 256, 192, 7, 7), (1, 2, 0, 2, 64, 64, 9, 10)])
-def test_bit_kernels_agree_and_match_oracle(dev, kernel, k, stride, pad, B, C_in, C_out, H, W):
+def test_bit_kernels_agree_and_match_oracle(dev, kernel, k, stride, pad, B, C_in, C_out, H, W, traces):
     """Every spike-bit kernel (halo-tiled via 'auto' where eligible, LDS-staged, direct-gather)
     against the oracle, on shapes whose position count is not a multiple of the workgroup tile."""
     ops.set_fused_kernel(kernel)
     try:
         case = ref.make_layer_case(40 + k + stride + B, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
                                    stride=stride, padding=pad, fp16_weights=True)
-        rep, x_err, _, v_fin = run_case(dev, case)
+        rep, x_err, _, v_fin = run_case(dev, case, traces=traces)
         assert rep.ok, str(rep)
-        assert x_err < 1e-4
+        assert x_err is None or x_err < 1e-4
     finally:
         ops.set_fused_kernel("auto")
 
 
+@pytest.mark.parametrize("traces", [True, False])
 @pytest.mark.parametrize("tile", ["0", "1", "2"])
 @pytest.mark.parametrize("H,W,C_in,C_out,B", [(13, 11, 64, 64, 2), (7, 7, 128, 128, 3), (28, 14, 192, 64, 1),
                                               (4, 17, 64, 192, 2)])
-def test_halo_tiles_against_oracle(dev, tile, H, W, C_in, C_out, B):
+def test_halo_tiles_against_oracle(dev, tile, H, W, C_in, C_out, B, traces):
     """3x3 tile kernel with each tile shape forced (0: 8x8, 1: 14x4, 2: 7x7), on images that
     leave ragged tiles, one to three input-channel chunks and several output-channel groups."""
     import os
@@ -146,36 +154,38 @@ def test_halo_tiles_against_oracle(dev, tile, H, W, C_in, C_out, B):
     try:
         case = ref.make_layer_case(60 + H + W + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
                                    fp16_weights=True)
-        rep, x_err, _, _ = run_case(dev, case)
+        rep, x_err, _, _ = run_case(dev, case, traces=traces)
         assert rep.ok, str(rep)
-        assert x_err < 1e-4
-        rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=None, out_enc=ops.ENC_F16)
+        assert x_err is None or x_err < 1e-4
+        rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=None, out_enc=ops.ENC_F16, traces=traces)
         assert rep2.ok, str(rep2)
     finally:
         ops.set_fused_kernel("auto")
         del os.environ["SENGINE_AMD_TILE_SHAPE"]
 
 
+@pytest.mark.parametrize("traces", [True, False])
 @pytest.mark.parametrize("T", [1, 2])
 @pytest.mark.parametrize("neuron,v_reset", [("lif", 0.0), ("if", 0.0), ("lif", None)])
-def test_halo_short_sequences_and_state(dev, T, neuron, v_reset):
+def test_halo_short_sequences_and_state(dev, T, neuron, v_reset, traces):
     case = ref.make_layer_case(70 + T, T=T, B=2, C_in=128, C_out=64, H=9, W=10, k=3, fp16_weights=True,
                                p_spike=0.3)
     g = torch.Generator().manual_seed(9)
     v0 = torch.rand((2, 64, 9, 10), generator=g) * 0.5
     ops.set_fused_kernel("tile")  # small test shapes would otherwise take the small-M kernel
     try:
-        rep, _, r, v_fin = run_case(dev, case, neuron=neuron, v_reset=v_reset, v_th=0.6, v0=v0)
+        rep, _, r, v_fin = run_case(dev, case, neuron=neuron, v_reset=v_reset, v_th=0.6, v0=v0, traces=traces)
     finally:
         ops.set_fused_kernel("auto")
     assert rep.ok, str(rep)
     assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("traces", [True, False])
 @pytest.mark.parametrize("gpw", ["1", "2"])
 @pytest.mark.parametrize("k,stride,H,W,C_in,C_out,B", [(3, 1, 9, 10, 128, 128, 2), (1, 1, 7, 9, 256, 256, 3),
                                                        (1, 2, 11, 10, 128, 128, 2), (1, 1, 5, 5, 64, 192, 1)])
-def test_tile_channel_blocking(dev, gpw, k, stride, H, W, C_in, C_out, B):
+def test_tile_channel_blocking(dev, gpw, k, stride, H, W, C_in, C_out, B, traces):
     """Tile kernels with one or two 64-channel groups per wave (SENGINE_AMD_TILE_GPW), for
     3x3 halo tiles and flat 1x1 tiles (stride 1 and 2), against the oracle."""
     import os
@@ -184,20 +194,21 @@ def test_tile_channel_blocking(dev, gpw, k, stride, H, W, C_in, C_out, B):
     try:
         case = ref.make_layer_case(80 + k + stride + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
                                    stride=stride, padding=k // 2, fp16_weights=True)
-        rep, x_err, _, _ = run_case(dev, case)
+        rep, x_err, _, _ = run_case(dev, case, traces=traces)
         assert rep.ok, str(rep)
-        assert x_err < 1e-4
-        rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0)
+        assert x_err is None or x_err < 1e-4
+        rep2, _, _, _ = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, traces=traces)
         assert rep2.ok, str(rep2)
     finally:
         ops.set_fused_kernel("auto")
         del os.environ["SENGINE_AMD_TILE_GPW"]
 
 
+@pytest.mark.parametrize("traces", [True, False])
 @pytest.mark.parametrize("ksplit", ["1", "2"])
 @pytest.mark.parametrize("shape", ["0", "1", "2"])
 @pytest.mark.parametrize("H,W,C_in,C_out,B", [(7, 7, 256, 128, 3), (13, 11, 128, 64, 2), (9, 16, 512, 64, 1)])
-def test_tile_reduction_split(dev, ksplit, shape, H, W, C_in, C_out, B):
+def test_tile_reduction_split(dev, ksplit, shape, H, W, C_in, C_out, B, traces):
     """3x3 halo tiles with the reduction split over two wave sets (SENGINE_AMD_TILE_KSPLIT),
     each tile shape, LIF (fast epilogue) and IF with state (generic epilogue), against the oracle."""
     import os
@@ -207,12 +218,12 @@ def test_tile_reduction_split(dev, ksplit, shape, H, W, C_in, C_out, B):
     try:
         case = ref.make_layer_case(110 + H + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
                                    fp16_weights=True, p_spike=0.2)
-        rep, x_err, _, _ = run_case(dev, case)
+        rep, x_err, _, _ = run_case(dev, case, traces=traces)
         assert rep.ok, str(rep)
-        assert x_err < 1e-4
+        assert x_err is None or x_err < 1e-4
         g = torch.Generator().manual_seed(3)
         v0 = torch.rand((B, C_out, H, W), generator=g) * 0.4
-        rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0)
+        rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0, traces=traces)
         assert rep2.ok, str(rep2)
         assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
     finally:
@@ -221,10 +232,11 @@ def test_tile_reduction_split(dev, ksplit, shape, H, W, C_in, C_out, B):
         del os.environ["SENGINE_AMD_TILE_SHAPE"]
 
 
+@pytest.mark.parametrize("traces", [True, False])
 @pytest.mark.parametrize("pf", ["1", "2"])
 @pytest.mark.parametrize("ksplit,shape", [("1", "0"), ("1", "1"), ("1", "2"), ("2", "2")])
 @pytest.mark.parametrize("H,W,C_in,C_out,B", [(7, 7, 256, 128, 3), (13, 11, 192, 64, 2), (14, 14, 128, 128, 1)])
-def test_tile_prefetch_depth(dev, pf, ksplit, shape, H, W, C_in, C_out, B):
+def test_tile_prefetch_depth(dev, pf, ksplit, shape, H, W, C_in, C_out, B, traces):
     """3x3 halo tiles with one- and two-deep operand prefetch (SENGINE_AMD_TILE_PF): A operands
     fetched across the 64-channel chunk boundary, B fragments two steps ahead; odd and even
     chunk counts, ragged tiles, LIF fast epilogue and IF with state, against the oracle."""
@@ -238,12 +250,12 @@ def test_tile_prefetch_depth(dev, pf, ksplit, shape, H, W, C_in, C_out, B):
     try:
         case = ref.make_layer_case(130 + H + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
                                    fp16_weights=True, p_spike=0.2)
-        rep, x_err, _, _ = run_case(dev, case)
+        rep, x_err, _, _ = run_case(dev, case, traces=traces)
         assert rep.ok, str(rep)
-        assert x_err < 1e-4
+        assert x_err is None or x_err < 1e-4
         g = torch.Generator().manual_seed(4)
         v0 = torch.rand((B, C_out, H, W), generator=g) * 0.4
-        rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0)
+        rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0, traces=traces)
         assert rep2.ok, str(rep2)
         assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
     finally:

@@ -129,16 +129,19 @@ def test_engine_end_to_end_graph(dev, ms_case):
     assert err < 5e-2, err  # a near-threshold flip upstream moves a logit by ~1/(T*HW) of a weight
 
 
-def test_engine_cfg3_shape_one_image(dev):
-    """BASELINE config 3's network shape on one image: MS-ResNet-34, 3x224x224 pixels ~N(0,1),
-    T=4, LIF tau 2 / V_th 1, 1000 classes, 2:4 convs.  Every block teacher-forced on the
-    oracle's block input (the parity rule is per layer call: over 16 blocks the real-valued
-    shortcut stream carries any allowed near-threshold flip forward, so whole-network spikes
-    drift apart); the captured graph's replays equal the eager forward."""
+@pytest.mark.parametrize("batch", [1, 32])
+def test_engine_cfg3_shape(dev, batch):
+    """BASELINE config 3's network: MS-ResNet-34, 3x224x224 pixels ~N(0,1), T=4, LIF tau 2 /
+    V_th 1, 1000 classes, 2:4 convs, on one image and at the benchmark's batch of 32 (whose
+    layers run on the tile-kernel instances the end-to-end figure times).  Every block
+    teacher-forced on the oracle's block input (the parity rule is per layer call: over 16
+    blocks the real-valued shortcut stream carries any allowed near-threshold flip forward,
+    so whole-network spikes drift apart); the captured graph's replays equal the eager
+    forward."""
     p = ms.make_params(21, 34, num_classes=1000, init="lively", fp16_weights=True)
-    x = torch.randn(1, 3, 224, 224, generator=torch.Generator().manual_seed(22))
+    x = torch.randn(batch, 3, 224, 224, generator=torch.Generator().manual_seed(22))
     logits, xs = ms.forward(p, x, T=4, depth=34, kind="lif", tau=2.0, v_threshold=1.0, keep=True)
-    eng = MSResNetEngine(p, batch=1, T=4, depth=34, neuron="lif", in_hw=(224, 224), device=dev)
+    eng = MSResNetEngine(p, batch=batch, T=4, depth=34, neuron="lif", in_hw=(224, 224), device=dev)
     assert eng.launches == 1 + 16 * 2 + 4 + 1
     eager = eng.forward(x.to(dev)).clone()
     eng.capture()
@@ -147,5 +150,5 @@ def test_engine_cfg3_shape_one_image(dev):
     assert torch.equal(y, eager)
     err = float((y.cpu() - logits).abs().max())
     print(f"end-to-end logits max |diff| {err:.3e} (scale {float(logits.abs().max()):.3e})")
-    rates = _check_blocks_teacher_forced(dev, eng, p, xs, "lif", 34, 4, 1)
+    rates = _check_blocks_teacher_forced(dev, eng, p, xs, "lif", 34, 4, batch)
     assert all(0.005 < r < 0.95 for r in rates), rates

@@ -297,10 +297,13 @@ def test_fused_add_up_to_five_planes(dev, kernel, res_planes, out_planes, k, H):
     assert float(r.spikes.sum()) > 0
 
 
-@pytest.fixture(scope="module")
-def sew_case():
+@pytest.fixture(scope="module", params=[2, 64])
+def sew_case(request):
+    """batch 2, and 64: BASELINE config 2's batch, so the blocks run on the kernel instances
+    the end-to-end benchmark times (random BN so that every block fires)."""
+    B = request.param
     p = sr.make_params(11, bn_random=True, fp16_weights=True)
-    x = sr.make_images(12, 2)
+    x = sr.make_images(12, B)
     rec = {}
     logits = sr.forward(p, x, record=rec)
     return p, x, rec, logits
@@ -310,9 +313,9 @@ def test_engine_blocks_teacher_forced(dev, sew_case):
     """Each block on the oracle's own block input: conv1 / downsample spikes and the conv2
     spikes inside the SEW sum, each against the oracle under the parity rule."""
     p, x, rec, _ = sew_case
-    eng = SEWResNet18Engine(p, batch=2, device=dev)
+    T, B = 4, x.shape[0]
+    eng = SEWResNet18Engine(p, batch=B, device=dev)
     eng.forward(x.to(dev))
-    T, B = 4, 2
     prev = "maxpool"
     for i, blk in enumerate(eng.blocks):
         xin = rec[prev].numpy()
@@ -351,11 +354,12 @@ def test_engine_end_to_end_graph(dev, sew_case):
     """Whole network from one hipGraph replay: stem/max-pool spikes under the parity rule,
     logits against the oracle, and replays identical to the eager run."""
     p, x, rec, logits = sew_case
-    eng = SEWResNet18Engine(p, batch=2, device=dev)
+    B = x.shape[0]
+    eng = SEWResNet18Engine(p, batch=B, device=dev)
     eager = eng.forward(x.to(dev)).clone()
     torch.cuda.synchronize()
-    stem = _bits_to_seq(eng.stem_spk, 4, 2, 64, eng.H1, eng.W1)
-    pool = _bits_to_seq(eng.pool_out, 4, 2, 64, eng.H2, eng.W2)
+    stem = _bits_to_seq(eng.stem_spk, 4, B, 64, eng.H1, eng.W1)
+    pool = _bits_to_seq(eng.pool_out, 4, B, 64, eng.H2, eng.W2)
     mism_stem = float(np.mean(stem != rec["stem"].numpy()))
     assert mism_stem <= 1e-4, mism_stem
     if mism_stem == 0:

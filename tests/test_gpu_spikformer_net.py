@@ -165,20 +165,26 @@ def test_engine_end_to_end_graph(dev, sf_case):
     assert eng.launches == 7 + 8 * 4 + 1
 
 
-def test_engine_cfg4_shape_one_image(dev):
-    """BASELINE config 4's shape on one image: 3x224x224 pixels ~N(0,1), T=4, embed 384,
-    8 heads, MLP ratio 4, 8 blocks (3,136 tokens), 1000 classes; the SPS stages and the
-    first block teacher-forced against the oracle, graph replays equal to the eager run."""
+@pytest.mark.parametrize("batch,nblocks", [(1, 1), (4, 2)])
+def test_engine_cfg4_shape(dev, batch, nblocks):
+    """BASELINE config 4's shape: 3x224x224 pixels ~N(0,1), T=4, embed 384, 8 heads, MLP ratio
+    4, 8 blocks (3,136 tokens), 1000 classes, on one image and on four (whose token layers
+    take the same tile-kernel instances as the benchmark's batch of 32); the SPS stages and
+    the first `nblocks` blocks teacher-forced against the oracle, graph replays equal to the
+    eager run."""
     p = sf.make_params(41, embed=384, depth=8, num_classes=1000)
-    x = torch.randn(1, 3, 224, 224, generator=torch.Generator().manual_seed(42))
-    eng = SpikformerEngine(p, batch=1, T=4, embed=384, heads=8, depth=8, in_hw=(224, 224), device=dev)
+    x = torch.randn(batch, 3, 224, 224, generator=torch.Generator().manual_seed(42))
+    eng = SpikformerEngine(p, batch=batch, T=4, embed=384, heads=8, depth=8, in_hw=(224, 224), device=dev)
     assert eng.N == 3136 and eng.final_planes == 5
     eager = eng.forward(x.to(dev)).clone()
     eng.capture()
     y = eng.forward(x.to(dev))
     torch.cuda.synchronize()
     assert torch.equal(y, eager)
-    rates = _check_sps(eng, p, x, 4, 1, 384)
+    rates = _check_sps(eng, p, x, 4, batch, 384)
     assert all(0.005 < r < 0.9 for r in rates), rates
-    x0 = _tok_planes(eng.x0, 2, 4, 1, eng.N, 384)  # the engine's own (parity-checked) SPS output
-    _check_block(dev, eng, p, 0, x0, 4, 1, 8)
+    xi = _tok_planes(eng.x0, 2, 4, batch, eng.N, 384)  # the engine's own (parity-checked) SPS output
+    for i in range(nblocks):
+        _check_block(dev, eng, p, i, xi, 4, batch, 8)
+        blk = eng.blocks[i]
+        xi = _tok_planes(blk.bufs["x2"], blk.planes_out, 4, batch, eng.N, 384)  # checked block output
