@@ -89,11 +89,14 @@ def run_layer(wk):
                                  out=wk["out"])
 
 
-def cpu_baseline(budget_s=12.0, min_runs=2):
+CPU_WARMUP, CPU_MIN_RUNS = 3, 10  # 3 warmups, median of >= 10 runs
+
+
+def cpu_baseline(budget_s=12.0, min_runs=CPU_MIN_RUNS):
     """The oracle (restated reference PyTorch path, torch CPU fp32) on the full sweep: the 15
     layers (5 shapes x 3 densities) at batch 32, T=4 -- the same workload as the GPU step.
-    One untimed warmup sweep, then whole sweeps until `budget_s` of timed CPU work (at least
-    `min_runs`); the median sweep time is the step time."""
+    3 untimed warmup sweeps, then whole sweeps until `budget_s` of timed CPU work and at least
+    `min_runs`; the median sweep time is the step time."""
     import torch
     from oracle import reference_path as ref
 
@@ -111,7 +114,8 @@ def cpu_baseline(budget_s=12.0, min_runs=2):
         for c in cases:
             ref.fused_layer(c.x_seq, c.w, c.bn, c.stride, c.padding, 1, "lif", 2.0, 1.0, 0.0)
 
-    sweep()
+    for _ in range(CPU_WARMUP):
+        sweep()
     ts = []
     while len(ts) < min_runs or sum(ts) < budget_s:
         t0 = time.perf_counter()
@@ -124,7 +128,7 @@ def cpu_baseline(budget_s=12.0, min_runs=2):
         pass
     return dict(step_s=statistics.median(ts), threads=torch.get_num_threads(), cpu_count=cores, model=model,
                 sample=f"the full step (15 sweep layers, batch {BATCH}, T={T_STEPS}) on the oracle: median of "
-                       f"{len(ts)} sweeps ({sum(ts):.1f} s timed) after 1 warmup")
+                       f"{len(ts)} sweeps ({sum(ts):.1f} s timed) after {CPU_WARMUP} warmups")
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -161,41 +165,54 @@ def measured_traffic():
 E2E_BATCH, E2E_HW, E2E_CLASSES = 64, 32, 100
 
 
-def bench_e2e(dev, warmup: int, iters: int):
+def bench_e2e(dev, warmup: int, iters: int, active: bool = False):
     """SEW-ResNet-18 (reference init, convs 2:4 except the stem, LIF
-    tau=2 V_th=1, ADD), 3x32x32 images ~U(0,1), batch 64, T=4, one hipGraph replay per
-    batch; images/s from HIP events around `iters` replays (the reference times graph
-    replays the same way, sengine/csrc/cpp_executor.cu:1298-1315)."""
+    tau=2 V_th=1, ADD), 3x32x32 images ~U(0,1), batch 64, T=4, run the way the reference runs
+    a network: state dict -> EngineIR (front end) -> optimize_ir -> compile_all ->
+    CUDAGraphEngine, one hipGraph replay per batch; images/s from HIP events around `iters`
+    replays (the reference times graph replays the same way, sengine/csrc/cpp_executor.cu:
+    1298-1315).  active=True draws BN statistics as config 0 does instead of the reference's
+    identity BN, so that every layer fires (the reference init leaves the network silent after
+    the stem; no kernel skips zero work, so the time is the same workload either way)."""
     import torch
-    from sparsesnn_amd.sew_resnet import SEWResNet18Engine, random_params
+    from sparsesnn_amd import frontend, passes
+    from sparsesnn_amd.compiler import SparseKernelCompiler
+    from sparsesnn_amd.runtime import CUDAGraphEngine
+    from sparsesnn_amd.sew_resnet import random_params
 
     params = random_params(2024, E2E_CLASSES)
-    eng = SEWResNet18Engine(params, batch=E2E_BATCH, T=T_STEPS, device=dev)
+    if active:
+        g = torch.Generator().manual_seed(2025)
+        for k in list(params):
+            if k.endswith(".running_var"):
+                pre = k[: -len(".running_var")]
+                c = params[k].numel()
+                params[pre + ".weight"] = (torch.rand(c, generator=g) + 0.5) * 2.0
+                params[pre + ".bias"] = torch.randn(c, generator=g) * 0.1 + 0.3
+                params[pre + ".running_mean"] = torch.randn(c, generator=g) * 0.1
+                params[pre + ".running_var"] = torch.rand(c, generator=g) + 0.5
+    ir = frontend.sew_resnet_ir(params, T=T_STEPS, batch=E2E_BATCH, in_hw=(E2E_HW, E2E_HW))
+    passes.optimize_ir(ir)
+    kernels = SparseKernelCompiler(ir, batch_size=E2E_BATCH).compile_all()
+    eng = CUDAGraphEngine().build(ir, kernels, T=T_STEPS, batch_size=E2E_BATCH, device=dev)
     g = torch.Generator().manual_seed(7)
     x = torch.rand((E2E_BATCH, 3, E2E_HW, E2E_HW), generator=g).to(dev)
-    eng.forward(x)
-    eng.capture()
-    for _ in range(warmup):
-        eng.forward(x)
-    torch.cuda.synchronize(dev)
-    stream = torch.cuda.current_stream(dev)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    eng.x_buf.copy_(x)
-    a.record(stream)
-    for _ in range(iters):
-        eng.graph.replay()
-    b.record(stream)
-    torch.cuda.synchronize(dev)
-    s = a.elapsed_time(b) * 1e-3 / iters
-    return dict(params=params, x=x.cpu(), batch_s=s, launches=eng.launches)
+    eng(x)
+    eng.capture_graph()
+    eng(x)
+    ms = eng.benchmark(warmup=warmup, n_iters=iters)
+    density = eng.spike_density()
+    return dict(params=params, x=x.cpu(), batch_s=ms * 1e-3, launches=eng.n_launches, density=density)
 
 
-def cpu_e2e(params, x, budget_s=6.0, min_runs=2):
-    """The oracle SEW-ResNet-18 (torch CPU fp32) on the same batch: median of whole batches."""
+def cpu_e2e(params, x, budget_s=6.0, min_runs=CPU_MIN_RUNS):
+    """The oracle SEW-ResNet-18 (torch CPU fp32) on the same batch: 3 warmups, then the
+    median of at least `min_runs` whole batches."""
     import torch
     from oracle import sew_resnet as sr
     with torch.no_grad():
-        sr.forward(params, x)
+        for _ in range(CPU_WARMUP):
+            sr.forward(params, x)
         ts = []
         while len(ts) < min_runs or sum(ts) < budget_s:
             t0 = time.perf_counter()
@@ -253,16 +270,26 @@ def bench_spikformer(dev, warmup: int, iters: int):
     return dict(params=params, x=x, batch_s=s, launches=eng.launches)
 
 
-def cpu_sample(fn, budget_s: float, min_runs: int = 1):
-    """Median seconds of fn() (the oracle on the host cores) over runs until budget_s."""
+def cpu_sample(fn, budget_s: float, min_runs: int = CPU_MIN_RUNS):
+    """Median seconds of fn() (the oracle on the host cores): 3 warmups, then runs until
+    budget_s and at least min_runs."""
     import torch
     with torch.no_grad():
+        for _ in range(CPU_WARMUP):
+            fn()
         ts = []
         while len(ts) < min_runs or sum(ts) < budget_s:
             t0 = time.perf_counter()
             fn()
             ts.append(time.perf_counter() - t0)
     return statistics.median(ts), len(ts), torch.get_num_threads()
+
+
+def spike_density_bits(t) -> float:
+    """Fraction of set bits of an int32 spike-bit tensor (off the timed path)."""
+    import torch
+    lut = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.int64, device=t.device)
+    return float(lut[t.contiguous().view(torch.uint8).long()].sum()) / (t.numel() * 32)
 
 
 def copy_calibration(dev, nbytes=256 << 20, reps=3):
@@ -303,7 +330,7 @@ def main():
         sys.exit(2)
 
     import torch
-    from sparsesnn_amd import _lib
+    from sparsesnn_amd import _lib, hw_calibrate
 
     _lib.load()
     dev = torch.device("cuda:0")
@@ -372,6 +399,9 @@ def main():
     torch.cuda.synchronize(dev)
     step_s = t0.elapsed_time(t1) * 1e-3 / args.steps
 
+    density = {wk["name"]: {"in": round(spike_density_bits(wk["data"]), 4), "out": round(spike_density_bits(wk["out"]), 5)}
+               for wk in work}
+    calib = hw_calibrate.calibrate(dev)
     ideal = sum(wk["ideal"] for wk in work)
     flops = sum(wk["flops"] for wk in work)
     launches = sum(len(v) for v in per.values())
@@ -403,7 +433,9 @@ def main():
             "step": "hipGraph replay of the 15 fused launches",
             "tflops_dense_equiv": round(flops / step_s / 1e12, 2),
             "per_layer_us": {wk["name"]: round(statistics.median(per[wk["name"]]) * 1e6, 2) for wk in work},
+            "spike_density": density,
         },
+        "calibration": calib,
         "roofline": {
             "bound": "mfma",
             "achieved": round(avg_flops / avg_launch / 1e12, 2),
@@ -416,6 +448,8 @@ def main():
                       "the 1x1 layer KS=1; mean over all 15 sweep launches)",
             "avg_launch_us": round(avg_launch * 1e6, 3),
             "note": "dense-equivalent FLOPs vs the 5.0 PFLOP/s 2:4 peak == useful FLOPs vs the 2.5 PFLOP/s dense peak",
+            "peak_measured": calib["smfmac_tflops_dense_equiv"],
+            "frac_of_measured": round(avg_flops / avg_launch / (calib["smfmac_tflops_dense_equiv"] * 1e12), 4),
         },
     }
     if not args.no_cpu_baseline:
@@ -433,12 +467,20 @@ def main():
         }
     if not args.no_e2e:
         e2e = bench_e2e(dev, warmup=20, iters=max(50, args.steps * 5))
+        act = bench_e2e(dev, warmup=20, iters=max(50, args.steps * 5), active=True)
         result["e2e"] = {
             "metric": "images/sec", "model": "SEW-ResNet-18 (ADD, LIF tau=2 V_th=1, 2:4 convs except the stem)",
             "value": round(E2E_BATCH / e2e["batch_s"], 1), "batch": E2E_BATCH, "timesteps": T_STEPS,
             "input": f"3x{E2E_HW}x{E2E_HW} ~U(0,1), direct-encoded", "ms_per_batch": round(e2e["batch_s"] * 1e3, 4),
-            "launches_per_batch": e2e["launches"], "step": "one hipGraph replay per batch",
+            "launches_per_batch": e2e["launches"],
+            "step": "one hipGraph replay per batch of the generic engine (EngineIR -> optimize_ir -> compile_all -> "
+                    "CUDAGraphEngine)",
             "data": "synthetic images, reference random init (models/sewresnet.py:155-160)",
+            "spike_density": {k: round(v, 5) for k, v in e2e["density"].items()},
+            "note": "with the reference init (identity BN) nothing fires after the stem; no kernel skips zero work",
+            "active_bn": {"value": round(E2E_BATCH / act["batch_s"], 1), "ms_per_batch": round(act["batch_s"] * 1e3, 4),
+                          "spike_density": {k: round(v, 5) for k, v in act["density"].items()},
+                          "data": "same network with BN drawn as config 0 (gamma x2) so every layer fires"},
         }
         if not args.no_cpu_baseline:
             cs, runs, thr = cpu_e2e(e2e["params"], e2e["x"])
@@ -468,16 +510,20 @@ def main():
         if not args.no_cpu_baseline:  # the oracle networks on the host cores (CPU baseline leg only)
             from oracle import ms_resnet as msr
             from oracle import spikformer as sfo
-            x1 = torch.randn((1, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(10))
-            cs, runs, thr = cpu_sample(lambda: msr.forward(m["params"], x1, T=T_STEPS, depth=34, kind="lif", tau=2.0,
+            b3 = 4
+            x3 = torch.randn((b3, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(10))
+            cs, runs, thr = cpu_sample(lambda: msr.forward(m["params"], x3, T=T_STEPS, depth=34, kind="lif", tau=2.0,
                                                            v_threshold=1.0), budget_s=4.0)
-            result["e2e_cfg3"]["cpu_baseline"] = {"value": round(1.0 / cs, 3), "unit": "images/sec", "cores": thr,
-                                                  "kind": "port", "sample": f"one image (batch 1), median of {runs} "
-                                                                            "forwards", "s_per_image": round(cs, 3)}
-            result["e2e_cfg3"]["speedup_vs_cpu"] = round(result["e2e_cfg3"]["value"] * cs, 1)
+            result["e2e_cfg3"]["cpu_baseline"] = {"value": round(b3 / cs, 3), "unit": "images/sec", "cores": thr,
+                                                  "kind": "port", "sample": f"batch {b3}: median of {runs} forwards "
+                                                                            f"after {CPU_WARMUP} warmups",
+                                                  "s_per_batch": round(cs, 3)}
+            result["e2e_cfg3"]["speedup_vs_cpu"] = round(result["e2e_cfg3"]["value"] / (b3 / cs), 1)
+            x1 = x3[:1]
             cs, runs, thr = cpu_sample(lambda: sfo.forward(f["params"], x1, T=T_STEPS, heads=8, depth=8), budget_s=0.0)
             result["e2e_cfg4"]["cpu_baseline"] = {"value": round(1.0 / cs, 3), "unit": "images/sec", "cores": thr,
-                                                  "kind": "port", "sample": "one image (batch 1), one forward",
+                                                  "kind": "port", "sample": f"batch 1: median of {runs} forwards after "
+                                                                            f"{CPU_WARMUP} warmups",
                                                   "s_per_image": round(cs, 3)}
             result["e2e_cfg4"]["speedup_vs_cpu"] = round(result["e2e_cfg4"]["value"] * cs, 1)
     line = json.dumps(result)

@@ -351,6 +351,19 @@ int sengine_amd_pack_spikes(const void* x, int32_t x_enc, int64_t n_pos, int32_t
 int sengine_amd_unpack_spikes(const uint32_t* bits, int64_t n_pos, int32_t C, void* out, int32_t out_enc,
                               hipStream_t stream);
 
+/*
+ * Peak calibration on the box (the role of the reference's sengine/tuning/hw_calibrate.py:
+ * 17-134, which times a memcpy and a dense fp16 GEMM).  Measurement entry points, not on
+ * the operator path.
+ *   calibrate_smfmac: `blocks` workgroups of 256 threads; every wave issues iters x 8
+ *     back-to-back v_smfmac_f32_16x16x64_f16 from registers (32,768 dense-equivalent FLOPs
+ *     each) and writes one float per thread to sink (blocks * 256 floats).
+ *   calibrate_copy: streams `bytes` (a multiple of 16, 16-byte aligned buffers) from src to
+ *     dst with 16-byte accesses (bytes read + bytes written of HBM traffic).
+ */
+int sengine_amd_calibrate_smfmac(int32_t blocks, int32_t iters, float* sink, hipStream_t stream);
+int sengine_amd_calibrate_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,9 @@ from .ops import ENC_BITS, ENC_F16, ConvSpec, SEngineError
 FUSED_VARIANTS = {"FusedSparseConvBNLIF", "TileLangFusedConvBNIF", "TileLangFusedConv1x1BNIF"}
 DENSE_VARIANTS = {"TileLangConvBN", "TileLangConv1x1BN"}
 NEURON_VARIANTS = {"CUDAVec4LIF", "CUDAVec4IF"}
+STEM_VARIANTS = {"TileLangStemConvBN"}
+HEAD_VARIANTS = {"CuBLASGemm"}
+POOL_VARIANTS = {"CuDNNPool"}
 
 
 class SparseWeight:
@@ -66,11 +69,14 @@ def _weight_layout(spec: ConvSpec, w: torch.Tensor) -> int:
 
 
 class FusedSparseConvBNLIFKernel:
-    """The fused 2:4 Conv+BN+neuron node (one HIP launch per call)."""
+    """The fused 2:4 Conv+BN+neuron node (one HIP launch per call).  in_planes > 1: the input
+    is an integer activation stored as that many bit planes (spec.C_in counts plane
+    channels); a raw weight of the conv's own C_in is expanded to planes here."""
 
-    def __init__(self, spec: ConvSpec, key: str):
+    def __init__(self, spec: ConvSpec, key: str, in_planes: int = 1):
         self.spec = spec  # in_enc/out_enc of `spec` are ignored; chosen per call
         self.key = key
+        self.in_planes = in_planes
         self._wcache: dict = {}
         self.OH, self.OW, self.M, self.K_red = ops.geometry(spec)
 
@@ -78,6 +84,12 @@ class FusedSparseConvBNLIFKernel:
         return dataclasses.replace(self.spec, in_enc=in_enc, out_enc=out_enc)
 
     def prepare_weight(self, w, device=None) -> SparseWeight:
+        if self.in_planes > 1 and not isinstance(w, SparseWeight):
+            from .sparsity import expand_planes
+            if isinstance(w, np.ndarray):
+                w = torch.from_numpy(np.ascontiguousarray(w))
+            if tuple(w.shape) == (self.spec.C_out, self.spec.C_in // self.in_planes, self.spec.KH, self.spec.KW):
+                w = expand_planes(w.float(), self.in_planes)
         return SparseWeight.from_weight(self.spec, w, device)
 
     def _weight(self, w) -> SparseWeight:
@@ -106,6 +118,47 @@ class FusedSparseConvBNLIFKernel:
         sw = self._weight(weight)
         return ops.fused_sparse_conv_bn_lif(spec, data, sw.values, sw.meta, bn_scale, bn_bias, state=state, out=out,
                                             h_trace=h_trace, x_trace=x_trace)
+
+
+class StemConvBNKernel:
+    """Dense fp32 stem conv + folded BN on the images (C_in = 3; TileLangStemConvBN), with the
+    absorbed neuron over the T repeats and the spike max-pool in the same launch when given
+    their buffers:  kern(x, weight, bn_scale, bn_bias, pooled=..., spikes=..., out=...)."""
+
+    def __init__(self, spec: ConvSpec, key: str, pool=None):
+        self.spec = spec
+        self.key = key
+        self.pool = pool  # (kernel, stride, pad) of the absorbed max-pool, or None
+
+    def prepare_weight(self, w, device=None) -> torch.Tensor:
+        if isinstance(w, np.ndarray):
+            w = torch.from_numpy(np.ascontiguousarray(w))
+        device = device or (w.device if w.is_cuda else torch.device("cuda"))
+        w = w.to(device).float()
+        if _weight_layout(self.spec, w) == ops.WLAYOUT_OIHW:
+            w = w.permute(2, 3, 1, 0)
+        return w.contiguous()  # HWIO: coalesced weight reads
+
+    def __call__(self, x, weight, bn_scale, bn_bias, pooled=None, spikes=None, out=None):
+        if pooled is not None:
+            k, st, pd = self.pool
+            return ops.stem_conv_bn_lif_pool(self.spec, x, weight, bn_scale, bn_bias, k, st, pd, pooled=pooled,
+                                             spikes=spikes)[0]
+        if spikes is not None:
+            return ops.stem_conv_bn_neuron(self.spec, x, weight, bn_scale, bn_bias, out=out, spikes=spikes,
+                                           want_out=out is not None)[1]
+        return ops.stem_conv_bn(self.spec, x, weight, bn_scale, bn_bias, out=out, layout=ops.WLAYOUT_HWIO)
+
+
+class SpikeHeadKernel:
+    """GlobalAvgPool -> Flatten -> TemporalMean -> Gemm on (integer) spike activations
+    (CuBLASGemm with the pool and mean absorbed): kern(x_bits, fc_weight, fc_bias, out=...)."""
+
+    def __init__(self, T: int, B: int, HW: int, C: int, planes: int, key: str):
+        self.T, self.B, self.HW, self.C, self.planes, self.key = T, B, HW, C, planes, key
+
+    def __call__(self, x, fc_weight, fc_bias, out=None):
+        return ops.sew_head(x, self.T, self.B, self.HW, self.C, self.planes, fc_weight, fc_bias, out=out)
 
 
 class DenseConvBNKernel:
@@ -210,7 +263,8 @@ class SparseKernelCompiler:
             raise SEngineError(f"node {node.name}: only square stride/pad/dilation and groups=1 are supported")
         is_lif = neuron_kind == "LIF"
         hard = True if np_ is None else bool(np_.hard_reset)
-        return ConvSpec(T=self.T, B=self.B, C_in=cp.in_channels, H=H, W=W, C_out=cp.out_channels,
+        planes = int(node.extra_attrs.get("in_planes", 1))
+        return ConvSpec(T=self.T, B=self.B, C_in=cp.in_channels * planes, H=H, W=W, C_out=cp.out_channels,
                         KH=cp.kernel_h, KW=cp.kernel_w, stride=cp.stride_h, padding=cp.pad_h,
                         dilation=cp.dilation_h, neuron="lif" if is_lif else "if", hard_reset=hard,
                         tau=float(np_.tau) if (np_ is not None and is_lif) else 2.0,
@@ -235,7 +289,7 @@ class SparseKernelCompiler:
                 key = f"sparse_{spec}_{self.precision}"
                 kern = self._kernel_cache.get(key)
                 if kern is None:
-                    kern = FusedSparseConvBNLIFKernel(spec, key)
+                    kern = FusedSparseConvBNLIFKernel(spec, key, int(node.extra_attrs.get("in_planes", 1)))
                     self._kernel_cache[key] = kern
                 node.tilelang_config = {"kernel": "fused_sparse_conv_bn_lif", "T": self.T, "waves": 4,
                                         "tile_channels": 64, "tile_positions": 64}
@@ -250,4 +304,39 @@ class SparseKernelCompiler:
                 kernels[nid] = kern
             elif name in NEURON_VARIANTS:
                 kernels[nid] = get_cuda_if()
+            elif name in STEM_VARIANTS:
+                kernels[nid] = self._stem(node)
+            elif name in HEAD_VARIANTS:
+                gap = self.ir.nodes[node.extra_attrs["absorbed_nids"][-1]]
+                N, C, H, W = gap.input_shapes[0]
+                key = f"head_{self.T}_{self.B}_{H * W}_{C}_{node.extra_attrs.get('in_planes', 1)}"
+                kernels[nid] = SpikeHeadKernel(self.T, self.B, H * W, C, int(node.extra_attrs.get("in_planes", 1)),
+                                               key)
         return kernels
+
+    def _stem(self, node):
+        cp = node.conv_params
+        N, C, H, W = node.input_shapes[0]
+        if N != self.B:
+            raise SEngineError(f"node {node.name}: stem input batch {N} != B = {self.B} (conv runs once per image)")
+        if cp.stride_h != cp.stride_w or cp.pad_h != cp.pad_w or cp.groups != 1:
+            raise SEngineError(f"node {node.name}: only square stride/pad and groups=1 are supported")
+        neuron = self.ir.nodes[node.extra_attrs["neuron_nid"]]
+        np_ = neuron.neuron_params
+        is_lif = neuron.op_type.name == "LIF"
+        spec = ConvSpec(T=self.T, B=self.B, C_in=C, H=H, W=W, C_out=cp.out_channels, KH=cp.kernel_h,
+                        KW=cp.kernel_w, stride=cp.stride_h, padding=cp.pad_h, neuron="lif" if is_lif else "if",
+                        hard_reset=bool(np_.hard_reset), tau=float(np_.tau) if is_lif else 2.0,
+                        v_threshold=float(np_.v_threshold), v_reset=float(np_.v_reset))
+        pool = None
+        for a in node.extra_attrs["absorbed_nids"]:
+            pn = self.ir.nodes[a]
+            if pn.op_type.name == "MaxPool":
+                pp = pn.pool_params or {}
+                pool = (int(pp.get("kernel_size", 3)), int(pp.get("stride", 2)), int(pp.get("padding", 1)))
+        key = f"stem_{spec}_{pool}"
+        kern = self._kernel_cache.get(key)
+        if kern is None:
+            kern = StemConvBNKernel(spec, key, pool)
+            self._kernel_cache[key] = kern
+        return kern

@@ -1,0 +1,146 @@
+"""Front end: EngineIR straight from a SEW-ResNet module tree (ONNX, the reference's route via
+sengine/parser.py:77-368, is not available to this build).
+
+`sew_resnet_ir` walks the structure of the reference's `sew_resnet18` (models/sewresnet.py:
+123-210): stem conv1 / bn1, the image repeated over T, sn1, maxpool, layer1..layer4 of
+BasicBlocks (conv1 = SeqToANNContainer(conv3x3, BN) -> sn1, conv2 -> sn2, optional downsample =
+Sequential(SeqToANNContainer(conv1x1, BN), neuron), out = sn2 + identity for connect_f 'ADD'),
+avgpool, flatten, mean over T, fc.  It reads the weights through the module's state_dict() key
+names (conv1.weight, layer1.0.conv1.module.0.weight, layer2.0.downsample.0.module.1.running_var,
+fc.bias, ...), so a reference model object or its state dict both work.  The node kinds and
+shapes (NCHW with N = T*B after the repeat) are those the reference's parser emits; the
+passes in sparsesnn_amd/passes.py then fuse them.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .ir import ConvParams, EngineIR, Node, NeuronParams, NeuronType, OpType, WeightInfo
+
+STAGES = ((64, 1), (128, 2), (256, 2), (512, 2))
+
+
+def _state(model) -> dict:
+    sd = model.state_dict() if hasattr(model, "state_dict") else model
+    return {k: (v.detach().float().cpu().numpy() if hasattr(v, "detach") else np.asarray(v, np.float32))
+            for k, v in sd.items()}
+
+
+def _neuron_attrs(model, neuron, tau, v_threshold, v_reset):
+    """Neuron hyper-parameters: taken from the model's first neuron module when it exposes
+    them (LIFNeuron keeps tau / v_threshold / v_reset, models/neurons.py:85-146), else the
+    arguments."""
+    sn = getattr(model, "sn1", None)
+    if sn is not None:
+        tau = float(getattr(sn, "tau", tau))
+        v_threshold = float(getattr(sn, "v_threshold", v_threshold))
+        v_reset = getattr(sn, "v_reset", v_reset)
+        v_reset = None if v_reset is None else float(v_reset)
+    return neuron, tau, v_threshold, v_reset
+
+
+class _Builder:
+    def __init__(self, ir: EngineIR, sd: dict, T: int, neuron, tau, v_threshold, v_reset):
+        self.ir, self.sd, self.T = ir, sd, T
+        is_lif = neuron == "lif"
+        self.op = OpType.LIF if is_lif else OpType.IF
+        self.np = NeuronParams(NeuronType.LIF if is_lif else NeuronType.IF, T, float(tau) if is_lif else 1.0,
+                               float(v_threshold), 0.0 if v_reset is None else float(v_reset), v_reset is not None)
+
+    def add(self, node: Node) -> str:
+        self.ir.add_node(node)
+        return node.output_names[0]
+
+    def conv(self, key, x, shape, stride, pad):
+        w = self.sd[key + ".weight"]
+        cout, cin, kh, kw = w.shape
+        N, C, H, W = shape
+        if C != cin:
+            raise ValueError(f"{key}: input has {C} channels, weight expects {cin}")
+        oh, ow = (H + 2 * pad - kh) // stride + 1, (W + 2 * pad - kw) // stride + 1
+        self.ir.weights[key + ".weight"] = w
+        out = (N, cout, oh, ow)
+        return self.add(Node(0, key, OpType.Conv2d, input_names=[x], output_names=[key + ".out"],
+                             input_shapes=[shape], output_shapes=[out],
+                             conv_params=ConvParams(cin, cout, kh, kw, stride, stride, pad, pad),
+                             weight_info=WeightInfo(key + ".weight", tuple(w.shape)))), out
+
+    def bn(self, key, x, shape):
+        names = {}
+        for attr, suffix in (("bn_scale_name", "weight"), ("bn_bias_name", "bias"), ("bn_mean_name", "running_mean"),
+                             ("bn_var_name", "running_var")):
+            self.ir.weights[f"{key}.{suffix}"] = self.sd[f"{key}.{suffix}"]
+            names[attr] = f"{key}.{suffix}"
+        return self.add(Node(0, key, OpType.BatchNorm, input_names=[x], output_names=[key + ".out"],
+                             input_shapes=[shape], output_shapes=[shape], extra_attrs=dict(names, epsilon=1e-5)))
+
+    def neuron(self, name, x, shape):
+        return self.add(Node(0, name, self.op, is_stateful=True, input_names=[x], output_names=[name + ".out"],
+                             input_shapes=[shape], output_shapes=[shape], neuron_params=self.np))
+
+    def simple(self, name, op, x, in_shape, out_shape, **kw):
+        return self.add(Node(0, name, op, input_names=[x] if isinstance(x, str) else list(x),
+                             output_names=[name + ".out"], input_shapes=[in_shape], output_shapes=[out_shape], **kw))
+
+
+def sew_resnet_ir(model, T: int = 4, batch: int = 1, in_hw=(32, 32), neuron: str = "lif", tau: float = 2.0,
+                  v_threshold: float = 1.0, v_reset=0.0, blocks=(2, 2, 2, 2), connect_f: str = "ADD") -> EngineIR:
+    """EngineIR of a SEW-ResNet (BasicBlock, `blocks` per stage; (2, 2, 2, 2) = sew_resnet18)
+    for `batch` images of in_hw pixels.  `model`: the module tree (its state_dict() is read,
+    and connect_f / neuron parameters from its attributes when present) or a state dict with
+    the same keys.  Only connect_f 'ADD' is served."""
+    connect_f = getattr(model, "connect_f", connect_f)
+    if connect_f != "ADD":
+        raise ValueError(f"connect_f {connect_f!r}: only 'ADD' is served by the fused SEW epilogue")
+    neuron, tau, v_threshold, v_reset = _neuron_attrs(model, neuron, tau, v_threshold, v_reset)
+    sd = _state(model)
+    ir = EngineIR()
+    ir.T = T
+    bld = _Builder(ir, sd, T, neuron, tau, v_threshold, v_reset)
+    H, W = in_hw
+    cin = sd["conv1.weight"].shape[1]
+
+    # stem: conv1 + bn1 once per image, repeated over T, sn1, maxpool
+    x, shp = bld.conv("conv1", "x", (batch, cin, H, W), 2, 3)
+    x = bld.bn("bn1", x, shp)
+    shp = (T * batch,) + shp[1:]
+    x = bld.simple("sn1.repeat", OpType.Tile, x, (batch,) + shp[1:], shp, extra_attrs={"repeats": T})
+    x = bld.neuron("sn1", x, shp)
+    ph, pw = (shp[2] + 2 - 3) // 2 + 1, (shp[3] + 2 - 3) // 2 + 1
+    pshape = shp[:2] + (ph, pw)
+    x = bld.simple("maxpool", OpType.MaxPool, x, shp, pshape,
+                   pool_params={"kernel_size": 3, "stride": 2, "padding": 1})
+    shp = pshape
+
+    inplanes = shp[1]
+    for si, (planes, stride) in enumerate(STAGES[:len(blocks)]):
+        for bi in range(blocks[si]):
+            s = stride if bi == 0 else 1
+            pre = f"layer{si + 1}.{bi}"
+            a, ashp = bld.conv(pre + ".conv1.module.0", x, shp, s, 1)
+            a = bld.bn(pre + ".conv1.module.1", a, ashp)
+            a = bld.neuron(pre + ".sn1", a, ashp)
+            b, bshp = bld.conv(pre + ".conv2.module.0", a, ashp, 1, 1)
+            b = bld.bn(pre + ".conv2.module.1", b, bshp)
+            b = bld.neuron(pre + ".sn2", b, bshp)
+            identity = x
+            if (pre + ".downsample.0.module.0.weight") in sd:
+                d, dshp = bld.conv(pre + ".downsample.0.module.0", x, shp, s, 0)
+                d = bld.bn(pre + ".downsample.0.module.1", d, dshp)
+                identity = bld.neuron(pre + ".downsample.1", d, dshp)
+            elif s != 1 or inplanes != planes:
+                raise ValueError(f"{pre}: stride/width change without a downsample branch")
+            x = bld.simple(pre + ".add", OpType.Add, [b, identity], bshp, bshp)
+            shp, inplanes = bshp, planes
+
+    # head: avgpool -> flatten -> mean over T -> fc
+    N, C = shp[0], shp[1]
+    x = bld.simple("avgpool", OpType.GlobalAvgPool, x, shp, (N, C, 1, 1))
+    x = bld.simple("flatten", OpType.Flatten, x, (N, C, 1, 1), (N, C))
+    x = bld.simple("mean", OpType.TemporalMean, x, (N, C), (batch, C))
+    fw, fb = sd["fc.weight"], sd["fc.bias"]
+    ir.weights["fc.weight"], ir.weights["fc.bias"] = fw, fb
+    bld.add(Node(0, "fc", OpType.Gemm, input_names=[x], output_names=["logits"], input_shapes=[(batch, C)],
+                 output_shapes=[(batch, fw.shape[0])], gemm_params={"transB": 1},
+                 weight_info=WeightInfo("fc.weight", tuple(fw.shape)), bias_info=WeightInfo("fc.bias", tuple(fb.shape))))
+    return ir

@@ -27,6 +27,11 @@ class OpType(Enum):
     Transpose = auto()
     Identity = auto()
     Flatten = auto()
+    MaxPool = auto()
+    GlobalAvgPool = auto()
+    Tile = auto()            # repeat over T (the static image fed to every timestep)
+    TemporalMean = auto()
+    Gemm = auto()            # classifier Linear
 
 
 class NeuronType(Enum):
@@ -44,7 +49,10 @@ class KernelVariant(Enum):
     here it is the gfx950 2:4 SMFMAC kernel.  TileLangFusedConvBNIF / TileLangFusedConv1x1BNIF
     (the reference's dense fused nodes) are served by the same kernel when the weights are
     2:4, otherwise by the dense fallback.  TileLangConvBN / TileLangConv1x1BN + CUDAVec4LIF /
-    CUDAVec4IF / StandaloneLIF are the unfused fallback halves.
+    CUDAVec4IF / StandaloneLIF are the unfused fallback halves.  TileLangStemConvBN,
+    CuDNNPool, Elementwise, TemporalMean, TileRepeat and CuBLASGemm are the network-level
+    node kinds around the fused op (sengine/cuda_graph_runtime.py:819-880); the passes in
+    sparsesnn_amd/passes.py absorb them into fused launches where the kernels allow.
     """
     CuDNNConv = auto()
     FusedSparseConvBNLIF = auto()
@@ -56,6 +64,12 @@ class KernelVariant(Enum):
     CUDAVec4LIF = auto()
     TileLangFusedConvBNIF = auto()
     TileLangFusedConv1x1BNIF = auto()
+    TileLangStemConvBN = auto()   # dense C_in=3 stem conv + BN on the images
+    CuDNNPool = auto()            # MaxPool / GlobalAvgPool
+    Elementwise = auto()          # Add
+    TemporalMean = auto()
+    TileRepeat = auto()
+    CuBLASGemm = auto()           # classifier
 
 
 class BoundType(Enum):
@@ -89,6 +103,12 @@ KERNEL_CONTRACTS = {
     KernelVariant.CUDAVec4LIF: None,
     KernelVariant.StandaloneLIF: None,
     KernelVariant.ZeroCost: None,
+    KernelVariant.TileLangStemConvBN: KernelLayoutContract(TensorLayout.NCHW, TensorLayout.NHWC),
+    KernelVariant.CuDNNPool: KernelLayoutContract(TensorLayout.NHWC, TensorLayout.NHWC),
+    KernelVariant.Elementwise: None,
+    KernelVariant.TemporalMean: None,
+    KernelVariant.TileRepeat: None,
+    KernelVariant.CuBLASGemm: KernelLayoutContract(TensorLayout.ND, TensorLayout.ND),
 }
 
 
@@ -137,6 +157,8 @@ class Node:
     output_shapes: list = field(default_factory=list)
     conv_params: Optional[ConvParams] = None
     neuron_params: Optional[NeuronParams] = None
+    pool_params: Optional[dict] = None    # kernel_size / stride / padding (MaxPool)
+    gemm_params: Optional[dict] = None
     extra_attrs: dict = field(default_factory=dict)
     assigned_kernel: KernelVariant = KernelVariant.ZeroCost
     layout: TensorLayout = TensorLayout.NCHW

@@ -4,6 +4,9 @@ nodes straight from torch modules (ONNX is not available to this build).
 
 Pass order (optimize_ir, sengine/optimizer.py:24-59, restricted to this path):
   fold_batchnorm -> detect_fusion_groups -> mark_sparsity -> assign_kernels
+  -> fuse_stem -> absorb_residual_add -> fuse_head -> assign_pools -> annotate_planes
+(the last five play the role of the reference's slicer for the network-level nodes,
+sengine/fusion_strategy.py:28-193 / graph_slicer.py:43-182).
 """
 from __future__ import annotations
 
@@ -145,13 +148,195 @@ def assign_kernels(ir: EngineIR) -> dict:
     return stats
 
 
+def _single_consumer(ir: EngineIR, nid: int):
+    succ = ir.successors(nid)
+    return ir.nodes[succ[0]] if len(succ) == 1 else None
+
+
+def fuse_stem(ir: EngineIR) -> int:
+    """Dense stem convs (C_in < 4: never 2:4 along C_in, optimizer.py:540-543) feeding
+    Tile (repeat over T) -> LIF/IF [-> MaxPool] run as one TileLangStemConvBN launch: the conv
+    + BN once per image, the neuron over the T repeats and the spike max-pool from the same
+    workgroup (the reference computes conv1/bn1 before repeating, models/sewresnet.py:199-201).
+    The absorbed nodes become ZeroCost; extra_attrs: fusion_slice, absorbed_nids,
+    fused_output (the tensor the launch writes)."""
+    n = 0
+    for nid in list(ir.topo_order):
+        conv = ir.nodes[nid]
+        if conv.op_type != OpType.Conv2d or conv.fusion_group_id >= 0 or conv.conv_params is None:
+            continue
+        if conv.conv_params.in_channels >= 4 or conv.conv_params.groups != 1 or conv.bn_scale is None:
+            continue
+        tile = _single_consumer(ir, nid)
+        if tile is None or tile.op_type != OpType.Tile:
+            continue
+        neuron = _single_consumer(ir, tile.id)
+        if neuron is None or neuron.op_type not in _NEURONS:
+            continue
+        absorbed, pattern, out = [tile.id, neuron.id], ["Conv2d", "Tile", neuron.op_type.name], neuron.output_names[0]
+        pool = _single_consumer(ir, neuron.id)
+        if pool is not None and pool.op_type == OpType.MaxPool:
+            absorbed.append(pool.id)
+            pattern.append("MaxPool")
+            out = pool.output_names[0]
+        conv.assigned_kernel = KernelVariant.TileLangStemConvBN
+        conv.bound_type = BoundType.COMPUTE
+        conv.layout = TensorLayout.NHWC
+        conv.extra_attrs.update(fusion_slice="+".join(pattern), absorbed_nids=absorbed, fused_output=out,
+                                neuron_nid=neuron.id)
+        for a in absorbed:
+            ir.nodes[a].assigned_kernel = KernelVariant.ZeroCost
+            ir.nodes[a].bound_type = BoundType.ZERO
+        n += 1
+    return n
+
+
+def _fused_anchor_of(ir: EngineIR, tensor: str):
+    """The fused conv anchor whose absorbed neuron writes `tensor` (None otherwise)."""
+    prod = ir._producer.get(tensor)
+    if prod is None:
+        return None
+    node = ir.nodes[prod]
+    if node.op_type not in _NEURONS or node.fusion_group_id < 0:
+        return None
+    anchor = ir.nodes[ir.fusion_groups[node.fusion_group_id].conv_node_id]
+    if anchor.assigned_kernel != KernelVariant.FusedSparseConvBNLIF or "residual_input" in anchor.extra_attrs:
+        return None
+    return anchor
+
+
+def absorb_residual_add(ir: EngineIR) -> int:
+    """SEW 'ADD' (models/sewresnet.py:58-59) into the epilogue of the fused conv whose neuron
+    feeds it -- the reference slicer's Conv2d+LIF+Add slice with one external residual input
+    (graph_slicer.py:109-178, fusion_strategy.py:135-138).  Of two fused producers the one
+    later in topological order absorbs the Add, so the residual exists when it runs.  The
+    anchor records residual_nid (producer of the residual), residual_input (its tensor) and
+    fused_output (the Add's output)."""
+    order = {nid: i for i, nid in enumerate(ir.topo_order)}
+    n = 0
+    for nid in list(ir.topo_order):
+        add = ir.nodes[nid]
+        if add.op_type != OpType.Add or len(add.input_names) != 2 or add.assigned_kernel != KernelVariant.ZeroCost:
+            continue
+        cands = []
+        for k, t in enumerate(add.input_names):
+            anchor = _fused_anchor_of(ir, t)
+            if anchor is not None and len(ir._consumers.get(t, [])) == 1:
+                cands.append((order[anchor.id], k, anchor))
+        if not cands:
+            continue
+        _, k, anchor = max(cands, key=lambda c: c[0])
+        res_t = add.input_names[1 - k]
+        anchor.extra_attrs["absorbed_nids"] = list(anchor.extra_attrs.get("absorbed_nids", [])) + [add.id]
+        anchor.extra_attrs["fusion_slice"] = anchor.extra_attrs.get("fusion_slice", "Conv2d+LIF") + "+Add"
+        anchor.extra_attrs["residual_nid"] = ir._producer.get(res_t)
+        anchor.extra_attrs["residual_input"] = res_t
+        anchor.extra_attrs["fused_output"] = add.output_names[0]
+        add.assigned_kernel = KernelVariant.ZeroCost
+        add.bound_type = BoundType.ZERO
+        add.extra_attrs["absorbed_into"] = anchor.id
+        n += 1
+    return n
+
+
+def fuse_head(ir: EngineIR) -> int:
+    """GlobalAvgPool -> Flatten -> TemporalMean -> Gemm (avgpool, flatten, x.mean(0), fc;
+    models/sewresnet.py:206-210) as one CuBLASGemm launch on the spike counts: the pooled
+    means are integer counts times 1/(HW*T), so the pool and mean run exactly on integers
+    before the Linear.  The Gemm node anchors it (fusion_slice, absorbed_nids, head_input)."""
+    n = 0
+    for nid in list(ir.topo_order):
+        gemm = ir.nodes[nid]
+        if gemm.op_type != OpType.Gemm:
+            continue
+        chain, cur = [], gemm
+        while True:
+            preds = ir.predecessors(cur.id)
+            if len(preds) != 1:
+                break
+            p = ir.nodes[preds[0]]
+            if p.op_type in (OpType.TemporalMean, OpType.Flatten, OpType.Reshape, OpType.GlobalAvgPool):
+                chain.append(p)
+                cur = p
+                if p.op_type == OpType.GlobalAvgPool:
+                    break
+            else:
+                break
+        kinds = {c.op_type for c in chain}
+        if OpType.GlobalAvgPool not in kinds or OpType.TemporalMean not in kinds:
+            continue
+        gap = chain[-1]
+        gemm.assigned_kernel = KernelVariant.CuBLASGemm
+        gemm.bound_type = BoundType.MEMORY
+        gemm.extra_attrs.update(fusion_slice="+".join([c.op_type.name for c in reversed(chain)] + ["Gemm"]),
+                                absorbed_nids=[c.id for c in chain], head_input=gap.input_names[0])
+        for c in chain:
+            c.assigned_kernel = KernelVariant.ZeroCost
+            c.bound_type = BoundType.ZERO
+        n += 1
+    return n
+
+
+def assign_pools(ir: EngineIR) -> int:
+    """Max-pools not absorbed by a stem run as CuDNNPool on spike bits (OR of the window)."""
+    n = 0
+    for node in ir.nodes.values():
+        if node.op_type == OpType.MaxPool and node.assigned_kernel == KernelVariant.ZeroCost and \
+                not any(node.id in a.extra_attrs.get("absorbed_nids", []) for a in ir.nodes.values()):
+            node.assigned_kernel = KernelVariant.CuDNNPool
+            node.bound_type = BoundType.MEMORY
+            node.layout = TensorLayout.NHWC
+            n += 1
+    return n
+
+
+def annotate_planes(ir: EngineIR) -> int:
+    """Integer range of every activation: spikes are 0/1, a fused SEW add yields
+    max(residual) + 1, max-pool keeps its input's range.  Fused convs record in_planes (the
+    bit planes of their input, which multiply the reduction, sparsity.expand_planes) and
+    out_planes; residual sums above 31 (5 planes) are rejected."""
+    vmax: dict = {}
+    for nid in ir.topo_order:
+        node = ir.nodes[nid]
+        kv = node.assigned_kernel
+        if node.op_type in _NEURONS:
+            for o in node.output_names:
+                vmax[o] = 1
+        if kv == KernelVariant.FusedSparseConvBNLIF:
+            inp = node.input_names[0]
+            node.extra_attrs["in_planes"] = max(1, int(vmax.get(inp, 1)).bit_length())
+            if "residual_input" in node.extra_attrs:
+                m = int(vmax.get(node.extra_attrs["residual_input"], 1)) + 1
+                if m > 31:
+                    raise ValueError(f"{node.name}: residual sums up to {m} need more than 5 bit planes")
+                vmax[node.extra_attrs["fused_output"]] = m
+                node.extra_attrs["res_planes"] = max(1, int(m - 1).bit_length())
+                node.extra_attrs["out_planes"] = m.bit_length()
+            else:
+                node.extra_attrs["out_planes"] = 1
+        elif node.op_type in (OpType.MaxPool, OpType.Flatten, OpType.Reshape, OpType.Identity):
+            for o in node.output_names:
+                vmax[o] = vmax.get(node.input_names[0], 1)
+        elif kv == KernelVariant.TileLangStemConvBN:
+            vmax[node.extra_attrs["fused_output"]] = 1
+        elif kv == KernelVariant.CuBLASGemm and "head_input" in node.extra_attrs:
+            node.extra_attrs["in_planes"] = max(1, int(vmax.get(node.extra_attrs["head_input"], 1)).bit_length())
+    return len(vmax)
+
+
 def optimize_ir(ir: EngineIR) -> dict:
-    """The hot-path subset of sengine's optimize_ir pipeline."""
+    """The hot-path subset of sengine's optimize_ir pipeline, plus the network-level fusions
+    the generic runtime serves (stem, SEW add, head, pools)."""
     folded = fold_batchnorm(ir)
     groups = detect_fusion_groups(ir)
     sparse = mark_sparsity(ir)
     stats = assign_kernels(ir)
-    stats.update(folded=folded, groups=groups, sparse=sparse)
+    stems = fuse_stem(ir)
+    adds = absorb_residual_add(ir)
+    heads = fuse_head(ir)
+    pools = assign_pools(ir)
+    annotate_planes(ir)
+    stats.update(folded=folded, groups=groups, sparse=sparse, stems=stems, adds=adds, heads=heads, pools=pools)
     return stats
 
 

@@ -6,8 +6,9 @@ __call__(x), reset_state(), benchmark()) so its callers drive this build unchang
 reference's buffer planning idea (build/buffer_planner.py: activation buffers reused once a
 tensor's last consumer has run).  Differences, MI355X-first:
 
-  * spike tensors between nodes are packed bits (1/16 of the reference's fp16 bytes); the
-    graph packs the input once and unpacks the output once, both inside the captured graph;
+  * spike tensors between nodes are packed bits (1/16 of the reference's fp16 bytes), and
+    integer activations (SEW sums) bit planes; a spike-input graph packs its input once and
+    unpacks its output once, both inside the captured graph;
   * fused nodes run with V0 = 0 and no membrane tensor: the reference zeroes every
     membrane before each replay (cuda_graph_runtime.py:158-159), which is the same thing;
     keep_membranes=True keeps per-node membranes instead (carried across calls until
@@ -15,9 +16,15 @@ tensor's last consumer has run).  Differences, MI355X-first:
   * everything the schedule touches is allocated in build(): capture and replay allocate
     nothing.
 
-Node kinds served: FusedSparseConvBNLIF (and the reference's TileLangFused* names) with the
-neuron absorbed, TileLangConvBN / TileLangConv1x1BN (dense fallback, fp32 out) followed by
-a CUDAVec4LIF / CUDAVec4IF neuron node, and ZeroCost nodes (views).  Anything else raises.
+Launches (one per non-absorbed node; the node kinds of cuda_graph_runtime.py:552-880 that
+this path needs):
+  * FusedSparseConvBNLIF (and the reference's TileLangFused* names), neuron absorbed, with
+    the SEW 'ADD' absorbed into its epilogue when the passes recorded a residual_input; two
+    fused convs reading the same input with no residual run as one paired launch;
+  * TileLangConvBN / TileLangConv1x1BN (dense fallback, fp32 out) + CUDAVec4LIF / CUDAVec4IF;
+  * TileLangStemConvBN: the dense image stem with its repeat, neuron and max-pool absorbed;
+  * CuDNNPool: spike max-pool; CuBLASGemm: the head (pool + mean over T + Linear absorbed);
+  * ZeroCost: views.  An unabsorbed Add / Tile / TemporalMean / GlobalAvgPool raises.
 """
 from __future__ import annotations
 
@@ -27,7 +34,8 @@ import numpy as np
 import torch
 
 from . import ops
-from .compiler import DENSE_VARIANTS, FUSED_VARIANTS, NEURON_VARIANTS, _kname
+from .compiler import (DENSE_VARIANTS, FUSED_VARIANTS, HEAD_VARIANTS, NEURON_VARIANTS, POOL_VARIANTS, STEM_VARIANTS,
+                       _kname)
 from .ops import ENC_BITS, SEngineError
 
 
@@ -82,12 +90,25 @@ def plan_buffers(schedule: list, produces: dict, consumes: dict, aliases: dict, 
     return root
 
 
+_VIEW_OPS = {"Reshape", "Transpose", "Identity", "Flatten"}
+
+
+class _Launch:
+    """One kernel launch of the schedule: the anchor node, what it reads and writes."""
+
+    def __init__(self, nid: int, kind: str, inputs: list, output: str):
+        self.nid, self.kind, self.inputs, self.output = nid, kind, inputs, output
+        self.pair_with: Optional[int] = None  # nid of a fused conv launched together with this one
+        self.skip = False                     # launched as the second half of a pair
+
+
 class CUDAGraphEngine:
     """Static-shape inference over an EngineIR with every launch captured in one hipGraph."""
 
     def __init__(self):
         self.ir = None
         self.schedule: list = []
+        self.launches: list = []
         self.kernels: dict = {}
         self.T, self.B, self.TB = 4, 1, 4
         self.graph: Optional[torch.cuda.CUDAGraph] = None
@@ -96,12 +117,90 @@ class CUDAGraphEngine:
         self.weights: dict = {}
         self.bn: dict = {}
         self.membranes: dict = {}
+        self.planes: dict = {}
         self._graph_input: Optional[torch.Tensor] = None
         self._graph_output: Optional[torch.Tensor] = None
+        self.image_input = False
+        self.logits_output = False
+
+    # ------------------------------------------------------------------ graph analysis
+    def _launch_of(self, node) -> Optional[_Launch]:
+        name = _kname(node)
+        ea = node.extra_attrs
+        if name in FUSED_VARIANTS:
+            ins = [node.input_names[0]] + ([ea["residual_input"]] if "residual_input" in ea else [])
+            return _Launch(node.id, "fused", ins, ea.get("fused_output", node.output_names[0]))
+        if name in DENSE_VARIANTS:
+            return _Launch(node.id, "dense", [node.input_names[0]], node.output_names[0])
+        if name in NEURON_VARIANTS:
+            return _Launch(node.id, "neuron", [node.input_names[0]], node.output_names[0])
+        if name in STEM_VARIANTS:
+            return _Launch(node.id, "stem", [node.input_names[0]], ea["fused_output"])
+        if name in HEAD_VARIANTS:
+            return _Launch(node.id, "head", [ea["head_input"]], node.output_names[0])
+        if name in POOL_VARIANTS:
+            if node.op_type.name != "MaxPool":
+                raise SEngineError(f"node {node.name}: only max-pool is served as a standalone pool")
+            return _Launch(node.id, "pool", [node.input_names[0]], node.output_names[0])
+        if name == "ZeroCost":
+            return None
+        raise SEngineError(f"node {node.name}: kernel {name} is not served by this build")
+
+    def _analyse(self, ir, order):
+        absorbed = set()
+        for node in ir.nodes.values():
+            absorbed.update(node.extra_attrs.get("absorbed_nids", []))
+        launches, aliases, shapes = [], {}, {}
+        written = set()
+        for nid in order:
+            node = ir.nodes[nid]
+            for i, t in enumerate(node.input_names):
+                if i < len(node.input_shapes):
+                    shapes.setdefault(t, tuple(node.input_shapes[i]))
+            for i, t in enumerate(node.output_names):
+                shapes[t] = tuple(node.output_shapes[i])
+            ln = self._launch_of(node)
+            if ln is not None:
+                launches.append(ln)
+                written.add(ln.output)
+        for nid in order:  # views (and absorbed single-input nodes) alias their input
+            node = ir.nodes[nid]
+            if _kname(node) != "ZeroCost":
+                continue
+            if nid not in absorbed and node.op_type.name not in _VIEW_OPS:
+                raise SEngineError(f"node {node.name}: {node.op_type.name} is not absorbed into a fused launch and "
+                                   "has no standalone kernel here")
+            if len(node.input_names) == 1 and node.output_names[0] not in written:
+                aliases[node.output_names[0]] = node.input_names[0]
+        return launches, aliases, shapes
+
+    @staticmethod
+    def _root(t, aliases):
+        while t in aliases:
+            t = aliases[t]
+        return t
+
+    def _order(self, launches, aliases, schedule):
+        """Launches in a dependency order (Kahn over what each reads and writes); the given
+        schedule (or the IR's topological order) breaks ties."""
+        prod = {self._root(l.output, aliases): l for l in launches}
+        rank = {nid: i for i, nid in enumerate(schedule)}
+        deps = {l.nid: {prod[self._root(t, aliases)].nid for t in l.inputs if self._root(t, aliases) in prod}
+                for l in launches}
+        by_id = {l.nid: l for l in launches}
+        done, out = set(), []
+        while len(out) < len(launches):
+            ready = [l for l in launches if l.nid not in done and deps[l.nid] <= done]
+            if not ready:
+                raise SEngineError("launch dependencies form a cycle")
+            nxt = min(ready, key=lambda l: rank.get(l.nid, 0))
+            out.append(by_id[nxt.nid])
+            done.add(nxt.nid)
+        return out
 
     # ------------------------------------------------------------------ build
     def build(self, ir, kernels: dict, schedule: Optional[list] = None, T: Optional[int] = None, batch_size: int = 1,
-              precision: str = "fp16", keep_membranes: bool = False, device="cuda"):
+              precision: str = "fp16", keep_membranes: bool = False, device="cuda", pair_launches: bool = True):
         self.ir = ir
         self.kernels = kernels
         self.schedule = list(schedule) if schedule is not None else list(ir.topo_order)
@@ -112,110 +211,206 @@ class CUDAGraphEngine:
         self.keep_membranes = keep_membranes
         self.dev = torch.device(device)
 
-        produces, consumes, aliases, shapes = {}, {}, {}, {}
-        for nid in self.schedule:
-            node = ir.nodes[nid]
-            name = _kname(node)
-            consumes[nid] = list(node.input_names[:1])
-            produces[nid] = list(node.output_names[:1])
-            shapes[node.output_names[0]] = tuple(node.output_shapes[0])
-            for i, t in enumerate(node.input_names[:1]):
-                shapes.setdefault(t, tuple(node.input_shapes[i]))
-            if name == "ZeroCost":
-                aliases[node.output_names[0]] = node.input_names[0]
-            elif name not in FUSED_VARIANTS | DENSE_VARIANTS | NEURON_VARIANTS:
-                raise SEngineError(f"node {node.name}: kernel {name} is not served by this build")
-        produced = {t for ts in produces.values() for t in ts}
-        inputs = [t for ts in consumes.values() for t in ts if t not in produced]
-        if len(set(inputs)) != 1:
-            raise SEngineError(f"expected one graph input tensor, found {sorted(set(inputs))}")
-        self.input_name = inputs[0]
-        consumed = {t for ts in consumes.values() for t in ts}
-        outs = [t for t in produced if t not in consumed]
+        launches, aliases, shapes = self._analyse(ir, self.schedule)
+        launches = self._order(launches, aliases, self.schedule)
+        root = lambda t: self._root(t, aliases)  # noqa: E731
+        produced = {root(l.output) for l in launches}
+        inputs = {root(t) for l in launches for t in l.inputs if root(t) not in produced}
+        if len(inputs) != 1:
+            raise SEngineError(f"expected one graph input tensor, found {sorted(inputs)}")
+        self.input_name = inputs.pop()
+        consumed = {root(t) for l in launches for t in l.inputs}
+        outs = [l.output for l in launches if root(l.output) not in consumed]
         if len(outs) != 1:
             raise SEngineError(f"expected one graph output tensor, found {sorted(outs)}")
         self.output_name = outs[0]
+        first = [l for l in launches if self.input_name in {root(t) for t in l.inputs}]
+        self.image_input = any(l.kind == "stem" for l in first)
+        if self.image_input and len(first) != 1:
+            raise SEngineError("the image input must feed the stem only")
+        self.logits_output = launches[-1].kind == "head" and launches[-1].output == self.output_name
 
-        # buffer classes: spike tensors as bits, dense conv outputs as fp32 NHWC
+        # activation ranges: bit planes per tensor
+        self.planes = {}
+        for l in launches:
+            node = ir.nodes[l.nid]
+            self.planes[root(l.output)] = int(node.extra_attrs.get("out_planes", 1)) if l.kind == "fused" else 1
+        self.planes.setdefault(self.input_name, 1)
+
+        # pair two fused convs on the same input (a block's conv1 and downsample): one launch
+        if pair_launches and not keep_membranes:
+            for i, a in enumerate(launches):
+                if a.kind != "fused" or a.skip or a.pair_with is not None or len(a.inputs) != 1:
+                    continue
+                for b in launches[i + 1:]:
+                    if b.kind == "fused" and not b.skip and b.pair_with is None and len(b.inputs) == 1 and \
+                            root(b.inputs[0]) == root(a.inputs[0]):
+                        a.pair_with, b.skip = b.nid, True
+                        break
+            # the partner is written by its pair's launch: schedule it right after, so buffer
+            # liveness (which follows schedule positions) is exact
+            ordered = []
+            partner = {l.pair_with: l for l in launches if l.pair_with is not None}
+            for l in launches:
+                if l.skip:
+                    continue
+                ordered.append(l)
+                if l.pair_with is not None:
+                    ordered.append(next(m for m in launches if m.nid == l.pair_with))
+            assert len(ordered) == len(launches) and len(partner) == sum(l.skip for l in launches)
+            launches = ordered
+        self.launches = launches
+
+        # buffers: spike bits (x planes), fp32 dense outputs, logits; graph input / output kept
         def cls(t):
-            N, C, H, W = shapes[t]
-            if self._is_real(t):
-                return ("f32", N * H * W * C)
-            if C % 32:
+            r = root(t)
+            shp = shapes[r]
+            kind = next((l.kind for l in launches if root(l.output) == r), None)
+            n = int(np.prod(shp))
+            if kind == "dense" or kind == "head":
+                return ("f32", n)
+            if r == self.input_name and self.image_input:
+                return ("f32", n)
+            N, C = shp[0], shp[1]
+            if (C * self.planes.get(r, 1)) % 32:
                 raise SEngineError(f"tensor {t}: {C} channels is not a multiple of 32 (spike bits)")
-            return ("bits", N * H * W * C // 32)
+            return ("bits", n * self.planes.get(r, 1) // 32)
 
-        self._producer_kind = {}
-        for nid in self.schedule:
-            self._producer_kind[self.ir.nodes[nid].output_names[0]] = _kname(self.ir.nodes[nid])
-        sizes = {t: cls(t) for t in shapes}
-        plan = plan_buffers(self.schedule, produces, consumes, aliases, sizes, {self.input_name, self.output_name})
+        produces = {l.nid: [root(l.output)] for l in launches}
+        consumes = {l.nid: [root(t) for t in l.inputs] for l in launches}
+        live = {root(t) for l in launches for t in l.inputs + [l.output]}
+        sizes = {t: cls(t) for t in live}
+        plan = plan_buffers([l.nid for l in launches], produces, consumes, {}, sizes,
+                            {self.input_name, root(self.output_name)})
         n_buf = 1 + max(b for b in plan.values() if b is not None)
-        bufcls = {}
-        for t, b in plan.items():
-            if b is not None:
-                bufcls[b] = sizes[t]
+        bufcls = {plan[t]: sizes[t] for t in sizes}
         self.buffers = [torch.empty(n, dtype=torch.float32 if k == "f32" else torch.int32, device=self.dev)
                         for k, n in (bufcls[i] for i in range(n_buf))]
         self.tensors = {}
-        for t, b in plan.items():
-            N, C, H, W = shapes[t]
-            if b is None:
-                continue
-            last = C if self._is_real(t) else C // 32
-            self.tensors[t] = self.buffers[b][: N * H * W * last].view(N, H, W, last)
-        Ni, Ci, Hi, Wi = shapes[self.input_name]
-        self._graph_input = torch.zeros(Ni, Hi, Wi, Ci, dtype=torch.float16, device=self.dev)
-        No, Co, Ho, Wo = shapes[self.output_name]
-        self._graph_output = torch.empty(No, Ho, Wo, Co, dtype=torch.float16, device=self.dev)
+        for t in live:
+            k, n = sizes[t]
+            self.tensors[t] = self.buffers[plan[t]][:n]
         self._shapes = shapes
+        self._root_fn = root
+
+        if self.image_input:
+            B, C, H, W = shapes[self.input_name]
+            self._graph_input = self.tensors[self.input_name].view(B, C, H, W)
+        else:
+            Ni, Ci, Hi, Wi = shapes[self.input_name]
+            self._graph_input = torch.zeros(Ni, Hi, Wi, Ci, dtype=torch.float16, device=self.dev)
+        if self.logits_output:
+            self._graph_output = self.tensors[root(self.output_name)].view(*shapes[self.output_name])
+        else:
+            No, Co, Ho, Wo = shapes[self.output_name]
+            self._graph_output = torch.empty(No, Ho, Wo, Co, dtype=torch.float16, device=self.dev)
 
         # weights, BN vectors, membranes
-        for nid in self.schedule:
-            node = ir.nodes[nid]
-            name = _kname(node)
-            if name in FUSED_VARIANTS or name in DENSE_VARIANTS:
+        for l in launches:
+            node = ir.nodes[l.nid]
+            if l.kind in ("fused", "dense", "stem"):
                 w = torch.from_numpy(np.ascontiguousarray(ir.weights[node.weight_info.name]))
-                self.weights[nid] = self.kernels[nid].prepare_weight(w.to(self.dev), device=self.dev)
-                self.bn[nid] = (torch.tensor(node.bn_scale, dtype=torch.float32, device=self.dev),
-                                torch.tensor(node.bn_bias, dtype=torch.float32, device=self.dev))
-                if keep_membranes and name in FUSED_VARIANTS:
+                self.weights[l.nid] = self.kernels[l.nid].prepare_weight(w.to(self.dev), device=self.dev)
+                self.bn[l.nid] = (torch.tensor(node.bn_scale, dtype=torch.float32, device=self.dev),
+                                  torch.tensor(node.bn_bias, dtype=torch.float32, device=self.dev))
+                if keep_membranes and l.kind == "fused":
                     N, C, H, W = node.output_shapes[0]
-                    self.membranes[nid] = torch.zeros(N // self.T * H * W, C, device=self.dev)
-            elif name in NEURON_VARIANTS and keep_membranes:
+                    self.membranes[l.nid] = torch.zeros(N // self.T * H * W, C, device=self.dev)
+            elif l.kind == "neuron" and keep_membranes:
                 N, C, H, W = node.output_shapes[0]
-                self.membranes[nid] = torch.zeros(N // self.T * H * W * C, device=self.dev)
+                self.membranes[l.nid] = torch.zeros(N // self.T * H * W * C, device=self.dev)
+            elif l.kind == "head":
+                self.weights[l.nid] = (
+                    torch.from_numpy(np.ascontiguousarray(ir.weights[node.weight_info.name])).float().to(self.dev),
+                    torch.from_numpy(np.ascontiguousarray(ir.weights[node.bias_info.name])).float().to(self.dev))
         self.graph = None
         return self
 
-    def _is_real(self, t: str) -> bool:
-        return self._producer_kind.get(t) in DENSE_VARIANTS
+    @property
+    def n_launches(self) -> int:
+        """Kernel launches per forward (pack / unpack of a spike-input graph included)."""
+        n = sum(1 for l in self.launches if not l.skip)
+        if not self.image_input:
+            n += 1
+        if not self.logits_output:
+            n += 1
+        return n
 
     # ------------------------------------------------------------------ execution
+    def _bits(self, t):
+        r = self._root_fn(t)
+        N, C, H, W = self._shapes[r]
+        return self.tensors[r].view(N, H, W, C * self.planes.get(r, 1) // 32)
+
+    def _run_fused(self, l):
+        node = self.ir.nodes[l.nid]
+        kern = self.kernels[l.nid]
+        x, y = self._bits(l.inputs[0]), self._bits(l.output)
+        sc, bi = self.bn[l.nid]
+        sw = self.weights[l.nid]
+        spec = kern.spec_for(ENC_BITS, ENC_BITS)
+        if len(l.inputs) == 2:  # SEW add absorbed
+            ea = node.extra_attrs
+            res = self._bits(l.inputs[1])
+            ops.fused_sparse_conv_bn_lif_add(spec, x.view(-1), sw.values, sw.meta, sc, bi, res,
+                                             int(self.planes.get(self._root_fn(l.inputs[1]), 1)),
+                                             int(ea.get("out_planes", 1)), state=self.membranes.get(l.nid), out=y)
+            return
+        if l.pair_with is not None:
+            o = next(m for m in self.launches if m.nid == l.pair_with)
+            k2 = self.kernels[o.nid]
+            sw2 = self.weights[o.nid]
+            sc2, bi2 = self.bn[o.nid]
+            ops.fused_sparse_conv_bn_lif_pair(spec, k2.spec_for(ENC_BITS, ENC_BITS), x.view(-1), sw.values, sw.meta,
+                                              sc, bi, sw2.values, sw2.meta, sc2, bi2, out0=y, out1=self._bits(o.output))
+            return
+        mem = self.membranes.get(l.nid)
+        args = (x, sw, mem, sc, bi) if mem is not None else (x, sw, sc, bi)
+        kern(*args, out_enc=ENC_BITS, out=y)
+
     def _execute_schedule(self):
-        ops.pack_spikes(self._graph_input, out=self.tensors[self.input_name])  # first op of the graph
-        for nid in self.schedule:
-            node = self.ir.nodes[nid]
-            name = _kname(node)
-            if name == "ZeroCost":
+        if not self.image_input:  # first op of the graph
+            ops.pack_spikes(self._graph_input, out=self._bits(self.input_name))
+        for l in self.launches:
+            if l.skip:
                 continue
-            x = self.tensors[node.input_names[0]]
-            y = self.tensors[node.output_names[0]]
-            if name in FUSED_VARIANTS:
-                sc, bi = self.bn[nid]
-                mem = self.membranes.get(nid)
-                args = (x, self.weights[nid], mem, sc, bi) if mem is not None else (x, self.weights[nid], sc, bi)
-                self.kernels[nid](*args, out_enc=ENC_BITS, out=y)
-            elif name in DENSE_VARIANTS:
-                sc, bi = self.bn[nid]
-                self.kernels[nid](x, self.weights[nid], sc, bi, out=y)
-            else:  # standalone neuron on a dense conv's fp32 output
+            node = self.ir.nodes[l.nid]
+            if l.kind == "fused":
+                self._run_fused(l)
+            elif l.kind == "dense":
+                sc, bi = self.bn[l.nid]
+                r = self._root_fn(l.output)
+                N, C, H, W = self._shapes[r]
+                self.kernels[l.nid](self._bits(l.inputs[0]), self.weights[l.nid], sc, bi,
+                                    out=self.tensors[r].view(N, H, W, C))
+            elif l.kind == "neuron":  # standalone neuron on a dense conv's fp32 output
                 p = node.neuron_params
                 kind = "lif" if node.op_type.name == "LIF" else "if"
                 v_reset = float(p.v_reset) if p.hard_reset else None
-                ops.multistep_neuron(x.view(-1), self.T, kind, float(p.tau), float(p.v_threshold), v_reset,
-                                     state=self.membranes.get(nid), out_enc=ENC_BITS, out=y.view(-1))
-        ops.unpack_spikes(self.tensors[self.output_name], self._graph_output.shape[-1], out=self._graph_output)
+                ops.multistep_neuron(self.tensors[self._root_fn(l.inputs[0])], self.T, kind, float(p.tau),
+                                     float(p.v_threshold), v_reset, state=self.membranes.get(l.nid), out_enc=ENC_BITS,
+                                     out=self._bits(l.output).view(-1))
+            elif l.kind == "stem":
+                sc, bi = self.bn[l.nid]
+                kern = self.kernels[l.nid]
+                y = self._bits(l.output)
+                if kern.pool is not None:
+                    kern(self._graph_input, self.weights[l.nid], sc, bi, pooled=y)
+                else:
+                    kern(self._graph_input, self.weights[l.nid], sc, bi, spikes=y)
+            elif l.kind == "pool":
+                r = self._root_fn(l.inputs[0])
+                N, C, H, W = self._shapes[r]
+                if self.planes.get(r, 1) != 1:
+                    raise SEngineError(f"node {node.name}: max-pool of integer activations is not served")
+                pp = node.pool_params or {}
+                ops.maxpool_spikes(self._bits(l.inputs[0]), N, H, W, C, int(pp.get("kernel_size", 3)),
+                                   int(pp.get("stride", 2)), int(pp.get("padding", 1)), out=self._bits(l.output))
+            elif l.kind == "head":
+                fw, fb = self.weights[l.nid]
+                self.kernels[l.nid](self._bits(l.inputs[0]).view(-1), fw, fb, out=self._graph_output)
+        if not self.logits_output:
+            ops.unpack_spikes(self._bits(self.output_name), self._graph_output.shape[-1], out=self._graph_output)
 
     def capture_graph(self):
         """Warm up on a side stream, then capture the whole schedule into one hipGraph."""
@@ -231,9 +426,12 @@ class CUDAGraphEngine:
         self.graph = g
         return g
 
-    def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        """x: spikes (B, C, H, W) (repeated over T, as the reference's static-image input) or
-        (T*B, C, H, W) NCHW, or (T*B, H, W, C) NHWC.  Returns fp16 NHWC spikes (T*B, OH, OW, C)."""
+    def _load_input(self, x: torch.Tensor):
+        if self.image_input:
+            if tuple(x.shape) != tuple(self._graph_input.shape):
+                raise SEngineError(f"input shape {tuple(x.shape)}: expected images {tuple(self._graph_input.shape)}")
+            self._graph_input.copy_(x)
+            return
         TB, H, W, C = self._graph_input.shape
         if tuple(x.shape) != (TB, H, W, C):  # NCHW, per image (repeated over T) or per (t, b)
             if x.ndim != 4 or tuple(x.shape[1:]) != (C, H, W) or x.shape[0] not in (self.B, TB):
@@ -243,6 +441,13 @@ class CUDAGraphEngine:
                 x = x.repeat(self.T, 1, 1, 1)
             x = x.permute(0, 2, 3, 1)
         self._graph_input.copy_(x)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        """Spike-input graphs: x spikes (B, C, H, W) (repeated over T, as the reference's
+        static-image input) or (T*B, C, H, W) NCHW, or (T*B, H, W, C) NHWC; returns fp16 NHWC
+        spikes (T*B, OH, OW, C).  Image-input graphs (a stem first): x (B, C, H, W) fp32
+        pixels; returns the head's logits (B, classes) fp32."""
+        self._load_input(x)
         if self.graph is not None:
             self.graph.replay()
         else:
@@ -260,13 +465,33 @@ class CUDAGraphEngine:
         for _ in range(warmup):
             run()
         torch.cuda.synchronize(self.dev)
+        s = torch.cuda.current_stream(self.dev)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
+        a.record(s)
         for _ in range(n_iters):
             run()
-        b.record()
+        b.record(s)
         torch.cuda.synchronize(self.dev)
         return a.elapsed_time(b) / n_iters
+
+    def spike_density(self) -> dict:
+        """Activity of every spike tensor of the last forward: fraction of set bits per
+        activation (for integer activations, of nonzero values).  Off the timed path."""
+        lut = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.int64, device=self.dev)
+        out = {}
+        for l in self.launches:
+            if l.kind in ("dense", "head"):
+                continue
+            r = self._root_fn(l.output)
+            N, C, H, W = self._shapes[r]
+            P = self.planes.get(r, 1)
+            words = self._bits(l.output).reshape(N * H * W, P, C // 32)
+            nz = words[:, 0]
+            for p in range(1, P):
+                nz = nz | words[:, p]
+            cnt = int(lut[nz.contiguous().view(torch.uint8).long()].sum())
+            out[self.ir.nodes[l.nid].name] = cnt / float(N * H * W * C)
+        return out
 
 
 HipGraphEngine = CUDAGraphEngine

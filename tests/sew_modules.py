@@ -1,0 +1,64 @@
+"""A module tree with the attribute names of the reference's sew_resnet18 (models/sewresnet.py:
+26-66, 123-210): conv1 / bn1 / sn1 / maxpool / layer1..layer4 of blocks with conv1 and conv2
+as containers holding `module = Sequential(conv, bn)`, sn1 / sn2 neurons, downsample =
+Sequential(container, neuron), avgpool, fc, connect_f.  Test helper for the front end: it
+holds the oracle's parameters under the same state_dict keys and carries no forward."""
+import torch
+from torch import nn
+
+
+class SeqToANN(nn.Module):
+    def __init__(self, *mods):
+        super().__init__()
+        self.module = nn.Sequential(*mods)
+
+
+class Neuron(nn.Module):
+    def __init__(self, tau=2.0, v_threshold=1.0, v_reset=0.0):
+        super().__init__()
+        self.tau, self.v_threshold, self.v_reset = tau, v_threshold, v_reset
+
+
+class Block(nn.Module):
+    def __init__(self, cin, planes, stride, downsample, neuron_kw):
+        super().__init__()
+        self.conv1 = SeqToANN(nn.Conv2d(cin, planes, 3, stride, 1, bias=False), nn.BatchNorm2d(planes))
+        self.sn1 = Neuron(**neuron_kw)
+        self.conv2 = SeqToANN(nn.Conv2d(planes, planes, 3, 1, 1, bias=False), nn.BatchNorm2d(planes))
+        self.sn2 = Neuron(**neuron_kw)
+        self.downsample = downsample
+        self.connect_f = "ADD"
+
+
+class SEWResNet18Modules(nn.Module):
+    def __init__(self, num_classes=100, in_channels=3, neuron_kw=None):
+        super().__init__()
+        kw = neuron_kw or {}
+        self.connect_f = "ADD"
+        self.conv1 = nn.Conv2d(in_channels, 64, 7, 2, 3, bias=False)
+        self.bn1 = nn.BatchNorm2d(64)
+        self.sn1 = Neuron(**kw)
+        self.maxpool = SeqToANN(nn.MaxPool2d(3, 2, 1))
+        inplanes = 64
+        for si, (planes, stride) in enumerate(((64, 1), (128, 2), (256, 2), (512, 2))):
+            blocks = []
+            for bi in range(2):
+                s = stride if bi == 0 else 1
+                ds = None
+                if bi == 0 and (s != 1 or inplanes != planes):
+                    ds = nn.Sequential(SeqToANN(nn.Conv2d(inplanes, planes, 1, s, bias=False), nn.BatchNorm2d(planes)),
+                                       Neuron(**kw))
+                blocks.append(Block(inplanes, planes, s, ds, kw))
+                inplanes = planes
+            setattr(self, f"layer{si + 1}", nn.Sequential(*blocks))
+        self.avgpool = SeqToANN(nn.AdaptiveAvgPool2d((1, 1)))
+        self.fc = nn.Linear(512, num_classes)
+
+    @classmethod
+    def from_params(cls, params: dict, **kw):
+        m = cls(num_classes=params["fc.weight"].shape[0], in_channels=params["conv1.weight"].shape[1], **kw)
+        sd = m.state_dict()
+        missing = [k for k in sd if k not in params and not k.endswith("num_batches_tracked")]
+        assert not missing, missing
+        m.load_state_dict({k: params.get(k, sd[k]) for k in sd})
+        return m.eval()

@@ -52,3 +52,27 @@ def test_sizes_are_not_mixed():
     sizes = {"x": ("bits", 8), "a": ("f32", 64), "b": ("bits", 8), "c": ("bits", 8)}
     plan = plan_buffers(schedule, produces, consumes, {}, sizes, {"x", "c"})
     assert plan["a"] not in (plan["b"], plan["c"], plan["x"])
+
+
+def test_engine_buffer_plan_reuses_sew_activations():
+    """The generic engine's plan for SEW-ResNet-18 (analysis only, no GPU): launches read and
+    write root tensors, buffers are reused across blocks, and no launch writes a buffer it
+    reads."""
+    from oracle import sew_resnet as sr
+    from sparsesnn_amd import frontend, passes
+    from sparsesnn_amd.runtime import CUDAGraphEngine
+    ir = frontend.sew_resnet_ir(sr.make_params(1, fp16_weights=True), T=4, batch=2)
+    passes.optimize_ir(ir)
+    eng = CUDAGraphEngine()
+    launches, aliases, shapes = eng._analyse(ir, ir.topo_order)
+    launches = eng._order(launches, aliases, ir.topo_order)
+    root = lambda t: CUDAGraphEngine._root(t, aliases)  # noqa: E731
+    produces = {l.nid: [root(l.output)] for l in launches}
+    consumes = {l.nid: [root(t) for t in l.inputs] for l in launches}
+    sizes = {t: ("bits", 1) for ts in list(produces.values()) + list(consumes.values()) for t in ts}
+    graph_in = {t for ts in consumes.values() for t in ts} - {t for ts in produces.values() for t in ts}
+    plan = plan_buffers([l.nid for l in launches], produces, consumes, {}, sizes, graph_in | {"logits"})
+    assert len(set(plan.values())) < len(sizes) // 2
+    for l in launches:
+        assert plan[root(l.output)] not in {plan[root(t)] for t in l.inputs}, ir.nodes[l.nid].name
+    _check_no_overlap([l.nid for l in launches], produces, consumes, {}, plan)
