@@ -68,6 +68,7 @@ def build_workloads(dev, T, B, seed=1234):
         spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=k, KW=k, stride=1, padding=k // 2,
                             neuron="lif", tau=2.0, v_threshold=1.0, v_reset=0.0)
         values, meta, _ = ops.compress_2_4(spec, w)
+        w_hwio = w.permute(2, 3, 1, 0).contiguous()  # the reference runtime's weight layout
         scale, bias = scale.to(dev), bias.to(dev)
         for p in DENSITIES:
             x = (torch.rand((T * B, H, W, C_in), generator=g, device=dev) < p).half()
@@ -77,7 +78,7 @@ def build_workloads(dev, T, B, seed=1234):
             out = torch.empty(T * B, OH, OW, C_out // 32, dtype=torch.int32, device=dev)
             flops, bmin = layer_work(C_in, C_out, H, W, k, T, B)
             work.append(dict(name=f"{C_in}->{C_out} {H}x{W} k{k} p{p}", spec=spec, data=data, values=values,
-                             meta=meta, scale=scale, bias=bias, out=out, flops=flops, bytes_min=bmin,
+                             meta=meta, w_hwio=w_hwio, scale=scale, bias=bias, out=out, flops=flops, bytes_min=bmin,
                              ideal=max(flops / P_SPARSE, bmin / BW_HBM)))
     torch.cuda.synchronize(dev)
     return work
@@ -87,6 +88,117 @@ def run_layer(wk):
     from sparsesnn_amd import ops
     ops.fused_sparse_conv_bn_lif(wk["spec"], wk["data"], wk["values"], wk["meta"], wk["scale"], wk["bias"],
                                  out=wk["out"])
+
+
+def abi_work(wk):
+    """fp16 bytes of the reference call() ABI: fp16 NHWC activations in and spikes out (2 bytes
+    per value), the fp16 2:4 weight blob, BN vectors."""
+    s = wk["spec"]
+    M, K_red = s.T * s.B * s.H * s.W, s.KH * s.KW * s.C_in  # stride 1, same padding
+    return (s.T * s.B * s.H * s.W * s.C_in) * 2 + M * s.C_out * 2 + s.C_out * K_red / 2 * 2 + s.C_out * K_red / 8 \
+        + 8 * s.C_out
+
+
+def bench_abi(dev, work, warmup: int, steps: int):
+    """The 15 sweep launches through the reference's native ABI: one exported per-node .so per
+    shape (export.export_kernel_so), call(data, weight, state, bn_scale, bn_bias, spikes, stream)
+    with fp16 NHWC spikes in and out and the runtime's fp16 (KH, KW, C_in, C_out) weight (the
+    library builds the 2:4 blob on the first eager call).  Per-launch durations from event-
+    bracketed bursts, the step from a hipGraph of the 15 calls; the fp16 output is checked
+    against the bit path's output of the same inputs."""
+    import ctypes
+    import tempfile
+    import torch
+    from sparsesnn_amd import _lib, export, ops
+    from sparsesnn_amd.compiler import FusedSparseConvBNLIFKernel
+
+    tmp = tempfile.mkdtemp(prefix="sengine_abi_")
+    stream = torch.cuda.current_stream(dev)
+    calls, sos = [], {}
+    for wk in work:
+        s = wk["spec"]
+        key = (s.C_in, s.C_out, s.H, s.W, s.KH)
+        if key not in sos:
+            kern = FusedSparseConvBNLIFKernel(s, "k%d_%d_%d_%d_%d" % key)
+            so = ctypes.CDLL(export.export_kernel_so(kern, os.path.join(tmp, "kern_%d_%d_%d_%d_%d.so" % key)))
+            so.call.restype = ctypes.c_int
+            so.call.argtypes = [ctypes.c_void_p] * 7
+            assert so.init() == 0
+            sos[key] = (so, wk["w_hwio"])
+        so, w = sos[key]
+        x = ops.unpack_spikes(wk["data"], s.C_in)
+        OH, OW, M, _ = ops.geometry(s)
+        out = torch.empty(s.T * s.B, OH, OW, s.C_out, dtype=torch.float16, device=dev)
+        args = (x.data_ptr(), w.data_ptr(), None, wk["scale"].data_ptr(), wk["bias"].data_ptr(), out.data_ptr())
+        calls.append(dict(wk=wk, so=so, args=args, x=x, out=out, bytes=abi_work(wk)))
+
+    def run(c, st):
+        rc = c["so"].call(*c["args"], st.cuda_stream)
+        if rc:
+            raise RuntimeError(f"call() of {c['wk']['name']} returned {rc}: "
+                               f"{_lib.load().sengine_amd_last_error().decode()}")
+
+    for _ in range(max(1, warmup)):
+        for c in calls:
+            run(c, stream)
+    torch.cuda.synchronize(dev)
+    mismatch = 0
+    for c in calls:
+        run_layer(c["wk"])
+        ref = ops.unpack_spikes(c["wk"]["out"], c["wk"]["spec"].C_out)
+        mismatch += int((ref != c["out"]).sum().item())
+    per = {c["wk"]["name"]: [] for c in calls}
+    evs = []
+    for _ in range(3):
+        for c in calls:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(BURST):
+                run(c, stream)
+            b.record(stream)
+            evs.append((c["wk"]["name"], a, b))
+    torch.cuda.synchronize(dev)
+    for name, a, b in evs:
+        per[name].append(a.elapsed_time(b) * 1e-3 / BURST)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cs = torch.cuda.current_stream(dev)
+        for c in calls:
+            run(c, cs)
+    for _ in range(max(1, warmup)):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize(dev)
+    step_s = t0.elapsed_time(t1) * 1e-3 / steps
+    ideal = sum(max(c["wk"]["flops"] / P_SPARSE, c["bytes"] / BW_HBM) for c in calls)
+    n = sum(len(v) for v in per.values())
+    avg = sum(sum(v) for v in per.values()) / n
+    hbm = [c for c in calls if c["bytes"] / BW_HBM > c["wk"]["flops"] / P_SPARSE]
+    res = {
+        "value": round(100.0 * ideal / step_s, 3),
+        "unit": "% of roofline (sum of per-layer max(F/5.0 PFLOP/s, B_fp16/8 TB/s) / step time)",
+        "ms_per_step": round(step_s * 1e3, 4),
+        "per_layer_us": {k: round(statistics.median(v) * 1e6, 2) for k, v in per.items()},
+        "spikes_differing_from_bit_path": mismatch,
+        "launches_per_step": len(calls),
+        "step": "hipGraph replay of the 15 exported-.so call()s",
+        "io": "fp16 NHWC spikes in and out, fp16 HWIO weight (2:4 blob built once by the library)",
+        "roofline": {
+            "bound": "hbm" if len(hbm) * 2 > len(calls) else "mfma",
+            "achieved_tflops": round(sum(c["wk"]["flops"] for c in calls) / len(calls) / avg / 1e12, 2),
+            "achieved_gbps": round(sum(c["bytes"] for c in calls) / len(calls) / avg / 1e9, 1),
+            "avg_launch_us": round(avg * 1e6, 3),
+            "hbm_bound_layers": [c["wk"]["name"] for c in hbm],
+        },
+    }
+    del calls
+    torch.cuda.empty_cache()
+    return res
 
 
 CPU_WARMUP, CPU_MIN_RUNS = 3, 10  # BASELINE.md section 4: 3 warmups, median of >= 10 runs
@@ -134,8 +246,8 @@ def cpu_baseline(budget_s=12.0, min_runs=CPU_MIN_RUNS):
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "fused_tile_kernel_cfg1_sweep_traffic.md")
 # the sources the sweep's kernels are built from (the halo-tiled fused kernel and its dispatch)
-SWEEP_KERNEL_SOURCES = ("common.h", "epilogue.h", "internal.h", "tile_kernel.h", "fused_tile1.hip", "fused_tile3.hip",
-                        "fused_sparse.hip")
+SWEEP_KERNEL_SOURCES = ("common.h", "epilogue.h", "internal.h", "tile_kernel.h", "tile1pm.h", "fused_tile1.hip",
+                        "fused_tile3.hip", "fused_sparse.hip")
 
 
 def kernel_source_hash() -> str:
@@ -314,6 +426,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--json-out", default="")
     ap.add_argument("--no-e2e", action="store_true", help="skip the SEW-ResNet-18 end-to-end measurement")
+    ap.add_argument("--no-abi", action="store_true",
+                    help="skip the sweep through the exported per-node .so (fp16 call() ABI)")
     ap.add_argument("--e2e-only", action="store_true",
                     help="only one end-to-end measurement (--e2e-model; prints its JSON object; for profiling)")
     ap.add_argument("--e2e-model", default="sew18", choices=("sew18", "msresnet34", "spikformer"),
@@ -452,6 +566,8 @@ def main():
             "frac_of_measured": round(avg_flops / avg_launch / (calib["smfmac_tflops_dense_equiv"] * 1e12), 4),
         },
     }
+    if not args.no_abi:
+        result["abi_f16"] = bench_abi(dev, work, warmup=args.warmup, steps=args.steps)
     if not args.no_cpu_baseline:
         cb = cpu_baseline()
         result["cpu_baseline"] = {

@@ -352,6 +352,28 @@ int sengine_amd_unpack_spikes(const uint32_t* bits, int64_t n_pos, int32_t C, vo
                               hipStream_t stream);
 
 /*
+ * The fused node called with the reference runtime's own weight tensor instead of a blob:
+ * the fp16 (KH, KW, C_in, C_out) weight of sengine/cuda_graph_runtime.py:233-235
+ * (w_enc = SENGINE_ENC_F16, w_layout = SENGINE_WLAYOUT_HWIO; any other encoding / layout the
+ * compressor accepts).  Replaces the body of the reference's per-node call()
+ * (sengine/build/export_standalone.py:37-103, called at sengine/csrc/cpp_executor.cu:909-913).
+ * The library keeps one 2:4 blob per (device, weight pointer, geometry): prepared on the first
+ * call outside stream capture (allocation, compression, one synchronising check of the 2:4
+ * pattern -- the reference executor runs three eager warm-ups before it captures,
+ * cpp_executor.cu:1270-1276) and reused by every later call, captured ones included.  A weight
+ * first seen during capture returns -4; a weight that is not 2:4 along C_in returns -5.
+ * The blob is not refreshed when the weight memory changes: call sengine_amd_release_weights()
+ * (no kernel of the library may be running) after updating weights in place.
+ * sengine_amd_prepare_weight does the preparation step alone.
+ */
+int sengine_amd_fused_call_raw_weight(const sengine_conv_lif_desc* d, const void* data, const void* weight,
+                                      int32_t w_enc, int32_t w_layout, float* state, const float* bn_scale,
+                                      const float* bn_bias, void* spikes, hipStream_t stream);
+int sengine_amd_prepare_weight(const sengine_conv_lif_desc* d, const void* weight, int32_t w_enc, int32_t w_layout,
+                               hipStream_t stream);
+int sengine_amd_release_weights(void);
+
+/*
  * Peak calibration on the box (the role of the reference's sengine/tuning/hw_calibrate.py:
  * 17-134, which times a memcpy and a dense fp16 GEMM).  Measurement entry points, not on
  * the operator path.

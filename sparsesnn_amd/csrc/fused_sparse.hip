@@ -420,6 +420,12 @@ static int plan_fused(const sengine_conv_lif_desc* d, const void* data, const vo
     plan.route = kRouteTiled;
     return 0;
   }
+  // fp16 activations (the reference's call() ABI): the tile kernel copies fp16 rows into its
+  // LDS layout; other geometries take the direct-gather kernel
+  if (!flat && d->in_enc == SENGINE_ENC_F16 && (choice == 0 || choice == 3) && tile_eligible(d)) {
+    plan.route = kRouteTiled;
+    return 0;
+  }
 
   FusedParams& p = plan.p;
   p.in = static_cast<const uint8_t*>(data);

@@ -1,5 +1,6 @@
 // Instantiations of the tile kernel (tile_kernel.h) for 1x1 / pad 0 convolutions (any
 // stride), and the host-side choice between tile shapes and channel blocking.
+#include "tile1pm.h"
 #include "tile_kernel.h"
 
 #include <stdio.h>
@@ -43,7 +44,11 @@ double shape_cost(const TileShape& s, int H, int W) {
 }  // namespace
 
 bool tile_eligible(const sengine_conv_lif_desc* d) {
-  if (d->in_enc != SENGINE_ENC_BITS || d->weight_planes != 1 || d->dil_h != 1 || d->dil_w != 1) return false;
+  if (d->weight_planes != 1 || d->dil_h != 1 || d->dil_w != 1) return false;
+  if (d->in_enc != SENGINE_ENC_BITS && !(d->in_enc == SENGINE_ENC_F16 && d->T == 4)) return false;
+  // fp16 input: 32-bit byte offsets of the fp16 rows
+  if (d->in_enc == SENGINE_ENC_F16 && (int64_t)d->T * d->B * d->H * d->W * d->C_in * 2 >= ((int64_t)1 << 31))
+    return false;
   // 32-bit input offsets in the kernel
   if ((int64_t)d->T * d->B * d->H * d->W * (d->C_in / 8) >= ((int64_t)1 << 31)) return false;
   if (d->T != 1 && d->T != 2 && d->T != 4) return false;
@@ -107,6 +112,25 @@ bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice
     const int fp = env_int_now("SENGINE_AMD_TILE_PF", 0);
     if (fp == 1 || fp == 2) c.pf = fp;
   }
+  // 1x1, T = 4: the position-major kernel (tile1pm.h) when the channels split into 4 waves of
+  // 128 (or 64) channels and the reduction into phases of 4 (or 2) chunks.
+  // SENGINE_AMD_TILE1_PM=0|1|2 forces the tile kernel, or that many channel groups per wave.
+  c.pm = 0;
+  c.cg = 0;
+  const int nchunk = d->C_in / 64;
+  c.cg = nchunk % 4 == 0 ? 4 : (nchunk % 2 == 0 ? 2 : 0);
+  if (d->in_enc == SENGINE_ENC_F16) {  // fp16 input: one channel group per wave, no reduction split
+    c.gpw = 1;
+    c.ksplit = 1;
+    c.pf = 1;
+    c.cg = 0;
+  }
+  if (!c.k3 && d->T == 4 && c.cg > 0) {
+    c.pm = d->C_out % 512 == 0 ? 2 : (d->C_out % 256 == 0 ? 1 : 0);
+    const int fpm = env_int_now("SENGINE_AMD_TILE1_PM", -1);
+    if (fpm == 0 || (fpm == 1 && d->C_out % 256 == 0) || (fpm == 2 && d->C_out % 512 == 0)) c.pm = fpm;
+    if (c.pm && ((geo.M + 15) / 16) * (int64_t)(d->C_out / (256 * c.pm)) > 0x7fffffff) c.pm = 0;
+  }
   return true;
 }
 
@@ -115,13 +139,26 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
   if (!choose_tile(d, geo, c)) return snprintf(buf, len, "none (grid too large)");
   static const char* const kEpi[] = {"generic", "lif_hard", "if_hard"};
   const char* oe = d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16";
-  const char* epi = d->out_enc == SENGINE_ENC_BITS ? kEpi[mode] : "generic";
+  const bool f16in = d->in_enc == SENGINE_ENC_F16;
+  const char* epi = d->out_enc == SENGINE_ENC_BITS || f16in ? kEpi[mode] : "generic";
+  if (f16in) {
+    if (c.k3) {
+      const TileShape s = kShapes3[c.shape];
+      return snprintf(buf, len, "tile<T=4,KS=3,TR=%d,TC=%d,GR=%d,GPW=1,KSP=1,PF=1,in=f16,out=%s,epi=%s> grid=%lld",
+                      s.TR, s.TC, s.GR, oe, epi, (long long)c.ntiles * (d->C_out / 64));
+    }
+    return snprintf(buf, len, "tile<T=4,KS=1,GPW=1,in=f16,out=%s,epi=%s> grid=%lld", oe, epi,
+                    (long long)c.ntiles * (d->C_out / 64));
+  }
   if (c.k3) {
     const TileShape s = kShapes3[c.shape];
     return snprintf(buf, len, "tile<T=%d,KS=3,TR=%d,TC=%d,GR=%d,GPW=%d,KSP=%d,PF=%d,out=%s,epi=%s> grid=%lld",
                     d->T, s.TR, s.TC, s.GR, c.gpw, c.ksplit, c.pf, oe, epi,
                     (long long)c.ntiles * (d->C_out / (64 * c.gpw)));
   }
+  if (c.pm)
+    return snprintf(buf, len, "tile1pm<T=%d,GPW=%d,CG=%d,out=%s,epi=%s> grid=%lld", d->T, c.pm, c.cg, oe, epi,
+                    (long long)((geo.M + 15) / 16) * (d->C_out / (256 * c.pm)));
   return snprintf(buf, len, "tile<T=%d,KS=1,GPW=%d,out=%s,epi=%s> grid=%lld", d->T, c.gpw, oe, epi,
                   (long long)c.ntiles * (d->C_out / (64 * c.gpw)));
 }
@@ -146,13 +183,21 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
   p.nchunk = d->C_in / 64;
   p.nq = d->KH * d->KW * p.nchunk;
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
-  p.enc_scale = 1.0f / kBitSpikeValue;
+  p.enc_scale = d->in_enc == SENGINE_ENC_BITS ? 1.0f / kBitSpikeValue : 1.0f;
   p.sew = a.sew;
   p.tiles_w = c.tiles_w;
   p.tiles_per_image = c.tiles_per_image;
   p.ntiles = c.ntiles;
   const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr || a.sew.real_out != nullptr);
+  if (d->in_enc == SENGINE_ENC_F16) {
+    if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
+    return launch_tile_f16in<1, 0, 0, 1>(p, d->out_enc, mode, stream);
+  }
   if (c.k3) return launch_tile3(p, d->T, c.shape, c.gpw, c.ksplit, c.pf, d->out_enc, mode, stream);
+  if (c.pm == 2) return c.cg == 4 ? launch_tile1pm<4, 2, 4>(p, d->out_enc, mode, stream)
+                                  : launch_tile1pm<4, 2, 2>(p, d->out_enc, mode, stream);
+  if (c.pm == 1) return c.cg == 4 ? launch_tile1pm<4, 1, 4>(p, d->out_enc, mode, stream)
+                                  : launch_tile1pm<4, 1, 2>(p, d->out_enc, mode, stream);
   return launch_tile1(p, d->T, c.gpw, d->out_enc, mode, stream);
 }
 

@@ -38,4 +38,10 @@ hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int kspl
   }
 }
 
+hipError_t launch_tile3_f16in(const TileParams& p, int shape, int out_enc, int mode, hipStream_t s) {
+  if (shape == 1) return launch_tile_f16in<3, 14, 4, 8>(p, out_enc, mode, s);
+  if (shape == 2) return launch_tile_f16in<3, 7, 7, 7>(p, out_enc, mode, s);
+  return launch_tile_f16in<3, 8, 8, 8>(p, out_enc, mode, s);
+}
+
 }  // namespace sengine

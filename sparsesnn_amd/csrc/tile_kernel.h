@@ -114,9 +114,18 @@ __device__ __forceinline__ void expand_word64(uint2 w, u32x4_t (&pc)[8]) {
 // ahead instead of one: for grids of at most two workgroups per CU, whose waves (two per
 // SIMD) have the registers for it and whose SMFMAC issue otherwise waits on L2 and LDS
 // latency.
-template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP, int PF = 1>
+//
+// IN_ENC = SENGINE_ENC_F16 (the reference's fp16 NHWC activations, any fp16 values): each
+// (t, pixel) unit of a chunk is 64 fp16 = eight 16-byte pieces, copied as they are into the
+// same LDS half-piece layout (no expansion); a thread moves pieces tid, tid + NTHR, ... and
+// the next chunk is fetched after the current one's reduction (the 16-byte pieces would
+// otherwise hold ~50 registers across the loop).
+template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP, int PF = 1,
+          int IN_ENC = SENGINE_ENC_BITS>
 __global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR * KSP))
-__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EPI_GENERIC ? 3 : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
+__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EPI_GENERIC && IN_ENC == SENGINE_ENC_BITS
+                                       ? 3
+                                       : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
   using Gm = TileGeom<KS, TR, TC, GR>;
   static_assert(PF == 1 || (PF == 2 && KS == 3), "two-deep prefetch needs the unrolled 9-tap loop");
   constexpr int NA = PF + 1;  // A operand sets in flight (ring over taps; 9 % 3 == 0)
@@ -201,6 +210,51 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
     for (int j = 0; j < UPT; ++j)
       v[j] = goff[j] >= 0 ? *reinterpret_cast<const uint2*>(p.in + goff[j] + c * 8) : uint2{0u, 0u};
   };
+  // fp16 input: 16-byte pieces; piece pc = tid + j*NTHR is piece pc & 7 of unit pc >> 3
+  constexpr int PPT = IN_ENC == SENGINE_ENC_F16 ? (UNITS * 8 + NTHR - 1) / NTHR : 1;
+  auto unit_off16 = [&](int u) {  // byte offset of unit u's fp16 pixel row, or -1 (zero)
+    const int t = u / NPIX;
+    const int px = u - t * NPIX;
+    int ib = b, ih, iw;
+    bool inb;
+    if (KS == 3) {
+      const int hr = px / Gm::HC;
+      ih = oh0 - 1 + hr;
+      iw = ow0 - 1 + (px - hr * Gm::HC);
+      inb = u < UNITS && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
+    } else {
+      const int m = m0 + px;
+      inb = u < UNITS && m < p.M;
+      const int ohw = p.OH * p.OW;
+      ib = inb ? m / ohw : 0;
+      const int r = m - ib * ohw;
+      const int oh = inb ? r / p.OW : 0;
+      ih = oh * p.S;
+      iw = (r - oh * p.OW) * p.S;
+    }
+    return inb ? (((t * p.B + ib) * p.H + ih) * p.W + iw) * (p.C * 2) : -1;
+  };
+  auto load_pieces = [&](u32x4_t (&v)[PPT], int c) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pc = tid + j * NTHR;
+      const int o = pc < UNITS * 8 ? unit_off16(pc >> 3) : -1;
+      v[j] = o >= 0 ? *reinterpret_cast<const u32x4_t*>(p.in + o + (c * 64 + (pc & 7) * 8) * 2) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_pieces = [&](int buf, const u32x4_t (&v)[PPT]) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pc = tid + j * NTHR;
+      if ((j + 1) * NTHR <= UNITS * 8 || pc < UNITS * 8) {
+        const int u = pc >> 3, i = pc & 7;
+        const int t = u / NPIX;
+        const int e = t * TS + (u - t * NPIX) + (i >> 1) * NPIX + (i & 1) * (8 * NPIX + PAD);
+        sB[buf][e] = uint2{v[j][0], v[j][1]};
+        sB[buf][e + 4 * NPIX] = uint2{v[j][2], v[j][3]};
+      }
+    }
+  };
   auto store_units = [&](int buf, const uint2 (&v)[UPT]) {
 #pragma unroll
     for (int j = 0; j < UPT; ++j) {
@@ -282,13 +336,19 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
 #pragma unroll
   for (int i = 0; i < PF; ++i) load_a(set, i, av[i], ix[i]);
   uint2 stg[UPT];
-  load_units(stg, set);
-  store_units(set * NBUF, stg);
+  if (IN_ENC == SENGINE_ENC_F16) {
+    u32x4_t pcs[PPT];
+    load_pieces(pcs, set);
+    store_pieces(set * NBUF, pcs);
+  } else {
+    load_units(stg, set);
+    store_units(set * NBUF, stg);
+  }
   __syncthreads();
   for (int c = set; c < p.nchunk; c += KSP) {  // host: nchunk % KSP == 0 (sets stay in step)
     const bool more = c + KSP < p.nchunk;
     const int buf = NBUF == 2 ? ((c / KSP) & 1) : 0;
-    if (more) load_units(stg, c + KSP);
+    if (IN_ENC == SENGINE_ENC_BITS && more) load_units(stg, c + KSP);
     // B fragments: four ds_read_b64 per (tap, t), issued PF steps ahead of their SMFMACs
     // and waited for with an explicit lgkmcnt (the loop issues no other LDS operation).
     // Written as asm so the compiler neither fuses them into 16-byte or paired reads nor
@@ -353,7 +413,13 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
     }
     if (more) {
       if (NBUF == 1) __syncthreads();  // every wave is done reading the single buffer
-      store_units(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), stg);
+      if (IN_ENC == SENGINE_ENC_F16) {
+        u32x4_t pcs[PPT];
+        load_pieces(pcs, c + KSP);
+        store_pieces(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), pcs);
+      } else {
+        store_units(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), stg);
+      }
       __syncthreads();
     }
   }
@@ -394,6 +460,28 @@ struct TileShape {
   int KS, TR, TC, GR;
 };
 
+// fp16-input instances: T = 4, one channel group per wave, no reduction split (the reference
+// ABI's fp16 activations), bit or fp16 output, every epilogue mode.
+template <int KS, int TR, int TC, int GR, int PF = 1>
+hipError_t launch_tile_f16in(const TileParams& p, int out_enc, int mode, hipStream_t s) {
+  constexpr int NTHR = TileGeom<KS, TR, TC, GR>::NTHR;
+  const dim3 grid((unsigned)(p.ntiles * (p.F / 64)));
+  constexpr int F16 = SENGINE_ENC_F16;
+#define SENGINE_TILE_F16(OE, MODE_)                                                                                 \
+  hipLaunchKernelGGL((fused_tile_kernel<4, KS, TR, TC, GR, 1, OE, MODE_, 1, PF, F16>), grid, dim3(NTHR), 0, s, p)
+  if (out_enc == SENGINE_ENC_BITS) {
+    if (mode == EPI_LIF_HARD) SENGINE_TILE_F16(SENGINE_ENC_BITS, EPI_LIF_HARD);
+    else if (mode == EPI_IF_HARD) SENGINE_TILE_F16(SENGINE_ENC_BITS, EPI_IF_HARD);
+    else SENGINE_TILE_F16(SENGINE_ENC_BITS, EPI_GENERIC);
+  } else {
+    if (mode == EPI_LIF_HARD) SENGINE_TILE_F16(SENGINE_ENC_F16, EPI_LIF_HARD);
+    else if (mode == EPI_IF_HARD) SENGINE_TILE_F16(SENGINE_ENC_F16, EPI_IF_HARD);
+    else SENGINE_TILE_F16(SENGINE_ENC_F16, EPI_GENERIC);
+  }
+#undef SENGINE_TILE_F16
+  return hipGetLastError();
+}
+
 template <int T, int KS, int TR, int TC, int GR, int GPW, int KSP = 1, int PF = 1>
 hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s) {
   constexpr int NTHR = TileGeom<KS, TR, TC, GR>::NTHR * KSP;
@@ -420,5 +508,7 @@ hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s
 hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int ksplit, int pf, int out_enc, int mode,
                         hipStream_t s);
 hipError_t launch_tile1(const TileParams& p, int T, int gpw, int out_enc, int mode, hipStream_t s);
+// fp16 input (T = 4): the 3x3 tile shapes (fused_tile3.hip), the 1x1 tile kernel (fused_tile1.hip)
+hipError_t launch_tile3_f16in(const TileParams& p, int shape, int out_enc, int mode, hipStream_t s);
 
 }  // namespace sengine

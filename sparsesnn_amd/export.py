@@ -6,9 +6,11 @@ dlopen'd and called by its C++ executor (sengine/csrc/cpp_executor.cu:631-662,89
 export_kernel_so() writes the same two symbols for a kernel object of this build as a
 small C shim (compiled with gcc) that bakes the node's descriptor and forwards to
 libsengine_amd.so.  The fused node's call() takes the reference's six pointers
-(data, weight, state, bn_scale, bn_bias, spikes) + stream; `weight` is the SparseWeight
-blob (values followed by metadata), `state` may be NULL.  call() never allocates or
-synchronises, so it can run inside hipStreamBeginCapture.
+(data, weight, state, bn_scale, bn_bias, spikes) + stream, `weight` being the runtime's fp16
+(KH, KW, C_in, C_out) tensor (cuda_graph_runtime.py:233-235): the library builds the 2:4
+blob on the first call outside capture and reuses it (sengine_amd_fused_call_raw_weight),
+so captured calls allocate and synchronise nothing.  call_blob() takes a pre-built
+SparseWeight blob (values followed by metadata) instead; `state` may be NULL in both.
 """
 from __future__ import annotations
 
@@ -38,6 +40,11 @@ int init(void) { return sengine_amd_version() > 0 ? 0 : -1; }
 
 _CALL_FUSED = r"""
 int call(void* data, void* weight, void* state, void* bn_scale, void* bn_bias, void* spikes, hipStream_t stream) {
+  return sengine_amd_fused_call_raw_weight(&kDesc, data, weight, SENGINE_ENC_F16, SENGINE_WLAYOUT_HWIO,
+                                           (float*)state, (const float*)bn_scale, (const float*)bn_bias, spikes,
+                                           stream);
+}
+int call_blob(void* data, void* weight, void* state, void* bn_scale, void* bn_bias, void* spikes, hipStream_t stream) {
   return sengine_amd_fused_sparse_conv_bn_lif(&kDesc, data, weight, (const char*)weight + kValueBytes,
                                               (float*)state, (const float*)bn_scale, (const float*)bn_bias,
                                               spikes, NULL, NULL, stream);
@@ -88,7 +95,7 @@ def export_kernel_so(kern, output_path: str, in_enc: int = ops.ENC_F16, out_enc:
 def get_call_signature(kern) -> list:
     """(c_type, name) pairs of call(), as export_standalone.get_call_signature (:213-227)."""
     if isinstance(kern, FusedSparseConvBNLIFKernel):
-        return [("half_t*", "data"), ("uint8_t*", "weight"), ("float*", "state"), ("float*", "bn_scale"),
+        return [("half_t*", "data"), ("half_t*", "weight"), ("float*", "state"), ("float*", "bn_scale"),
                 ("float*", "bn_bias"), ("half_t*", "spikes")]
     return [("half_t*", "data"), ("int16_t*", "weight"), ("float*", "bn_scale"), ("float*", "bn_bias"),
             ("float*", "output")]

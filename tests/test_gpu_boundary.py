@@ -4,8 +4,9 @@
 2. kernel-object contract: compile_all()[nid](data, weight, state, bn_scale, bn_bias),
    called the way sengine/cuda_graph_runtime.py:616-643 calls it (fp16 NHWC in/out,
    HWIO weight tensor as the runtime allocates it, membrane (B*OH*OW, C_out));
-3. native ABI: the exported per-node .so, dlopen'd, init() then call(6 ptrs, stream),
-   also captured into a hipGraph and replayed with eager work in between.
+3. native ABI: the exported per-node .so, dlopen'd, init() then call(6 ptrs, stream) with
+   the runtime's fp16 HWIO weight (call_blob() with a pre-built blob), also captured into a
+   hipGraph and replayed with eager work in between.
 """
 import ctypes
 
@@ -14,7 +15,7 @@ import pytest
 import torch
 
 from oracle import reference_path as ref
-from sparsesnn_amd import export, passes, sparsity
+from sparsesnn_amd import export, ops, passes, sparsity
 from sparsesnn_amd.compiler import SparseKernelCompiler
 from sparsesnn_amd.ir import EngineIR, KernelVariant
 from tests.parity import compare, nhwc_seq
@@ -81,46 +82,104 @@ def test_kernel_object_contract(dev, neuron):
 
 
 def test_exported_so_call_and_graph_replay(dev, tmp_path):
+    """call() takes the runtime's fp16 (KH, KW, C_in, C_out) weight: the first (eager) call
+    builds the 2:4 blob, later calls and a captured call reuse it; call_blob() takes a pre-built
+    blob; a weight first seen inside a capture is refused with -4."""
+    from sparsesnn_amd import _lib
     ir, cid, conv, bn = build()
     node = ir.nodes[cid]
     kern = SparseKernelCompiler(ir, batch_size=B).compile_all()[cid]
     so_path = export.export_all_kernels({cid: kern}, ir, str(tmp_path))[cid]
     so = ctypes.CDLL(so_path)
     so.init.restype = ctypes.c_int
-    so.call.restype = ctypes.c_int
-    so.call.argtypes = [ctypes.c_void_p] * 7
+    for fn in (so.call, so.call_blob):
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p] * 7
     assert so.init() == 0
-    sw = kern.prepare_weight(torch.from_numpy(ir.weights[node.weight_info.name]).to(dev))
+    w_oihw = torch.from_numpy(ir.weights[node.weight_info.name])
+    w_hwio = w_oihw.permute(2, 3, 1, 0).contiguous().half().to(dev)
+    sw = kern.prepare_weight(w_oihw.to(dev))
     sc = torch.tensor(node.bn_scale, dtype=torch.float32, device=dev)
     bi = torch.tensor(node.bn_bias, dtype=torch.float32, device=dev)
     x, data = inputs(dev, seed=4)
     mem = torch.zeros(B * H * W, F, device=dev)
     out = torch.empty(T * B, H, W, F, dtype=torch.float16, device=dev)
     stream = torch.cuda.current_stream(dev)
+    try:
+        def call(fn=so.call, w=w_hwio, s=stream):
+            return fn(data.data_ptr(), w.data_ptr(), mem.data_ptr(), sc.data_ptr(), bi.data_ptr(), out.data_ptr(),
+                      s.cuda_stream)
 
-    def call():
-        return so.call(data.data_ptr(), sw.data_ptr(), mem.data_ptr(), sc.data_ptr(), bi.data_ptr(), out.data_ptr(),
-                       stream.cuda_stream)
-
-    assert call() == 0
-    torch.cuda.synchronize()
-    r = oracle(x, conv, bn)
-    check(out.float().cpu(), r)
-    eager = out.clone()
-
-    # capture call() into a hipGraph; membranes are zeroed by a fill kernel before each replay
-    g = torch.cuda.CUDAGraph()
-    mem.zero_()
-    torch.cuda.synchronize()
-    with torch.cuda.graph(g):
-        stream_c = torch.cuda.current_stream(dev)
-        rc = so.call(data.data_ptr(), sw.data_ptr(), mem.data_ptr(), sc.data_ptr(), bi.data_ptr(), out.data_ptr(),
-                     stream_c.cuda_stream)
-    assert rc == 0
-    for i in range(4):
-        out.fill_(7.0)
-        mem.zero_()
-        g.replay()
+        assert call() == 0
         torch.cuda.synchronize()
-        assert torch.equal(out, eager), f"replay {i} differs"
-        _ = (torch.ones(1000, device=dev) * i).sum().item()  # eager work between replays
+        r = oracle(x, conv, bn)
+        check(out.float().cpu(), r)
+        eager = out.clone()
+        assert torch.allclose(mem.view(B, H, W, F).permute(0, 3, 1, 2).cpu(), r.v_final, atol=1e-4)
+        # the pre-built blob gives the same spikes
+        mem.zero_()
+        out.fill_(7.0)
+        assert call(so.call_blob, sw) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+        # capture call() into a hipGraph; membranes are zeroed by a fill kernel before each replay
+        g = torch.cuda.CUDAGraph()
+        mem.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            rc = call(s=torch.cuda.current_stream(dev))
+        assert rc == 0
+        for i in range(4):
+            out.fill_(7.0)
+            mem.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {i} differs"
+            _ = (torch.ones(1000, device=dev) * i).sum().item()  # eager work between replays
+
+        # a weight never called eagerly cannot be prepared inside a capture
+        w_new = w_hwio.clone()
+        g2 = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g2):
+            out.fill_(0.0)
+            rc = call(w=w_new, s=torch.cuda.current_stream(dev))
+        assert rc == -4, rc
+        assert "capture" in _lib.load().sengine_amd_last_error().decode()
+        # ... and is served once it has been seen eagerly
+        mem.zero_()
+        assert call(w=w_new) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    finally:
+        torch.cuda.synchronize()
+        assert _lib.load().sengine_amd_release_weights() == 0
+
+
+def test_raw_weight_rejects_dense(dev):
+    """A weight that is not 2:4 along C_in is refused (-5) and leaves no blob behind."""
+    from sparsesnn_amd import _lib
+    ir, cid, conv, bn = build()
+    node = ir.nodes[cid]
+    kern = SparseKernelCompiler(ir, batch_size=B).compile_all()[cid]
+    dense = torch.randn(3, 3, C, F, device=dev).half()
+    data = torch.zeros(T * B, H, W, C, dtype=torch.float16, device=dev)
+    sc = torch.ones(F, device=dev)
+    bi = torch.zeros(F, device=dev)
+    out = torch.empty(T * B, H, W, F, dtype=torch.float16, device=dev)
+    d = ops.make_desc(kern.spec_for(ops.ENC_F16, ops.ENC_F16))
+    lib = _lib.load()
+    try:
+        rc = lib.sengine_amd_fused_call_raw_weight(ctypes.byref(d), data.data_ptr(), dense.data_ptr(), ops.ENC_F16,
+                                                   ops.WLAYOUT_HWIO, None, sc.data_ptr(), bi.data_ptr(),
+                                                   out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+        assert rc == -5, rc
+        assert "2:4" in lib.sengine_amd_last_error().decode()
+        # refused again on the next call: nothing was cached
+        rc = lib.sengine_amd_prepare_weight(ctypes.byref(d), dense.data_ptr(), ops.ENC_F16, ops.WLAYOUT_HWIO,
+                                            torch.cuda.current_stream(dev).cuda_stream)
+        assert rc == -5, rc
+    finally:
+        torch.cuda.synchronize()
+        assert _lib.load().sengine_amd_release_weights() == 0

@@ -48,7 +48,8 @@ def test_cfg1_layer_full_size(dev, C_in, C_out, H, W, k, p_spike):
                         neuron="lif", tau=2.0, v_threshold=1.0, v_reset=0.0)
     plan = ops.fused_plan(spec)
     print(f"{C_in}->{C_out} {H}x{W} k{k} p{p_spike}: {plan}", flush=True)
-    assert plan.startswith("tile<T=4,") and "epi=lif_hard" in plan and "out=bits" in plan, plan
+    assert plan.startswith(("tile<T=4,", "tile1pm<T=4,")), plan
+    assert "epi=lif_hard" in plan and "out=bits" in plan, plan
     assert ops.fused_plan(spec, state=True).split(" ")[0] == plan.split(" ")[0]
 
     OH, OW, M, _ = ops.geometry(spec)

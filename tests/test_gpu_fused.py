@@ -325,3 +325,100 @@ def test_flat_compressor_matches_numpy(dev, H, W, k, stride, pad, flat):
     assert np.array_equal(values.cpu().numpy().view(np.uint16), ev.reshape(-1))
     assert np.array_equal(meta.cpu().numpy().view(np.uint32), em.reshape(-1))
     assert int(viol.sum()) == 0
+
+
+@pytest.mark.parametrize("traces", [True, False])
+@pytest.mark.parametrize("pm", ["1", "2"])
+@pytest.mark.parametrize("C_in,C_out,H,W,stride,B", [(256, 512, 7, 9, 1, 3), (128, 1024, 6, 5, 1, 2),
+                                                     (384, 512, 9, 10, 2, 2), (512, 256, 4, 13, 1, 2)])
+def test_tile1_position_major(dev, pm, C_in, C_out, H, W, stride, B, traces):
+    """1x1 convs on the position-major kernel (tile1pm.h: 16 positions x 4 waves of 64*GPW
+    channels per workgroup, 2 or 4 chunks per staging phase) with GPW forced to 1 or 2, ragged
+    position counts, stride 2, LIF (fast or generic epilogue) and IF with a carried membrane."""
+    import os
+    if pm == "2" and C_out % 512:
+        pytest.skip("two channel groups per wave need C_out % 512 == 0")
+    os.environ["SENGINE_AMD_TILE1_PM"] = pm
+    ops.set_fused_kernel("tile")  # small test shapes would otherwise take the small-M kernel
+    try:
+        case = ref.make_layer_case(150 + C_in // 64 + C_out // 64 + stride, T=4, B=B, C_in=C_in, C_out=C_out, H=H,
+                                   W=W, k=1, stride=stride, padding=0, fp16_weights=True, p_spike=0.2)
+        spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=stride, padding=0)
+        plan = ops.fused_plan(spec, traces=traces)
+        assert plan.startswith(f"tile1pm<T=4,GPW={pm},"), plan
+        rep, x_err, _, _ = run_case(dev, case, traces=traces)
+        assert rep.ok, str(rep)
+        assert x_err is None or x_err < 1e-4
+        g = torch.Generator().manual_seed(5)
+        OH = (H - 1) // stride + 1
+        OW = (W - 1) // stride + 1
+        v0 = torch.rand((B, C_out, OH, OW), generator=g) * 0.4
+        rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0, traces=traces)
+        assert rep2.ok, str(rep2)
+        assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
+    finally:
+        ops.set_fused_kernel("auto")
+        del os.environ["SENGINE_AMD_TILE1_PM"]
+
+
+
+F16_TILE_CASES = [(3, 1, "0", 13, 11, 128, 64, 2), (3, 1, "1", 16, 9, 64, 128, 1), (3, 1, "2", 7, 7, 192, 64, 3),
+                  (1, 1, None, 7, 9, 256, 128, 3), (1, 2, None, 11, 10, 128, 192, 2)]
+
+
+@pytest.mark.parametrize("traces", [True, False])
+@pytest.mark.parametrize("out_enc", [ops.ENC_BITS, ops.ENC_F16])
+@pytest.mark.parametrize("k,stride,shape,H,W,C_in,C_out,B", F16_TILE_CASES)
+def test_tile_f16_input(dev, k, stride, shape, H, W, C_in, C_out, B, out_enc, traces):
+    """fp16 NHWC activations (the reference's call() ABI) through the tile kernels: each 3x3
+    halo-tile shape and 1x1 at stride 1 and 2, bit and fp16 output, LIF with hard reset (fast
+    epilogue), IF with a carried membrane and LIF with soft reset (generic epilogue)."""
+    import os
+    if shape is not None:
+        os.environ["SENGINE_AMD_TILE_SHAPE"] = shape
+    ops.set_fused_kernel("tile")  # small test shapes would otherwise take the small-M kernel
+    try:
+        spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=k, KW=k, stride=stride, padding=k // 2,
+                            in_enc=ops.ENC_F16, out_enc=out_enc)
+        plan = ops.fused_plan(spec, traces=traces)
+        assert plan.startswith(f"tile<T=4,KS={k},") and "in=f16" in plan, plan
+        case = ref.make_layer_case(170 + k + stride + C_in // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k,
+                                   stride=stride, padding=k // 2, fp16_weights=True, p_spike=0.2)
+        rep, x_err, _, _ = run_case(dev, case, in_enc=ops.ENC_F16, out_enc=out_enc, traces=traces)
+        assert rep.ok, str(rep)
+        assert x_err is None or x_err < 1e-4
+        OH, OW = (H - 1) // stride + 1, (W - 1) // stride + 1
+        g = torch.Generator().manual_seed(7)
+        v0 = torch.rand((B, C_out, OH, OW), generator=g) * 0.4
+        rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0, in_enc=ops.ENC_F16,
+                                      out_enc=out_enc, traces=traces)
+        assert rep2.ok, str(rep2)
+        assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
+        rep3, _, _, _ = run_case(dev, case, v_th=0.5, v_reset=None, in_enc=ops.ENC_F16, out_enc=out_enc,
+                                 traces=traces)
+        assert rep3.ok, str(rep3)
+    finally:
+        ops.set_fused_kernel("auto")
+        os.environ.pop("SENGINE_AMD_TILE_SHAPE", None)
+
+
+@pytest.mark.parametrize("k", [3, 1])
+def test_tile_f16_input_real_valued(dev, k):
+    """Any fp16 activation, not only 0/1 spikes: fp16 values in [-2, 2) (exact in fp16) on the
+    fp16-input tile kernel; sums of exact fp16 products in fp32 agree with the fp32 oracle
+    within the membrane tolerance, spikes by the flip rule."""
+    case = ref.make_layer_case(190 + k, T=4, B=2, C_in=128, C_out=128, H=10, W=9, k=k, fp16_weights=True)
+    g = torch.Generator().manual_seed(11)
+    x = (torch.rand(case.x_seq.shape, generator=g) * 4 - 2).half().float()
+    case = ref.LayerCase(x * (torch.rand(x.shape, generator=g) < 0.5), case.w, case.bn, case.stride, case.padding)
+    ops.set_fused_kernel("tile")
+    try:
+        spec = ops.ConvSpec(T=4, B=2, C_in=128, H=10, W=9, C_out=128, KH=k, KW=k, stride=1, padding=k // 2,
+                            in_enc=ops.ENC_F16)
+        assert "in=f16" in ops.fused_plan(spec)
+        rep, x_err, r, _ = run_case(dev, case, in_enc=ops.ENC_F16)
+        print(rep, x_err, float(r.spikes.mean()))
+        assert rep.ok, str(rep)
+        assert x_err < 1e-3
+    finally:
+        ops.set_fused_kernel("auto")
