@@ -16,7 +16,7 @@
 
 namespace sengine {
 
-enum { EPI_GENERIC = 0, EPI_LIF_HARD = 1, EPI_IF_HARD = 2 };
+enum { EPI_GENERIC = 0, EPI_LIF_HARD = 1, EPI_IF_HARD = 2, EPI_SHORTCUT = 3 };
 
 // One hard-reset fire step: spike = h >= v_th (VCC), v = spike ? v_reset : h, and the spike
 // shifted into `word` as its new lowest bit (word = 2*word + spike, with VCC as carry-in).
@@ -163,6 +163,114 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
   }
 }
 
+// 4x4 transpose of 16-byte chunks across the four 16-lane rows of a wave: afterwards chunk q of
+// row r holds what chunk r of row q held (rows r = lane / 16).  Two v_permlane32_swap and two
+// v_permlane16_swap (gfx950) per dword position; every lane of the wave must execute it.
+__device__ __forceinline__ void transpose_rows4(float4_t (&x)[4]) {
+  // (through whole-vector integer copies: the swap builtins fed with per-element float bit
+  // casts were compiled into wrong code by this toolchain; this form is checked on the GPU)
+  uint32_t a[4][4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const u32x4_t w = __builtin_bit_cast(u32x4_t, x[q]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[q][e] = w[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    // rows 2, 3 of chunks 0 / 1 <-> rows 0, 1 of chunks 2 / 3
+    auto s02 = __builtin_amdgcn_permlane32_swap(a[0][e], a[2][e], false, false);
+    auto s13 = __builtin_amdgcn_permlane32_swap(a[1][e], a[3][e], false, false);
+    // odd rows of the first <-> even rows of the second
+    auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    a[0][e] = s01[0];
+    a[1][e] = s01[1];
+    a[2][e] = s23[0];
+    a[3][e] = s23[1];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) x[q] = __builtin_bit_cast(float4_t, u32x4_t{a[q][0], a[q][1], a[q][2], a[q][3]});
+}
+
+// Membrane-shortcut form with bit output and no traces (EPI_SHORTCUT): y = BN(acc) + residual
+// (fp32 rows, rounded once as torch's out + sc) is stored and the neuron runs on y (times 1/tau
+// when folded), with an optional membrane state.  Same values as the generic path; written for
+// three waves per SIMD: one timestep's residual rows are in flight while the previous step is
+// computed and stored (a later step's rows are never written by an earlier step's stores, so
+// the prefetch is safe when the residual and output rows alias), the BN coefficients are read
+// from LDS where used.  Rows move as whole 64-byte lines when all lanes are active and every
+// position's four lanes agree (see transpose_rows4).
+template <int T, int OUT_ENC>
+__device__ __forceinline__ void shortcut_epilogue(const float4_t (&acc)[T][4], bool valid, int m, int M, int F, int cob,
+                                                  const NeuronParams& np, const EpiCoeffs& cf, float* state,
+                                                  uint8_t* __restrict__ out, const SewAdd& sa) {
+  const bool fold = np.neuron == SENGINE_NEURON_LIF && np.pow2;
+  float v[16];
+  float* st = state ? state + (size_t)m * F + cob : nullptr;
+#pragma unroll
+  for (int j = 0; j < 16; j += 4) {
+    float4_t v4 = float4_t{0.f, 0.f, 0.f, 0.f};
+    if (st && valid) v4 = *reinterpret_cast<const float4_t*>(st + j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[j + e] = v4[e];
+  }
+  const int g4 = (int)(threadIdx.x & 63) >> 4;
+  const int mv = valid ? m : -1;
+  const bool rowwise = __builtin_amdgcn_read_exec() == ~0ull &&
+                       __all((cob & 63) == 16 * g4 && __shfl_xor(mv, 16) == mv && __shfl_xor(mv, 32) == mv);
+  const int cq = rowwise ? 16 : 4;
+  const int c0 = rowwise ? cob - 12 * g4 : cob;
+  auto load_rows = [&](int t, float4_t (&r)[4]) {
+    const size_t row = ((size_t)t * M + m) * F + c0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      r[q] = (valid && sa.real_res) ? *reinterpret_cast<const float4_t*>(sa.real_res + row + cq * q)
+                                    : float4_t{0.f, 0.f, 0.f, 0.f};
+    if (rowwise) transpose_rows4(r);
+  };
+  float4_t cur[4], nxt[4];
+  load_rows(0, cur);
+  const uint32_t zres[kResWords] = {};
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    if (t + 1 < T) load_rows(t + 1, nxt);
+    uint32_t word = 0;
+#pragma unroll
+    for (int j4 = 0; j4 < 16; j4 += 4) {
+      const float4_t s4 = *reinterpret_cast<const float4_t*>(cf.sc + j4);
+      const float4_t b4 = *reinterpret_cast<const float4_t*>(cf.bi + j4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = j4 + e;
+        const float xraw = __builtin_fmaf(acc[t][j >> 2][j & 3], s4[e], b4[e]);
+        const float y = sa.real_res ? __fadd_rn(xraw, cur[j >> 2][j & 3]) : xraw;
+        cur[j >> 2][j & 3] = y;
+        const float h = neuron_charge(np, v[j], fold ? y * np.rtau : y);
+        const bool spike = h >= np.vth;
+        v[j] = neuron_reset(np, h, spike);
+        word |= (uint32_t)spike << j;
+      }
+    }
+    if (rowwise) transpose_rows4(cur);
+    if (valid) {
+      const size_t row = ((size_t)t * M + m) * F + c0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) *reinterpret_cast<float4_t*>(sa.real_out + row + cq * q) = cur[q];
+      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, zres);
+    }
+    if (t + 1 < T) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) cur[q] = nxt[q];
+    }
+  }
+  if (st && valid) {
+#pragma unroll
+    for (int j = 0; j < 16; j += 4)
+      *reinterpret_cast<float4_t*>(st + j) = float4_t{v[j], v[j + 1], v[j + 2], v[j + 3]};
+  }
+}
+
 // `valid` false (a padding position past M) computes but stores nothing: keeping the call
 // unconditional avoids a divergent branch whose join reshuffles the accumulators.  `pre`:
 // residual words the kernel loaded earlier (else they are loaded here).
@@ -173,6 +281,11 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
                                              const SewAdd& sa, const SewRes<T>* pre = nullptr) {
   if ((MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD) && state == nullptr) {  // uniform branch
     fast_epilogue_stateless<T, OUT_ENC, MODE>(acc, valid, m, M, F, cob, np, cf, out, sa, pre);
+    return;
+  }
+  if (MODE == EPI_SHORTCUT) {
+    static_assert(MODE != EPI_SHORTCUT || OUT_ENC == SENGINE_ENC_BITS, "the shortcut mode writes spike bits");
+    shortcut_epilogue<T, OUT_ENC>(acc, valid, m, M, F, cob, np, cf, state, out, sa);
     return;
   }
   SewRes<T> res;
@@ -196,6 +309,17 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
     // loaded before any is used: the stores of y could alias them, so loads issued per t
     // would each wait out one memory latency.
     constexpr int RCH = T <= 4 ? 16 : 4;  // channels whose T residual rows are loaded together
+    // Whole-line access: the four lanes of a position (rows g = lane / 16 of the wave, channels
+    // cob = base + 16g) read and write the position's 64 channels as 64-byte lines -- load q
+    // of lane g covers channels base + 16q + 4g .. +3 -- and a 4x4 chunk transpose across the
+    // rows converts between that and the accumulator layout.  Used when all 64 lanes are active
+    // and every position's four lanes agree; otherwise each lane moves its own 64 contiguous bytes.
+    const int g4 = (int)(threadIdx.x & 63) >> 4;
+    const int mv = valid ? m : -1;
+    const bool rowwise = RCH == 16 && __builtin_amdgcn_read_exec() == ~0ull &&  // the transpose reads every lane
+                         __all((cob & 63) == 16 * g4 && __shfl_xor(mv, 16) == mv && __shfl_xor(mv, 32) == mv);
+    const int cq = rowwise ? 16 : 4;           // channel step between a lane's loads / stores
+    const int c0 = rowwise ? cob - 12 * g4 : cob;  // base + 4g (row-wise) or cob
     uint32_t words[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) words[t] = 0;
@@ -204,11 +328,15 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
       float4_t rr[T][RCH / 4];
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const size_t row = ((size_t)t * M + m) * F + cob + RCH * hf;
+        const size_t row = ((size_t)t * M + m) * F + c0 + RCH * hf;
 #pragma unroll
         for (int q = 0; q < RCH / 4; ++q)
-          rr[t][q] = (valid && sa.real_res) ? *reinterpret_cast<const float4_t*>(sa.real_res + row + 4 * q)
+          rr[t][q] = (valid && sa.real_res) ? *reinterpret_cast<const float4_t*>(sa.real_res + row + cq * q)
                                             : float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      if (RCH == 16 && rowwise) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) transpose_rows4(*reinterpret_cast<float4_t(*)[4]>(&rr[t][0]));
       }
 #pragma unroll
       for (int t = 0; t < T; ++t) {
@@ -226,10 +354,11 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
           v[j] = neuron_reset(np, h, spike);
           words[t] |= (uint32_t)spike << j;
         }
+        if (RCH == 16 && rowwise) transpose_rows4(*reinterpret_cast<float4_t(*)[4]>(&rr[t][0]));
         if (valid) {
-          const size_t row = ((size_t)t * M + m) * F + cob + RCH * hf;
+          const size_t row = ((size_t)t * M + m) * F + c0 + RCH * hf;
 #pragma unroll
-          for (int q = 0; q < RCH / 4; ++q) *reinterpret_cast<float4_t*>(sa.real_out + row + 4 * q) = rr[t][q];
+          for (int q = 0; q < RCH / 4; ++q) *reinterpret_cast<float4_t*>(sa.real_out + row + cq * q) = rr[t][q];
         }
       }
     }

@@ -134,10 +134,21 @@ bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice
   return true;
 }
 
-int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len) {
+// The membrane-shortcut launches (fp32 y stored, no traces, bit output, no SEW residual) of the
+// 3x3 T = 4 tile kernel with one channel group per wave take the lean EPI_SHORTCUT epilogue.
+static int tile_epilogue_mode(const sengine_conv_lif_desc* d, const TileChoice& c, int mode, bool shortcut_only) {
+  if (shortcut_only && c.k3 && d->T == 4 && c.gpw == 1 && d->in_enc == SENGINE_ENC_BITS &&
+      d->out_enc == SENGINE_ENC_BITS)
+    return EPI_SHORTCUT;
+  return mode;
+}
+
+int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool shortcut_only, char* buf,
+                  size_t len) {
   TileChoice c;
   if (!choose_tile(d, geo, c)) return snprintf(buf, len, "none (grid too large)");
-  static const char* const kEpi[] = {"generic", "lif_hard", "if_hard"};
+  mode = tile_epilogue_mode(d, c, mode, shortcut_only);
+  static const char* const kEpi[] = {"generic", "lif_hard", "if_hard", "shortcut"};
   const char* oe = d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16";
   const bool f16in = d->in_enc == SENGINE_ENC_F16;
   const char* epi = d->out_enc == SENGINE_ENC_BITS || f16in ? kEpi[mode] : "generic";
@@ -188,7 +199,11 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
   p.tiles_w = c.tiles_w;
   p.tiles_per_image = c.tiles_per_image;
   p.ntiles = c.ntiles;
-  const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr || a.sew.real_out != nullptr);
+  const bool shortcut_only = a.sew.real_out != nullptr && a.h_trace == nullptr && a.x_trace == nullptr &&
+                             a.sew.res == nullptr;
+  const int mode = tile_epilogue_mode(
+      d, c, epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr || a.sew.real_out != nullptr),
+      shortcut_only);
   if (d->in_enc == SENGINE_ENC_F16) {
     if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
     return launch_tile_f16in<1, 0, 0, 1>(p, d->out_enc, mode, stream);

@@ -493,6 +493,10 @@ hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s
     else if (mode == EPI_IF_HARD)
       hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_IF_HARD, KSP, PF>), grid,
                          dim3(NTHR), 0, s, p);
+    else if (T == 4 && GPW == 1 && KS == 3 && mode == EPI_SHORTCUT)
+      hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS,
+                                            (T == 4 && GPW == 1 && KS == 3) ? EPI_SHORTCUT : EPI_GENERIC, KSP, PF>),
+                         grid, dim3(NTHR), 0, s, p);
     else
       hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_GENERIC, KSP, PF>), grid,
                          dim3(NTHR), 0, s, p);

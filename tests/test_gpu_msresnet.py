@@ -97,3 +97,50 @@ def test_membrane_shortcut_options(dev, with_res, with_state, T):
     assert np.allclose(y_gpu, r.x.numpy(), rtol=1e-4, atol=1e-4)
     rep = compare(s_gpu, None, r.spikes.numpy(), r.h.numpy(), THRESH)
     assert rep.ok, str(rep)
+
+
+@pytest.mark.parametrize("with_res,with_state", [(True, False), (True, True), (False, False)])
+@pytest.mark.parametrize("neuron,tau,v_th", [("ms", DECAY, THRESH), ("lif", 2.0, 1.0)])
+@pytest.mark.parametrize("H,W,C_in,C_out,B,shape", [(8, 8, 64, 128, 3, "0"), (13, 11, 128, 64, 2, "0"),
+                                                    (14, 8, 64, 64, 2, "1"), (9, 10, 256, 128, 2, "2")])
+def test_shortcut_mode_tile(dev, with_res, with_state, neuron, tau, v_th, H, W, C_in, C_out, B, shape):
+    """The lean membrane-shortcut epilogue of the 3x3 tile kernel (epi=shortcut: next timestep's
+    residual rows prefetched, rows moved as whole lines through the cross-row transpose) with
+    each tile shape, ragged tiles, with and without residual and membrane state: y, spikes and
+    the final membrane against the oracle."""
+    import os
+    os.environ["SENGINE_AMD_TILE_SHAPE"] = shape
+    ops.set_fused_kernel("tile")
+    try:
+        T = 4
+        spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=3, KW=3, stride=1, padding=1,
+                            neuron=neuron, hard_reset=True, tau=tau, v_threshold=v_th, v_reset=0.0)
+        plan = ops.fused_plan(spec, state=with_state, shortcut=True)
+        assert "epi=shortcut" in plan and plan.startswith("tile<T=4,KS=3,"), plan
+        case = ref.make_layer_case(300 + H + W + C_in // 64, T=T, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3,
+                                   fp16_weights=True, p_spike=0.3)
+        g = torch.Generator().manual_seed(H * W)
+        res = torch.randn(T, B, C_out, H, W, generator=g) * 0.5 if with_res else None
+        v0 = torch.rand(B, C_out, H, W, generator=g) * 0.4 if with_state else None
+        values, meta, _ = ops.compress_2_4(spec, case.w.to(dev))
+        sc, bi = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
+        data = torch.from_numpy(pk.seq_to_nhwc_bits(case.x_seq.numpy()).view(np.int32)).to(dev)
+        res_d = None if res is None else res.permute(0, 1, 3, 4, 2).reshape(T * B, H, W, C_out).contiguous().to(dev)
+        state = None if v0 is None else v0.permute(0, 2, 3, 1).reshape(-1, C_out).contiguous().to(dev)
+        y, spk = ops.fused_sparse_conv_bn_add_neuron(spec, data, values, meta, torch.from_numpy(sc).to(dev),
+                                                     torch.from_numpy(bi).to(dev), residual=res_d, state=state)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_fused_kernel("auto")
+        del os.environ["SENGINE_AMD_TILE_SHAPE"]
+    r = ref.shortcut_layer(case.x_seq, case.w, case.bn, res, 1, 1, neuron, tau, v_th, 0.0, v0)
+    s_gpu = pk.unpack_bits(spk.cpu().numpy().view(np.uint32).reshape(-1, C_out // 32), C_out)
+    s_gpu = nhwc_seq(torch.from_numpy(s_gpu.reshape(T * B, H, W, C_out)), T)
+    y_gpu = nhwc_seq(y, T)
+    assert np.allclose(y_gpu, r.x.numpy(), rtol=1e-4, atol=1e-4), float(np.abs(y_gpu - r.x.numpy()).max())
+    rep = compare(s_gpu, None, r.spikes.numpy(), r.h.numpy(), v_th)
+    assert rep.ok, str(rep)
+    assert 0.01 < float(r.spikes.mean()) < 0.99
+    if with_state:
+        v_fin = state.view(B, H, W, C_out).permute(0, 3, 1, 2).cpu()
+        assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
