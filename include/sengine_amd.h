@@ -199,7 +199,10 @@ int sengine_amd_fused_sparse_conv_bn_lif_pair(const sengine_conv_lif_desc* d0, c
  * Spikformer's residual stream: up to 5).
  * A conv whose input is such a P-plane tensor is an ordinary spike-bit conv with C_in =
  * P*C and weights [W, 2W, 4W, ...] along the input channels (sparsesnn_amd.sparsity).
- * Requires out_enc = BITS; state may be NULL; no traces.
+ * out_enc = F16 is the reference kernel's own form: out is fp16 NHWC (T*B, OH, OW, C_out),
+ * out = spike + residual (exact for integer values below 2048), the residual fp16 of the same
+ * shape when residual_planes == 0, else residual_planes bit planes as above; out_planes is
+ * ignored; C_out % 32 == 0.  state may be NULL; no traces.
  */
 int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_desc* d, const void* data,
                                              const void* blob_values, const void* blob_meta, float* state,
@@ -314,9 +317,11 @@ int sengine_amd_maxpool_spikes(int32_t NT, int32_t H, int32_t W, int32_t C, int3
 /*
  * Head: AdaptiveAvgPool2d(1) per timestep, mean over T, Linear (models/sewresnet.py:152-153,
  * 208-210; the same values as MS-ResNet's mean over T then pool, models/msresnet.py:155-160).
- * in: integer activations as `planes` bit planes, (T*B, HW) positions x planes*C bits;
+ * in: integer activations as `planes` bit planes, (T*B, HW) positions x planes*C bits, or
+ * (planes = 0) as integer-valued fp16 (T*B, HW, C) (Spikformer's residual stream, whose
+ * reference tensor is the float sum of spikes, models/spikformer.py:148-149);
  * fc_weight (N_out, C) fp32 (nn.Linear layout), fc_bias (N_out); out (B, N_out) fp32.
- * C % 32 == 0, 1 <= planes <= 5, planes * C <= 8192.
+ * C % 32 == 0, 0 <= planes <= 5, planes * C <= 8192.
  */
 int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t planes, const uint32_t* in,
                          const float* fc_weight, const float* fc_bias, int32_t N_out, float* out,

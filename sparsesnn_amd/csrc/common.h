@@ -101,6 +101,9 @@ struct SewAdd {
   // real_out (fp32, the layout of the traces) and the neuron runs on y.
   const float* real_res;
   float* real_out;
+  // fp16 residual stream (the reference add kernel's own form): with fp16 output the stored
+  // value is spike + res16 at the same (t, position, channel); res == nullptr then.
+  const _Float16* res16;
 };
 
 // One charge step: returns the charged membrane h given the previous membrane v and

@@ -110,6 +110,44 @@ __host__ __device__ inline int epilogue_mode(const NeuronParams& np, bool traces
   return EPI_GENERIC;
 }
 
+// The 16 spikes of a lane as fp16 0 / 1 at out + row (fp16 elements).  With a residual the
+// stored value is spike + residual (exact for integers below 2048): an fp16 residual stream
+// (sa.res16) at the same element, or a bit-plane residual (sa.res, its plane words r).
+__device__ __forceinline__ void store_spike_f16(uint32_t word, size_t row, uint8_t* out, const SewAdd& sa,
+                                                const uint32_t (&r)[kResWords]) {
+  half8_t o0, o1;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    o0[j] = (word >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+    o1[j] = (word >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+  }
+  if (sa.res) {
+    uint32_t val[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) val[j] = 0;
+#pragma unroll
+    for (int pl = 0; pl < kMaxPlanes; ++pl) {
+      if (pl >= sa.res_planes) break;
+      const uint32_t rp = r[pl >> 1] >> (16 * (pl & 1));
+#pragma unroll
+      for (int j = 0; j < 16; ++j) val[j] |= ((rp >> j) & 1u) << pl;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o0[j] += (_Float16)(float)val[j];
+      o1[j] += (_Float16)(float)val[8 + j];
+    }
+  }
+  if (sa.res16) {
+    const half8_t* r = reinterpret_cast<const half8_t*>(sa.res16 + row);
+    o0 += r[0];
+    o1 += r[1];
+  }
+  half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(out) + row);
+  dst[0] = o0;
+  dst[1] = o1;
+}
+
 // Hard-reset fast modes without a state buffer: V0 = 0, so t = 0 charges h = x exactly
 // (fma(0, decay, x) == x), and the membrane after the last step is not kept (no reset).
 template <int T, int OUT_ENC, int MODE>
@@ -150,15 +188,7 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
     if (OUT_ENC == SENGINE_ENC_BITS) {
       store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, res.r[t]);
     } else {
-      half8_t o0, o1;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        o0[j] = (word >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
-        o1[j] = (word >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
-      }
-      half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(out) + row);
-      dst[0] = o0;
-      dst[1] = o1;
+      store_spike_f16(word, row, out, sa, res.r[t]);
     }
   }
 }
@@ -368,15 +398,7 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
       if (OUT_ENC == SENGINE_ENC_BITS) {
         store_spike_word(words[t], (size_t)t * M + m, F, cob, out, sa, res.r[t]);
       } else {
-        half8_t o0, o1;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          o0[j] = (words[t] >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
-          o1[j] = (words[t] >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
-        }
-        half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(out) + ((size_t)t * M + m) * F + cob);
-        dst[0] = o0;
-        dst[1] = o1;
+        store_spike_f16(words[t], ((size_t)t * M + m) * F + cob, out, sa, res.r[t]);
       }
     }
     if (has_state && valid) {
@@ -452,15 +474,7 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
     if (OUT_ENC == SENGINE_ENC_BITS) {
       store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, res.r[t]);
     } else {
-      half8_t o0, o1;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        o0[j] = (word >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
-        o1[j] = (word >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
-      }
-      half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(out) + row);
-      dst[0] = o0;
-      dst[1] = o1;
+      store_spike_f16(word, row, out, sa, res.r[t]);
     }
   }
   if (has_state && valid) {

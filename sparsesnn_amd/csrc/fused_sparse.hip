@@ -586,7 +586,20 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif_add(const sengine_conv_lif_d
                                                         int32_t out_planes, hipStream_t stream) {
   if (!d) return set_error(-1, "fused_sparse_conv_bn_lif_add: null descriptor");
   if (!residual) return set_error(-1, "fused_sparse_conv_bn_lif_add: null residual");
-  if (d->out_enc != SENGINE_ENC_BITS) return set_error(-2, "fused_sparse_conv_bn_lif_add: out_enc must be BITS");
+  if (d->out_enc == SENGINE_ENC_F16) {  // fp16 output: out = spike + residual as fp16
+    if (d->C_out % 32 != 0) return set_error(-2, "fused_sparse_conv_bn_lif_add: C_out % 32 != 0");
+    if (residual_planes == 0)  // fp16 residual stream
+      return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, out, nullptr, nullptr,
+                         SewAdd{nullptr, 0, 0, d->C_out, nullptr, nullptr, static_cast<const _Float16*>(residual)},
+                         stream);
+    if (residual_planes < 1 || residual_planes > kMaxPlanes)
+      return set_error(-2, "fused_sparse_conv_bn_lif_add: need 0 <= residual_planes <= 5 with fp16 output");
+    return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, out, nullptr, nullptr,
+                       SewAdd{static_cast<const uint8_t*>(residual), residual_planes, residual_planes, d->C_out,
+                              nullptr, nullptr, nullptr},
+                       stream);
+  }
+  if (d->out_enc != SENGINE_ENC_BITS) return set_error(-2, "fused_sparse_conv_bn_lif_add: out_enc must be BITS or F16");
   if (residual_planes < 1 || residual_planes > kMaxPlanes || out_planes < residual_planes || out_planes > kMaxPlanes)
     return set_error(-2, "fused_sparse_conv_bn_lif_add: need 1 <= residual_planes <= out_planes <= 5");
   if (d->C_out % 32 != 0) return set_error(-2, "fused_sparse_conv_bn_lif_add: C_out % 32 != 0");

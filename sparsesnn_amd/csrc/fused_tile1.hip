@@ -116,6 +116,7 @@ bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice
   // 128 (or 64) channels and the reduction into phases of 4 (or 2) chunks.
   // SENGINE_AMD_TILE1_PM=0|1|2 forces the tile kernel, or that many channel groups per wave.
   c.pm = 0;
+  c.pmw = 4;
   c.cg = 0;
   const int nchunk = d->C_in / 64;
   c.cg = nchunk % 4 == 0 ? 4 : (nchunk % 2 == 0 ? 2 : 0);
@@ -123,7 +124,17 @@ bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice
     c.gpw = 1;
     c.ksplit = 1;
     c.pf = 1;
+    // 1x1: the position-major kernel stages each fp16 value once per 384 or 256 output
+    // channels (6 or 4 waves), phases of 2 chunks (4 chunks hold too many prefetch registers)
     c.cg = 0;
+    if (!c.k3 && d->T == 4 && nchunk % 2 == 0 && env_int_now("SENGINE_AMD_TILE1_PM", -1) != 0) {
+      c.pmw = d->C_out % 384 == 0 ? 6 : (d->C_out % 256 == 0 ? 4 : 0);
+      if (c.pmw && ((geo.M + 15) / 16) * (int64_t)(d->C_out / (64 * c.pmw)) <= 0x7fffffff) {
+        c.pm = 1;
+        c.cg = 2;
+      }
+    }
+    return true;
   }
   if (!c.k3 && d->T == 4 && c.cg > 0) {
     c.pm = d->C_out % 512 == 0 ? 2 : (d->C_out % 256 == 0 ? 1 : 0);
@@ -151,7 +162,13 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
   static const char* const kEpi[] = {"generic", "lif_hard", "if_hard", "shortcut"};
   const char* oe = d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16";
   const bool f16in = d->in_enc == SENGINE_ENC_F16;
-  const char* epi = d->out_enc == SENGINE_ENC_BITS || f16in ? kEpi[mode] : "generic";
+  // fp16 output runs the generic epilogue except in launch_tile's 1x1 fast case and the fp16-input
+  // tile instances (every mode)
+  const bool fast_f16out = f16in ? c.pm == 0 : (!c.k3 && d->T == 4 && c.pm == 0 && mode == EPI_LIF_HARD);
+  const char* epi = d->out_enc == SENGINE_ENC_BITS || fast_f16out ? kEpi[mode] : "generic";
+  if (f16in && c.pm)
+    return snprintf(buf, len, "tile1pm<T=4,GPW=1,CG=2,NW=%d,in=f16,out=%s,epi=%s> grid=%lld", c.pmw, oe, epi,
+                    (long long)((geo.M + 15) / 16) * (d->C_out / (64 * c.pmw)));
   if (f16in) {
     if (c.k3) {
       const TileShape s = kShapes3[c.shape];
@@ -206,6 +223,9 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
       shortcut_only);
   if (d->in_enc == SENGINE_ENC_F16) {
     if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
+    if (c.pm)
+      return c.pmw == 6 ? launch_tile1pm<4, 1, 2, 6, SENGINE_ENC_F16>(p, d->out_enc, mode, stream)
+                        : launch_tile1pm<4, 1, 2, 4, SENGINE_ENC_F16>(p, d->out_enc, mode, stream);
     return launch_tile_f16in<1, 0, 0, 1>(p, d->out_enc, mode, stream);
   }
   if (c.k3) return launch_tile3(p, d->T, c.shape, c.gpw, c.ksplit, c.pf, d->out_enc, mode, stream);

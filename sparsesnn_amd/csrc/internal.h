@@ -71,6 +71,7 @@ struct TileChoice {
   int shape, gpw, ksplit, pf;
   int tiles_w, tiles_per_image, ntiles;
   int pm;  // 1x1 only: channel groups per wave of the position-major kernel (0: the tile kernel)
+  int pmw;  // position-major kernel: waves per workgroup (4 or 6)
   int cg;  // position-major kernel: 64-channel chunks per staging phase
 };
 bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice& c);

@@ -441,11 +441,34 @@ __global__ __launch_bounds__(NT) void sew_head_kernel(HeadParams p) {
   __shared__ int cnt[HEAD_MAX_PC];
   __shared__ float feat[HEAD_MAX_PC];
   const int bimg = blockIdx.x;
-  const int words = p.planes * p.C / 32;
+  const int fp16in = p.planes == 0;  // integer-valued fp16 stream instead of bit planes
+  const int planes = fp16in ? 1 : p.planes;
+  const int words = fp16in ? 0 : planes * p.C / 32;
   const int npos = p.T * p.HW;  // (t, s) positions of this image
-  for (int i = threadIdx.x; i < p.planes * p.C; i += NT) cnt[i] = 0;
+  for (int i = threadIdx.x; i < planes * p.C; i += NT) cnt[i] = 0;
   __syncthreads();
-  const int per = words < NT ? words : NT;  // word columns per pass
+  if (fp16in) {
+    // 8 channels (16 bytes) per thread and position, integer sums (exact) per channel
+    const int per8 = p.C / 8;
+    const int nsl = NT / per8;
+    const int sl = (int)threadIdx.x / per8;
+    const int c8 = ((int)threadIdx.x - sl * per8) * 8;
+    if (sl < nsl) {
+      int s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      const _Float16* base = reinterpret_cast<const _Float16*>(p.in);
+      for (int q = sl; q < npos; q += nsl) {
+        const int t = q / p.HW;
+        const int sp = q - t * p.HW;
+        const half8_t v = *reinterpret_cast<const half8_t*>(base + (((int64_t)t * p.B + bimg) * p.HW + sp) * p.C + c8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s8[e] += (int)(float)v[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (s8[e]) atomicAdd(&cnt[c8 + e], s8[e]);
+    }
+  }
+  const int per = words < NT ? (words > 0 ? words : 1) : NT;  // word columns per pass
   const int nslice = NT / per;
   const int slice = (int)threadIdx.x / per;
   // Bit counting in SWAR lanes: nibble n of a / b / c / d counts channel 4n / 4n+1 / 4n+2 /
@@ -520,7 +543,7 @@ __global__ __launch_bounds__(NT) void sew_head_kernel(HeadParams p) {
   // channel c of plane pl is bit (pl*C + c) of a position's words
   for (int c = threadIdx.x; c < p.C; c += NT) {
     int sum = 0;
-    for (int pl = 0; pl < p.planes; ++pl) sum += cnt[pl * p.C + c] << pl;
+    for (int pl = 0; pl < planes; ++pl) sum += cnt[pl * p.C + c] << pl;
     // mean over HW then over T: both exact or one rounding for the integer sums here
     feat[c] = ((float)sum / (float)p.HW) / (float)p.T;
   }
@@ -711,11 +734,12 @@ extern "C" int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C,
                                     const uint32_t* in, const float* fc_weight, const float* fc_bias, int32_t N_out,
                                     float* out, hipStream_t stream) {
   if (!in || !fc_weight || !fc_bias || !out) return set_error(-1, "sew_head: null pointer");
-  if (T < 1 || B < 1 || HW < 1 || C < 32 || C % 32 != 0 || planes < 1 || planes > kMaxPlanes || N_out < 1 ||
-      (int64_t)planes * C > HEAD_MAX_PC)
-    return set_error(-2, "sew_head: invalid shape (C % 32 == 0, 1 <= planes <= 5, planes * C <= 8192)");
+  if (T < 1 || B < 1 || HW < 1 || C < 32 || C % 32 != 0 || planes < 0 || planes > kMaxPlanes || N_out < 1 ||
+      (int64_t)std::max(planes, 1) * C > HEAD_MAX_PC)
+    return set_error(-2, "sew_head: invalid shape (C % 32 == 0, 0 <= planes <= 5, planes * C <= 8192)");
   HeadParams p{in, fc_weight, fc_bias, out, T, B, HW, C, planes, N_out};
-  const int64_t words_per_image = (int64_t)T * HW * planes * C / 32;
+  // fp16 input (planes 0) reads 16 bits per value: weighed as 16 planes for the launch shape
+  const int64_t words_per_image = (int64_t)T * HW * (planes ? planes : 16) * C / 32;
   if (words_per_image >= 16384) {
     // counting dominates (token grids): one 1024-thread workgroup per image counts once
     hipLaunchKernelGGL(sew_head_kernel<1024>, dim3((unsigned)B, 1u), dim3(1024), 0, stream, p);

@@ -19,19 +19,26 @@
 // (channels 8*(q&7) + 4*(q>>3) .. +3 of the chunk, i.e. piece q&7, half q>>3) of position
 // pos: a B fragment (half-pieces g, 8+g, 4+g, 12+g) is four ds_read_b64 whose 32-lane
 // halves cover 256 consecutive bytes (every bank once).
+//
+// NW waves per workgroup (4, or 6 for 384-channel outputs such as Spikformer's token
+// Linears).  IN_ENC = SENGINE_ENC_F16 takes fp16 activations (the reference call() ABI, or an
+// integer-valued fp16 stream): a (chunk, t, position) unit is eight 16-byte pieces copied as
+// they are into the same layout, and each input value is staged once per NW*64*GPW output
+// channels instead of once per 64 (the 64-position tile kernel).
 #pragma once
 #include "tile_kernel.h"
 
 namespace sengine {
 
-template <int T, int GPW, int CG, int OUT_ENC, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 || MODE == EPI_GENERIC ? 2 : 3))) void fused_tile1pm_kernel(
-    TileParams p) {
-  constexpr int NW = 4;                    // waves per workgroup
+template <int T, int GPW, int CG, int OUT_ENC, int MODE, int NW = 4, int IN_ENC = SENGINE_ENC_BITS>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(GPW == 2 || MODE == EPI_GENERIC ? 2 : 3)))
+void fused_tile1pm_kernel(TileParams p) {
+  constexpr int NTH = 64 * NW;             // threads per workgroup
   constexpr int NCH = 64 * GPW;            // output channels per wave
   constexpr int CE = T * 16 * 16;          // LDS entries (8 bytes) per staged chunk
   constexpr int UNITS = CG * T * 16;       // (chunk, t, position) words per staging phase
-  constexpr int UPT = (UNITS + 255) / 256;
+  constexpr int UPT = IN_ENC == SENGINE_ENC_BITS ? (UNITS + NTH - 1) / NTH : 1;
+  constexpr int PPT = IN_ENC == SENGINE_ENC_F16 ? (UNITS * 8 + NTH - 1) / NTH : 1;  // fp16: 16-byte pieces
   static_assert(CG % 2 == 0 && CG <= 4, "the A-operand ring alternates between two register sets");
   __shared__ uint2 sB[2][CG * CE];
   __shared__ float sCoef[4][NW * NCH];
@@ -52,7 +59,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 ||
   const int G0 = (sb * NW + wave) * GPW;  // this wave's first 64-channel group
 
   const bool fold = MODE == EPI_LIF_HARD || (MODE == EPI_GENERIC && p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2);
-  for (int i = tid; i < NW * NCH; i += 256) {
+  for (int i = tid; i < NW * NCH; i += NTH) {
     const int ch = sb * NW * NCH + i;
     const float sc = p.scale[ch] * p.enc_scale;  // exact: enc_scale is a power of two
     const float bi = p.bias[ch];
@@ -62,13 +69,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 ||
     sCoef[3][i] = bi;
   }
 
-  // ---- staging identity: unit u = tid + j*256 -> (chunk in phase cc, t, position pos)
+  // ---- staging identity: unit u = tid + j*NTH -> (chunk in phase cc, t, position pos)
   const int cbytes = p.C >> 3;
   int goff[UPT];  // byte offset of the unit's 64-bit word in phase 0; -1: zero word
   int soff[UPT];
 #pragma unroll
   for (int j = 0; j < UPT; ++j) {
-    const int u = tid + j * 256;
+    const int u = tid + j * NTH;
     const int pos = u & 15;
     const int t = (u >> 4) % T;
     const int cc = u / (16 * T);
@@ -82,6 +89,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 ||
     goff[j] = inb ? (((t * p.B + ib) * p.H + ih) * p.W + iw) * cbytes + cc * 8 : -1;
     soff[j] = (cc * T + t) * 256 + pos;
   }
+  // fp16 input: piece pc = tid + j*NTH is piece pc & 7 of unit pc >> 3; off16 its byte offset
+  // in phase 0 (-1: zero piece), poff its half-piece entry (the other half 128 entries on)
+  int off16[PPT], poff[PPT];
+  if (IN_ENC == SENGINE_ENC_F16) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pc = tid + j * NTH;
+      const int u = pc >> 3, i = pc & 7;
+      const int pos = u & 15;
+      const int t = (u >> 4) % T;
+      const int cc = u / (16 * T);
+      const int m = m0 + pos;
+      const bool inb = u < UNITS && m < p.M;
+      const int ohw = p.OH * p.OW;
+      const int ib = inb ? m / ohw : 0;
+      const int r = m - ib * ohw;
+      const int oh = inb ? r / p.OW : 0;
+      const int ih = oh * p.S, iw = (r - oh * p.OW) * p.S;
+      off16[j] = inb ? (((t * p.B + ib) * p.H + ih) * p.W + iw) * (p.C * 2) + cc * 128 + i * 16 : -1;
+      poff[j] = (cc * T + t) * 256 + pos + i * 16;
+    }
+  }
+  auto load_pieces = [&](u32x4_t (&v)[PPT], int phase) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j)
+      v[j] = off16[j] >= 0 ? *reinterpret_cast<const u32x4_t*>(p.in + off16[j] + phase * CG * 128)
+                           : u32x4_t{0u, 0u, 0u, 0u};
+  };
+  auto store_pieces = [&](int buf, const u32x4_t (&v)[PPT]) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      if ((j + 1) * NTH <= UNITS * 8 || tid + j * NTH < UNITS * 8) {
+        sB[buf][poff[j]] = uint2{v[j][0], v[j][1]};
+        sB[buf][poff[j] + 8 * 16] = uint2{v[j][2], v[j][3]};
+      }
+    }
+  };
   auto load_units = [&](uint2 (&v)[UPT], int phase) {
 #pragma unroll
     for (int j = 0; j < UPT; ++j)
@@ -90,7 +134,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 ||
   auto store_units = [&](int buf, const uint2 (&v)[UPT]) {
 #pragma unroll
     for (int j = 0; j < UPT; ++j) {
-      if ((j + 1) * 256 <= UNITS || tid + j * 256 < UNITS) {
+      if ((j + 1) * NTH <= UNITS || tid + j * NTH < UNITS) {
         u32x4_t pc[8];
         expand_word64(v[j], pc);
 #pragma unroll
@@ -136,8 +180,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 ||
   uint32_t ix[2][GPW][4];
   load_a(0, av[0], ix[0]);
   uint2 stg[UPT];
-  load_units(stg, 0);
-  store_units(0, stg);
+  // fp16: pieces two phases ahead, in two register sets (phase ph's in pst[ph & 1]): a phase's
+  // loads have a whole phase of SMFMACs before the phase that stores them
+  u32x4_t pst[2][PPT];
+  if (IN_ENC == SENGINE_ENC_F16) {
+    load_pieces(pst[0], 0);
+    store_pieces(0, pst[0]);
+    if (nphase > 1) load_pieces(pst[1], 1);
+  } else {
+    load_units(stg, 0);
+    store_units(0, stg);
+  }
   __syncthreads();
 
   // LDS byte address of this lane's half-piece g of position col in chunk slot 0, t = 0
@@ -146,7 +199,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 ||
   for (int ph = 0; ph < nphase; ++ph) {
     const int buf = ph & 1;
     const bool more = ph + 1 < nphase;
-    if (more) load_units(stg, ph + 1);
+    if (IN_ENC == SENGINE_ENC_F16) {
+      if (ph + 2 < nphase) {  // into the set phase ph came from (stored already)
+        if (ph & 1) load_pieces(pst[1], ph + 2);
+        else load_pieces(pst[0], ph + 2);
+      }
+    } else if (more) {
+      load_units(stg, ph + 1);
+    }
     const uint32_t lbase = lds0 + (uint32_t)buf * (uint32_t)(CG * CE * 8);
     constexpr int NSTEP = CG * T;
     uint2 fr[2][4];
@@ -184,7 +244,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 ||
                                                                      acc[gg][t][a], (int)ix[ra][gg][a], 0, 0);
       }
     }
-    if (more) store_units(buf ^ 1, stg);
+    if (more) {
+      if (IN_ENC == SENGINE_ENC_F16) {
+        if (ph & 1) store_pieces(buf ^ 1, pst[0]);  // phase ph + 1 is even
+        else store_pieces(buf ^ 1, pst[1]);
+      } else {
+        store_units(buf ^ 1, stg);
+      }
+    }
     __syncthreads();
   }
 
@@ -199,18 +266,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GPW == 2 ||
   }
 }
 
-template <int T, int GPW, int CG>
+template <int T, int GPW, int CG, int NW = 4, int IN_ENC = SENGINE_ENC_BITS>
 hipError_t launch_tile1pm(const TileParams& p, int out_enc, int mode, hipStream_t s) {
-  const dim3 grid((unsigned)(((p.M + 15) / 16) * (p.F / (4 * 64 * GPW))));
+  const dim3 grid((unsigned)(((p.M + 15) / 16) * (p.F / (NW * 64 * GPW)))), block(64 * NW);
   if (out_enc == SENGINE_ENC_BITS) {
     if (mode == EPI_LIF_HARD)
-      hipLaunchKernelGGL((fused_tile1pm_kernel<T, GPW, CG, SENGINE_ENC_BITS, EPI_LIF_HARD>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((fused_tile1pm_kernel<T, GPW, CG, SENGINE_ENC_BITS, EPI_LIF_HARD, NW, IN_ENC>), grid, block, 0,
+                         s, p);
     else if (mode == EPI_IF_HARD)
-      hipLaunchKernelGGL((fused_tile1pm_kernel<T, GPW, CG, SENGINE_ENC_BITS, EPI_IF_HARD>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((fused_tile1pm_kernel<T, GPW, CG, SENGINE_ENC_BITS, EPI_IF_HARD, NW, IN_ENC>), grid, block, 0,
+                         s, p);
     else
-      hipLaunchKernelGGL((fused_tile1pm_kernel<T, GPW, CG, SENGINE_ENC_BITS, EPI_GENERIC>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((fused_tile1pm_kernel<T, GPW, CG, SENGINE_ENC_BITS, EPI_GENERIC, NW, IN_ENC>), grid, block, 0,
+                         s, p);
   } else {
-    hipLaunchKernelGGL((fused_tile1pm_kernel<T, GPW, CG, SENGINE_ENC_F16, EPI_GENERIC>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fused_tile1pm_kernel<T, GPW, CG, SENGINE_ENC_F16, EPI_GENERIC, NW, IN_ENC>), grid, block, 0, s,
+                       p);
   }
   return hipGetLastError();
 }

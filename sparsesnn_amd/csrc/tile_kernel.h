@@ -118,8 +118,8 @@ __device__ __forceinline__ void expand_word64(uint2 w, u32x4_t (&pc)[8]) {
 // IN_ENC = SENGINE_ENC_F16 (the reference's fp16 NHWC activations, any fp16 values): each
 // (t, pixel) unit of a chunk is 64 fp16 = eight 16-byte pieces, copied as they are into the
 // same LDS half-piece layout (no expansion); a thread moves pieces tid, tid + NTHR, ... and
-// the next chunk is fetched after the current one's reduction (the 16-byte pieces would
-// otherwise hold ~50 registers across the loop).
+// the next chunk's pieces are loaded into registers when a chunk's reduction starts (up to
+// ~52 registers: these instances run two waves per SIMD).
 template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP, int PF = 1,
           int IN_ENC = SENGINE_ENC_BITS>
 __global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR * KSP))
@@ -152,8 +152,12 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
   const int col = lane & 15;
 
   const int L = tile_remap(blockIdx.x, gridDim.x);
-  const int Gb = L / p.ntiles;  // channel block: 64-channel groups Gb*GPW .. Gb*GPW+GPW-1
-  const int tile = L - Gb * p.ntiles;
+  // Bit input: channel-block-major ids (an XCD's workgroups share few blocks' weights).  fp16
+  // input: tile-major ids, so the channel blocks of one tile run together on one XCD and read
+  // its 16-bit activations from HBM once (the other blocks hit L2) instead of once per block.
+  const int ncb = p.F / (64 * GPW);
+  const int Gb = IN_ENC == SENGINE_ENC_F16 ? L % ncb : L / p.ntiles;  // channel block: groups Gb*GPW ..
+  const int tile = IN_ENC == SENGINE_ENC_F16 ? L / ncb : L - Gb * p.ntiles;
   const int G0 = Gb * GPW;
   int b = 0, oh0 = 0, ow0 = 0, m0 = 0;
   if (KS == 3) {
@@ -234,13 +238,20 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
     }
     return inb ? (((t * p.B + ib) * p.H + ih) * p.W + iw) * (p.C * 2) : -1;
   };
-  auto load_pieces = [&](u32x4_t (&v)[PPT], int c) {
+  // byte offsets of this thread's pieces' fp16 rows (fixed over the chunks; -1 = zero piece)
+  int off16[IN_ENC == SENGINE_ENC_F16 ? PPT : 1];
+  if (IN_ENC == SENGINE_ENC_F16) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int pc = tid + j * NTHR;
       const int o = pc < UNITS * 8 ? unit_off16(pc >> 3) : -1;
-      v[j] = o >= 0 ? *reinterpret_cast<const u32x4_t*>(p.in + o + (c * 64 + (pc & 7) * 8) * 2) : u32x4_t{0u, 0u, 0u, 0u};
+      off16[j] = o < 0 ? -1 : o + (pc & 7) * 16;
     }
+  }
+  auto load_pieces = [&](u32x4_t (&v)[PPT], int c) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j)
+      v[j] = off16[j] >= 0 ? *reinterpret_cast<const u32x4_t*>(p.in + off16[j] + c * 128) : u32x4_t{0u, 0u, 0u, 0u};
   };
   auto store_pieces = [&](int buf, const u32x4_t (&v)[PPT]) {
 #pragma unroll
@@ -336,6 +347,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
 #pragma unroll
   for (int i = 0; i < PF; ++i) load_a(set, i, av[i], ix[i]);
   uint2 stg[UPT];
+  u32x4_t pnext[IN_ENC == SENGINE_ENC_F16 ? PPT : 1];  // fp16 input: the next chunk's pieces
   if (IN_ENC == SENGINE_ENC_F16) {
     u32x4_t pcs[PPT];
     load_pieces(pcs, set);
@@ -349,6 +361,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
     const bool more = c + KSP < p.nchunk;
     const int buf = NBUF == 2 ? ((c / KSP) & 1) : 0;
     if (IN_ENC == SENGINE_ENC_BITS && more) load_units(stg, c + KSP);
+    if (IN_ENC == SENGINE_ENC_F16 && more) load_pieces(pnext, c + KSP);
     // B fragments: four ds_read_b64 per (tap, t), issued PF steps ahead of their SMFMACs
     // and waited for with an explicit lgkmcnt (the loop issues no other LDS operation).
     // Written as asm so the compiler neither fuses them into 16-byte or paired reads nor
@@ -414,9 +427,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
     if (more) {
       if (NBUF == 1) __syncthreads();  // every wave is done reading the single buffer
       if (IN_ENC == SENGINE_ENC_F16) {
-        u32x4_t pcs[PPT];
-        load_pieces(pcs, c + KSP);
-        store_pieces(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), pcs);
+        store_pieces(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), pnext);
       } else {
         store_units(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), stg);
       }
@@ -500,6 +511,11 @@ hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s
     else
       hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_GENERIC, KSP, PF>), grid,
                          dim3(NTHR), 0, s, p);
+  } else if (KS == 1 && T == 4 && mode == EPI_LIF_HARD) {
+    // fp16 output of 1x1 layers (token Linears writing the fp16 residual stream): fast epilogue
+    hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16,
+                                          (KS == 1 && T == 4) ? EPI_LIF_HARD : EPI_GENERIC, KSP, PF>),
+                       grid, dim3(NTHR), 0, s, p);
   } else {
     hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16, EPI_GENERIC, KSP, PF>), grid,
                        dim3(NTHR), 0, s, p);

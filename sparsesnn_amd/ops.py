@@ -331,10 +331,13 @@ def fused_sparse_conv_bn_lif_add(s: ConvSpec, data: torch.Tensor, values: torch.
                                  residual_planes: int, out_planes: int, state: Optional[torch.Tensor] = None,
                                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused 2:4 Conv + BN + neuron + SEW 'ADD' residual: out = spike + residual as
-    `out_planes` bit planes, int32 (T*B, OH, OW, out_planes*C_out/32)."""
+    `out_planes` bit planes, int32 (T*B, OH, OW, out_planes*C_out/32).  With s.out_enc ==
+    ENC_F16, out is fp16 (T*B, OH, OW, C_out) and the residual fp16 of that shape
+    (residual_planes == 0) or `residual_planes` bit planes; out_planes is unused."""
     lib = _lib.load()
-    if s.out_enc != ENC_BITS:
-        raise SEngineError("fused_sparse_conv_bn_lif_add: out_enc must be ENC_BITS")
+    f16 = s.out_enc == ENC_F16
+    if s.out_enc != ENC_BITS and not f16:
+        raise SEngineError("fused_sparse_conv_bn_lif_add: out_enc must be ENC_BITS or ENC_F16")
     OH, OW, M, _ = geometry(s)
     d = make_desc(s)
     vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
@@ -349,15 +352,23 @@ def fused_sparse_conv_bn_lif_add(s: ConvSpec, data: torch.Tensor, values: torch.
         raise SEngineError("fused_sparse_conv_bn_lif_add: weight blob does not match the descriptor")
     _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
     _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
-    _require_numel(residual, s.T * M * residual_planes * s.C_out // 32, torch.int32, "residual")
+    if f16 and residual_planes == 0:
+        out_planes = 0
+        _require_numel(residual, s.T * M * s.C_out, torch.float16, "residual")
+    else:
+        _require_numel(residual, s.T * M * residual_planes * s.C_out // 32, torch.int32, "residual")
     if state is not None:
         _require_cuda(state, "state")
         _require_numel(state, M * s.C_out, torch.float32, "state")
     if out is None:
-        out = torch.empty(s.T * s.B, OH, OW, out_planes * s.C_out // 32, dtype=torch.int32, device=dev)
+        out = (torch.empty(s.T * s.B, OH, OW, s.C_out, dtype=torch.float16, device=dev) if f16 else
+               torch.empty(s.T * s.B, OH, OW, out_planes * s.C_out // 32, dtype=torch.int32, device=dev))
     else:
         _require_cuda(out, "out")
-        _require_numel(out, s.T * M * out_planes * s.C_out // 32, torch.int32, "out")
+        if f16:
+            _require_numel(out, s.T * M * s.C_out, torch.float16, "out")
+        else:
+            _require_numel(out, s.T * M * out_planes * s.C_out // 32, torch.int32, "out")
     rc = lib.sengine_amd_fused_sparse_conv_bn_lif_add(
         ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta), _ptr(state), _ptr(bn_scale), _ptr(bn_bias),
         _ptr(residual), int(residual_planes), _ptr(out), int(out_planes), _stream(dev))
@@ -601,12 +612,16 @@ def maxpool_spikes(x: torch.Tensor, NT: int, H: int, W: int, C: int, k: int = 3,
 
 def sew_head(x: torch.Tensor, T: int, B: int, HW: int, C: int, planes: int, fc_weight: torch.Tensor,
              fc_bias: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Average pool + mean over T + Linear on `planes`-plane integer activations -> (B, N_out) fp32.
-    fc_weight: (N_out, C) contiguous, nn.Linear layout."""
+    """Average pool + mean over T + Linear on `planes`-plane integer activations (planes = 0:
+    integer-valued fp16 (T*B, HW, C)) -> (B, N_out) fp32.  fc_weight: (N_out, C) contiguous,
+    nn.Linear layout."""
     lib = _lib.load()
     for t, n in ((x, "x"), (fc_weight, "fc_weight"), (fc_bias, "fc_bias")):
         _require_cuda(t, n)
-    _require_numel(x, T * B * HW * planes * C // 32, torch.int32, "x")
+    if planes == 0:
+        _require_numel(x, T * B * HW * C, torch.float16, "x")
+    else:
+        _require_numel(x, T * B * HW * planes * C // 32, torch.int32, "x")
     N_out = fc_weight.shape[0]
     _require_numel(fc_weight, N_out * C, torch.float32, "fc_weight")
     _require_numel(fc_bias, N_out, torch.float32, "fc_bias")

@@ -14,10 +14,13 @@ Linear head (:273-288).  SpikformerEngine maps it onto this library:
   (embed/8 = 48, embed/4 = 96 for embed 384) are padded with zero weights and a zero BN
   affine: the padded channels never fire (V_th > 0) and multiply zero weights downstream;
 * blocks: the token stream x (T*B, N tokens, embed) is integer-valued (the residual adds of
-  spikes, :148-149) and stored as bit planes; q, k, v (Linear + BN1d + LIF, :103-125) are
-  fused 1x1 convs over the token grid with plane-expanded weights and the Linear bias
-  folded into the BN affine; SSA runs as the two-kernel Q (K^T V) path with the attention
-  LIF (V_th 0.5); proj and MLP fc2 add their spikes to the stream in their epilogues;
+  spikes, :148-149).  stream="f16" (default) keeps it as fp16 integers, the reference's own
+  representation: q, k, v and fc1 (Linear + BN1d + LIF, :103-125) are fused 1x1 convs over
+  the token grid reading it as fp16 activations (K = embed), and proj / MLP fc2 write
+  spike + x as fp16 in their epilogues.  stream="planes" stores it as bit planes instead:
+  the token Linears then run on spike bits with plane-expanded weights (K = planes * embed)
+  and the adds write planes.  The Linear bias is folded into the BN affine; SSA runs as the
+  two-kernel Q (K^T V) path with the attention LIF (V_th 0.5);
 * head: mean over tokens and T of the integer stream and the Linear (sengine_amd_sew_head).
 
 Every buffer is allocated once; the launch sequence is captured into one hipGraph.
@@ -109,9 +112,13 @@ class SpikformerEngine:
     `heads` heads, `depth` blocks, MLP ratio `mlp_ratio`)."""
 
     def __init__(self, params: dict, batch: int, T: int = 4, embed: int = 384, heads: int = 8, depth: int = 8,
-                 mlp_ratio: int = 4, in_hw=(224, 224), in_channels: int = 3, device="cuda"):
+                 mlp_ratio: int = 4, in_hw=(224, 224), in_channels: int = 3, device="cuda", stream: str = "f16"):
         if embed % 64 or embed % heads:
             raise SEngineError("embed must be a multiple of 64 and of heads")
+        if stream not in ("f16", "planes"):
+            raise SEngineError("stream must be 'f16' or 'planes'")
+        self.stream = stream
+        f16 = stream == "f16"
         H, W = in_hw
         if H % 4 or W % 4:
             raise SEngineError("image sides must be multiples of 4 (two stride-2 max-pools)")
@@ -155,7 +162,15 @@ class SpikformerEngine:
         self.rpe = self._conv(p, "rpe_conv", embed, embed, embed, embed, self.H4, self.W4)
         self.N = self.H4 * self.W4
         maxv = 2  # rpe spike + max-pooled feature spike
-        self.x0 = torch.empty(TB, self.N, _planes(maxv) * embed // 32, **i32)
+        f16t = dict(dtype=torch.float16, device=self.dev)
+
+        def stream_buf(planes):
+            return torch.empty(TB, self.N, embed, **f16t) if f16 else torch.empty(TB, self.N, planes * embed // 32, **i32)
+
+        self.x0 = stream_buf(_planes(maxv))
+        if f16:  # rpe spikes + the pooled features (1 plane) written as fp16
+            self.rpe = Fused(dataclasses.replace(self.rpe.spec, out_enc=ops.ENC_F16), self.rpe.values, self.rpe.meta,
+                             self.rpe.scale, self.rpe.bias)
 
         # ---- blocks
         hidden = embed * mlp_ratio
@@ -163,26 +178,30 @@ class SpikformerEngine:
         for i in range(depth):
             pre = f"block.{i}"
             P0, P1, P2 = _planes(maxv), _planes(maxv + 1), _planes(maxv + 2)
-            if P2 > 5:
+            if f16:
+                if maxv + 2 >= 2048:
+                    raise SEngineError("the residual stream exceeds fp16's exact integers (depth too large)")
+                P0 = P1 = P2 = 0
+            elif P2 > 5:
                 raise SEngineError("the residual stream needs more than 5 bit planes (depth too large)")
             blk = SBlock(pre, P0, P1, P2,
                          q=self._linear(p, pre + ".attn.q", embed, embed, P0),
                          k=self._linear(p, pre + ".attn.k", embed, embed, P0),
                          v=self._linear(p, pre + ".attn.v", embed, embed, P0),
-                         proj=self._linear(p, pre + ".attn.proj", embed, embed, 1),
+                         proj=self._linear(p, pre + ".attn.proj", embed, embed, 1, out_f16=f16),
                          fc1=self._linear(p, pre + ".mlp.fc1", embed, hidden, P1),
-                         fc2=self._linear(p, pre + ".mlp.fc2", hidden, embed, 1),
+                         fc2=self._linear(p, pre + ".mlp.fc2", hidden, embed, 1, out_f16=f16),
                          bufs={})
             d = embed // heads
             for n in ("q", "k", "v", "a"):
                 blk.bufs[n] = torch.empty(TB, self.N, embed // 32, **i32)
             blk.bufs["kv"] = torch.empty(TB, heads, d, d, **i32)
-            blk.bufs["x1"] = torch.empty(TB, self.N, P1 * embed // 32, **i32)
+            blk.bufs["x1"] = stream_buf(P1)
             blk.bufs["h"] = torch.empty(TB, self.N, hidden // 32, **i32)
-            blk.bufs["x2"] = torch.empty(TB, self.N, P2 * embed // 32, **i32)
+            blk.bufs["x2"] = stream_buf(P2)
             self.blocks.append(blk)
             maxv += 2
-        self.final_planes = self.blocks[-1].planes_out if self.blocks else _planes(2)
+        self.final_planes = 0 if f16 else (self.blocks[-1].planes_out if self.blocks else _planes(2))
         self.head_w = p["head.weight"].contiguous().to(self.dev)
         self.head_b = p["head.bias"].contiguous().to(self.dev)
         self.logits = torch.empty(batch, self.head_w.shape[0], dtype=torch.float32, device=self.dev)
@@ -217,7 +236,9 @@ class SpikformerEngine:
         sc, bi = self._bn(p, f"patch_embed.{name.replace('conv', 'bn')}", pad_to=cout_p)
         return self._prepare(self._spec(cin_p, cout_p, 3, h, w, 1), wp, sc, bi)
 
-    def _linear(self, p, name, cin, cout, planes) -> Fused:
+    def _linear(self, p, name, cin, cout, planes, out_f16=False) -> Fused:
+        """planes 0: fp16 input (the integer stream as fp16); 1: spike bits; > 1: bit planes
+        (plane-expanded weights).  out_f16: the spike + residual add writes the fp16 stream."""
         wk = name + "_linear.weight"
         w_ = p[wk]
         if tuple(w_.shape) != (cout, cin):
@@ -228,7 +249,12 @@ class SpikformerEngine:
         sc, bi = self._bn(p, name + "_bn", conv_bias=p[name + "_linear.bias"])
         wx = expand_planes(w4, planes) if planes > 1 else w4
         # tokens as a (T*B, N, 1) grid of pixels: a Linear is a 1x1 conv
-        return self._prepare(self._spec(cin * planes, cout, 1, self.N, 1, 0), wx, sc, bi)
+        spec = self._spec(cin * max(planes, 1), cout, 1, self.N, 1, 0)
+        if planes == 0:
+            spec = dataclasses.replace(spec, in_enc=ops.ENC_F16)
+        if out_f16:
+            spec = dataclasses.replace(spec, out_enc=ops.ENC_F16)
+        return self._prepare(spec, wx, sc, bi)
 
     # ------------------------------------------------------------------ execution
     def _fused(self, f: Fused, data, out):
@@ -251,9 +277,9 @@ class SpikformerEngine:
         self._fused_add(self.rpe, self.p3, self.p3, 1, self.x0, _planes(2))
 
     def block_input(self, i: int):
-        """(token stream, its planes) entering block i."""
+        """(token stream, its planes; 0 = fp16) entering block i."""
         if i == 0:
-            return self.x0, _planes(2)
+            return self.x0, 0 if self.stream == "f16" else _planes(2)
         prev = self.blocks[i - 1]
         return prev.bufs["x2"], prev.planes_out
 

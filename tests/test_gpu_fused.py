@@ -422,3 +422,62 @@ def test_tile_f16_input_real_valued(dev, k):
         assert x_err < 1e-3
     finally:
         ops.set_fused_kernel("auto")
+
+
+@pytest.mark.parametrize("traces", [True, False])
+@pytest.mark.parametrize("out_enc", [ops.ENC_BITS, ops.ENC_F16])
+@pytest.mark.parametrize("C_in,C_out,H,W,stride,B", [(384, 384, 7, 9, 1, 3), (128, 768, 6, 5, 1, 2),
+                                                     (256, 256, 9, 10, 2, 2), (128, 512, 4, 13, 1, 1)])
+def test_tile1pm_f16_input(dev, C_in, C_out, H, W, stride, B, out_enc, traces):
+    """fp16 activations on the position-major 1x1 kernel (6 waves for 384-channel multiples,
+    else 4; phases of two chunks), ragged position counts, stride 2, bit and fp16 output, LIF
+    (fast or generic epilogue) and IF with a carried membrane, against the oracle."""
+    spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=stride, padding=0,
+                        in_enc=ops.ENC_F16, out_enc=out_enc)
+    plan = ops.fused_plan(spec, traces=traces)
+    nw = 6 if C_out % 384 == 0 else 4
+    assert plan.startswith(f"tile1pm<T=4,GPW=1,CG=2,NW={nw},in=f16,"), plan
+    case = ref.make_layer_case(230 + C_in // 64 + C_out // 64 + stride, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W,
+                               k=1, stride=stride, padding=0, fp16_weights=True, p_spike=0.2)
+    rep, x_err, _, _ = run_case(dev, case, in_enc=ops.ENC_F16, out_enc=out_enc, traces=traces)
+    assert rep.ok, str(rep)
+    assert x_err is None or x_err < 1e-4
+    g = torch.Generator().manual_seed(6)
+    OH, OW = (H - 1) // stride + 1, (W - 1) // stride + 1
+    v0 = torch.rand((B, C_out, OH, OW), generator=g) * 0.4
+    rep2, _, r2, v_fin = run_case(dev, case, neuron="if", v_th=0.5, v_reset=0.0, v0=v0, in_enc=ops.ENC_F16,
+                                  out_enc=out_enc, traces=traces)
+    assert rep2.ok, str(rep2)
+    assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("C_out", [384, 128])
+def test_fp16_residual_stream_add(dev, C_out):
+    """out = spike + residual as fp16 (the reference add kernel's form) with an fp16 residual
+    and with a one-plane bit residual, against the oracle's spikes plus the residual; the
+    residual holds integers up to 17 (Spikformer's stream after eight blocks)."""
+    T, B, C_in, H, W = 4, 2, 128, 6, 7
+    case = ref.make_layer_case(250 + C_out // 64, T=T, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=1, padding=0,
+                               fp16_weights=True, p_spike=0.3)
+    spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
+                        out_enc=ops.ENC_F16)
+    values, meta, _ = ops.compress_2_4(spec, case.w.to(dev))
+    sc, bi = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
+    sc_d, bi_d = torch.from_numpy(sc).to(dev), torch.from_numpy(bi).to(dev)
+    data = torch.from_numpy(pk.seq_to_nhwc_bits(case.x_seq.numpy()).view(np.int32)).to(dev)
+    r = ref.fused_layer(case.x_seq, case.w, case.bn, 1, 0, 1, "lif", 2.0, 1.0, 0.0)
+    s_ref = r.spikes.numpy()  # (T, B, C_out, H, W)
+    g = torch.Generator().manual_seed(C_out)
+    res_int = torch.randint(0, 18, (T * B, H, W, C_out), generator=g)
+    out = ops.fused_sparse_conv_bn_lif_add(spec, data, values, meta, sc_d, bi_d, res_int.half().to(dev), 0, 0)
+    torch.cuda.synchronize()
+    spk = out.float().cpu() - res_int.float()
+    rep = compare(nhwc_seq(spk, T), None, s_ref, r.h.numpy(), 1.0)
+    assert rep.ok, str(rep)
+    assert set(np.unique(spk.numpy())) <= {0.0, 1.0}
+    # one-plane bit residual (the spikes of another layer), fp16 output
+    res_bits = (torch.rand((T * B, H, W, C_out), generator=g) < 0.4).half()
+    out2 = ops.fused_sparse_conv_bn_lif_add(spec, data, values, meta, sc_d, bi_d, ops.pack_spikes(res_bits.to(dev)),
+                                            1, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(out2.float().cpu() - res_bits.float(), spk)

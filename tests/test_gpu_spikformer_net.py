@@ -42,6 +42,21 @@ def _planes_of(x, planes, dev):
     return torch.from_numpy(pk.seq_to_planes(seq, planes).view(np.int32)).to(dev)
 
 
+def _tok_stream(eng, buf, planes, T, B, N, C):
+    """The engine's integer token stream -> (T, B, N, C) float (fp16 stream or bit planes)."""
+    if eng.stream == "f16":
+        return buf.float().cpu().view(T, B, N, C)
+    return _tok_planes(buf, planes, T, B, N, C)
+
+
+def _stream_of(eng, x, planes, dev):
+    """integer tokens (T, B, N, C) -> the engine's stream representation on the device."""
+    if eng.stream == "f16":
+        T, B, N, C = x.shape
+        return x.reshape(T * B, N, C).half().contiguous().to(dev)
+    return _planes_of(x, planes, dev)
+
+
 def _stage(p, name, x_seq):
     bn = sf.bn_of(p, f"patch_embed.{name.replace('conv', 'bn')}")
     return ref.fused_layer(x_seq, p[f"patch_embed.{name}.weight"], bn, 1, 1, 1, "lif", 2.0, 1.0, 0.0)
@@ -81,7 +96,7 @@ def _check_sps(eng, p, x_img, T, B, embed):
     p3 = _img_bits(eng.p3, T, B, embed, eng.H4, eng.W4)
     assert torch.equal(p3, _pool(s3))
     rr = _stage(p, "rpe_conv", p3)
-    x0 = _tok_planes(eng.x0, 2, T, B, eng.N, embed)
+    x0 = _tok_stream(eng, eng.x0, 2, T, B, eng.N, embed)
     srpe = x0 - p3.flatten(-2).transpose(-1, -2)
     assert set(np.unique(srpe.numpy())) <= {0.0, 1.0}
     rep = compare(srpe.transpose(-1, -2).reshape(rr.spikes.shape).numpy(), None, rr.spikes.numpy(), rr.h.numpy(),
@@ -97,7 +112,7 @@ def _check_block(dev, eng, p, i, x, T, B, heads):
     blk = eng.blocks[i]
     N, C = x.shape[2], x.shape[3]
     pre = blk.name
-    eng.run_block(i, x=_planes_of(x, blk.planes_in, dev))
+    eng.run_block(i, x=_stream_of(eng, x, blk.planes_in, dev))
     torch.cuda.synchronize()
     b = blk.bufs
 
@@ -116,13 +131,13 @@ def _check_block(dev, eng, p, i, x, T, B, heads):
     a_ref = sf.ssa(q, k, v, heads)[0]
     a = _tok_bits(b["a"], T, B, N, C)
     assert torch.equal(a, a_ref), f"{pre} ssa"
-    x1 = _tok_planes(b["x1"], blk.planes_mid, T, B, N, C)
+    x1 = _tok_stream(eng, b["x1"], blk.planes_mid, T, B, N, C)
     sp = x1 - x
     assert set(np.unique(sp.numpy())) <= {0.0, 1.0}
     lin("attn.proj", a, sp)
     h = _tok_bits(b["h"], T, B, N, C * 4)
     lin("mlp.fc1", x1, h)
-    x2 = _tok_planes(b["x2"], blk.planes_out, T, B, N, C)
+    x2 = _tok_stream(eng, b["x2"], blk.planes_out, T, B, N, C)
     s2 = x2 - x1
     assert set(np.unique(s2.numpy())) <= {0.0, 1.0}
     lin("mlp.fc2", h, s2)
@@ -137,9 +152,10 @@ def sf_case():
     return p, x, logits, xs
 
 
-def test_engine_sps_and_blocks_teacher_forced(dev, sf_case):
+@pytest.mark.parametrize("stream", ["f16", "planes"])
+def test_engine_sps_and_blocks_teacher_forced(dev, sf_case, stream):
     p, x, _, xs = sf_case
-    eng = SpikformerEngine(p, batch=2, T=4, embed=128, heads=2, depth=4, in_hw=(32, 32), device=dev)
+    eng = SpikformerEngine(p, batch=2, T=4, embed=128, heads=2, depth=4, in_hw=(32, 32), device=dev, stream=stream)
     eng.forward(x.to(dev))
     torch.cuda.synchronize()
     rates = _check_sps(eng, p, x, 4, 2, 128)
@@ -149,24 +165,25 @@ def test_engine_sps_and_blocks_teacher_forced(dev, sf_case):
         assert 0.005 < ra < 0.95
 
 
-def test_engine_end_to_end_graph(dev, sf_case):
+@pytest.mark.parametrize("stream", ["f16", "planes"])
+def test_engine_end_to_end_graph(dev, sf_case, stream):
     p, x, logits, xs = sf_case
-    eng = SpikformerEngine(p, batch=2, T=4, embed=128, heads=2, depth=4, in_hw=(32, 32), device=dev)
+    eng = SpikformerEngine(p, batch=2, T=4, embed=128, heads=2, depth=4, in_hw=(32, 32), device=dev, stream=stream)
     eager = eng.forward(x.to(dev)).clone()
     eng.capture()
     for _ in range(3):
         y = eng.forward(x.to(dev))
         torch.cuda.synchronize()
         assert torch.equal(y, eager)
-    final = _tok_planes(eng.blocks[-1].bufs["x2"], eng.final_planes, 4, 2, eng.N, 128)
+    final = _tok_stream(eng, eng.blocks[-1].bufs["x2"], eng.final_planes, 4, 2, eng.N, 128)
     assert float((final != xs[-1]).float().mean()) <= 1e-3
     err = float((eager.cpu() - logits).abs().max())
     assert err < 5e-2, err
     assert eng.launches == 7 + 8 * 4 + 1
 
 
-@pytest.mark.parametrize("batch,nblocks", [(1, 1), (4, 2)])
-def test_engine_cfg4_shape(dev, batch, nblocks):
+@pytest.mark.parametrize("batch,nblocks,stream", [(1, 1, "f16"), (4, 2, "f16"), (1, 1, "planes")])
+def test_engine_cfg4_shape(dev, batch, nblocks, stream):
     """BASELINE config 4's shape: 3x224x224 pixels ~N(0,1), T=4, embed 384, 8 heads, MLP ratio
     4, 8 blocks (3,136 tokens), 1000 classes, on one image and on four (whose token layers
     take the same tile-kernel instances as the benchmark's batch of 32); the SPS stages and
@@ -174,8 +191,9 @@ def test_engine_cfg4_shape(dev, batch, nblocks):
     eager run."""
     p = sf.make_params(41, embed=384, depth=8, num_classes=1000)
     x = torch.randn(batch, 3, 224, 224, generator=torch.Generator().manual_seed(42))
-    eng = SpikformerEngine(p, batch=batch, T=4, embed=384, heads=8, depth=8, in_hw=(224, 224), device=dev)
-    assert eng.N == 3136 and eng.final_planes == 5
+    eng = SpikformerEngine(p, batch=batch, T=4, embed=384, heads=8, depth=8, in_hw=(224, 224), device=dev,
+                           stream=stream)
+    assert eng.N == 3136 and eng.final_planes == (5 if stream == "planes" else 0)
     eager = eng.forward(x.to(dev)).clone()
     eng.capture()
     y = eng.forward(x.to(dev))
@@ -183,8 +201,8 @@ def test_engine_cfg4_shape(dev, batch, nblocks):
     assert torch.equal(y, eager)
     rates = _check_sps(eng, p, x, 4, batch, 384)
     assert all(0.005 < r < 0.9 for r in rates), rates
-    xi = _tok_planes(eng.x0, 2, 4, batch, eng.N, 384)  # the engine's own (parity-checked) SPS output
+    xi = _tok_stream(eng, eng.x0, 2, 4, batch, eng.N, 384)  # the engine's own (parity-checked) SPS output
     for i in range(nblocks):
         _check_block(dev, eng, p, i, xi, 4, batch, 8)
         blk = eng.blocks[i]
-        xi = _tok_planes(blk.bufs["x2"], blk.planes_out, 4, batch, eng.N, 384)  # checked block output
+        xi = _tok_stream(eng, blk.bufs["x2"], blk.planes_out, 4, batch, eng.N, 384)  # checked block output
