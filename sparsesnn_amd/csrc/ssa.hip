@@ -317,6 +317,11 @@ extern "C" int sengine_amd_ssa_attend_neuron(int32_t T, int32_t B, int32_t N, in
   void* fn = p.d == 16 ? attend_fn<16>(T, fast) : p.d == 32 ? attend_fn<32>(T, fast)
                                                  : p.d == 48 ? attend_fn<48>(T, fast) : attend_fn<64>(T, fast);
   if (fast) p.xscale *= p.np.rtau;  // exact: both powers of two
+  // the K^T V entries (integers <= N) go to fp16 as (x & 63) * xscale and ((x >> 6) << 6) *
+  // xscale: exact only while the larger stays finite and the smaller's unit is representable
+  if ((double)N * p.xscale > 65504.0 || p.xscale < 0x1p-24f)
+    return set_error(-2, "ssa_attend_neuron: scale out of range for exact fp16 attention pieces (needs "
+                         "N * scale / 2 <= 65504 and scale / 2 >= 2^-24, times 1/tau for LIF)");
   if (lds > 65536) {  // opt in to more than 64 KB of dynamic LDS (a host-side attribute)
     const hipError_t e2 = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSsaMaxLds);
     if (e2 != hipSuccess) return (int)e2;

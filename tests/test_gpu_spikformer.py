@@ -61,6 +61,26 @@ def test_ssa_rejects_bad_shapes(dev):
         ops.spiking_self_attention(z2, z2, z2, 2, 1, 10, 384, 8, scale=0.1)
 
 
+@pytest.mark.parametrize("neuron,xs", [("lif", 0.25), ("if", 0.5)])  # xscale = scale * xs (LIF folds 1/tau)
+def test_ssa_scale_range(dev, neuron, xs):
+    """The attention's fp16 pieces are exact only for N * xscale <= 65504 and xscale >= 2^-24:
+    scales at the bounds run (bit-exact against the oracle), one step past them is refused."""
+    T, B, N, C, heads = 1, 1, 2048, 64, 4
+    q, k, v = (_spikes((T, B, N, C), 0.9, s) for s in (31, 32, 33))
+    qb, kb, vb = (_bits(a).to(dev) for a in (q, k, v))
+    top = 2.0 ** int(np.floor(np.log2(65504.0 / N / xs)))  # largest power of two in range
+    bottom = 2.0 ** -24 / xs
+    for scale in (top, bottom):
+        out = ops.spiking_self_attention(qb, kb, vb, T, B, N, C, heads, scale=scale, neuron=neuron)
+        torch.cuda.synchronize()
+        if neuron == "lif":
+            s_ref = sf.ssa(q, k, v, heads, scale=scale)[0]
+            assert np.array_equal(_unbits(out, T, B, N, C), s_ref.numpy())
+    for scale in (top * 2, bottom / 2):
+        with pytest.raises(ops.SEngineError, match="scale out of range"):
+            ops.spiking_self_attention(qb, kb, vb, T, B, N, C, heads, scale=scale, neuron=neuron)
+
+
 @pytest.mark.parametrize("N,C_in,C_out", [(197, 384, 384), (196, 384, 1536), (50, 1536, 384)])
 def test_linear_bn_lif_as_fused_1x1(dev, N, C_in, C_out):
     """Spikformer's Linear (with bias) + BN1d + LIF on tokens = the fused 1x1 conv over the
