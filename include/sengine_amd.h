@@ -257,6 +257,22 @@ int sengine_amd_ssa_attend_neuron(int32_t T, int32_t B, int32_t N, int32_t C, in
                                   const uint32_t* q_bits, const int32_t* kv, uint32_t* out_bits, hipStream_t stream);
 
 /*
+ * Allocation-free spiking self-attention: sengine_amd_ssa_kv followed by
+ * sengine_amd_ssa_attend_neuron with the K^T V partial sums in a library-owned device array
+ * instead of a caller workspace.  No counterpart in the reference: for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * The array holds at most 4,194,304 int32 (16 MiB, T * B * heads * (C/heads)^2 entries; larger
+ * calls return -2), every GPU the library runs on keeps one until the process ends, and the
+ * call allocates nothing (the array's address is looked up once per device).  All calls on
+ * one GPU share the array: calls that overlap on that GPU (other streams, or threads) race.
+ * Arguments and results as the two entries above.
+ */
+int sengine_amd_ssa_attention_noalloc(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, float scale,
+                                      int32_t neuron, int32_t hard_reset, float tau, float v_threshold, float v_reset,
+                                      const uint32_t* q_bits, const uint32_t* k_bits, const uint32_t* v_bits,
+                                      uint32_t* out_bits, hipStream_t stream);
+
+/*
  * Dense stem convolution on images + folded BN (the reference runs it through cuDNN,
  * sengine/csrc/cpp_executor.cu:306-347; models/sewresnet.py:140-141,199-200):
  * x NCHW fp32 (d->B images, d->C_in, d->H, d->W), weight fp32 in w_layout (HWIO reads

@@ -65,6 +65,8 @@ SIGNATURES = {
     "sengine_amd_ssa_kv": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
     "sengine_amd_ssa_attend_neuron": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _F, _I32, _I32, _F, _F, _F,
                                                      _P, _P, _P, _P]),
+    "sengine_amd_ssa_attention_noalloc": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _F, _I32, _I32, _F, _F, _F,
+                                                         _P, _P, _P, _P, _P]),
     "sengine_amd_stem_conv_bn_lif_pool": (ctypes.c_int, [_DP, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P]),
     "sengine_amd_stem_conv_bn_neuron": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P]),
     "sengine_amd_multistep_neuron_repeat": (ctypes.c_int, [_I32, _I64, _I32, _I32, _F, _F, _F, _P, _P, _P]),

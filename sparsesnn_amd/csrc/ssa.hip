@@ -16,6 +16,8 @@
 //                      from bits, one fp32 accumulator), the neuron over T in
 //                      registers, 16 output channels of a token assembled across lanes
 //                      and stored as one u16.
+#include <mutex>
+
 #include "common.h"
 #include "epilogue.h"
 #include "internal.h"
@@ -266,33 +268,48 @@ static const char* ssa_check(int T, int B, int N, int C, int H) {
   return nullptr;
 }
 
-}  // namespace sengine
+namespace {
 
-using namespace sengine;
+struct KvLaunch {
+  SsaParams p;
+  size_t lds;
+};
 
-extern "C" int sengine_amd_ssa_kv(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, const uint32_t* k_bits,
-                                  const uint32_t* v_bits, int32_t* kv, hipStream_t stream) {
+int kv_setup(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, const uint32_t* k_bits,
+             const uint32_t* v_bits, int32_t* kv, KvLaunch& L) {
   if (const char* why = ssa_check(T, B, N, C, heads)) return set_error(-2, why);
   if (!k_bits || !v_bits || !kv) return set_error(-1, "ssa_kv: null pointer");
-  SsaParams p{};
+  SsaParams& p = L.p;
+  p = SsaParams{};
   p.k = k_bits; p.v = v_bits; p.kv = kv;
   p.T = T; p.B = B; p.N = N; p.C = C; p.H = heads; p.d = C / heads;
-  const size_t lds = (2 * (size_t)p.d + 2) * ((N + 63) / 64) * sizeof(uint64_t) + (size_t)p.d * p.d * sizeof(uint32_t);
-  if (lds > 65536) return set_error(-2, "ssa_kv: (C/heads) * ceil(N/64) too large for the token masks in LDS");
-  const dim3 grid((unsigned)(T * B * heads)), block(64 * kSsaKvWaves);
+  L.lds = (2 * (size_t)p.d + 2) * ((N + 63) / 64) * sizeof(uint64_t) + (size_t)p.d * p.d * sizeof(uint32_t);
+  if (L.lds > 65536) return set_error(-2, "ssa_kv: (C/heads) * ceil(N/64) too large for the token masks in LDS");
+  return 0;
+}
+
+int kv_launch(const KvLaunch& L, hipStream_t stream) {
+  const SsaParams& p = L.p;
+  const dim3 grid((unsigned)(p.T * p.B * p.H)), block(64 * kSsaKvWaves);
   switch (p.d) {
-    case 16: hipLaunchKernelGGL(ssa_kv_kernel<16>, grid, block, lds, stream, p); break;
-    case 32: hipLaunchKernelGGL(ssa_kv_kernel<32>, grid, block, lds, stream, p); break;
-    case 48: hipLaunchKernelGGL(ssa_kv_kernel<48>, grid, block, lds, stream, p); break;
-    default: hipLaunchKernelGGL(ssa_kv_kernel<64>, grid, block, lds, stream, p); break;
+    case 16: hipLaunchKernelGGL(ssa_kv_kernel<16>, grid, block, L.lds, stream, p); break;
+    case 32: hipLaunchKernelGGL(ssa_kv_kernel<32>, grid, block, L.lds, stream, p); break;
+    case 48: hipLaunchKernelGGL(ssa_kv_kernel<48>, grid, block, L.lds, stream, p); break;
+    default: hipLaunchKernelGGL(ssa_kv_kernel<64>, grid, block, L.lds, stream, p); break;
   }
   return (int)hipGetLastError();
 }
 
-extern "C" int sengine_amd_ssa_attend_neuron(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, float scale,
-                                             int32_t neuron, int32_t hard_reset, float tau, float v_threshold,
-                                             float v_reset, const uint32_t* q_bits, const int32_t* kv,
-                                             uint32_t* out_bits, hipStream_t stream) {
+struct AttendLaunch {
+  SsaParams p;
+  void* fn;
+  size_t lds;
+  int splits;
+};
+
+int attend_setup(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, float scale, int32_t neuron,
+                 int32_t hard_reset, float tau, float v_threshold, float v_reset, const uint32_t* q_bits,
+                 const int32_t* kv, uint32_t* out_bits, AttendLaunch& L) {
   if (const char* why = ssa_check(T, B, N, C, heads)) return set_error(-2, why);
   if (!q_bits || !kv || !out_bits) return set_error(-1, "ssa_attend_neuron: null pointer");
   if (const char* why = neuron_invalid(neuron, tau)) return set_error(-2, why);
@@ -300,32 +317,109 @@ extern "C" int sengine_amd_ssa_attend_neuron(int32_t T, int32_t B, int32_t N, in
   int e;
   if (!(scale > 0.f) || frexpf(scale, &e) != 0.5f)
     return set_error(-2, "ssa_attend_neuron: scale must be a power of two (exact attention arithmetic)");
-  SsaParams p{};
+  SsaParams& p = L.p;
+  p = SsaParams{};
   p.q = q_bits; p.kv = const_cast<int32_t*>(kv); p.out = reinterpret_cast<uint16_t*>(out_bits);
   p.T = T; p.B = B; p.N = N; p.C = C; p.H = heads; p.d = C / heads;
   p.xscale = scale * 0.5f;
   p.np = make_neuron_params(neuron, hard_reset, tau, v_threshold, v_reset);
   // token ranges per (b, head): enough workgroups for every CU several times over
   const int tiles = (N + 15) / 16;
-  const int splits = std::max(1, std::min((tiles + 3) / 4, (2048 + B * heads - 1) / (B * heads)));
-  const int per = (tiles + splits - 1) / splits;
-  const size_t lds = (size_t)T * 2 * p.d * kSsaRow * sizeof(_Float16) + (size_t)T * per * 16 * sizeof(uint64_t);
-  if (lds > kSsaMaxLds)
+  L.splits = std::max(1, std::min((tiles + 3) / 4, (2048 + B * heads - 1) / (B * heads)));
+  const int per = (tiles + L.splits - 1) / L.splits;
+  L.lds = (size_t)T * 2 * p.d * kSsaRow * sizeof(_Float16) + (size_t)T * per * 16 * sizeof(uint64_t);
+  if (L.lds > kSsaMaxLds)
     return set_error(-2, "ssa_attend_neuron: T * (C/heads) and the token range too large for LDS");
   // fast path: LIF with an exact power-of-two 1/tau and decay, hard reset (the reference's attn_lif)
   const bool fast = epilogue_mode(p.np, false) == EPI_LIF_HARD;
-  void* fn = p.d == 16 ? attend_fn<16>(T, fast) : p.d == 32 ? attend_fn<32>(T, fast)
-                                                 : p.d == 48 ? attend_fn<48>(T, fast) : attend_fn<64>(T, fast);
+  L.fn = p.d == 16 ? attend_fn<16>(T, fast) : p.d == 32 ? attend_fn<32>(T, fast)
+                                             : p.d == 48 ? attend_fn<48>(T, fast) : attend_fn<64>(T, fast);
   if (fast) p.xscale *= p.np.rtau;  // exact: both powers of two
   // the K^T V entries (integers <= N) go to fp16 as (x & 63) * xscale and ((x >> 6) << 6) *
   // xscale: exact only while the larger stays finite and the smaller's unit is representable
   if ((double)N * p.xscale > 65504.0 || p.xscale < 0x1p-24f)
     return set_error(-2, "ssa_attend_neuron: scale out of range for exact fp16 attention pieces (needs "
                          "N * scale / 2 <= 65504 and scale / 2 >= 2^-24, times 1/tau for LIF)");
-  if (lds > 65536) {  // opt in to more than 64 KB of dynamic LDS (a host-side attribute)
-    const hipError_t e2 = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSsaMaxLds);
+  return 0;
+}
+
+int attend_launch(AttendLaunch& L, hipStream_t stream) {
+  if (L.lds > 65536) {  // opt in to more than 64 KB of dynamic LDS (a host-side attribute)
+    const hipError_t e2 = hipFuncSetAttribute(L.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSsaMaxLds);
     if (e2 != hipSuccess) return (int)e2;
   }
-  void* args[] = {&p, const_cast<int*>(&splits)};
-  return (int)hipLaunchKernel(fn, dim3((unsigned)(B * heads * splits)), dim3(256), args, lds, stream);
+  void* args[] = {&L.p, &L.splits};
+  return (int)hipLaunchKernel(L.fn, dim3((unsigned)(L.p.B * L.p.H * L.splits)), dim3(256), args, L.lds, stream);
+}
+
+// Allocation-free attention: K^T V in a file-scope device array instead of a caller workspace.
+// Each GPU holds its own copy; its address is taken once per device (host code never passes
+// the array's name itself, which on the host is only a stand-in for the symbol).
+constexpr size_t kSsaScratchInts = size_t(1) << 22;  // 16 MiB: T*B*heads*d*d int32 at most
+static __device__ __align__(256) int32_t scratch[kSsaScratchInts];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch[kMaxDevices] = {};
+
+int scratch_for_current_device(int32_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return set_error(-2, "ssa_attention_noalloc: device index beyond 64");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return set_error(-1, "ssa_attention_noalloc: no address for the scratch array");
+    g_scratch[dev] = static_cast<int32_t*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return 0;
+}
+
+}  // namespace
+}  // namespace sengine
+
+using namespace sengine;
+
+extern "C" int sengine_amd_ssa_kv(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, const uint32_t* k_bits,
+                                  const uint32_t* v_bits, int32_t* kv, hipStream_t stream) {
+  KvLaunch L;
+  const int rc = kv_setup(T, B, N, C, heads, k_bits, v_bits, kv, L);
+  return rc ? rc : kv_launch(L, stream);
+}
+
+extern "C" int sengine_amd_ssa_attend_neuron(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, float scale,
+                                             int32_t neuron, int32_t hard_reset, float tau, float v_threshold,
+                                             float v_reset, const uint32_t* q_bits, const int32_t* kv,
+                                             uint32_t* out_bits, hipStream_t stream) {
+  AttendLaunch L;
+  const int rc = attend_setup(T, B, N, C, heads, scale, neuron, hard_reset, tau, v_threshold, v_reset, q_bits, kv,
+                              out_bits, L);
+  return rc ? rc : attend_launch(L, stream);
+}
+
+extern "C" int sengine_amd_ssa_attention_noalloc(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads,
+                                                 float scale, int32_t neuron, int32_t hard_reset, float tau,
+                                                 float v_threshold, float v_reset, const uint32_t* q_bits,
+                                                 const uint32_t* k_bits, const uint32_t* v_bits, uint32_t* out_bits,
+                                                 hipStream_t stream) {
+  if (const char* why = ssa_check(T, B, N, C, heads)) return set_error(-2, why);
+  const size_t d = (size_t)(C / heads);
+  if ((size_t)T * B * heads * d * d > kSsaScratchInts)
+    return set_error(-2, "ssa_attention_noalloc: T * B * heads * (C/heads)^2 exceeds the 4,194,304-entry scratch");
+  int32_t* kv = nullptr;
+  int rc = scratch_for_current_device(&kv);
+  if (rc) return rc;
+  // every argument is checked before anything is launched
+  KvLaunch K;
+  if ((rc = kv_setup(T, B, N, C, heads, k_bits, v_bits, kv, K))) return rc;
+  AttendLaunch A;
+  if ((rc = attend_setup(T, B, N, C, heads, scale, neuron, hard_reset, tau, v_threshold, v_reset, q_bits, kv,
+                         out_bits, A)))
+    return rc;
+  // the K^T V kernel writes every entry the attend kernel reads: nothing to clear
+  if ((rc = kv_launch(K, stream))) return rc;
+  return attend_launch(A, stream);
 }
