@@ -336,10 +336,18 @@ def cpu_e2e(params, x, budget_s=6.0, min_runs=CPU_MIN_RUNS):
 CFG34_BATCH, CFG34_HW, CFG34_CLASSES = 32, 224, 1000
 
 
-def bench_graph_engine(eng, x, warmup: int, iters: int) -> float:
-    """Seconds per batch of a captured engine: HIP events around `iters` hipGraph replays."""
+def bench_graph_engine(eng, x, warmup: int, iters: int, eager: bool = False) -> float:
+    """Seconds per batch of a captured engine: HIP events around `iters` hipGraph replays.
+    eager=True times eager forwards instead (no graph: the counter-collection pass)."""
     import torch
     eng.forward(x)
+    if eager:
+        torch.cuda.synchronize(x.device)
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            eng.forward(x)
+        torch.cuda.synchronize(x.device)
+        return (time.perf_counter() - t0) / iters
     eng.capture()
     for _ in range(warmup):
         eng.forward(x)
@@ -355,7 +363,7 @@ def bench_graph_engine(eng, x, warmup: int, iters: int) -> float:
     return a.elapsed_time(b) * 1e-3 / iters
 
 
-def bench_msresnet34(dev, warmup: int, iters: int):
+def bench_msresnet34(dev, warmup: int, iters: int, eager: bool = False):
     """MS-ResNet-34 (membrane shortcut, LIF tau 2 / V_th 1, 2:4 convs but the
     stem, reference initialisation), 3x224x224 pixels ~N(0,1), T=4, batch 32, 1000 classes."""
     import torch
@@ -364,11 +372,11 @@ def bench_msresnet34(dev, warmup: int, iters: int):
     eng = MSResNetEngine(params, batch=CFG34_BATCH, T=T_STEPS, depth=34, neuron="lif", in_hw=(CFG34_HW, CFG34_HW),
                          device=dev)
     x = torch.randn((CFG34_BATCH, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(8))
-    s = bench_graph_engine(eng, x.to(dev), warmup, iters)
+    s = bench_graph_engine(eng, x.to(dev), warmup, iters, eager)
     return dict(params=params, x=x, batch_s=s, launches=eng.launches)
 
 
-def bench_spikformer(dev, warmup: int, iters: int):
+def bench_spikformer(dev, warmup: int, iters: int, eager: bool = False):
     """Spikformer, 8 blocks, embed 384, 8 heads, MLP ratio 4, SPS stem on
     3x224x224 pixels ~N(0,1) (3,136 tokens), T=4, batch 32, 1000 classes, the stem convs after
     the first and every block Linear 2:4 with fused BN+LIF, the model's own initialisation."""
@@ -378,7 +386,7 @@ def bench_spikformer(dev, warmup: int, iters: int):
     eng = SpikformerEngine(params, batch=CFG34_BATCH, T=T_STEPS, embed=384, heads=8, depth=8,
                            in_hw=(CFG34_HW, CFG34_HW), device=dev)
     x = torch.randn((CFG34_BATCH, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(9))
-    s = bench_graph_engine(eng, x.to(dev), warmup, iters)
+    s = bench_graph_engine(eng, x.to(dev), warmup, iters, eager)
     return dict(params=params, x=x, batch_s=s, launches=eng.launches)
 
 
@@ -436,7 +444,8 @@ def main():
                     help="skip the config-3 (MS-ResNet-34) and config-4 (Spikformer) end-to-end measurements")
     ap.add_argument("--profile-pass", action="store_true",
                     help="counter-collection pass for rocprofv3 --pmc: eager launches only (no graph, no "
-                         "JSON line), followed by the copy-calibration kernel")
+                         "JSON line), followed by the copy-calibration kernel; with --e2e-only (msresnet34, "
+                         "spikformer): eager forwards instead of graph replays")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU fused operator only; multi-GPU runs are not part of this "
@@ -449,12 +458,15 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     if args.e2e_only:
+        eager = args.profile_pass  # counter collection: eager forwards, no graph
         if args.e2e_model == "sew18":
             e2e, batch = bench_e2e(dev, warmup=args.warmup, iters=args.steps), E2E_BATCH
         elif args.e2e_model == "msresnet34":
-            e2e, batch = bench_msresnet34(dev, warmup=args.warmup, iters=args.steps), CFG34_BATCH
+            e2e, batch = bench_msresnet34(dev, warmup=args.warmup, iters=args.steps, eager=eager), CFG34_BATCH
         else:
-            e2e, batch = bench_spikformer(dev, warmup=args.warmup, iters=args.steps), CFG34_BATCH
+            e2e, batch = bench_spikformer(dev, warmup=args.warmup, iters=args.steps, eager=eager), CFG34_BATCH
+        if eager:
+            copy_calibration(dev)  # the counters' scale: a copy of known size
         print(json.dumps({"metric": "images/sec", "model": args.e2e_model, "value": round(batch / e2e["batch_s"], 1),
                           "ms_per_batch": round(e2e["batch_s"] * 1e3, 4), "batch": batch, "timesteps": T_STEPS,
                           "replays": args.steps, "warmup": args.warmup}))
