@@ -1,6 +1,7 @@
 // Instantiations of the tile kernel (tile_kernel.h) for 1x1 / pad 0 convolutions (any
 // stride), and the host-side choice between tile shapes and channel blocking.
 #include "tile1pm.h"
+#include "tile1ps.h"
 #include "tile_kernel.h"
 
 #include <stdio.h>
@@ -154,6 +155,44 @@ static int tile_epilogue_mode(const sengine_conv_lif_desc* d, const TileChoice& 
   return mode;
 }
 
+// Compute units of the current device (cached per device; the persistent 1x1 kernel sizes its
+// grid to the resident workgroups).
+static int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// The persistent fp16-input 1x1 kernel (tile1ps.h) serves the position-major fp16 case when the
+// layer is what it is written for: stride 1, T = 4, 16 | M, an even chunk count, spike-bit
+// output, a fast stateless neuron, no residual or traces; channels in 256-channel super-blocks
+// (4 waves, phases of 2 chunks) or 384-channel ones (6 waves, phases of 3 chunks, an even
+// phase count).  Returns the waves per workgroup, or 0.  SENGINE_AMD_TILE1_PS=0 turns it off.
+static int tile1ps_waves(const sengine_conv_lif_desc* d, const Geometry& geo, const TileChoice& c, int mode,
+                         const FusedArgs* a) {
+  const int nchunk = d->C_in / 64;
+  if (d->in_enc != SENGINE_ENC_F16 || c.k3 || !c.pm || d->T != 4 || d->stride_h != 1 || d->stride_w != 1 ||
+      geo.M % 16 != 0 || nchunk % 2 != 0 || d->out_enc != SENGINE_ENC_BITS ||
+      (mode != EPI_LIF_HARD && mode != EPI_IF_HARD))
+    return 0;
+  if ((int64_t)d->T * geo.M * d->C_in * 2 > 0x7fffffff) return 0;  // piece offsets are 32-bit
+  if (a && (a->state || a->sew.res || a->sew.res16 || a->sew.real_out || a->h_trace || a->x_trace)) return 0;
+  if (env_int_now("SENGINE_AMD_TILE1_PS", -1) == 0) return 0;
+  if (d->C_out % 256 == 0) return 4;
+  if (d->C_out % 384 == 0 && nchunk % 6 == 0) return 6;
+  return 0;
+}
+
+// Resident workgroups of the persistent kernel (two waves per SIMD): two 4-wave workgroups per
+// CU, or one 6-wave workgroup (the waves of a second would not all find a SIMD).
+static int tile1ps_slots(int nw) { return device_cus() * (nw == 6 ? 1 : 2); }
+
 int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool shortcut_only, char* buf,
                   size_t len) {
   TileChoice c;
@@ -166,6 +205,12 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
   // tile instances (every mode)
   const bool fast_f16out = f16in ? c.pm == 0 : (!c.k3 && d->T == 4 && c.pm == 0 && mode == EPI_LIF_HARD);
   const char* epi = d->out_enc == SENGINE_ENC_BITS || fast_f16out ? kEpi[mode] : "generic";
+  if (const int nw = f16in ? tile1ps_waves(d, geo, c, mode, nullptr) : 0) {
+    const int npg = (int)(geo.M / 16), nsb = d->C_out / (64 * nw);
+    const int per = std::max(1, std::min(tile1ps_slots(nw) / nsb, npg));
+    return snprintf(buf, len, "tile1ps<T=4,NW=%d,CG=%d,in=f16,out=%s,epi=%s> grid=%d (persistent, %d groups)", nw,
+                    nw == 6 ? 3 : 2, oe, epi, per * nsb, npg);
+  }
   if (f16in && c.pm)
     return snprintf(buf, len, "tile1pm<T=4,GPW=1,CG=2,NW=%d,in=f16,out=%s,epi=%s> grid=%lld", c.pmw, oe, epi,
                     (long long)((geo.M + 15) / 16) * (d->C_out / (64 * c.pmw)));
@@ -223,6 +268,9 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
       shortcut_only);
   if (d->in_enc == SENGINE_ENC_F16) {
     if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
+    if (const int nw = tile1ps_waves(d, geo, c, mode, &a))
+      return nw == 6 ? launch_tile1ps<6, 3>(p, mode, tile1ps_slots(6), stream)
+                     : launch_tile1ps<4, 2>(p, mode, tile1ps_slots(4), stream);
     if (c.pm)
       return c.pmw == 6 ? launch_tile1pm<4, 1, 2, 6, SENGINE_ENC_F16>(p, d->out_enc, mode, stream)
                         : launch_tile1pm<4, 1, 2, 4, SENGINE_ENC_F16>(p, d->out_enc, mode, stream);

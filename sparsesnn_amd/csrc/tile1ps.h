@@ -1,0 +1,253 @@
+// Fused 2:4-sparse 1x1 Conv + BN + multi-step neuron on fp16 activations, persistent form
+// (gfx950).
+//
+// Same operator, weight blob, LDS layout and epilogue as the position-major kernel
+// (tile1pm.h; the reference's conv1x1_bn_lif, sengine/kernels/interleaved_templates.py:95-154,
+// fed the fp16 NHWC activations of its native call() ABI, cpp_executor.cu:909-913), for the
+// token Linears of a spiking transformer: thousands of 16-position groups, a short reduction
+// (a few 64-channel chunks) and fp16 rows 16x the size of spike bits.  One 16-position
+// workgroup per (group, channel block) spends most of its life in dependent memory round
+// trips (weights, first staging, the phase barriers), and the waves of a CU cannot hide them.
+// Here each workgroup stays resident and walks a strided sequence of position groups of one
+// channel super-block (NW waves x 64 channels):
+//
+//  * the reduction phases (CG = 2 chunks each) of consecutive groups form one flat sequence;
+//    the fp16 pieces of phase f + 2 are loaded when phase f starts and stored into the other
+//    LDS buffer when it ends (one barrier per phase), so a group's first staging overlaps the
+//    previous group's SMFMACs and epilogue instead of starting cold;
+//  * the A operands keep cycling through the two-set ring across group boundaries (the
+//    chunk count is even, so chunk 0 of the next group lands in set 0);
+//  * a group's epilogue (BN + neuron over T, spike bits stored) runs after its last phase,
+//    then the accumulators are cleared for the next group;
+//  * workgroup ids are remapped so the NW-wave super-blocks of the same position groups sit
+//    on one XCD (their shared fp16 rows are fetched into one L2).
+//
+// Restricted to what the token Linears need: T = 4, stride 1 (position m's input row is
+// t*M + m), M a multiple of 16, an even chunk count, spike-bit output, a hard-reset LIF or IF
+// without state or traces and no residual.
+#pragma once
+#include "tile1pm.h"
+
+namespace sengine {
+
+// The stateless hard-reset epilogue of fast_epilogue_stateless with spike-bit output and no
+// residual, reading the folded BN coefficients from LDS where they are used (16 registers
+// instead of 48 held across the timesteps: the persistent loop keeps the next group's operands
+// live meanwhile).
+template <int MODE>
+__device__ __forceinline__ void tile1ps_epilogue(const float4_t (&acc)[4][4], int m, int F, int cob,
+                                                 const NeuronParams& np, const float* fsc, const float* fbi,
+                                                 uint8_t* __restrict__ out, int M) {
+  constexpr int T = 4;
+  float v[16];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j4 = 12; j4 >= 0; j4 -= 4) {
+      const float4_t s4 = *reinterpret_cast<const float4_t*>(fsc + j4);
+      const float4_t b4 = *reinterpret_cast<const float4_t*>(fbi + j4);
+#pragma unroll
+      for (int e = 3; e >= 0; --e) {
+        const int j = j4 + e;
+        const float xin = __builtin_fmaf(acc[t][j >> 2][j & 3], s4[e], b4[e]);
+        const float h = t == 0 ? xin
+                               : (MODE == EPI_LIF_HARD ? __builtin_fmaf(v[j], np.decay, xin) : __fadd_rn(v[j], xin));
+        if (t + 1 < T)
+          fire_hard(h, np.vth, np.vreset, v[j], word);
+        else
+          fire_only(h, np.vth, word);
+      }
+    }
+    *reinterpret_cast<uint16_t*>(out + ((((size_t)t * M + m) * F + cob) >> 3)) = (uint16_t)word;
+  }
+}
+
+// CG: chunks per phase (2; or 3 for 6-wave super-blocks of 384 channels, whose 384 threads
+// then move four pieces each -- the host also requires an even phase count, so phase f and its
+// position in the group have the same parity).
+template <int NW, int CG, int MODE>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
+  constexpr int T = 4;
+  constexpr int NTH = 64 * NW;
+  constexpr int CE = T * 16 * 16;              // LDS entries (8 bytes) per staged chunk
+  constexpr int PIECES = CG * T * 16 * 8;      // 16-byte pieces per phase
+  constexpr int PPT = (PIECES + NTH - 1) / NTH;
+  static_assert(MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD, "fast stateless modes only");
+  static_assert(PIECES % NTH == 0, "every thread moves the same number of pieces");
+  __shared__ uint2 sB[2][CG * CE];
+  __shared__ float sCoef[2][NW * 64];
+
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4;
+  const int col = lane & 15;
+
+  // workgroup -> (channel super-block sb, first group j0); groups j0, j0 + J, j0 + 2J, ...
+  const int L = tile_remap(blockIdx.x, gridDim.x);
+  const int sb = L % nsb;
+  const int j0 = L / nsb;
+  const int J = (int)gridDim.x / nsb;  // host: gridDim.x % nsb == 0, gridDim.x / nsb <= npg
+  const int nblk = (npg - j0 + J - 1) / J;
+  const int G0 = sb * NW + wave;  // this wave's 64-channel group
+
+  for (int i = tid; i < NW * 64; i += NTH) {
+    const int ch = sb * NW * 64 + i;
+    const float sc = p.scale[ch] * p.enc_scale;
+    const float bi = p.bias[ch];
+    const bool fold = MODE == EPI_LIF_HARD;
+    sCoef[0][i] = fold ? sc * p.np.rtau : sc;  // exact: rtau is a power of two
+    sCoef[1][i] = fold ? bi * p.np.rtau : bi;
+  }
+
+  // piece q = tid + j*NTH of a phase is piece q & 7 of unit (cc, t, pos) = q >> 3; its fp16
+  // row is t*M + m0 + pos, its bytes cc*128 + (q & 7)*16 of the phase's 256-byte span
+  const int64_t rowb = (int64_t)p.C * 2;  // bytes per input row
+  int rel[PPT], poff[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int q = tid + j * NTH;
+    const int u = q >> 3, i = q & 7;
+    const int pos = u & 15;
+    const int t = (u >> 4) & (T - 1);
+    const int cc = u >> 6;
+    rel[j] = (int)(((int64_t)t * p.M + pos) * rowb) + cc * 128 + i * 16;
+    poff[j] = (cc * T + t) * 256 + pos + i * 16;
+  }
+  const int nphase = p.nchunk / CG;
+  const int nf = nblk * nphase;
+  // byte offset of flat phase f's data relative to rel[]: group j0 + (f / nphase) * J
+  auto phase_base = [&](int f) -> int64_t {
+    const int blk = f / nphase;
+    const int ph = f - blk * nphase;
+    return (int64_t)(j0 + blk * J) * 16 * rowb + ph * CG * 128;
+  };
+  // through a buffer resource based at the phase's data: the lane offset is one 32-bit VGPR
+  auto load_pieces = [&](u32x4_t (&v)[PPT], int f) {
+    const __amdgpu_buffer_rsrc_t rin = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(p.in + phase_base(f)), 0, 0x7fffffff, kBufferDword3);
+#pragma unroll
+    for (int j = 0; j < PPT; ++j)
+      v[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rin, rel[j], 0, 0));
+  };
+  auto store_pieces = [&](int buf, const u32x4_t (&v)[PPT]) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      sB[buf][poff[j]] = uint2{v[j][0], v[j][1]};
+      sB[buf][poff[j] + 8 * 16] = uint2{v[j][2], v[j][3]};
+    }
+  };
+
+  const size_t wgroup = (size_t)p.nq * 4 * 64;
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u32x4_t*>(p.wvals + (size_t)G0 * wgroup), 0, (int)(wgroup * sizeof(u32x4_t)), kBufferDword3);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(p.wmeta + (size_t)G0 * wgroup), 0, (int)(wgroup * sizeof(uint32_t)), kBufferDword3);
+  const int lv = lane * (int)sizeof(u32x4_t), lm = lane * 4;
+  auto load_a = [&](int c, u32x4_t (&av)[4], uint32_t (&ix)[4]) {
+    const int e = c * 4 * 64;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      av[a] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rv, lv + a * 64 * (int)sizeof(u32x4_t), e * (int)sizeof(u32x4_t), 0));
+      ix[a] = __builtin_amdgcn_raw_buffer_load_b32(rm, lm + a * 64 * 4, e * 4, 0);
+    }
+  };
+
+  float4_t acc[T][4];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) acc[t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  u32x4_t av[2][4];
+  uint32_t ix[2][4];
+  u32x4_t pst[2][PPT];  // pieces of phase f live in set f & 1 from their load to their store
+  if (nf > 0) {
+    load_a(0, av[0], ix[0]);
+    load_pieces(pst[0], 0);
+    store_pieces(0, pst[0]);
+    if (nf > 1) load_pieces(pst[1], 1);
+  }
+  __syncthreads();
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint2*)&sB[0][0] +
+                        (uint32_t)(g * 16 + col) * 8u;
+  const NeuronParams np = p.np;
+  // one phase; PAR = f & 1 (LDS buffer and piece set) is a compile-time constant
+  auto phase = [&](int f, auto par) {
+    constexpr int PAR = decltype(par)::value;
+    const int blk = f / nphase;
+    const int ph = f - blk * nphase;
+    if (f + 2 < nf) load_pieces(pst[PAR], f + 2);  // phase f's own pieces were stored already
+    const uint32_t lbase = lds0 + (uint32_t)PAR * (uint32_t)(CG * CE * 8);
+    constexpr int NSTEP = CG * T;
+    uint2 fr[2][4];
+    auto issue = [&](int step, uint2 (&fq)[4]) {
+      const int o = step * 256 * 8;
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[0]) : "v"(lbase), "i"(o));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[1]) : "v"(lbase), "i"(o + 8 * 16 * 8));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[2]) : "v"(lbase), "i"(o + 4 * 16 * 8));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[3]) : "v"(lbase), "i"(o + 12 * 16 * 8));
+    };
+    issue(0, fr[0]);
+#pragma unroll
+    for (int cc = 0; cc < CG; ++cc) {
+      const int c = ph * CG + cc;
+      const int ra = (CG % 2 == 0 ? cc : PAR + cc) & 1;  // chunk c uses set c & 1
+      if (c + 1 < p.nchunk) load_a(c + 1, av[ra ^ 1], ix[ra ^ 1]);
+      else if (f + 1 < nf) load_a(0, av[ra ^ 1], ix[ra ^ 1]);  // nchunk even: set 0, the next group
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int step = cc * T + t;
+        uint2(&fq)[4] = fr[step & 1];
+        if (step + 1 < NSTEP) {
+          issue(step + 1, fr[(step + 1) & 1]);
+          asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(fq[0]), "+v"(fq[1]), "+v"(fq[2]), "+v"(fq[3]) :: "memory");
+        } else {
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fq[0]), "+v"(fq[1]), "+v"(fq[2]), "+v"(fq[3]) :: "memory");
+        }
+        const half16_t bf = __builtin_bit_cast(
+            half16_t, u32x8_t{fq[0].x, fq[0].y, fq[1].x, fq[1].y, fq[2].x, fq[2].y, fq[3].x, fq[3].y});
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+          acc[t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(half8_t, av[ra][a]), bf, acc[t][a],
+                                                               (int)ix[ra][a], 0, 0);
+      }
+    }
+    if (f + 1 < nf) store_pieces(PAR ^ 1, pst[PAR ^ 1]);
+    __syncthreads();
+    if (ph == nphase - 1) {  // the group's reduction is complete
+      const int m = (j0 + blk * J) * 16 + col;
+      const int cl = wave * 64 + g * 16;
+      tile1ps_epilogue<MODE>(acc, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl], &sCoef[1][cl], p.out, p.M);
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) acc[t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  for (int f = 0; f < nf; f += 2) {
+    phase(f, std::integral_constant<int, 0>{});
+    if (f + 1 < nf) phase(f + 1, std::integral_constant<int, 1>{});
+  }
+}
+
+// Launch on `slots` resident workgroups (a multiple of the super-block count, at most one per
+// (group, super-block) pair).
+template <int NW, int CG>
+hipError_t launch_tile1ps(const TileParams& p, int mode, int slots, hipStream_t s) {
+  const int npg = p.M / 16;
+  const int nsb = p.F / (NW * 64);
+  int per = std::max(1, std::min(slots / nsb, npg));
+  const dim3 grid((unsigned)(per * nsb)), block(64 * NW);
+  if (mode == EPI_LIF_HARD)
+    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD>), grid, block, 0, s, p, npg, nsb);
+  else
+    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD>), grid, block, 0, s, p, npg, nsb);
+  return hipGetLastError();
+}
+
+}  // namespace sengine

@@ -4,6 +4,8 @@ Every case runs the reference PyTorch path (oracle.reference_path) on the CPU an
 HIP kernel through the C ABI on the same seeded inputs, then applies the acceptance
 rule of tests/parity.py.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -449,6 +451,30 @@ def test_tile1pm_f16_input(dev, C_in, C_out, H, W, stride, B, out_enc, traces):
                                   out_enc=out_enc, traces=traces)
     assert rep2.ok, str(rep2)
     assert torch.allclose(v_fin, r2.v_final, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("neuron", ["lif", "if"])
+@pytest.mark.parametrize("C_in,C_out,H,W,B", [(384, 512, 64, 40, 2), (128, 1024, 8, 16, 2), (128, 256, 4, 4, 1),
+                                             (384, 384, 64, 40, 2), (384, 1152, 4, 8, 1)])
+def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron):
+    """The persistent fp16-input 1x1 kernel (token Linears: stride 1, 16 | M, spike bits out,
+    stateless hard-reset neuron): 4-wave super-blocks with resident workgroups walking 1 or 2
+    position groups each (5,120 positions over 256 workgroups per super-block), a single group,
+    four super-blocks; 6-wave 384-channel super-blocks (phases of three chunks), one per CU
+    walking 1 or 2 groups, or three super-blocks; LIF and IF, against the oracle."""
+    spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
+                        neuron=neuron, in_enc=ops.ENC_F16)
+    plan = ops.fused_plan(spec)
+    nw, cg = (4, 2) if C_out % 256 == 0 else (6, 3)
+    assert plan.startswith(f"tile1ps<T=4,NW={nw},CG={cg},in=f16,out=bits,"), plan
+    print(plan)
+    case = ref.make_layer_case(260 + C_in // 64 + C_out // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=1,
+                               padding=0, fp16_weights=True, p_spike=0.2)
+    kw = dict(neuron="if", v_th=0.5, v_reset=0.0) if neuron == "if" else {}
+    rep, _, r, _ = run_case(dev, case, in_enc=ops.ENC_F16, traces=False, **kw)
+    print(rep, float(r.spikes.mean()))
+    assert rep.ok, str(rep)
+    assert float(r.spikes.mean()) > 0.002  # the comparison covers firing neurons
 
 
 @pytest.mark.parametrize("C_out", [384, 128])
