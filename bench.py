@@ -246,8 +246,8 @@ def cpu_baseline(budget_s=12.0, min_runs=CPU_MIN_RUNS):
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "fused_tile_kernel_cfg1_sweep_traffic.md")
 # the sources the sweep's kernels are built from (the halo-tiled fused kernel and its dispatch)
-SWEEP_KERNEL_SOURCES = ("common.h", "epilogue.h", "internal.h", "tile_kernel.h", "tile1pm.h", "fused_tile1.hip",
-                        "fused_tile3.hip", "fused_sparse.hip")
+SWEEP_KERNEL_SOURCES = ("common.h", "epilogue.h", "internal.h", "tile_kernel.h", "tile1pm.h", "tile1ps.h",
+                        "fused_tile1.hip", "fused_tile3.hip", "fused_sparse.hip")
 
 
 def kernel_source_hash() -> str:
@@ -570,8 +570,9 @@ def main():
             "frac": round(avg_flops / avg_launch / P_SPARSE, 4),
             "traffic": measured_traffic(),
             "traffic_algorithmic": round(sum(wk["bytes_min"] for wk in work) / len(work)),
-            "kernel": "sengine::fused_tile_kernel<T=4,...> (halo-tiled spike-bit kernel: 3x3 layers KS=3, "
-                      "the 1x1 layer KS=1; mean over all 15 sweep launches)",
+            "kernel": "sengine::fused_tile_kernel<T=4,KS=3,...> (halo-tiled spike-bit kernel, the 3x3 layers) and "
+                      "sengine::fused_tile1ps_kernel (persistent 1x1, the 256->1024 layer); mean over all 15 "
+                      "sweep launches",
             "avg_launch_us": round(avg_launch * 1e6, 3),
             "note": "dense-equivalent FLOPs vs the 5.0 PFLOP/s 2:4 peak == useful FLOPs vs the 2.5 PFLOP/s dense peak",
             "peak_measured": calib["smfmac_tflops_dense_equiv"],

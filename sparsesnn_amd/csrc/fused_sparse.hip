@@ -524,7 +524,8 @@ extern "C" int sengine_amd_fused_plan(const sengine_conv_lif_desc* d, int32_t fl
   if (plan.route == kRouteTiled) {
     const int choice = fused_kernel_choice();
     const bool shortcut_only = shortcut && !traces && !(flags & SENGINE_PLAN_SEW_ADD);
-    n = (choice == 0 || choice == 3) && tile_eligible(d) ? describe_tile(d, plan.geo, mode, shortcut_only, buf, len)
+    const FusedArgs fa{nz, nz, nz, state ? fz : nullptr, fz, fz, fz, traces ? fz : nullptr, traces ? fz : nullptr, sew};
+    n = (choice == 0 || choice == 3) && tile_eligible(d) ? describe_tile(d, plan.geo, mode, shortcut_only, fa, buf, len)
                                                          : describe_lds(d, plan.geo, mode, buf, len);
   } else if (plan.route == kRouteSmall) {
     n = snprintf(buf, len, "smallm<T=%d,planes=%d,out=%s,epi=%s,flat=%d>", d->T, d->weight_planes,

@@ -169,23 +169,33 @@ static int device_cus() {
   return cus[dev];
 }
 
-// The persistent fp16-input 1x1 kernel (tile1ps.h) serves the position-major fp16 case when the
-// layer is what it is written for: stride 1, T = 4, 16 | M, an even chunk count, spike-bit
-// output, a fast stateless neuron, no residual or traces; channels in 256-channel super-blocks
-// (4 waves, phases of 2 chunks) or 384-channel ones (6 waves, phases of 3 chunks, an even
-// phase count).  Returns the waves per workgroup, or 0.  SENGINE_AMD_TILE1_PS=0 turns it off.
-static int tile1ps_waves(const sengine_conv_lif_desc* d, const Geometry& geo, const TileChoice& c, int mode,
-                         const FusedArgs* a) {
+// The persistent 1x1 kernel (tile1ps.h) serves the token Linears when a layer is what it is
+// written for: stride 1, T = 4, 16 | M, an even chunk count, a fast stateless neuron, no trace,
+// state or bit-plane residual.  fp16 input with spike-bit output (q/k/v, fc1): 256-channel
+// super-blocks (4 waves, phases of 2 chunks) or 384-channel ones (6 waves, phases of 3 chunks,
+// an even phase count).  Spike-bit input with fp16 output, optionally + the fp16 residual (proj,
+// fc2) or spike bits (1x1 layers of convolutional networks): 384-channel super-blocks with
+// phases of 6 chunks, or 256-channel ones with 4.  SENGINE_AMD_TILE1_PS=0 turns it off.
+// Returns waves * 16 + chunks per phase, or 0.
+static int tile1ps_config(const sengine_conv_lif_desc* d, const Geometry& geo, const TileChoice& c, int mode,
+                          const FusedArgs* a) {
   const int nchunk = d->C_in / 64;
-  if (d->in_enc != SENGINE_ENC_F16 || c.k3 || !c.pm || d->T != 4 || d->stride_h != 1 || d->stride_w != 1 ||
-      geo.M % 16 != 0 || nchunk % 2 != 0 || d->out_enc != SENGINE_ENC_BITS ||
-      (mode != EPI_LIF_HARD && mode != EPI_IF_HARD))
+  const int env = env_int_now("SENGINE_AMD_TILE1_PS", -1);
+  if (env == 0 || c.k3 || d->T != 4 || d->stride_h != 1 || d->stride_w != 1 || d->weight_planes != 1 ||
+      geo.M % 16 != 0 || nchunk % 2 != 0 || (mode != EPI_LIF_HARD && mode != EPI_IF_HARD))
     return 0;
-  if ((int64_t)d->T * geo.M * d->C_in * 2 > 0x7fffffff) return 0;  // piece offsets are 32-bit
-  if (a && (a->state || a->sew.res || a->sew.res16 || a->sew.real_out || a->h_trace || a->x_trace)) return 0;
-  if (env_int_now("SENGINE_AMD_TILE1_PS", -1) == 0) return 0;
-  if (d->C_out % 256 == 0) return 4;
-  if (d->C_out % 384 == 0 && nchunk % 6 == 0) return 6;
+  if (a && (a->state || a->sew.res || a->sew.real_out || a->h_trace || a->x_trace)) return 0;
+  if (d->in_enc == SENGINE_ENC_F16) {
+    if (d->out_enc != SENGINE_ENC_BITS || !c.pm || (a && a->sew.res16)) return 0;
+    if ((int64_t)d->T * geo.M * d->C_in * 2 > 0x7fffffff) return 0;  // piece offsets are 32-bit
+    if (d->C_out % 256 == 0) return 4 * 16 + 2;
+    if (d->C_out % 384 == 0 && nchunk % 6 == 0) return 6 * 16 + 3;
+    return 0;
+  }
+  if (d->in_enc != SENGINE_ENC_BITS) return 0;
+  if (d->out_enc == SENGINE_ENC_BITS && a && a->sew.res16) return 0;
+  if (d->C_out % 384 == 0 && nchunk % 6 == 0) return 6 * 16 + 6;
+  if (d->C_out % 256 == 0 && nchunk % 4 == 0) return 4 * 16 + 4;
   return 0;
 }
 
@@ -193,8 +203,8 @@ static int tile1ps_waves(const sengine_conv_lif_desc* d, const Geometry& geo, co
 // CU, or one 6-wave workgroup (the waves of a second would not all find a SIMD).
 static int tile1ps_slots(int nw) { return device_cus() * (nw == 6 ? 1 : 2); }
 
-int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool shortcut_only, char* buf,
-                  size_t len) {
+int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool shortcut_only,
+                  const FusedArgs& a, char* buf, size_t len) {
   TileChoice c;
   if (!choose_tile(d, geo, c)) return snprintf(buf, len, "none (grid too large)");
   mode = tile_epilogue_mode(d, c, mode, shortcut_only);
@@ -205,11 +215,11 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
   // tile instances (every mode)
   const bool fast_f16out = f16in ? c.pm == 0 : (!c.k3 && d->T == 4 && c.pm == 0 && mode == EPI_LIF_HARD);
   const char* epi = d->out_enc == SENGINE_ENC_BITS || fast_f16out ? kEpi[mode] : "generic";
-  if (const int nw = f16in ? tile1ps_waves(d, geo, c, mode, nullptr) : 0) {
-    const int npg = (int)(geo.M / 16), nsb = d->C_out / (64 * nw);
-    const int per = std::max(1, std::min(tile1ps_slots(nw) / nsb, npg));
-    return snprintf(buf, len, "tile1ps<T=4,NW=%d,CG=%d,in=f16,out=%s,epi=%s> grid=%d (persistent, %d groups)", nw,
-                    nw == 6 ? 3 : 2, oe, epi, per * nsb, npg);
+  if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
+    const int nw = ps >> 4, npg = (int)(geo.M / 16), nsb = d->C_out / (64 * nw);
+    const int per = tile1ps_per(npg, nsb, tile1ps_slots(nw));
+    return snprintf(buf, len, "tile1ps<T=4,NW=%d,CG=%d,in=%s,out=%s,epi=%s> grid=%d (persistent, %d groups)", nw,
+                    ps & 15, f16in ? "f16" : "bits", oe, kEpi[mode], per * nsb, npg);
   }
   if (f16in && c.pm)
     return snprintf(buf, len, "tile1pm<T=4,GPW=1,CG=2,NW=%d,in=f16,out=%s,epi=%s> grid=%lld", c.pmw, oe, epi,
@@ -268,15 +278,23 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
       shortcut_only);
   if (d->in_enc == SENGINE_ENC_F16) {
     if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
-    if (const int nw = tile1ps_waves(d, geo, c, mode, &a))
-      return nw == 6 ? launch_tile1ps<6, 3>(p, mode, tile1ps_slots(6), stream)
-                     : launch_tile1ps<4, 2>(p, mode, tile1ps_slots(4), stream);
+    if (const int ps = tile1ps_config(d, geo, c, mode, &a))
+      return ps == 6 * 16 + 3 ? launch_tile1ps<6, 3, SENGINE_ENC_F16, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(6), stream)
+                              : launch_tile1ps<4, 2, SENGINE_ENC_F16, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(4), stream);
     if (c.pm)
       return c.pmw == 6 ? launch_tile1pm<4, 1, 2, 6, SENGINE_ENC_F16>(p, d->out_enc, mode, stream)
                         : launch_tile1pm<4, 1, 2, 4, SENGINE_ENC_F16>(p, d->out_enc, mode, stream);
     return launch_tile_f16in<1, 0, 0, 1>(p, d->out_enc, mode, stream);
   }
   if (c.k3) return launch_tile3(p, d->T, c.shape, c.gpw, c.ksplit, c.pf, d->out_enc, mode, stream);
+  if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
+    const int nw = ps >> 4;
+    if (d->out_enc == SENGINE_ENC_F16)
+      return nw == 6 ? launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_F16>(p, mode, tile1ps_slots(6), stream)
+                     : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_F16>(p, mode, tile1ps_slots(4), stream);
+    return nw == 6 ? launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(6), stream)
+                   : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(4), stream);
+  }
   if (c.pm == 2) return c.cg == 4 ? launch_tile1pm<4, 2, 4>(p, d->out_enc, mode, stream)
                                   : launch_tile1pm<4, 2, 2>(p, d->out_enc, mode, stream);
   if (c.pm == 1) return c.cg == 4 ? launch_tile1pm<4, 1, 4>(p, d->out_enc, mode, stream)

@@ -76,9 +76,10 @@ struct TileChoice {
 };
 bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice& c);
 
-// Human-readable names of the kernel instance a launch would run (snprintf semantics).
-int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool shortcut_only, char* buf,
-                  size_t len);
+// Human-readable names of the kernel instance a launch would run (snprintf semantics); `a`
+// carries which optional buffers (state, traces, residuals) the launch passes.
+int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool shortcut_only,
+                  const FusedArgs& a, char* buf, size_t len);
 int describe_lds(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len);
 
 // Kernel selection for the fused op with spike-bit input: 0 = automatic (the split-K

@@ -22,9 +22,14 @@
 //  * workgroup ids are remapped so the NW-wave super-blocks of the same position groups sit
 //    on one XCD (their shared fp16 rows are fetched into one L2).
 //
+// Spike-bit inputs (IN_ENC = SENGINE_ENC_BITS: the Linears fed by spikes, proj and fc2) stage
+// 8-byte words per (chunk, t, position) instead, expanded to fp16 into the same LDS layout, and
+// their outputs may be fp16 spikes plus the fp16 residual stream (the reference add kernel's
+// form, the transformer's residual).
+//
 // Restricted to what the token Linears need: T = 4, stride 1 (position m's input row is
-// t*M + m), M a multiple of 16, an even chunk count, spike-bit output, a hard-reset LIF or IF
-// without state or traces and no residual.
+// t*M + m), M a multiple of 16, an even chunk count, a hard-reset LIF or IF without state or
+// traces, spike bits out or fp16 spikes (+ an fp16 residual) out.
 #pragma once
 #include "tile1pm.h"
 
@@ -34,10 +39,10 @@ namespace sengine {
 // residual, reading the folded BN coefficients from LDS where they are used (16 registers
 // instead of 48 held across the timesteps: the persistent loop keeps the next group's operands
 // live meanwhile).
-template <int MODE>
+template <int MODE, int OUT_ENC>
 __device__ __forceinline__ void tile1ps_epilogue(const float4_t (&acc)[4][4], int m, int F, int cob,
                                                  const NeuronParams& np, const float* fsc, const float* fbi,
-                                                 uint8_t* __restrict__ out, int M) {
+                                                 uint8_t* __restrict__ out, int M, const SewAdd& sa) {
   constexpr int T = 4;
   float v[16];
 #pragma unroll
@@ -59,23 +64,32 @@ __device__ __forceinline__ void tile1ps_epilogue(const float4_t (&acc)[4][4], in
           fire_only(h, np.vth, word);
       }
     }
-    *reinterpret_cast<uint16_t*>(out + ((((size_t)t * M + m) * F + cob) >> 3)) = (uint16_t)word;
+    if (OUT_ENC == SENGINE_ENC_BITS) {
+      *reinterpret_cast<uint16_t*>(out + ((((size_t)t * M + m) * F + cob) >> 3)) = (uint16_t)word;
+    } else {
+      const uint32_t zr[kResWords] = {};
+      store_spike_f16(word, ((size_t)t * M + m) * F + cob, out, sa, zr);
+    }
   }
 }
 
-// CG: chunks per phase (2; or 3 for 6-wave super-blocks of 384 channels, whose 384 threads
-// then move four pieces each -- the host also requires an even phase count, so phase f and its
-// position in the group have the same parity).
-template <int NW, int CG, int MODE>
+// CG: chunks per phase, chosen so every thread stages the same number of items (fp16: 2, or
+// 3 for 6-wave super-blocks of 384 channels -- the host then also requires an even phase count,
+// so phase f and its position in the group have the same parity; bits: as many chunks as waves).
+template <int NW, int CG, int MODE, int IN_ENC, int OUT_ENC>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   constexpr int T = 4;
   constexpr int NTH = 64 * NW;
-  constexpr int CE = T * 16 * 16;              // LDS entries (8 bytes) per staged chunk
-  constexpr int PIECES = CG * T * 16 * 8;      // 16-byte pieces per phase
-  constexpr int PPT = (PIECES + NTH - 1) / NTH;
+  constexpr int CE = T * 16 * 16;  // LDS entries (8 bytes) per staged chunk
+  constexpr bool F16IN = IN_ENC == SENGINE_ENC_F16;
+  // staged items per phase: 16-byte fp16 pieces, or 8-byte spike words of (chunk, t, position)
+  constexpr int ITEMS = F16IN ? CG * T * 16 * 8 : CG * T * 16;
+  constexpr int PPT = ITEMS / NTH;
+  constexpr int CHB = F16IN ? 128 : 8;  // bytes of one 64-channel chunk in an input row
+  using Item = std::conditional_t<F16IN, u32x4_t, uint2>;
   static_assert(MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD, "fast stateless modes only");
-  static_assert(PIECES % NTH == 0, "every thread moves the same number of pieces");
+  static_assert(ITEMS % NTH == 0, "every thread stages the same number of items");
   __shared__ uint2 sB[2][CG * CE];
   __shared__ float sCoef[2][NW * 64];
 
@@ -102,18 +116,18 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
     sCoef[1][i] = fold ? bi * p.np.rtau : bi;
   }
 
-  // piece q = tid + j*NTH of a phase is piece q & 7 of unit (cc, t, pos) = q >> 3; its fp16
-  // row is t*M + m0 + pos, its bytes cc*128 + (q & 7)*16 of the phase's 256-byte span
-  const int64_t rowb = (int64_t)p.C * 2;  // bytes per input row
+  // fp16: piece q = tid + j*NTH of a phase is piece q & 7 of unit (cc, t, pos) = q >> 3, at
+  // bytes cc*128 + (q & 7)*16 of row t*M + m0 + pos; bits: unit u = tid + j*NTH, at bytes cc*8
+  const int64_t rowb = F16IN ? (int64_t)p.C * 2 : (int64_t)(p.C >> 3);  // bytes per input row
   int rel[PPT], poff[PPT];
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
     const int q = tid + j * NTH;
-    const int u = q >> 3, i = q & 7;
+    const int u = F16IN ? q >> 3 : q, i = F16IN ? q & 7 : 0;
     const int pos = u & 15;
     const int t = (u >> 4) & (T - 1);
     const int cc = u >> 6;
-    rel[j] = (int)(((int64_t)t * p.M + pos) * rowb) + cc * 128 + i * 16;
+    rel[j] = (int)(((int64_t)t * p.M + pos) * rowb) + cc * CHB + i * 16;
     poff[j] = (cc * T + t) * 256 + pos + i * 16;
   }
   const int nphase = p.nchunk / CG;
@@ -122,21 +136,35 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   auto phase_base = [&](int f) -> int64_t {
     const int blk = f / nphase;
     const int ph = f - blk * nphase;
-    return (int64_t)(j0 + blk * J) * 16 * rowb + ph * CG * 128;
+    return (int64_t)(j0 + blk * J) * 16 * rowb + ph * CG * CHB;
   };
   // through a buffer resource based at the phase's data: the lane offset is one 32-bit VGPR
-  auto load_pieces = [&](u32x4_t (&v)[PPT], int f) {
+  auto load_pieces = [&](Item (&v)[PPT], int f) {
     const __amdgpu_buffer_rsrc_t rin = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(p.in + phase_base(f)), 0, 0x7fffffff, kBufferDword3);
 #pragma unroll
-    for (int j = 0; j < PPT; ++j)
-      v[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rin, rel[j], 0, 0));
+    for (int j = 0; j < PPT; ++j) {
+      if constexpr (F16IN)
+        v[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rin, rel[j], 0, 0));
+      else
+        v[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rin, rel[j], 0, 0));
+    }
   };
-  auto store_pieces = [&](int buf, const u32x4_t (&v)[PPT]) {
+  auto store_pieces = [&](int buf, const Item (&v)[PPT]) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      sB[buf][poff[j]] = uint2{v[j][0], v[j][1]};
-      sB[buf][poff[j] + 8 * 16] = uint2{v[j][2], v[j][3]};
+      if constexpr (F16IN) {
+        sB[buf][poff[j]] = uint2{v[j][0], v[j][1]};
+        sB[buf][poff[j] + 8 * 16] = uint2{v[j][2], v[j][3]};
+      } else {
+        u32x4_t pc[8];
+        expand_word64(v[j], pc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // piece i: half-pieces i (channels 8i..8i+3) and 8 + i (8i+4..8i+7)
+          sB[buf][poff[j] + i * 16] = uint2{pc[i][0], pc[i][1]};
+          sB[buf][poff[j] + (8 + i) * 16] = uint2{pc[i][2], pc[i][3]};
+        }
+      }
     }
   };
 
@@ -164,7 +192,7 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
 
   u32x4_t av[2][4];
   uint32_t ix[2][4];
-  u32x4_t pst[2][PPT];  // pieces of phase f live in set f & 1 from their load to their store
+  Item pst[2][PPT];  // items of phase f live in set f & 1 from their load to their store
   if (nf > 0) {
     load_a(0, av[0], ix[0]);
     load_pieces(pst[0], 0);
@@ -222,7 +250,8 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
     if (ph == nphase - 1) {  // the group's reduction is complete
       const int m = (j0 + blk * J) * 16 + col;
       const int cl = wave * 64 + g * 16;
-      tile1ps_epilogue<MODE>(acc, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl], &sCoef[1][cl], p.out, p.M);
+      tile1ps_epilogue<MODE, OUT_ENC>(acc, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl], &sCoef[1][cl], p.out, p.M,
+                                      p.sew);
 #pragma unroll
       for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -235,18 +264,26 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   }
 }
 
-// Launch on `slots` resident workgroups (a multiple of the super-block count, at most one per
-// (group, super-block) pair).
-template <int NW, int CG>
+// Workgroups per super-block on `slots` resident workgroups: as few as give every workgroup the
+// same number of groups (up to one) as the most loaded one would have anyway.
+inline int tile1ps_per(int npg, int nsb, int slots) {
+  const int most = std::max(1, std::min(slots / nsb, npg));
+  const int rounds = (npg + most - 1) / most;
+  return (npg + rounds - 1) / rounds;
+}
+
+// Launch on at most `slots` resident workgroups (a multiple of the super-block count, at most
+// one per (group, super-block) pair).
+template <int NW, int CG, int IN_ENC, int OUT_ENC>
 hipError_t launch_tile1ps(const TileParams& p, int mode, int slots, hipStream_t s) {
   const int npg = p.M / 16;
   const int nsb = p.F / (NW * 64);
-  int per = std::max(1, std::min(slots / nsb, npg));
+  const int per = tile1ps_per(npg, nsb, slots);
   const dim3 grid((unsigned)(per * nsb)), block(64 * NW);
   if (mode == EPI_LIF_HARD)
-    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD>), grid, block, 0, s, p, npg, nsb);
+    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC>), grid, block, 0, s, p, npg, nsb);
   else
-    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD>), grid, block, 0, s, p, npg, nsb);
+    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD, IN_ENC, OUT_ENC>), grid, block, 0, s, p, npg, nsb);
   return hipGetLastError();
 }
 

@@ -9,9 +9,10 @@ sengine_amd_fused_plan); the oracle is the restated reference PyTorch path
 (oracle.reference_path: models/layers.py:26-31 conv + eval BN, models/neurons.py:121-146
 LIF).  Per case:
   * spikes of the bench call against the oracle under the acceptance rule of tests/parity.py;
-  * a second call with a zeroed state buffer (same instance, membrane written back): spikes
-    bit-identical to the first call, final membranes within 1e-3 relative of the oracle's
-    wherever the spike history agrees;
+  * a second call with a zeroed state buffer (same instance for the 3x3 layers; for the 1x1 the
+    position-major kernel, the persistent one having no state epilogue), membrane written back:
+    spikes bit-identical to the first call, final membranes within 1e-3 relative of the
+    oracle's wherever the spike history agrees;
   * the same launch at V_th = 0.25, where far more neurons fire (the config's own threshold
     leaves ~0.5 % of outputs spiking), against the oracle on the same conv output.
 """
@@ -48,9 +49,13 @@ def test_cfg1_layer_full_size(dev, C_in, C_out, H, W, k, p_spike):
                         neuron="lif", tau=2.0, v_threshold=1.0, v_reset=0.0)
     plan = ops.fused_plan(spec)
     print(f"{C_in}->{C_out} {H}x{W} k{k} p{p_spike}: {plan}", flush=True)
-    assert plan.startswith(("tile<T=4,", "tile1pm<T=4,")), plan
+    assert plan.startswith(("tile<T=4,", "tile1ps<T=4,")), plan
     assert "epi=lif_hard" in plan and "out=bits" in plan, plan
-    assert ops.fused_plan(spec, state=True).split(" ")[0] == plan.split(" ")[0]
+    plan_st = ops.fused_plan(spec, state=True)
+    if k == 3:
+        assert plan_st.split(" ")[0] == plan.split(" ")[0]
+    else:  # the persistent 1x1 kernel has no state epilogue: the state call runs the position-major one
+        assert plan_st.startswith("tile1pm<T=4,"), plan_st
 
     OH, OW, M, _ = ops.geometry(spec)
     values, meta, _ = ops.compress_2_4(spec, case.w.to(dev))

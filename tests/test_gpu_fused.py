@@ -477,6 +477,55 @@ def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron):
     assert float(r.spikes.mean()) > 0.002  # the comparison covers firing neurons
 
 
+@pytest.mark.parametrize("C_in,C_out,H,W,B,mode", [(768, 384, 64, 40, 2, "res16"), (256, 512, 32, 32, 2, "f16"),
+                                                    (384, 384, 48, 32, 1, "res16"), (256, 1024, 16, 16, 2, "bits")])
+def test_tile1ps_bits_input(dev, C_in, C_out, H, W, B, mode):
+    """The persistent 1x1 kernel on spike bits (the token Linears fed by spikes: proj, fc2):
+    fp16 spikes + the fp16 residual stream out (6-wave 384-channel super-blocks with phases of
+    six chunks, one per CU walking 1 or 2 of 320 position groups, or one group each), plain fp16
+    spikes (4-wave super-blocks, phases of four chunks), and spike bits out (the opt-in
+    SENGINE_AMD_TILE1_PS=2), against the oracle."""
+    T = 4
+    out_enc = ops.ENC_BITS if mode == "bits" else ops.ENC_F16
+    spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
+                        out_enc=out_enc)
+    if mode == "bits":
+        os.environ["SENGINE_AMD_TILE1_PS"] = "2"
+    try:
+        plan = ops.fused_plan(spec)
+        nw, cg = (6, 6) if C_out % 384 == 0 else (4, 4)
+        assert plan.startswith(f"tile1ps<T=4,NW={nw},CG={cg},in=bits,out={'bits' if mode == 'bits' else 'f16'},"), plan
+        print(plan)
+        case = ref.make_layer_case(270 + C_in // 64 + C_out // 64, T=T, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=1,
+                                   padding=0, fp16_weights=True, p_spike=0.15)
+        values, meta, _ = ops.compress_2_4(spec, case.w.to(dev))
+        sc, bi = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
+        sc_d, bi_d = torch.from_numpy(sc).to(dev), torch.from_numpy(bi).to(dev)
+        data = torch.from_numpy(pk.seq_to_nhwc_bits(case.x_seq.numpy()).view(np.int32)).to(dev)
+        r = ref.fused_layer(case.x_seq, case.w, case.bn, 1, 0, 1, "lif", 2.0, 1.0, 0.0)
+        if mode == "res16":
+            g = torch.Generator().manual_seed(C_out)
+            res_int = torch.randint(0, 18, (T * B, H, W, C_out), generator=g)
+            out = ops.fused_sparse_conv_bn_lif_add(spec, data, values, meta, sc_d, bi_d, res_int.half().to(dev), 0, 0)
+            torch.cuda.synchronize()
+            spk = out.float().cpu() - res_int.float()
+        else:
+            out = ops.fused_sparse_conv_bn_lif(spec, data, values, meta, sc_d, bi_d)
+            torch.cuda.synchronize()
+            if mode == "bits":
+                spk = torch.from_numpy(pk.unpack_bits(out.cpu().numpy().view(np.uint32).reshape(-1, C_out // 32),
+                                                      C_out).reshape(T * B, H, W, C_out)).float()
+            else:
+                spk = out.float().cpu()
+        assert set(np.unique(spk.numpy())) <= {0.0, 1.0}
+        rep = compare(nhwc_seq(spk, T), None, r.spikes.numpy(), r.h.numpy(), 1.0)
+        print(rep, float(r.spikes.mean()))
+        assert rep.ok, str(rep)
+        assert float(r.spikes.mean()) > 0.002
+    finally:
+        os.environ.pop("SENGINE_AMD_TILE1_PS", None)
+
+
 @pytest.mark.parametrize("C_out", [384, 128])
 def test_fp16_residual_stream_add(dev, C_out):
     """out = spike + residual as fp16 (the reference add kernel's form) with an fp16 residual
