@@ -201,7 +201,30 @@ static int tile1ps_config(const sengine_conv_lif_desc* d, const Geometry& geo, c
 
 // Resident workgroups of the persistent kernel (two waves per SIMD): two 4-wave workgroups per
 // CU, or one 6-wave workgroup (the waves of a second would not all find a SIMD).
-static int tile1ps_slots(int nw) { return device_cus() * (nw == 6 ? 1 : 2); }
+static int tile1ps_slots(int nw) {
+  const int n = env_int_now("SENGINE_AMD_PS_SLOTS", 0);
+  return n > 0 ? n : device_cus() * (nw == 6 ? 1 : 2);
+}
+
+// The persistent 3x3 kernel (tile3ps.h) takes the tile launches it is written for: T = 4, spike
+// bits in and out, one channel group per wave, no reduction split, one-tap prefetch, a fast
+// stateless neuron, no trace, state or residual, and at least two tiles per resident workgroup
+// (three per CU).  SENGINE_AMD_TILE3_PS=0 turns it off, =2 lifts the two-tile rule.
+// SENGINE_AMD_PS_SLOTS=n launches the persistent kernels on n workgroups instead (tests use it
+// to make small layers walk several tiles or groups per workgroup).
+static int ps_slots_override() { return env_int_now("SENGINE_AMD_PS_SLOTS", 0); }
+static int tile3ps_slots() { return ps_slots_override() > 0 ? ps_slots_override() : device_cus() * 3; }
+static bool tile3ps_eligible(const sengine_conv_lif_desc* d, const TileChoice& c, int mode, const FusedArgs* a) {
+  if (!c.k3 || d->T != 4 || d->in_enc != SENGINE_ENC_BITS || d->out_enc != SENGINE_ENC_BITS || c.gpw != 1 ||
+      c.ksplit != 1 || c.pf != 1 || (mode != EPI_LIF_HARD && mode != EPI_IF_HARD))
+    return false;
+  // at least two tiles per resident workgroup: with fewer, the hardware's dispatch of a partial
+  // second round of one-tile workgroups balances the CUs better than a fixed assignment (measured)
+  const int env = env_int_now("SENGINE_AMD_TILE3_PS", -1);
+  if (env == 0 || (env != 2 && (int64_t)c.ntiles * (d->C_out / 64) < 2LL * tile3ps_slots())) return false;
+  if (a && (a->state || a->sew.res || a->sew.res16 || a->sew.real_out || a->h_trace || a->x_trace)) return false;
+  return true;
+}
 
 int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool shortcut_only,
                   const FusedArgs& a, char* buf, size_t len) {
@@ -232,6 +255,13 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
     }
     return snprintf(buf, len, "tile<T=4,KS=1,GPW=1,in=f16,out=%s,epi=%s> grid=%lld", oe, epi,
                     (long long)c.ntiles * (d->C_out / 64));
+  }
+  if (c.k3 && tile3ps_eligible(d, c, mode, &a)) {
+    const TileShape s = kShapes3[c.shape];
+    const int ncb = d->C_out / 64;
+    const int per = std::max(1, std::min(tile3ps_slots() / ncb, c.ntiles));
+    return snprintf(buf, len, "tile3ps<T=4,TR=%d,TC=%d,GR=%d,out=bits,epi=%s> grid=%d (persistent, %d tiles)", s.TR,
+                    s.TC, s.GR, kEpi[mode], per * ncb, c.ntiles);
   }
   if (c.k3) {
     const TileShape s = kShapes3[c.shape];
@@ -286,6 +316,7 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
                         : launch_tile1pm<4, 1, 2, 4, SENGINE_ENC_F16>(p, d->out_enc, mode, stream);
     return launch_tile_f16in<1, 0, 0, 1>(p, d->out_enc, mode, stream);
   }
+  if (c.k3 && tile3ps_eligible(d, c, mode, &a)) return launch_tile3_persistent(p, c.shape, mode, tile3ps_slots(), stream);
   if (c.k3) return launch_tile3(p, d->T, c.shape, c.gpw, c.ksplit, c.pf, d->out_enc, mode, stream);
   if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
     const int nw = ps >> 4;

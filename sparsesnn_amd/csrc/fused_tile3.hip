@@ -1,5 +1,6 @@
 // Instantiations of the tile kernel (tile_kernel.h) for 3x3 / stride 1 / pad 1 convolutions.
 #include "tile_kernel.h"
+#include "tile3ps.h"
 
 namespace sengine {
 
@@ -36,6 +37,12 @@ hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int kspl
     default:
       return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_tile3_persistent(const TileParams& p, int shape, int mode, int slots, hipStream_t s) {
+  if (shape == 1) return launch_tile3ps<14, 4, 8>(p, mode, slots, s);
+  if (shape == 2) return launch_tile3ps<7, 7, 7>(p, mode, slots, s);
+  return launch_tile3ps<8, 8, 8>(p, mode, slots, s);
 }
 
 hipError_t launch_tile3_f16in(const TileParams& p, int shape, int out_enc, int mode, hipStream_t s) {

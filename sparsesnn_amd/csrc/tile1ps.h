@@ -264,16 +264,12 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   }
 }
 
-// Workgroups per super-block on `slots` resident workgroups: as few as give every workgroup the
-// same number of groups (up to one) as the most loaded one would have anyway.
-inline int tile1ps_per(int npg, int nsb, int slots) {
-  const int most = std::max(1, std::min(slots / nsb, npg));
-  const int rounds = (npg + most - 1) / most;
-  return (npg + rounds - 1) / rounds;
-}
+// Workgroups per super-block on `slots` resident workgroups (every slot: with fewer, the CUs
+// left with an extra workgroup would carry more groups than any CU does otherwise).
+inline int tile1ps_per(int npg, int nsb, int slots) { return std::max(1, std::min(slots / nsb, npg)); }
 
-// Launch on at most `slots` resident workgroups (a multiple of the super-block count, at most
-// one per (group, super-block) pair).
+// Launch on `slots` resident workgroups (a multiple of the super-block count, at most one per
+// (group, super-block) pair).
 template <int NW, int CG, int IN_ENC, int OUT_ENC>
 hipError_t launch_tile1ps(const TileParams& p, int mode, int slots, hipStream_t s) {
   const int npg = p.M / 16;

@@ -530,5 +530,7 @@ hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int kspl
 hipError_t launch_tile1(const TileParams& p, int T, int gpw, int out_enc, int mode, hipStream_t s);
 // fp16 input (T = 4): the 3x3 tile shapes (fused_tile3.hip), the 1x1 tile kernel (fused_tile1.hip)
 hipError_t launch_tile3_f16in(const TileParams& p, int shape, int out_enc, int mode, hipStream_t s);
+// The persistent 3x3 form (tile3ps.h) of a tile shape, on `slots` resident workgroups.
+hipError_t launch_tile3_persistent(const TileParams& p, int shape, int mode, int slots, hipStream_t s);
 
 }  // namespace sengine

@@ -454,27 +454,64 @@ def test_tile1pm_f16_input(dev, C_in, C_out, H, W, stride, B, out_enc, traces):
 
 
 @pytest.mark.parametrize("neuron", ["lif", "if"])
+@pytest.mark.parametrize("shape,C_in,C_out,H,W,B,slots", [("0", 64, 64, 13, 11, 2, 5), ("1", 128, 128, 15, 9, 3, 8),
+                                                         ("2", 192, 64, 7, 7, 4, 3), ("0", 64, 192, 17, 8, 2, 7)])
+def test_tile3ps_walks(dev, shape, C_in, C_out, H, W, B, slots, neuron):
+    """The persistent 3x3 kernel (tile3ps.h), forced onto small layers (SENGINE_AMD_TILE3_PS=2)
+    with few resident workgroups (SENGINE_AMD_PS_SLOTS) so each walks several ragged tiles: one,
+    two and three reduction chunks, one and three channel blocks, every tile shape, LIF and IF,
+    against the oracle."""
+    os.environ.update(SENGINE_AMD_TILE3_PS="2", SENGINE_AMD_PS_SLOTS=str(slots), SENGINE_AMD_TILE_SHAPE=shape,
+                      SENGINE_AMD_TILE_PF="1", SENGINE_AMD_TILE_KSPLIT="1")
+    ops.set_fused_kernel("tile")
+    try:
+        spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=3, KW=3, stride=1, padding=1,
+                            neuron=neuron)
+        plan = ops.fused_plan(spec)
+        assert plan.startswith("tile3ps<T=4,"), plan
+        print(plan)
+        case = ref.make_layer_case(280 + C_in // 64 + C_out // 64 + H, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W,
+                                   k=3, fp16_weights=True, p_spike=0.25)
+        kw = dict(neuron="if", v_th=0.5, v_reset=0.0) if neuron == "if" else {}
+        rep, _, r, _ = run_case(dev, case, traces=False, **kw)
+        print(rep, float(r.spikes.mean()))
+        assert rep.ok, str(rep)
+        assert float(r.spikes.mean()) > 0.002
+    finally:
+        for k in ("SENGINE_AMD_TILE3_PS", "SENGINE_AMD_PS_SLOTS", "SENGINE_AMD_TILE_SHAPE", "SENGINE_AMD_TILE_PF",
+                  "SENGINE_AMD_TILE_KSPLIT"):
+            os.environ.pop(k, None)
+        ops.set_fused_kernel("auto")
+
+
+@pytest.mark.parametrize("slots", [0, 3])
+@pytest.mark.parametrize("neuron", ["lif", "if"])
 @pytest.mark.parametrize("C_in,C_out,H,W,B", [(384, 512, 64, 40, 2), (128, 1024, 8, 16, 2), (128, 256, 4, 4, 1),
                                              (384, 384, 64, 40, 2), (384, 1152, 4, 8, 1)])
-def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron):
+def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron, slots):
     """The persistent fp16-input 1x1 kernel (token Linears: stride 1, 16 | M, spike bits out,
     stateless hard-reset neuron): 4-wave super-blocks with resident workgroups walking 1 or 2
     position groups each (5,120 positions over 256 workgroups per super-block), a single group,
     four super-blocks; 6-wave 384-channel super-blocks (phases of three chunks), one per CU
     walking 1 or 2 groups, or three super-blocks; LIF and IF, against the oracle."""
-    spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
-                        neuron=neuron, in_enc=ops.ENC_F16)
-    plan = ops.fused_plan(spec)
-    nw, cg = (4, 2) if C_out % 256 == 0 else (6, 3)
-    assert plan.startswith(f"tile1ps<T=4,NW={nw},CG={cg},in=f16,out=bits,"), plan
-    print(plan)
-    case = ref.make_layer_case(260 + C_in // 64 + C_out // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=1,
-                               padding=0, fp16_weights=True, p_spike=0.2)
-    kw = dict(neuron="if", v_th=0.5, v_reset=0.0) if neuron == "if" else {}
-    rep, _, r, _ = run_case(dev, case, in_enc=ops.ENC_F16, traces=False, **kw)
-    print(rep, float(r.spikes.mean()))
-    assert rep.ok, str(rep)
-    assert float(r.spikes.mean()) > 0.002  # the comparison covers firing neurons
+    if slots:  # few resident workgroups: every one walks many groups
+        os.environ["SENGINE_AMD_PS_SLOTS"] = str(slots)
+    try:
+        spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
+                            neuron=neuron, in_enc=ops.ENC_F16)
+        plan = ops.fused_plan(spec)
+        nw, cg = (4, 2) if C_out % 256 == 0 else (6, 3)
+        assert plan.startswith(f"tile1ps<T=4,NW={nw},CG={cg},in=f16,out=bits,"), plan
+        print(plan)
+        case = ref.make_layer_case(260 + C_in // 64 + C_out // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=1,
+                                   padding=0, fp16_weights=True, p_spike=0.2)
+        kw = dict(neuron="if", v_th=0.5, v_reset=0.0) if neuron == "if" else {}
+        rep, _, r, _ = run_case(dev, case, in_enc=ops.ENC_F16, traces=False, **kw)
+        print(rep, float(r.spikes.mean()))
+        assert rep.ok, str(rep)
+        assert float(r.spikes.mean()) > 0.002  # the comparison covers firing neurons
+    finally:
+        os.environ.pop("SENGINE_AMD_PS_SLOTS", None)
 
 
 @pytest.mark.parametrize("C_in,C_out,H,W,B,mode", [(768, 384, 64, 40, 2, "res16"), (256, 512, 32, 32, 2, "f16"),
