@@ -193,6 +193,45 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
   }
 }
 
+// The stateless hard-reset epilogue of fast_epilogue_stateless (T = 4) with spike bits, or fp16
+// spikes plus an fp16 residual, out, reading the folded BN coefficients from LDS where they are
+// used (16 registers instead of 48 held across the timesteps: the persistent kernels keep the
+// next step's operands live meanwhile).  Lanes with `valid` false compute but store nothing.
+template <int MODE, int OUT_ENC>
+__device__ __forceinline__ void lean_epilogue_stateless(const float4_t (&acc)[4][4], bool valid, int m, int F, int cob,
+                                                 const NeuronParams& np, const float* fsc, const float* fbi,
+                                                 uint8_t* __restrict__ out, int M, const SewAdd& sa) {
+  constexpr int T = 4;
+  float v[16];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j4 = 12; j4 >= 0; j4 -= 4) {
+      const float4_t s4 = *reinterpret_cast<const float4_t*>(fsc + j4);
+      const float4_t b4 = *reinterpret_cast<const float4_t*>(fbi + j4);
+#pragma unroll
+      for (int e = 3; e >= 0; --e) {
+        const int j = j4 + e;
+        const float xin = __builtin_fmaf(acc[t][j >> 2][j & 3], s4[e], b4[e]);
+        const float h = t == 0 ? xin
+                               : (MODE == EPI_LIF_HARD ? __builtin_fmaf(v[j], np.decay, xin) : __fadd_rn(v[j], xin));
+        if (t + 1 < T)
+          fire_hard(h, np.vth, np.vreset, v[j], word);
+        else
+          fire_only(h, np.vth, word);
+      }
+    }
+    if (!valid) continue;
+    if (OUT_ENC == SENGINE_ENC_BITS) {
+      *reinterpret_cast<uint16_t*>(out + ((((size_t)t * M + m) * F + cob) >> 3)) = (uint16_t)word;
+    } else {
+      const uint32_t zr[kResWords] = {};
+      store_spike_f16(word, ((size_t)t * M + m) * F + cob, out, sa, zr);
+    }
+  }
+}
+
 // 4x4 transpose of 16-byte chunks across the four 16-lane rows of a wave: afterwards chunk q of
 // row r holds what chunk r of row q held (rows r = lane / 16).  Two v_permlane32_swap and two
 // v_permlane16_swap (gfx950) per dword position; every lane of the wave must execute it.

@@ -323,8 +323,10 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
     if (d->out_enc == SENGINE_ENC_F16)
       return nw == 6 ? launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_F16>(p, mode, tile1ps_slots(6), stream)
                      : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_F16>(p, mode, tile1ps_slots(4), stream);
-    return nw == 6 ? launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(6), stream)
-                   : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(4), stream);
+    if (nw == 6) return launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(6), stream);
+    // one 4-chunk phase (C_in = 256): the A operands stay resident
+    return p.nchunk == 4 ? launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_BITS, 1>(p, mode, tile1ps_slots(4), stream)
+                         : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(4), stream);
   }
   if (c.pm == 2) return c.cg == 4 ? launch_tile1pm<4, 2, 4>(p, d->out_enc, mode, stream)
                                   : launch_tile1pm<4, 2, 2>(p, d->out_enc, mode, stream);

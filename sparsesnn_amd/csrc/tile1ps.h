@@ -35,48 +35,14 @@
 
 namespace sengine {
 
-// The stateless hard-reset epilogue of fast_epilogue_stateless with spike-bit output and no
-// residual, reading the folded BN coefficients from LDS where they are used (16 registers
-// instead of 48 held across the timesteps: the persistent loop keeps the next group's operands
-// live meanwhile).
-template <int MODE, int OUT_ENC>
-__device__ __forceinline__ void tile1ps_epilogue(const float4_t (&acc)[4][4], int m, int F, int cob,
-                                                 const NeuronParams& np, const float* fsc, const float* fbi,
-                                                 uint8_t* __restrict__ out, int M, const SewAdd& sa) {
-  constexpr int T = 4;
-  float v[16];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int j4 = 12; j4 >= 0; j4 -= 4) {
-      const float4_t s4 = *reinterpret_cast<const float4_t*>(fsc + j4);
-      const float4_t b4 = *reinterpret_cast<const float4_t*>(fbi + j4);
-#pragma unroll
-      for (int e = 3; e >= 0; --e) {
-        const int j = j4 + e;
-        const float xin = __builtin_fmaf(acc[t][j >> 2][j & 3], s4[e], b4[e]);
-        const float h = t == 0 ? xin
-                               : (MODE == EPI_LIF_HARD ? __builtin_fmaf(v[j], np.decay, xin) : __fadd_rn(v[j], xin));
-        if (t + 1 < T)
-          fire_hard(h, np.vth, np.vreset, v[j], word);
-        else
-          fire_only(h, np.vth, word);
-      }
-    }
-    if (OUT_ENC == SENGINE_ENC_BITS) {
-      *reinterpret_cast<uint16_t*>(out + ((((size_t)t * M + m) * F + cob) >> 3)) = (uint16_t)word;
-    } else {
-      const uint32_t zr[kResWords] = {};
-      store_spike_f16(word, ((size_t)t * M + m) * F + cob, out, sa, zr);
-    }
-  }
-}
-
 // CG: chunks per phase, chosen so every thread stages the same number of items (fp16: 2, or
 // 3 for 6-wave super-blocks of 384 channels -- the host then also requires an even phase count,
 // so phase f and its position in the group have the same parity; bits: as many chunks as waves).
-template <int NW, int CG, int MODE, int IN_ENC, int OUT_ENC>
+//
+// ARES = 1 (spike-bit input whose whole reduction is one phase, nchunk == CG == 4): the wave's
+// A operands for all chunks (80 registers) are loaded once and stay resident, since its channel
+// block never changes; the loop then issues no A-operand loads at all.
+template <int NW, int CG, int MODE, int IN_ENC, int OUT_ENC, int ARES = 0>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   constexpr int T = 4;
@@ -190,11 +156,18 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
 #pragma unroll
     for (int a = 0; a < 4; ++a) acc[t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  u32x4_t av[2][4];
-  uint32_t ix[2][4];
+  static_assert(ARES == 0 || (CG == 4 && !F16IN), "resident A operands: one 4-chunk phase of spike bits");
+  constexpr int NAS = ARES ? CG : 2;  // A-operand sets: resident chunks, or the two-set ring
+  u32x4_t av[NAS][4];
+  uint32_t ix[NAS][4];
   Item pst[2][PPT];  // items of phase f live in set f & 1 from their load to their store
   if (nf > 0) {
-    load_a(0, av[0], ix[0]);
+    if (ARES) {
+#pragma unroll
+      for (int c = 0; c < NAS; ++c) load_a(c, av[c], ix[c]);
+    } else {
+      load_a(0, av[0], ix[0]);
+    }
     load_pieces(pst[0], 0);
     store_pieces(0, pst[0]);
     if (nf > 1) load_pieces(pst[1], 1);
@@ -209,7 +182,6 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
     constexpr int PAR = decltype(par)::value;
     const int blk = f / nphase;
     const int ph = f - blk * nphase;
-    if (f + 2 < nf) load_pieces(pst[PAR], f + 2);  // phase f's own pieces were stored already
     const uint32_t lbase = lds0 + (uint32_t)PAR * (uint32_t)(CG * CE * 8);
     constexpr int NSTEP = CG * T;
     uint2 fr[2][4];
@@ -224,9 +196,16 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
 #pragma unroll
     for (int cc = 0; cc < CG; ++cc) {
       const int c = ph * CG + cc;
-      const int ra = (CG % 2 == 0 ? cc : PAR + cc) & 1;  // chunk c uses set c & 1
-      if (c + 1 < p.nchunk) load_a(c + 1, av[ra ^ 1], ix[ra ^ 1]);
-      else if (f + 1 < nf) load_a(0, av[ra ^ 1], ix[ra ^ 1]);  // nchunk even: set 0, the next group
+      // chunk c uses set c & 1 (ring), or set cc (resident)
+      const int ra = ARES ? cc : (CG % 2 == 0 ? cc : PAR + cc) & 1;
+      if (!ARES) {
+        if (c + 1 < p.nchunk) load_a(c + 1, av[ra ^ 1], ix[ra ^ 1]);
+        else if (f + 1 < nf) load_a(0, av[ra ^ 1], ix[ra ^ 1]);  // nchunk even: set 0, the next group
+      }
+      // Phase f + 2's items go out after this phase's last A-operand load: vector memory counts
+      // complete in issue order, so a wait for a later-issued A operand would also wait for
+      // these.  Set PAR is free: phase f's own items were stored at the end of phase f - 1.
+      if (cc == CG - 1 && f + 2 < nf) load_pieces(pst[PAR], f + 2);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int step = cc * T + t;
@@ -250,8 +229,8 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
     if (ph == nphase - 1) {  // the group's reduction is complete
       const int m = (j0 + blk * J) * 16 + col;
       const int cl = wave * 64 + g * 16;
-      tile1ps_epilogue<MODE, OUT_ENC>(acc, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl], &sCoef[1][cl], p.out, p.M,
-                                      p.sew);
+      lean_epilogue_stateless<MODE, OUT_ENC>(acc, true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl], &sCoef[1][cl],
+                                             p.out, p.M, p.sew);
 #pragma unroll
       for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -270,16 +249,18 @@ inline int tile1ps_per(int npg, int nsb, int slots) { return std::max(1, std::mi
 
 // Launch on `slots` resident workgroups (a multiple of the super-block count, at most one per
 // (group, super-block) pair).
-template <int NW, int CG, int IN_ENC, int OUT_ENC>
+template <int NW, int CG, int IN_ENC, int OUT_ENC, int ARES = 0>
 hipError_t launch_tile1ps(const TileParams& p, int mode, int slots, hipStream_t s) {
   const int npg = p.M / 16;
   const int nsb = p.F / (NW * 64);
   const int per = tile1ps_per(npg, nsb, slots);
   const dim3 grid((unsigned)(per * nsb)), block(64 * NW);
   if (mode == EPI_LIF_HARD)
-    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC>), grid, block, 0, s, p, npg, nsb);
+    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC, ARES>), grid, block, 0, s, p, npg,
+                       nsb);
   else
-    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD, IN_ENC, OUT_ENC>), grid, block, 0, s, p, npg, nsb);
+    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD, IN_ENC, OUT_ENC, ARES>), grid, block, 0, s, p, npg,
+                       nsb);
   return hipGetLastError();
 }
 

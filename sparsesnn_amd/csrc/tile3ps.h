@@ -158,7 +158,6 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
     const int c = f - k * p.nchunk;
     const bool more = f + 1 < nf;
     const int cn = c + 1 < p.nchunk ? c + 1 : 0;  // chunk of step f + 1
-    if (more) load_units(stg, f + 1);
     uint2 fr[2][4];
     auto issue = [&](int step, uint2 (&fq)[4]) {
       const int tp = step / T, t = step - (step / T) * T;
@@ -193,6 +192,7 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
                                                                (int)ix[ra][a], 0, 0);
       }
     }
+    if (more) load_units(stg, f + 1);
     // tap 8 used set 0 and loaded step f + 1's first tap into set 1: move it to set 0
 #pragma unroll
     for (int a = 0; a < 4; ++a) {

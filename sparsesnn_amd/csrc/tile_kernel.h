@@ -346,21 +346,29 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
   uint32_t ix[NA][GPW][4];
 #pragma unroll
   for (int i = 0; i < PF; ++i) load_a(set, i, av[i], ix[i]);
-  uint2 stg[UPT];
+  // Spike bits: the words of this set's next NQ chunks wait in registers, stq[i] holding chunk
+  // c + (i + 1)*KSP while chunk c is reduced; they are loaded before the first barrier (all of
+  // them for reductions of at most NQ + 1 chunks per set), not at the start of each chunk:
+  // vector memory counts complete in issue order, so the wait for an A operand issued after a
+  // staging load would also wait for that load, one or two taps later.
+  constexpr int NQ = (PF == 2 || KSP == 2) ? 3 : 1;
+  uint2 stq[NQ][UPT];
   u32x4_t pnext[IN_ENC == SENGINE_ENC_F16 ? PPT : 1];  // fp16 input: the next chunk's pieces
   if (IN_ENC == SENGINE_ENC_F16) {
     u32x4_t pcs[PPT];
     load_pieces(pcs, set);
     store_pieces(set * NBUF, pcs);
   } else {
+    uint2 stg[UPT];
     load_units(stg, set);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) load_units(stq[i], std::min(set + (i + 1) * KSP, p.nchunk - KSP + set));
     store_units(set * NBUF, stg);
   }
   __syncthreads();
   for (int c = set; c < p.nchunk; c += KSP) {  // host: nchunk % KSP == 0 (sets stay in step)
     const bool more = c + KSP < p.nchunk;
     const int buf = NBUF == 2 ? ((c / KSP) & 1) : 0;
-    if (IN_ENC == SENGINE_ENC_BITS && more) load_units(stg, c + KSP);
     if (IN_ENC == SENGINE_ENC_F16 && more) load_pieces(pnext, c + KSP);
     // B fragments: four ds_read_b64 per (tap, t), issued PF steps ahead of their SMFMACs
     // and waited for with an explicit lgkmcnt (the loop issues no other LDS operation).
@@ -386,8 +394,10 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
       // A operands PF taps ahead (crossing into the next chunk: they do not depend on LDS)
       const int ra = PF == 1 ? 0 : tap % NA;            // ring slot in use (PF = 2)
       const int rn = PF == 1 ? 1 : (tap + PF) % NA;     // ring slot being filled
+      // unconditional (after the last chunk: this chunk's operands again, unused), so the
+      // compiler's wait counts need not merge a path with fewer loads in flight
       if (tap + PF < NTAP) load_a(c, tap + PF, av[rn], ix[rn]);
-      else if (more) load_a(c + KSP, tap + PF - NTAP, av[rn], ix[rn]);
+      else load_a(more ? c + KSP : c, tap + PF - NTAP, av[rn], ix[rn]);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int step = tap * T + t;
@@ -414,7 +424,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
             acc[gg][t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(half8_t, av[ra][gg][a]), bf,
                                                                      acc[gg][t][a], (int)ix[ra][gg][a], 0, 0);
       }
-      if (PF == 1 && (tap + 1 < NTAP || more)) {
+      if (PF == 1) {
 #pragma unroll
         for (int gg = 0; gg < GPW; ++gg)
 #pragma unroll
@@ -429,7 +439,13 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
       if (IN_ENC == SENGINE_ENC_F16) {
         store_pieces(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), pnext);
       } else {
-        store_units(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), stg);
+        store_units(set * NBUF + (NBUF == 2 ? (buf ^ 1) : 0), stq[0]);
+#pragma unroll
+        for (int i = 0; i + 1 < NQ; ++i)
+#pragma unroll
+          for (int j = 0; j < UPT; ++j) stq[i][j] = stq[i + 1][j];
+        // unconditional (clamped to this set's last chunk, then unused): no merged wait counts
+        load_units(stq[NQ - 1], std::min(c + (NQ + 1) * KSP, p.nchunk - KSP + set));
       }
       __syncthreads();
     }
