@@ -8,7 +8,7 @@ and known-answer placements, not by reference vectors.
 Spike bits: (n_pos, C) -> uint32 (n_pos, C/32), channel c at bit c%32 of word c/32.
 
 Sparse blob (v_smfmac_f32_16x16x64_f16 A operand), K_red ordered (kh, kw, c_in):
-  values[G][q][plane][a][lane][8] fp16, meta[G][q][a][lane] uint32 (low 16 bits)
+  values[G][q][plane][a][lane][8] fp16, meta[G][q][lane][a] uint32 (low 16 bits)
   lane l of tile a holds row r = l%16 <-> output channel 64G + 16*(r//4) + 4a + r%4,
   reduction indices 64q + 16*(l//16) + [0,16): four 4-groups, two kept values each,
   value j's in-group position in meta bits [2j+1:2j].
@@ -107,7 +107,7 @@ def compress_2_4(w: np.ndarray, planes: int = 1):
     # vals: (C_out, K_red/4, 2); meta bits per group: pos0 | pos1 << 2
     gbits = (pos[..., 0] | (pos[..., 1] << 2)).astype(np.uint32)
     values = np.zeros((nG, nq, planes, 4, 64, 8), np.float16)
-    meta = np.zeros((nG, nq, 4, 64), np.uint32)
+    meta = np.zeros((nG, nq, 64, 4), np.uint32)
     lanes = np.arange(64)
     r = lanes % 16
     for G in range(nG):
@@ -122,7 +122,7 @@ def compress_2_4(w: np.ndarray, planes: int = 1):
                 m = np.zeros(64, np.uint32)
                 for gi in range(4):
                     m |= bits[:, gi] << np.uint32(4 * gi)
-                meta[G, q, a] = m
+                meta[G, q, :, a] = m
     return values.view(np.uint16), meta, violations.reshape(-1)
 
 
@@ -161,7 +161,7 @@ def decompress_2_4(values: np.ndarray, meta: np.ndarray, shape) -> np.ndarray:
         for a in range(4):
             co = _row_to_channel(G, a, r)
             for q in range(nq):
-                m = meta[G, q, a]
+                m = meta[G, q, :, a]
                 for j in range(8):
                     gi = j // 2
                     p = (m >> np.uint32(2 * j)) & 3

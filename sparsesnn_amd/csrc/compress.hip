@@ -9,7 +9,8 @@
 // Sparse blob, per 64-output-channel group G and 64-wide reduction chunk q
 // (K_red ordered (kh, kw, c_in)):
 //   values[G][q][plane][tile a][lane][8 x fp16]   (16 B per lane, one A operand)
-//   meta  [G][q][tile a][lane] u32                (low 16 bits: 8 x 2-bit positions)
+//   meta  [G][q][lane][tile a] u32                (low 16 bits: 8 x 2-bit positions; a lane's
+//                                                  four tiles in one 16-byte load)
 // Row permutation: A tile a, row r <-> output channel 64G + 16*(r/4) + 4a + r%4, so the
 // accumulator of lane group g holds channels 16g..16g+15 (see fused_sparse.hip).
 // Planes: plane 0 = fp16(w); plane 1 (optional) = fp16(w - plane0), which makes the
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(256) void compress_2_4_kernel(WeightParams p, half8
   const size_t base = ((size_t)gq * p.planes) * 4 * 64 + (size_t)a * 64 + lane;
   vals[base] = v0;
   if (p.planes == 2) vals[base + 4 * 64] = v1;
-  meta[(size_t)gq * 4 * 64 + (size_t)a * 64 + lane] = bits;
+  meta[(size_t)gq * 4 * 64 + (size_t)lane * 4 + a] = bits;
 }
 
 // Dense blob: values[G][q32][plane][tile a][lane][8 x fp16], A operand of

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
   const int nq = p.nq;
   const int chunks_per_tap = p.C >> 6;
   const half8_t* wv = p.wvals + (size_t)G * nq * PLANES * 4 * 64 + lane;
-  const uint32_t* wm = p.wmeta + (size_t)G * nq * 4 * 64 + lane;
+  const uint32_t* wm = p.wmeta + (size_t)G * nq * 4 * 64 + lane * 4;  // [q][lane][tile]
   // Byte selector pulling bits [8g, 8g+8) of each 32-bit half of a 64-channel chunk.
   const uint32_t sel = 0x0c0c0000u | ((uint32_t)(4 + g) << 8) | (uint32_t)g;
 
@@ -115,7 +115,11 @@ __global__ __launch_bounds__(256) void fused_sparse_conv_bn_lif_kernel(FusedPara
     for (int a = 0; a < 4; ++a) {
 #pragma unroll
       for (int pl = 0; pl < PLANES; ++pl) av[pl][a] = wv[((size_t)(q * PLANES + pl) * 4 + a) * 64];
-      ix[a] = wm[((size_t)q * 4 + a) * 64];
+    }
+    {
+      const u32x4_t m4 = *reinterpret_cast<const u32x4_t*>(wm + (size_t)q * 4 * 64);
+#pragma unroll
+      for (int a = 0; a < 4; ++a) ix[a] = m4[a];
     }
 
 #pragma unroll
@@ -215,7 +219,7 @@ __device__ __forceinline__ void smallm_body(const FusedParams& p, const int bx, 
   const int chunks_per_tap = p.C >> 6;
   const size_t tstride = (size_t)p.in_t_stride * cbytes;
   const half8_t* wv = p.wvals + (size_t)G * nq * PLANES * 4 * 64 + lane;
-  const uint32_t* wm = p.wmeta + (size_t)G * nq * 4 * 64 + lane;
+  const uint32_t* wm = p.wmeta + (size_t)G * nq * 4 * 64 + lane * 4;  // [q][lane][tile]
   const uint32_t sel = 0x0c0c0000u | ((uint32_t)(4 + g) << 8) | (uint32_t)g;
 
   auto load = [&](int q, SmallOperands<T, PLANES>& o) {
@@ -223,7 +227,11 @@ __device__ __forceinline__ void smallm_body(const FusedParams& p, const int bx, 
     for (int a = 0; a < 4; ++a) {
 #pragma unroll
       for (int pl = 0; pl < PLANES; ++pl) o.av[pl][a] = wv[((size_t)(q * PLANES + pl) * 4 + a) * 64];
-      o.ix[a] = wm[((size_t)q * 4 + a) * 64];
+    }
+    {
+      const u32x4_t m4 = *reinterpret_cast<const u32x4_t*>(wm + (size_t)q * 4 * 64);
+#pragma unroll
+      for (int a = 0; a < 4; ++a) o.ix[a] = m4[a];
     }
     const int tap = q / chunks_per_tap;
     const int c0 = q - tap * chunks_per_tap;

@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void fused_sparse_lds_kernel(LdsParams p) {
     for (int gg = 0; gg < GPW; ++gg) {
 #pragma unroll
       for (int pl = 0; pl < PL; ++pl) sA[buf][c][gg][pl][tid] = R.aw[gg][pl];
-      sM[buf][c][gg][tid] = R.mw[gg];
+      sM[buf][c][gg][(tid & 3) * 64 + (tid >> 2)] = R.mw[gg];  // blob [lane][tile] -> LDS [tile][lane]
     }
   };
 

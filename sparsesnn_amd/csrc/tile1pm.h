@@ -153,7 +153,7 @@ void fused_tile1pm_kernel(TileParams p) {
       const_cast<u32x4_t*>(p.wvals + (size_t)G0 * wgroup), 0, (int)(GPW * wgroup * sizeof(u32x4_t)), kBufferDword3);
   const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(p.wmeta + (size_t)G0 * wgroup), 0, (int)(GPW * wgroup * sizeof(uint32_t)), kBufferDword3);
-  const int lv = lane * (int)sizeof(u32x4_t), lm = lane * 4;
+  const int lv = lane * (int)sizeof(u32x4_t), lm = lane * 16;
   auto load_a = [&](int c, u32x4_t (&av)[GPW][4], uint32_t (&ix)[GPW][4]) {
     const int q = c * 4 * 64;
 #pragma unroll
@@ -163,8 +163,14 @@ void fused_tile1pm_kernel(TileParams p) {
         const int e = gg * (int)wgroup + q;
         av[gg][a] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                     rv, lv + a * 64 * (int)sizeof(u32x4_t), e * (int)sizeof(u32x4_t), 0));
-        ix[gg][a] = __builtin_amdgcn_raw_buffer_load_b32(rm, lm + a * 64 * 4, e * 4, 0);
       }
+#pragma unroll
+    for (int gg = 0; gg < GPW; ++gg) {  // the lane's four tiles' metadata: one 16-byte load
+      const u32x4_t m4 =
+          __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rm, lm, (gg * (int)wgroup + q) * 4, 0));
+#pragma unroll
+      for (int a = 0; a < 4; ++a) ix[gg][a] = m4[a];
+    }
   };
 
   float4_t acc[GPW][T][4];

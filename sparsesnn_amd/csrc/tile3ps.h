@@ -125,15 +125,18 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
       const_cast<u32x4_t*>(p.wvals + (size_t)Gb * wgroup), 0, (int)(wgroup * sizeof(u32x4_t)), kBufferDword3);
   const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(p.wmeta + (size_t)Gb * wgroup), 0, (int)(wgroup * sizeof(uint32_t)), kBufferDword3);
-  const int lv = lane * (int)sizeof(u32x4_t), lm = lane * 4;
+  const int lv = lane * (int)sizeof(u32x4_t), lm = lane * 16;
   auto load_a = [&](int c, int tap, u32x4_t (&av)[4], uint32_t (&ix)[4]) {
     const int e = (tap * p.nchunk + c) * 4 * 64;
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       av[a] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                               rv, lv + a * 64 * (int)sizeof(u32x4_t), e * (int)sizeof(u32x4_t), 0));
-      ix[a] = __builtin_amdgcn_raw_buffer_load_b32(rm, lm + a * 64 * 4, e * 4, 0);
     }
+    // the lane's four tiles' metadata ([lane][tile] in the blob): one 16-byte load
+    const u32x4_t m4 = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rm, lm, e * 4, 0));
+#pragma unroll
+    for (int a = 0; a < 4; ++a) ix[a] = m4[a];
   };
 
   float4_t acc[T][4];

@@ -217,7 +217,7 @@ def test_compress_known_answer_slot():
     nz = np.argwhere(v != 0)
     assert nz.tolist() == [[G, q, 0, a, lane, 2 * gi + 1]]  # kept positions {0? no: pad 0, 1} -> slot 1
     assert v[G, q, 0, a, lane, 2 * gi + 1] == 0.625
-    assert ((meta[G, q, a, lane] >> (4 * gi)) & 0xF) == (0 | (1 << 2))  # positions (0, 1)
+    assert ((meta[G, q, lane, a] >> (4 * gi)) & 0xF) == (0 | (1 << 2))  # positions (0, 1)
     assert viol.sum() == 0
 
 
