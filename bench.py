@@ -246,8 +246,8 @@ def cpu_baseline(budget_s=12.0, min_runs=CPU_MIN_RUNS):
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "fused_tile_kernel_cfg1_sweep_traffic.md")
 # the sources the sweep's kernels are built from (the halo-tiled fused kernel and its dispatch)
-SWEEP_KERNEL_SOURCES = ("common.h", "epilogue.h", "internal.h", "tile_kernel.h", "tile1pm.h", "tile1ps.h",
-                        "fused_tile1.hip", "fused_tile3.hip", "fused_sparse.hip")
+SWEEP_KERNEL_SOURCES = ("common.h", "epilogue.h", "internal.h", "tile_kernel.h", "tile1pm.h", "tile1ps.h", "tile3ps.h",
+                        "fused_tile1.hip", "fused_tile3.hip", "fused_sparse.hip", "compress.hip")
 
 
 def kernel_source_hash() -> str:

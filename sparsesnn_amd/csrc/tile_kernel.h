@@ -368,7 +368,8 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
     uint2 stg[UPT];
     load_units(stg, set);
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) load_units(stq[i], std::min(set + (i + 1) * KSP, p.nchunk - KSP + set));
+    for (int i = 0; i < NQ; ++i)
+      if (set + (i + 1) * KSP < p.nchunk) load_units(stq[i], set + (i + 1) * KSP);
     store_units(set * NBUF, stg);
   }
   __syncthreads();
@@ -400,10 +401,12 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
       // A operands PF taps ahead (crossing into the next chunk: they do not depend on LDS)
       const int ra = PF == 1 ? 0 : tap % NA;            // ring slot in use (PF = 2)
       const int rn = PF == 1 ? 1 : (tap + PF) % NA;     // ring slot being filled
-      // unconditional (after the last chunk: this chunk's operands again, unused), so the
-      // compiler's wait counts need not merge a path with fewer loads in flight
+      // PF = 2: unconditional (after the last chunk: this chunk's operands again, unused), so
+      // the compiler's wait counts at the last taps need not merge a path with fewer loads in
+      // flight; PF = 1 copies them into place at the end of the same tap (a wait for them), so
+      // the last chunk skips them (one-chunk layers reach their epilogue without that wait)
       if (tap + PF < NTAP) load_a(c, tap + PF, av[rn], ix[rn]);
-      else load_a(more ? c + KSP : c, tap + PF - NTAP, av[rn], ix[rn]);
+      else if (PF == 2 || more) load_a(more ? c + KSP : c, tap + PF - NTAP, av[rn], ix[rn]);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int step = tap * T + t;
@@ -430,7 +433,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
             acc[gg][t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(half8_t, av[ra][gg][a]), bf,
                                                                      acc[gg][t][a], (int)ix[ra][gg][a], 0, 0);
       }
-      if (PF == 1) {
+      if (PF == 1 && (tap + 1 < NTAP || more)) {
 #pragma unroll
         for (int gg = 0; gg < GPW; ++gg)
 #pragma unroll
