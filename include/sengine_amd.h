@@ -344,6 +344,18 @@ int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t pl
                          hipStream_t stream);
 
 /*
+ * The same head for an fp16 stream (planes = 0; other planes values behave as
+ * sengine_amd_sew_head) with the per-channel sums split over up to 64 workgroups per image
+ * (Spikformer's x.mean(2).mean(0) + head, models/spikformer.py:277-288, over its 3,136-token
+ * grid): partial integer sums go to the caller's workspace, at least B * 64 * C int32
+ * (workspace_elems), then the head adds them.  Same values as sengine_amd_sew_head (the sums
+ * are exact integers).  C % 32 == 0, C <= 2048.
+ */
+int sengine_amd_sew_head_ws(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t planes, const uint32_t* in,
+                            const float* fc_weight, const float* fc_bias, int32_t N_out, float* out,
+                            int32_t* workspace, int64_t workspace_elems, hipStream_t stream);
+
+/*
  * Unfused fallback, half 1: dense Conv + folded BN, fp32 output (T*B*OH*OW, C_out).
  * Mirrors conv2d_bn_t4_kernel / conv1x1_bn_t4_kernel (conv2d_bn_if_t4.py:551-673), but
  * keeps the BN output in fp32 (the reference rounds it to fp16).

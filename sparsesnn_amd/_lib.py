@@ -72,6 +72,7 @@ SIGNATURES = {
     "sengine_amd_multistep_neuron_repeat": (ctypes.c_int, [_I32, _I64, _I32, _I32, _F, _F, _F, _P, _P, _P]),
     "sengine_amd_maxpool_spikes": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P]),
     "sengine_amd_sew_head": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _P, _P, _P, _I32, _P, _P]),
+    "sengine_amd_sew_head_ws": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _P, _P, _P, _I32, _P, _P, _I64, _P]),
     "sengine_amd_dense_conv_bn": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P]),
     "sengine_amd_multistep_neuron": (ctypes.c_int, [_I32, _I64, _I32, _I32, _F, _F, _F, _P, _P, _I32, _P, _P, _P]),
     "sengine_amd_pack_spikes": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _P]),

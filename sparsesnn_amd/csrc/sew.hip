@@ -428,7 +428,47 @@ struct HeadParams {
   const float* b;  // (N_out)
   float* out;      // (B, N_out)
   int T, B, HW, C, planes, N_out;
+  const int32_t* partial = nullptr;  // fp16 input split over workgroups: (B, nsplit, C) sums
+  int nsplit = 0;
 };
+
+// Per-channel integer sums of an integer-valued fp16 stream (T*B, HW, C), split over
+// `nsplit` workgroups per image: workgroup (s, b) sums positions q = t*HW + p in
+// [s*P/nsplit, (s+1)*P/nsplit) of image b (P = T*HW; exact in int32) into
+// partial[(b*nsplit + s)*C + c].  The head then adds the nsplit sums of a channel.  One
+// workgroup per image had each CU stream an image's whole 16-bit stream alone.
+__global__ __launch_bounds__(256) void token_sums_kernel(const _Float16* in, int T, int B, int HW, int C, int nsplit,
+                                                         int32_t* partial) {
+  __shared__ int cnt[HEAD_MAX_PC];
+  const int s = blockIdx.x, b = blockIdx.y;
+  for (int i = threadIdx.x; i < C; i += 256) cnt[i] = 0;
+  __syncthreads();
+  const int64_t P = (int64_t)T * HW;
+  const int q0 = (int)(P * s / nsplit), q1 = (int)(P * (s + 1) / nsplit);
+  const int per8 = C / 8;              // 16-byte column groups
+  const int nsl = 256 / per8;          // position slices of the workgroup
+  const int sl = (int)threadIdx.x / per8;
+  const int c8 = ((int)threadIdx.x - sl * per8) * 8;
+  if (sl < nsl) {
+    int s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int t = (q0 + sl) / HW, sp = q0 + sl - t * HW;
+    for (int q = q0 + sl; q < q1; q += nsl) {
+      const half8_t v = *reinterpret_cast<const half8_t*>(in + (((int64_t)t * B + b) * HW + sp) * C + c8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s8[e] += (int)(float)v[e];
+      sp += nsl;
+      while (sp >= HW) {
+        sp -= HW;
+        ++t;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (s8[e]) atomicAdd(&cnt[c8 + e], s8[e]);
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < C; c += 256) partial[((int64_t)b * nsplit + s) * C + c] = cnt[c];
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -447,7 +487,13 @@ __global__ __launch_bounds__(NT) void sew_head_kernel(HeadParams p) {
   const int npos = p.T * p.HW;  // (t, s) positions of this image
   for (int i = threadIdx.x; i < planes * p.C; i += NT) cnt[i] = 0;
   __syncthreads();
-  if (fp16in) {
+  if (p.partial) {  // fp16 input summed by token_sums_kernel: add its nsplit partial sums
+    for (int c = threadIdx.x; c < p.C; c += NT) {
+      int sum = 0;
+      for (int s = 0; s < p.nsplit; ++s) sum += p.partial[((int64_t)bimg * p.nsplit + s) * p.C + c];
+      cnt[c] = sum;
+    }
+  } else if (fp16in) {
     // 8 channels (16 bytes) per thread and position, integer sums (exact) per channel
     const int per8 = p.C / 8;
     const int nsl = NT / per8;
@@ -572,6 +618,27 @@ __global__ __launch_bounds__(NT) void sew_head_kernel(HeadParams p) {
       if (lane == 0 && o0 + j < p.N_out) p.out[(int64_t)bimg * p.N_out + o0 + j] = v + p.b[o0 + j];
     }
   }
+}
+
+constexpr int kHeadMaxSplit = 64;  // summing workgroups per image (sengine_amd_sew_head_ws)
+
+// One head launch for checked parameters (the count phase reads p.partial when set).
+int launch_head(const HeadParams& p, hipStream_t stream) {
+  const int T = p.T, B = p.B, HW = p.HW, C = p.C, planes = p.planes, N_out = p.N_out;
+  // fp16 input (planes 0) reads 16 bits per value: weighed as 16 planes for the launch shape;
+  // with precomputed sums there is nothing left to count
+  const int64_t words_per_image = p.partial ? 0 : (int64_t)T * HW * (planes ? planes : 16) * C / 32;
+  if (words_per_image >= 16384) {
+    // counting dominates (token grids): one 1024-thread workgroup per image counts once
+    hipLaunchKernelGGL(sew_head_kernel<1024>, dim3((unsigned)B, 1u), dim3(1024), 0, stream, p);
+  } else {
+    // a few output slices per image (each counts its image again), so that about 512
+    // workgroups share the chip
+    const int passes = (N_out + 4 * HEAD_OPW - 1) / (4 * HEAD_OPW);
+    const int slices = std::max(1, std::min(passes, (512 + B - 1) / B));
+    hipLaunchKernelGGL(sew_head_kernel<256>, dim3((unsigned)B, (unsigned)slices), dim3(256), 0, stream, p);
+  }
+  return (int)hipGetLastError();
 }
 
 }  // namespace sengine
@@ -738,17 +805,27 @@ extern "C" int sengine_amd_sew_head(int32_t T, int32_t B, int32_t HW, int32_t C,
       (int64_t)std::max(planes, 1) * C > HEAD_MAX_PC)
     return set_error(-2, "sew_head: invalid shape (C % 32 == 0, 0 <= planes <= 5, planes * C <= 8192)");
   HeadParams p{in, fc_weight, fc_bias, out, T, B, HW, C, planes, N_out};
-  // fp16 input (planes 0) reads 16 bits per value: weighed as 16 planes for the launch shape
-  const int64_t words_per_image = (int64_t)T * HW * (planes ? planes : 16) * C / 32;
-  if (words_per_image >= 16384) {
-    // counting dominates (token grids): one 1024-thread workgroup per image counts once
-    hipLaunchKernelGGL(sew_head_kernel<1024>, dim3((unsigned)B, 1u), dim3(1024), 0, stream, p);
-  } else {
-    // a few output slices per image (each counts its image again), so that about 512
-    // workgroups share the chip
-    const int passes = (N_out + 4 * HEAD_OPW - 1) / (4 * HEAD_OPW);
-    const int slices = std::max(1, std::min(passes, (512 + B - 1) / B));
-    hipLaunchKernelGGL(sew_head_kernel<256>, dim3((unsigned)B, (unsigned)slices), dim3(256), 0, stream, p);
-  }
-  return (int)hipGetLastError();
+  return launch_head(p, stream);
+}
+
+extern "C" int sengine_amd_sew_head_ws(int32_t T, int32_t B, int32_t HW, int32_t C, int32_t planes,
+                                       const uint32_t* in, const float* fc_weight, const float* fc_bias,
+                                       int32_t N_out, float* out, int32_t* workspace, int64_t workspace_elems,
+                                       hipStream_t stream) {
+  if (planes != 0) return sengine_amd_sew_head(T, B, HW, C, planes, in, fc_weight, fc_bias, N_out, out, stream);
+  if (!in || !fc_weight || !fc_bias || !out || !workspace) return set_error(-1, "sew_head_ws: null pointer");
+  if (T < 1 || B < 1 || HW < 1 || C < 32 || C % 32 != 0 || C > 2048 || N_out < 1)
+    return set_error(-2, "sew_head_ws: invalid shape (C % 32 == 0, C <= 2048)");
+  // about 2048 summing workgroups in all, at least 64 positions each
+  const int64_t P = (int64_t)T * HW;
+  const int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({(int64_t)kHeadMaxSplit, (2048 + B - 1) / B, P / 64}));
+  if (workspace_elems < (int64_t)B * kHeadMaxSplit * C)
+    return set_error(-2, "sew_head_ws: workspace smaller than B * 64 * C int32");
+  hipLaunchKernelGGL(token_sums_kernel, dim3((unsigned)nsplit, (unsigned)B), dim3(256), 0, stream,
+                     reinterpret_cast<const _Float16*>(in), T, B, HW, C, nsplit, workspace);
+  if (hipError_t e = hipGetLastError()) return (int)e;
+  HeadParams p{in, fc_weight, fc_bias, out, T, B, HW, C, 0, N_out};
+  p.partial = workspace;
+  p.nsplit = nsplit;
+  return launch_head(p, stream);
 }

@@ -610,11 +610,16 @@ def maxpool_spikes(x: torch.Tensor, NT: int, H: int, W: int, C: int, k: int = 3,
     return out
 
 
+HEAD_WS_SPLIT = 64  # summing workgroups per image of sengine_amd_sew_head_ws (workspace B * 64 * C)
+
+
 def sew_head(x: torch.Tensor, T: int, B: int, HW: int, C: int, planes: int, fc_weight: torch.Tensor,
-             fc_bias: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+             fc_bias: torch.Tensor, out: Optional[torch.Tensor] = None,
+             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Average pool + mean over T + Linear on `planes`-plane integer activations (planes = 0:
     integer-valued fp16 (T*B, HW, C)) -> (B, N_out) fp32.  fc_weight: (N_out, C) contiguous,
-    nn.Linear layout."""
+    nn.Linear layout.  With `workspace` (int32, at least B * 64 * C elements) an fp16 stream's
+    sums are split over many workgroups per image (sengine_amd_sew_head_ws)."""
     lib = _lib.load()
     for t, n in ((x, "x"), (fc_weight, "fc_weight"), (fc_bias, "fc_bias")):
         _require_cuda(t, n)
@@ -630,6 +635,14 @@ def sew_head(x: torch.Tensor, T: int, B: int, HW: int, C: int, planes: int, fc_w
     else:
         _require_cuda(out, "out")
         _require_numel(out, B * N_out, torch.float32, "out")
+    if workspace is not None:
+        _require_cuda(workspace, "workspace")
+        if workspace.dtype != torch.int32 or workspace.numel() < B * HEAD_WS_SPLIT * C:
+            raise SEngineError(f"workspace: need >= {B * HEAD_WS_SPLIT * C} int32 elements")
+        check(lib.sengine_amd_sew_head_ws(T, B, HW, C, planes, _ptr(x), _ptr(fc_weight), _ptr(fc_bias), N_out,
+                                          _ptr(out), _ptr(workspace), workspace.numel(), _stream(x.device)),
+              "sew_head_ws")
+        return out
     check(lib.sengine_amd_sew_head(T, B, HW, C, planes, _ptr(x), _ptr(fc_weight), _ptr(fc_bias), N_out, _ptr(out),
                                    _stream(x.device)), "sew_head")
     return out

@@ -205,6 +205,8 @@ class SpikformerEngine:
         self.head_w = p["head.weight"].contiguous().to(self.dev)
         self.head_b = p["head.bias"].contiguous().to(self.dev)
         self.logits = torch.empty(batch, self.head_w.shape[0], dtype=torch.float32, device=self.dev)
+        # the head's split per-channel sums of the fp16 stream (sengine_amd_sew_head_ws)
+        self.head_ws = torch.empty(batch * ops.HEAD_WS_SPLIT * embed, dtype=torch.int32, device=self.dev)
 
     # ------------------------------------------------------------------ build helpers
     @staticmethod
@@ -299,7 +301,8 @@ class SpikformerEngine:
 
     def run_head(self):
         x, planes = self.block_input(len(self.blocks))
-        ops.sew_head(x, self.T, self.B, self.N, self.embed, planes, self.head_w, self.head_b, out=self.logits)
+        ops.sew_head(x, self.T, self.B, self.N, self.embed, planes, self.head_w, self.head_b, out=self.logits,
+                     workspace=self.head_ws if planes == 0 else None)
 
     def _run_all(self):
         self.run_sps()
@@ -309,7 +312,8 @@ class SpikformerEngine:
 
     @property
     def launches(self) -> int:
-        return 7 + 8 * len(self.blocks) + 1
+        # SPS 7, 8 per block, the head 1 (bit planes) or 2 (fp16 stream: split sums, then the head)
+        return 7 + 8 * len(self.blocks) + (2 if self.block_input(len(self.blocks))[1] == 0 else 1)
 
     def capture(self):
         """Capture the whole forward into a hipGraph (replayed by forward())."""

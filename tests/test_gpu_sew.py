@@ -234,6 +234,29 @@ def test_sew_head(dev, planes, HW, C, N_out, T):
     assert torch.allclose(y, exp, rtol=1e-5, atol=1e-5), float((y - exp).abs().max())
 
 
+@pytest.mark.parametrize("HW,C,N_out,T,B", [(3136, 384, 1000, 4, 3), (700, 224, 5, 4, 2), (1, 64, 10, 4, 5),
+                                             (63, 96, 7, 2, 40)])
+def test_sew_head_fp16_stream_split(dev, HW, C, N_out, T, B):
+    """The head over an integer-valued fp16 stream (Spikformer's residual stream): counted by one
+    workgroup per image (sengine_amd_sew_head) and with the sums split over up to 64 workgroups
+    per image through a workspace (sengine_amd_sew_head_ws): identical logits, equal to numpy's
+    mean over positions and T followed by the Linear."""
+    rng = np.random.default_rng(HW + C)
+    a = rng.integers(0, 19, size=(T * B, HW, C))
+    x = torch.from_numpy(a).half().to(dev)
+    w = torch.randn(N_out, C) * 0.1
+    b = torch.randn(N_out) * 0.1
+    y1 = ops.sew_head(x, T, B, HW, C, 0, w.to(dev), b.to(dev)).cpu()
+    ws = torch.full((B * ops.HEAD_WS_SPLIT * C,), -7, dtype=torch.int32, device=dev)  # stale contents are overwritten
+    y2 = ops.sew_head(x, T, B, HW, C, 0, w.to(dev), b.to(dev), workspace=ws).cpu()
+    assert torch.equal(y1, y2)
+    feat = torch.from_numpy(a.reshape(T, B, HW, C).astype(np.float64)).mean(2).mean(0)
+    exp = (feat @ w.T.double() + b.double()).float()
+    assert torch.allclose(y2, exp, rtol=1e-5, atol=1e-5), float((y2 - exp).abs().max())
+    with pytest.raises(ops.SEngineError):
+        ops.sew_head(x, T, B, HW, C, 0, w.to(dev), b.to(dev), workspace=ws[: B * ops.HEAD_WS_SPLIT * C - 1])
+
+
 @pytest.mark.parametrize("k,stride,in_planes,res_planes,C_in,C_out,H", [(3, 1, 2, 2, 64, 64, 9), (3, 1, 1, 1, 128, 64, 8),
                                                                         (3, 2, 2, 1, 64, 128, 8), (1, 2, 2, 1, 64, 64, 6)])
 def test_fused_add_with_bit_plane_inputs(dev, k, stride, in_planes, res_planes, C_in, C_out, H):
