@@ -148,6 +148,20 @@ int sengine_amd_pack_dense_weights(const sengine_conv_lif_desc* d, const void* w
  *   x_trace  : optional fp32 (T, B*OH*OW, C_out): BN output (LIF input current)
  * Requires C_in % 64 == 0, C_out % 64 == 0, T in {1,2,4,8}.
  */
+/*
+ * The fused call with its spike bits split by channel into planes of split_channels:
+ * output channel c goes to plane c / split_channels, channel c % split_channels, each plane a
+ * (T*B*OH*OW, split_channels) bit matrix, planes back to back (ceil(C_out / split_channels)
+ * of them).  For several layers that read the same input and were concatenated along C_out
+ * (Spikformer's q, k and v Linears, models/spikformer.py:72-86): one launch, each layer's
+ * spikes in its own tensor.  split_channels % 64 == 0; spike-bit output; no traces; not in
+ * the flat small-output layout.  Same values as sengine_amd_fused_sparse_conv_bn_lif.
+ */
+int sengine_amd_fused_sparse_conv_bn_lif_split(const sengine_conv_lif_desc* d, const void* data,
+                                               const void* blob_values, const void* blob_meta, float* state,
+                                               const float* bn_scale, const float* bn_bias, void* spikes,
+                                               int32_t split_channels, hipStream_t stream);
+
 int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const void* data,
                                          const void* blob_values, const void* blob_meta,
                                          float* state, const float* bn_scale, const float* bn_bias,

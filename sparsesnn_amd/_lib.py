@@ -50,6 +50,7 @@ SIGNATURES = {
     "sengine_amd_pack_dense_weights": (ctypes.c_int, [_DP, _P, _I32, _I32, _P, _P]),
     "sengine_amd_fused_sparse_conv_bn_lif": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sengine_amd_fused_plan": (ctypes.c_int, [_DP, _I32, ctypes.c_char_p, ctypes.c_size_t]),
+    "sengine_amd_fused_sparse_conv_bn_lif_split": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P, _I32, _P]),
     "sengine_amd_calibrate_smfmac": (ctypes.c_int, [_I32, _I32, _P, _P]),
     "sengine_amd_fused_call_raw_weight": (ctypes.c_int, [_DP, _P, _P, _I32, _I32, _P, _P, _P, _P, _P]),
     "sengine_amd_prepare_weight": (ctypes.c_int, [_DP, _P, _I32, _I32, _P]),

@@ -104,6 +104,10 @@ struct SewAdd {
   // fp16 residual stream (the reference add kernel's own form): with fp16 output the stored
   // value is spike + res16 at the same (t, position, channel); res == nullptr then.
   const _Float16* res16;
+  // Channel-split spike-bit output (no residual): channel c goes to plane c / split_c, channel
+  // c % split_c, planes split_bytes apart, each a (rows, split_c) bit matrix; 0 = one plane.
+  int split_c = 0;
+  int64_t split_bytes = 0;
 };
 
 // One charge step: returns the charged membrane h given the previous membrane v and

@@ -87,6 +87,12 @@ __device__ __forceinline__ void load_sew_res(const SewAdd& sa, int M, int m, int
 __device__ __forceinline__ void store_spike_word(uint32_t word, size_t row_pos, int F, int cob, uint8_t* out,
                                                  const SewAdd& sa, const uint32_t (&r)[kResWords]) {
   if (sa.res == nullptr) {
+    if (sa.split_c) {  // 16 | split_c: a lane's 16 channels sit in one plane
+      const int k = cob / sa.split_c;
+      out += k * sa.split_bytes;
+      cob -= k * sa.split_c;
+      F = sa.split_c;
+    }
     *reinterpret_cast<uint16_t*>(out + ((row_pos * F + cob) >> 3)) = (uint16_t)word;
     return;
   }
@@ -224,7 +230,8 @@ __device__ __forceinline__ void lean_epilogue_stateless(const float4_t (&acc)[4]
     }
     if (!valid) continue;
     if (OUT_ENC == SENGINE_ENC_BITS) {
-      *reinterpret_cast<uint16_t*>(out + ((((size_t)t * M + m) * F + cob) >> 3)) = (uint16_t)word;
+      const uint32_t zr[kResWords] = {};
+      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, zr);
     } else {
       const uint32_t zr[kResWords] = {};
       store_spike_f16(word, ((size_t)t * M + m) * F + cob, out, sa, zr);

@@ -556,6 +556,23 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
                      SewAdd{nullptr, 0, 0, 0, nullptr, nullptr}, stream);
 }
 
+extern "C" int sengine_amd_fused_sparse_conv_bn_lif_split(const sengine_conv_lif_desc* d, const void* data,
+                                                          const void* blob_values, const void* blob_meta,
+                                                          float* state, const float* bn_scale, const float* bn_bias,
+                                                          void* spikes, int32_t split_channels, hipStream_t stream) {
+  if (!d) return set_error(-1, "fused_split: null descriptor");
+  if (d->out_enc != SENGINE_ENC_BITS) return set_error(-2, "fused_split: spike-bit output only");
+  if (split_channels < 64 || split_channels % 64 != 0)
+    return set_error(-2, "fused_split: split_channels must be a positive multiple of 64");
+  Geometry geo;
+  if (const int rc = check_desc(d, &geo, true)) return rc;
+  if (flat_layout(d, geo)) return set_error(-2, "fused_split: not available for the flat small-output layout");
+  SewAdd sew{nullptr, 0, 0, 0, nullptr, nullptr};
+  sew.split_c = split_channels;
+  sew.split_bytes = (int64_t)d->T * geo.M * split_channels / 8;
+  return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, nullptr, nullptr, sew, stream);
+}
+
 extern "C" int sengine_amd_fused_sparse_conv_bn_lif_pair(const sengine_conv_lif_desc* d0,
                                                          const sengine_conv_lif_desc* d1, const void* data,
                                                          const void* values0, const void* meta0,

@@ -23,7 +23,7 @@ __all__ = [
     "multistep_neuron_repeat", "maxpool_spikes", "sew_head", "dense_conv_bn", "multistep_neuron", "SEngineError",
     "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "NEURON_MS", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
     "neuron_code", "fused_sparse_conv_bn_add_neuron", "spiking_self_attention", "stem_conv_bn_neuron",
-    "fused_sparse_conv_bn_lif_pair", "fused_plan",
+    "fused_sparse_conv_bn_lif_pair", "fused_sparse_conv_bn_lif_split", "fused_plan",
 ]
 
 
@@ -277,6 +277,39 @@ def fused_sparse_conv_bn_lif(s: ConvSpec, data: torch.Tensor, values: torch.Tens
         ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta), _ptr(state), _ptr(bn_scale), _ptr(bn_bias),
         _ptr(out), _ptr(h_trace), _ptr(x_trace), _stream(dev))
     check(rc, "fused_sparse_conv_bn_lif")
+    return out
+
+
+def fused_sparse_conv_bn_lif_split(s: ConvSpec, data: torch.Tensor, values: torch.Tensor, meta: torch.Tensor,
+                                   bn_scale: torch.Tensor, bn_bias: torch.Tensor, split: int,
+                                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fused_sparse_conv_bn_lif with the spike bits split by channel into planes of `split`
+    channels (layers concatenated along C_out that read the same input): returns int32
+    (ceil(C_out / split), T*B, OH, OW, split/32); plane k holds channels [k*split, (k+1)*split)."""
+    lib = _lib.load()
+    if s.out_enc != ENC_BITS:
+        raise SEngineError("fused_sparse_conv_bn_lif_split: spike-bit output only")
+    OH, OW, M, _ = geometry(s)
+    d = make_desc(s)
+    vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+    check(lib.sengine_amd_sparse_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)), "sparse_blob_bytes")
+    for t, n in ((data, "data"), (values, "values"), (meta, "meta"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    dt, n_in = _enc_numel(s.in_enc, s.T * s.B * s.H * s.W * s.C_in)
+    _require_numel(data, n_in, dt, "data")
+    if values.numel() * values.element_size() != vb.value or meta.numel() * meta.element_size() != mb.value:
+        raise SEngineError("fused_sparse_conv_bn_lif_split: weight blob does not match the descriptor")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    nplanes = -(-s.C_out // split)
+    if out is None:
+        out = torch.empty(nplanes, s.T * s.B, OH, OW, split // 32, dtype=torch.int32, device=data.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, nplanes * s.T * M * split // 32, torch.int32, "out")
+    check(lib.sengine_amd_fused_sparse_conv_bn_lif_split(
+        ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta), None, _ptr(bn_scale), _ptr(bn_bias), _ptr(out), split,
+        _stream(data.device)), "fused_sparse_conv_bn_lif_split")
     return out
 
 

@@ -19,9 +19,13 @@ Linear head (:273-288).  SpikformerEngine maps it onto this library:
   the token grid reading it as fp16 activations (K = embed), and proj / MLP fc2 write
   spike + x as fp16 in their epilogues.  stream="planes" stores it as bit planes instead:
   the token Linears then run on spike bits with plane-expanded weights (K = planes * embed)
-  and the adds write planes.  The Linear bias is folded into the BN affine; SSA runs as the
-  two-kernel Q (K^T V) path with the attention LIF (V_th 0.5);
-* head: mean over tokens and T of the integer stream and the Linear (sengine_amd_sew_head).
+  and the adds write planes.  The Linear bias is folded into the BN affine.  q, k and v read
+  the same stream: their weights are concatenated along C_out (zero-padded to a multiple of
+  256) and run as one launch whose spike bits are split into one plane per Linear
+  (sengine_amd_fused_sparse_conv_bn_lif_split).  SSA runs as the two-kernel Q (K^T V) path
+  with the attention LIF (V_th 0.5);
+* head: mean over tokens and T of the integer stream and the Linear (sengine_amd_sew_head, or
+  with the fp16 stream sengine_amd_sew_head_ws: the sums split over many workgroups).
 
 Every buffer is allocated once; the launch sequence is captured into one hipGraph.
 """
@@ -98,9 +102,7 @@ class SBlock:
     planes_in: int
     planes_mid: int
     planes_out: int
-    q: Fused
-    k: Fused
-    v: Fused
+    qkv: Fused  # attn.q, .k, .v concatenated: one launch, spikes split into one plane each
     proj: Fused
     fc1: Fused
     fc2: Fused
@@ -185,16 +187,19 @@ class SpikformerEngine:
             elif P2 > 5:
                 raise SEngineError("the residual stream needs more than 5 bit planes (depth too large)")
             blk = SBlock(pre, P0, P1, P2,
-                         q=self._linear(p, pre + ".attn.q", embed, embed, P0),
-                         k=self._linear(p, pre + ".attn.k", embed, embed, P0),
-                         v=self._linear(p, pre + ".attn.v", embed, embed, P0),
+                         qkv=self._concat_qkv(p, pre, embed, P0),
                          proj=self._linear(p, pre + ".attn.proj", embed, embed, 1, out_f16=f16),
                          fc1=self._linear(p, pre + ".mlp.fc1", embed, hidden, P1),
                          fc2=self._linear(p, pre + ".mlp.fc2", hidden, embed, 1, out_f16=f16),
                          bufs={})
             d = embed // heads
-            for n in ("q", "k", "v", "a"):
-                blk.bufs[n] = torch.empty(TB, self.N, embed // 32, **i32)
+            # q, k and v read the same stream: one launch over their concatenated weights, its
+            # spike bits split into one plane per Linear (the fourth plane holds the padding)
+            nplanes = -(-blk.qkv.spec.C_out // embed)
+            blk.bufs["qkv"] = torch.empty(nplanes, TB, self.N, embed // 32, **i32)
+            for j, n in enumerate(("q", "k", "v")):
+                blk.bufs[n] = blk.bufs["qkv"][j]
+            blk.bufs["a"] = torch.empty(TB, self.N, embed // 32, **i32)
             blk.bufs["kv"] = torch.empty(TB, heads, d, d, **i32)
             blk.bufs["x1"] = stream_buf(P1)
             blk.bufs["h"] = torch.empty(TB, self.N, hidden // 32, **i32)
@@ -238,7 +243,25 @@ class SpikformerEngine:
         sc, bi = self._bn(p, f"patch_embed.{name.replace('conv', 'bn')}", pad_to=cout_p)
         return self._prepare(self._spec(cin_p, cout_p, 3, h, w, 1), wp, sc, bi)
 
+    def _concat_qkv(self, p, pre, cin, planes) -> Fused:
+        """attn.q, .k and .v concatenated along C_out, padded with zero rows (and a zero BN
+        affine: never fire) up to a multiple of 256 output channels, the persistent 1x1
+        kernel's four-wave super-blocks."""
+        parts = [self._linear_parts(p, f"{pre}.attn.{n}", cin, cin, planes) for n in ("q", "k", "v")]
+        spec = parts[0][0]
+        cp = -(-3 * cin // 256) * 256
+        w = torch.zeros(cp, spec.C_in, 1, 1)
+        w[:3 * cin] = torch.cat([wx for _, wx, _, _ in parts])
+        zeros = torch.zeros(cp - 3 * cin)
+        sc = torch.cat([s for _, _, s, _ in parts] + [zeros])
+        bi = torch.cat([b for _, _, _, b in parts] + [zeros])
+        return self._prepare(dataclasses.replace(spec, C_out=cp), w, sc, bi)
+
     def _linear(self, p, name, cin, cout, planes, out_f16=False) -> Fused:
+        spec, wx, sc, bi = self._linear_parts(p, name, cin, cout, planes, out_f16)
+        return self._prepare(spec, wx, sc, bi)
+
+    def _linear_parts(self, p, name, cin, cout, planes, out_f16=False):
         """planes 0: fp16 input (the integer stream as fp16); 1: spike bits; > 1: bit planes
         (plane-expanded weights).  out_f16: the spike + residual add writes the fp16 stream."""
         wk = name + "_linear.weight"
@@ -256,7 +279,7 @@ class SpikformerEngine:
             spec = dataclasses.replace(spec, in_enc=ops.ENC_F16)
         if out_f16:
             spec = dataclasses.replace(spec, out_enc=ops.ENC_F16)
-        return self._prepare(spec, wx, sc, bi)
+        return spec, wx, sc, bi
 
     # ------------------------------------------------------------------ execution
     def _fused(self, f: Fused, data, out):
@@ -290,9 +313,9 @@ class SpikformerEngine:
         if x is None:
             x, _ = self.block_input(i)
         b = blk.bufs
-        self._fused(blk.q, x, b["q"])
-        self._fused(blk.k, x, b["k"])
-        self._fused(blk.v, x, b["v"])
+        qkv = blk.qkv
+        ops.fused_sparse_conv_bn_lif_split(qkv.spec, x.view(-1), qkv.values, qkv.meta, qkv.scale, qkv.bias,
+                                           self.embed, out=b["qkv"])
         ops.spiking_self_attention(b["q"], b["k"], b["v"], self.T, self.B, self.N, self.embed, self.heads,
                                    v_threshold=ATTN_VTH, kv=b["kv"], out=b["a"])
         self._fused_add(blk.proj, b["a"], x, blk.planes_in, b["x1"], blk.planes_mid)
@@ -312,8 +335,9 @@ class SpikformerEngine:
 
     @property
     def launches(self) -> int:
-        # SPS 7, 8 per block, the head 1 (bit planes) or 2 (fp16 stream: split sums, then the head)
-        return 7 + 8 * len(self.blocks) + (2 if self.block_input(len(self.blocks))[1] == 0 else 1)
+        # SPS 7, 6 per block (q/k/v, SSA 2, proj, fc1, fc2), the head 1 (bit planes) or 2 (fp16
+        # stream: split sums, then the head)
+        return 7 + 6 * len(self.blocks) + (2 if self.block_input(len(self.blocks))[1] == 0 else 1)
 
     def capture(self):
         """Capture the whole forward into a hipGraph (replayed by forward())."""

@@ -593,3 +593,37 @@ def test_fp16_residual_stream_add(dev, C_out):
                                             1, 0)
     torch.cuda.synchronize()
     assert torch.equal(out2.float().cpu() - res_bits.float(), spk)
+
+
+@pytest.mark.parametrize("C_in,C_out,split,H,W,B,in_enc", [(384, 1280, 384, 64, 40, 2, "f16"), (128, 512, 128, 16, 8, 2, "f16"),
+                                                         (128, 384, 128, 16, 16, 2, "bits"),
+                                                         (64, 192, 64, 9, 7, 2, "bits")])
+def test_fused_split_output(dev, C_in, C_out, split, H, W, B, in_enc):
+    """The channel-split spike output (sengine_amd_fused_sparse_conv_bn_lif_split: channel c
+    in plane c / split): equal, plane by plane, to the plain call's bits, for the persistent
+    fp16-input 1x1 kernel (Spikformer's concatenated q/k/v, padded to 1280 channels), another
+    1x1 route and a 3x3 layer, and the plain call is against the oracle."""
+    k = 3 if C_in == 64 else 1
+    f16 = in_enc == "f16"
+    spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=k, KW=k, stride=1, padding=k // 2,
+                        in_enc=ops.ENC_F16 if f16 else ops.ENC_BITS)
+    case = ref.make_layer_case(330 + C_out // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=k, padding=k // 2,
+                               fp16_weights=True, p_spike=0.2)
+    rep, _, _, _ = run_case(dev, case, in_enc=spec.in_enc, traces=False)
+    assert rep.ok, str(rep)
+    values, meta, _ = ops.compress_2_4(spec, case.w.to(dev))
+    sc, bi = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
+    sc_d, bi_d = torch.from_numpy(sc).to(dev), torch.from_numpy(bi).to(dev)
+    T = 4
+    if f16:
+        data = case.x_seq.permute(0, 1, 3, 4, 2).reshape(T * B, H, W, C_in).contiguous().half().to(dev)
+    else:
+        data = torch.from_numpy(pk.seq_to_nhwc_bits(case.x_seq.numpy()).view(np.int32)).to(dev)
+    plain = ops.fused_sparse_conv_bn_lif(spec, data, values, meta, sc_d, bi_d)
+    planes = ops.fused_sparse_conv_bn_lif_split(spec, data, values, meta, sc_d, bi_d, split)
+    torch.cuda.synchronize()
+    print(ops.fused_plan(spec), tuple(planes.shape))
+    full = plain.view(T * B * H * W, C_out // 32)
+    for j in range(-(-C_out // split)):
+        n = min(split, C_out - j * split) // 32
+        assert torch.equal(planes[j].reshape(T * B * H * W, split // 32)[:, :n], full[:, j * split // 32:j * split // 32 + n])
