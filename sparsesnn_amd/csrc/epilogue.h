@@ -82,17 +82,32 @@ __device__ __forceinline__ void load_sew_res(const SewAdd& sa, int M, int m, int
   }
 }
 
+// Where a lane's 16 spike bits go: the output, its row width F and the lane's first channel,
+// moved into the lane's plane when the output is channel-split (16 | split_c, no residual).
+// Computed once before an epilogue's timestep loop; stepping plane by plane (a few planes)
+// instead of dividing keeps the loop itself the same for split and unsplit outputs.
+struct SpikeDst {
+  uint8_t* out;
+  int F;
+  int cob;
+};
+__device__ __forceinline__ SpikeDst spike_dst(const SewAdd& sa, uint8_t* out, int F, int cob) {
+  SpikeDst d{out, F, cob};
+  if (sa.split_c) {
+    while (d.cob >= sa.split_c) {
+      d.cob -= sa.split_c;
+      d.out += sa.split_bytes;
+    }
+    d.F = sa.split_c;
+  }
+  return d;
+}
+
 // Store the 16 spike bits of (position row_pos = t*M + m, channels cob..cob+15), plus the
 // residual r (its planes, packed as in SewRes) when the SEW add is fused.
 __device__ __forceinline__ void store_spike_word(uint32_t word, size_t row_pos, int F, int cob, uint8_t* out,
                                                  const SewAdd& sa, const uint32_t (&r)[kResWords]) {
   if (sa.res == nullptr) {
-    if (sa.split_c) {  // 16 | split_c: a lane's 16 channels sit in one plane
-      const int k = cob / sa.split_c;
-      out += k * sa.split_bytes;
-      cob -= k * sa.split_c;
-      F = sa.split_c;
-    }
     *reinterpret_cast<uint16_t*>(out + ((row_pos * F + cob) >> 3)) = (uint16_t)word;
     return;
   }
@@ -161,6 +176,7 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
                                                         int cob, const NeuronParams& np, const EpiCoeffs& cf,
                                                         uint8_t* __restrict__ out, const SewAdd& sa,
                                                         const SewRes<T>* pre) {
+  const SpikeDst sd = spike_dst(sa, out, F, cob);
   SewRes<T> res;
   if (pre) res = *pre;
   else load_sew_res<T>(sa, M, m, F, cob, valid, res);
@@ -192,7 +208,7 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
     if (!valid) continue;
     const size_t row = ((size_t)t * M + m) * F + cob;
     if (OUT_ENC == SENGINE_ENC_BITS) {
-      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, res.r[t]);
+      store_spike_word(word, (size_t)t * M + m, sd.F, sd.cob, sd.out, sa, res.r[t]);
     } else {
       store_spike_f16(word, row, out, sa, res.r[t]);
     }
@@ -208,6 +224,8 @@ __device__ __forceinline__ void lean_epilogue_stateless(const float4_t (&acc)[4]
                                                  const NeuronParams& np, const float* fsc, const float* fbi,
                                                  uint8_t* __restrict__ out, int M, const SewAdd& sa) {
   constexpr int T = 4;
+  // Spike bits take no SEW residual here (the callers route residual layers elsewhere).
+  const SpikeDst sd = spike_dst(sa, out, F, cob);
   float v[16];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -230,8 +248,7 @@ __device__ __forceinline__ void lean_epilogue_stateless(const float4_t (&acc)[4]
     }
     if (!valid) continue;
     if (OUT_ENC == SENGINE_ENC_BITS) {
-      const uint32_t zr[kResWords] = {};
-      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, zr);
+      *reinterpret_cast<uint16_t*>(sd.out + ((((size_t)t * M + m) * sd.F + sd.cob) >> 3)) = (uint16_t)word;
     } else {
       const uint32_t zr[kResWords] = {};
       store_spike_f16(word, ((size_t)t * M + m) * F + cob, out, sa, zr);
@@ -281,6 +298,7 @@ template <int T, int OUT_ENC>
 __device__ __forceinline__ void shortcut_epilogue(const float4_t (&acc)[T][4], bool valid, int m, int M, int F, int cob,
                                                   const NeuronParams& np, const EpiCoeffs& cf, float* state,
                                                   uint8_t* __restrict__ out, const SewAdd& sa) {
+  const SpikeDst sd = spike_dst(sa, out, F, cob);
   const bool fold = np.neuron == SENGINE_NEURON_LIF && np.pow2;
   float v[16];
   float* st = state ? state + (size_t)m * F + cob : nullptr;
@@ -333,7 +351,7 @@ __device__ __forceinline__ void shortcut_epilogue(const float4_t (&acc)[T][4], b
       const size_t row = ((size_t)t * M + m) * F + c0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) *reinterpret_cast<float4_t*>(sa.real_out + row + cq * q) = cur[q];
-      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, zres);
+      store_spike_word(word, (size_t)t * M + m, sd.F, sd.cob, sd.out, sa, zres);
     }
     if (t + 1 < T) {
 #pragma unroll
@@ -355,6 +373,7 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
                                              const NeuronParams& np, const EpiCoeffs& cf, float* state,
                                              uint8_t* __restrict__ out, float* h_trace, float* x_trace,
                                              const SewAdd& sa, const SewRes<T>* pre = nullptr) {
+  const SpikeDst sd = spike_dst(sa, out, F, cob);
   if ((MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD) && state == nullptr) {  // uniform branch
     fast_epilogue_stateless<T, OUT_ENC, MODE>(acc, valid, m, M, F, cob, np, cf, out, sa, pre);
     return;
@@ -442,7 +461,7 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
     for (int t = 0; t < T; ++t) {
       if (!valid) continue;
       if (OUT_ENC == SENGINE_ENC_BITS) {
-        store_spike_word(words[t], (size_t)t * M + m, F, cob, out, sa, res.r[t]);
+        store_spike_word(words[t], (size_t)t * M + m, sd.F, sd.cob, sd.out, sa, res.r[t]);
       } else {
         store_spike_f16(words[t], ((size_t)t * M + m) * F + cob, out, sa, res.r[t]);
       }
@@ -518,7 +537,7 @@ __device__ __forceinline__ void lif_epilogue(const float4_t (&acc)[T][4], bool v
     }
     if (!valid) continue;
     if (OUT_ENC == SENGINE_ENC_BITS) {
-      store_spike_word(word, (size_t)t * M + m, F, cob, out, sa, res.r[t]);
+      store_spike_word(word, (size_t)t * M + m, sd.F, sd.cob, sd.out, sa, res.r[t]);
     } else {
       store_spike_f16(word, row, out, sa, res.r[t]);
     }

@@ -222,7 +222,10 @@ static bool tile3ps_eligible(const sengine_conv_lif_desc* d, const TileChoice& c
   // second round of one-tile workgroups balances the CUs better than a fixed assignment (measured)
   const int env = env_int_now("SENGINE_AMD_TILE3_PS", -1);
   if (env == 0 || (env != 2 && (int64_t)c.ntiles * (d->C_out / 64) < 2LL * tile3ps_slots())) return false;
-  if (a && (a->state || a->sew.res || a->sew.res16 || a->sew.real_out || a->h_trace || a->x_trace)) return false;
+  // (its epilogue stores plain spike-bit rows: no SEW sum, no channel-split planes)
+  if (a && (a->state || a->sew.res || a->sew.res16 || a->sew.real_out || a->sew.split_c || a->h_trace ||
+            a->x_trace))
+    return false;
   return true;
 }
 

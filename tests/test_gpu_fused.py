@@ -597,13 +597,18 @@ def test_fp16_residual_stream_add(dev, C_out):
 
 @pytest.mark.parametrize("C_in,C_out,split,H,W,B,in_enc", [(384, 1280, 384, 64, 40, 2, "f16"), (128, 512, 128, 16, 8, 2, "f16"),
                                                          (128, 384, 128, 16, 16, 2, "bits"),
-                                                         (64, 192, 64, 9, 7, 2, "bits")])
-def test_fused_split_output(dev, C_in, C_out, split, H, W, B, in_enc):
+                                                         (64, 192, 64, 9, 7, 2, "bits"),
+                                                         (64, 128, 64, 16, 16, 2, "bits")])
+def test_fused_split_output(dev, C_in, C_out, split, H, W, B, in_enc, monkeypatch):
     """The channel-split spike output (sengine_amd_fused_sparse_conv_bn_lif_split: channel c
     in plane c / split): equal, plane by plane, to the plain call's bits, for the persistent
     fp16-input 1x1 kernel (Spikformer's concatenated q/k/v, padded to 1280 channels), another
-    1x1 route and a 3x3 layer, and the plain call is against the oracle."""
+    1x1 route and 3x3 layers (the 16x16 one with the persistent 3x3 kernel forced where it is
+    eligible, which a split output must make it not be), and the plain call is against the
+    oracle."""
     k = 3 if C_in == 64 else 1
+    if H == 16 and k == 3:
+        monkeypatch.setenv("SENGINE_AMD_TILE3_PS", "2")
     f16 = in_enc == "f16"
     spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=k, KW=k, stride=1, padding=k // 2,
                         in_enc=ops.ENC_F16 if f16 else ops.ENC_BITS)
