@@ -67,64 +67,19 @@ __device__ inline void stem_touch8(const float* base, const int (&off)[8]) {
         "s"(off[7]));
 }
 
-// Workgroup = (image n, block of kStemPix output pixels in (oh, ow) order, 16-channel group
-// fg); thread = one output pixel x CPT channels (CPT = 8: two threads per pixel, waves
-// 0-3 channels 0-7 of the group and waves 4-7 channels 8-15, so a small grid still has two
-// waves per SIMD).  The workgroup stages the input rows the block reads, with the padding
-// as zeros, in dynamic LDS sized to the block; the tap loop then has no bounds checks.  The
-// weights of a wave's channels are the same for all its lanes, so they are read from global
-// memory at wave-uniform addresses (constant address space: scalar loads into SGPRs, which
-// the FMAs take as operands) -- read from LDS, every 16 FMAs would need a 1 KB wave-wide
-// float4 broadcast read, which kept the tap loop LDS-bound.
-// What the LDS stem kernel does after the convolution.
-enum StemMode : int {
-  kStemOut = 0,    // folded BN -> fp32 NHWC out
-  kStemPool = 1,   // folded BN -> neuron over T repeats -> spike max-pool (whole image per workgroup)
-  kStemSpikes = 2  // folded BN -> fp32 out (if p.out) and neuron over T repeats -> spike bits
-};
-
-template <int KW_, int MODE, int CPT>
-__global__ __launch_bounds__(kStemPix * 16 / CPT) void stem_conv_bn_lds_kernel(StemParams p) {
-  static_assert(CPT == 16 || CPT == 8, "8 or 16 channels per thread");
-  constexpr int NT = kStemPix * 16 / CPT;
+// Stages the C x nrows input rows (from ih0) of image xn into sx, zero-padded by PW columns on
+// each side (row c * nrows + r, then column; WP = W + 2 * PW) with the NT threads of a
+// workgroup.  Rows of at least 128 floats: wave w copies staged rows w, w + NW, ..., lane l
+// columns l, l + 64, ..., the loads of kStemRows rows x 4 column chunks issued before any of
+// them is stored; narrow rows: thread i copies staged floats i, i + NT, ..., FLAT loads in flight.
+template <int NT>
+__device__ __forceinline__ void stem_stage_rows(const StemParams& p, float* sx, const float* xn, int ih0, int nrows,
+                                                int WP) {
   constexpr int NW = NT / 64;
-  constexpr int FLAT = kStemFlat * 256 / NT;  // flat staging: loads per thread in flight
-  extern __shared__ float sx[];  // staged input (row = c * nrows + r, then column); fused: spike words after it
-  const int KW = KW_ > 0 ? KW_ : p.KW;
-  const int fgroups = p.F / 16;
-  const int pblocks = (p.OH * p.OW + kStemPix - 1) / kStemPix;
-  const int fg = blockIdx.x % fgroups;
-  const int pb = (blockIdx.x / fgroups) % pblocks;
-  const int n = blockIdx.x / (fgroups * pblocks);
-  const int pix0 = pb * kStemPix;
-  const int oh_first = pix0 / p.OW;
-  const int oh_last = min(p.OH - 1, (pix0 + kStemPix - 1) / p.OW);
-  const int ih0 = oh_first * p.SH - p.PH;
-  const int nrows = (oh_last - oh_first) * p.SH + p.KH;
-  const int WP = p.W + 2 * p.PW;  // padded row
+  constexpr int FLAT = kStemFlat * 256 / NT;
   const int nrow_st = p.C * nrows;
   const int nx = nrow_st * WP;
-  const float* xn = p.x + (int64_t)n * p.C * p.H * p.W;
-  // Weight prefetch: the tap loop's scalar loads come one (c, kh) row at a time, each row
-  // waited for before its FMAs, so a workgroup that finds the scalar cache cold (small
-  // grids: one workgroup per CU) would pay one L2/HBM round trip per row.  Wave w first
-  // touches the 64-byte lines of taps w, w + NW, ... with scalar loads issued eight at a
-  // time, one round trip per eight lines.
-  {
-    const int last = p.KH * KW * p.C - 1;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const float* wl = p.w + fg * 16;
-#pragma unroll
-    for (int i0 = 0; i0 < (kStemTouchTaps + NW - 1) / NW; i0 += 8) {
-      int off[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) off[i] = min(wv + NW * (i0 + i), last) * p.F * (int)sizeof(float);
-      stem_touch8(wl, off);
-    }
-  }
   if (WP >= 128) {
-    // Row-wise: wave w copies staged rows w, w + NW, ..., lane l columns l, l + 64, ...; the
-    // loads of kStemRows rows x 4 column chunks are issued before any of them is stored.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     for (int col0 = 0; col0 < WP; col0 += 4 * 64)
@@ -154,7 +109,6 @@ __global__ __launch_bounds__(kStemPix * 16 / CPT) void stem_conv_bn_lds_kernel(S
         }
       }
   } else {
-    // Flat (narrow rows): thread i copies staged floats i, i + NT, ..., FLAT loads in flight.
     const StemDiv by_wp(WP), by_rows(nrows);
     for (int i0 = threadIdx.x; i0 < nx; i0 += FLAT * NT) {
       float v[FLAT];
@@ -172,6 +126,62 @@ __global__ __launch_bounds__(kStemPix * 16 / CPT) void stem_conv_bn_lds_kernel(S
         if (i0 + u * NT < nx) sx[i0 + u * NT] = v[u];
     }
   }
+}
+
+// Workgroup = (image n, block of kStemPix output pixels in (oh, ow) order, 16-channel group
+// fg); thread = one output pixel x CPT channels (CPT = 8: two threads per pixel, waves
+// 0-3 channels 0-7 of the group and waves 4-7 channels 8-15, so a small grid still has two
+// waves per SIMD).  The workgroup stages the input rows the block reads, with the padding
+// as zeros, in dynamic LDS sized to the block; the tap loop then has no bounds checks.  The
+// weights of a wave's channels are the same for all its lanes, so they are read from global
+// memory at wave-uniform addresses (constant address space: scalar loads into SGPRs, which
+// the FMAs take as operands) -- read from LDS, every 16 FMAs would need a 1 KB wave-wide
+// float4 broadcast read, which kept the tap loop LDS-bound.
+// What the LDS stem kernel does after the convolution.
+enum StemMode : int {
+  kStemOut = 0,    // folded BN -> fp32 NHWC out
+  kStemPool = 1,   // folded BN -> neuron over T repeats -> spike max-pool (whole image per workgroup)
+  kStemSpikes = 2  // folded BN -> fp32 out (if p.out) and neuron over T repeats -> spike bits
+};
+
+template <int KW_, int MODE, int CPT>
+__global__ __launch_bounds__(kStemPix * 16 / CPT) void stem_conv_bn_lds_kernel(StemParams p) {
+  static_assert(CPT == 16 || CPT == 8, "8 or 16 channels per thread");
+  constexpr int NT = kStemPix * 16 / CPT;
+  constexpr int NW = NT / 64;
+  extern __shared__ float sx[];  // staged input (row = c * nrows + r, then column); fused: spike words after it
+  const int KW = KW_ > 0 ? KW_ : p.KW;
+  const int fgroups = p.F / 16;
+  const int pblocks = (p.OH * p.OW + kStemPix - 1) / kStemPix;
+  const int fg = blockIdx.x % fgroups;
+  const int pb = (blockIdx.x / fgroups) % pblocks;
+  const int n = blockIdx.x / (fgroups * pblocks);
+  const int pix0 = pb * kStemPix;
+  const int oh_first = pix0 / p.OW;
+  const int oh_last = min(p.OH - 1, (pix0 + kStemPix - 1) / p.OW);
+  const int ih0 = oh_first * p.SH - p.PH;
+  const int nrows = (oh_last - oh_first) * p.SH + p.KH;
+  const int WP = p.W + 2 * p.PW;  // padded row
+  const int nx = p.C * nrows * WP;
+  const float* xn = p.x + (int64_t)n * p.C * p.H * p.W;
+  // Weight prefetch: the tap loop's scalar loads come one (c, kh) row at a time, each row
+  // waited for before its FMAs, so a workgroup that finds the scalar cache cold (small
+  // grids: one workgroup per CU) would pay one L2/HBM round trip per row.  Wave w first
+  // touches the 64-byte lines of taps w, w + NW, ... with scalar loads issued eight at a
+  // time, one round trip per eight lines.
+  {
+    const int last = p.KH * KW * p.C - 1;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const float* wl = p.w + fg * 16;
+#pragma unroll
+    for (int i0 = 0; i0 < (kStemTouchTaps + NW - 1) / NW; i0 += 8) {
+      int off[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) off[i] = min(wv + NW * (i0 + i), last) * p.F * (int)sizeof(float);
+      stem_touch8(wl, off);
+    }
+  }
+  stem_stage_rows<NT>(p, sx, xn, ih0, nrows, WP);
   __syncthreads();
   const int part = CPT == 16 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kStemPix));
   const int tpix = (int)(threadIdx.x % kStemPix);
@@ -320,6 +330,114 @@ __global__ __launch_bounds__(kStemPix * 16 / CPT) void stem_conv_bn_lds_kernel(S
       }
     }
     p.pooled[((int64_t)(t * p.N + n) * npool + q) * fw + fg] = (uint16_t)m;
+  }
+}
+
+// Stem + neuron on the fp32 matrix cores (v_mfma_f32_16x16x4_f32, 4 taps per instruction):
+// the convolution as a GEMM of (output pixels) x (C_ * KH_ * KW_ taps, HWIO order: tap k =
+// (kh * KW + kw) * C + c, zero weights past the last tap) x (channels).  Workgroup = (image n,
+// 16 NB output pixels), NWV waves, wave w = channels 16w..16w+15 of all of them (NB 16-pixel
+// blocks, 4 NB accumulators per lane); the staged input rows are read by all waves.
+// Lane l supplies, per 4-tap step s, the input value of pixel l % 16 of each block at tap
+// 4s + l / 16 (the taps' staged-input offsets in an LDS table, its weights in registers) and
+// its weight for channel l % 16; it ends holding pixels 4 (l / 16) + r, r < 4, of each block for that channel.
+// Epilogue as in stem_conv_bn_lds_kernel<..., kStemSpikes, ...> (same BN, neuron arithmetic
+// and output layouts); a wave's 16-channel spike word of a pixel is the ballot of its spike
+// compare, picked out of the 64-lane mask by the lane that stores it.  The products are
+// summed in a different order than the FMA kernels', so outputs agree to fp32 rounding.
+// FASTN: hard-reset LIF with power-of-two 1/tau and 1 - 1/tau, or hard-reset IF, whose charge
+// is one fma (IF: v * 1 + x, the same single rounding as v + x); else the generic neuron.
+template <int C_, int KH_, int KW_, int NWV, bool FASTN, int NB>
+__global__ __launch_bounds__(64 * NWV) void stem_mfma_kernel(StemParams p) {
+  constexpr int NT = 64 * NWV;
+  constexpr int K = C_ * KH_ * KW_;
+  constexpr int KS = (K + 3) / 4;
+  constexpr int PIX = 16 * NB;  // output pixels per workgroup
+  // LDS: the staged-input offsets of the 4 KS taps (int), then the staged input rows
+  extern __shared__ float lds_stem[];
+  int* const sk = reinterpret_cast<int*>(lds_stem);
+  float* const sx = lds_stem + 4 * KS;
+  const int npix = p.OH * p.OW;
+  const int pblocks = (npix + PIX - 1) / PIX;
+  const int pb = blockIdx.x % pblocks;
+  const int n = blockIdx.x / pblocks;
+  const int pix0 = pb * PIX;
+  const int oh_first = pix0 / p.OW;
+  const int oh_last = min(p.OH - 1, (pix0 + PIX - 1) / p.OW);
+  const int ih0 = oh_first * p.SH - p.PH;
+  const int nrows = (oh_last - oh_first) * p.SH + KH_;
+  const int WP = p.W + 2 * p.PW;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int q = lane >> 4, j = lane & 15;
+  const int ch = wv * 16 + j;
+  float wb[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int k = 4 * s + q;
+    wb[s] = k < K ? p.w[(int64_t)k * p.F + ch] : 0.f;
+  }
+  for (int k = threadIdx.x; k < 4 * KS; k += NT) {
+    const int kk = k < K ? k : K - 1;  // a real tap of the same pixel; its weight is zero
+    const int c = kk % C_, khw = kk / C_;
+    sk[k] = (c * nrows + khw / KW_) * WP + khw % KW_;
+  }
+  stem_stage_rows<NT>(p, sx, p.x + (int64_t)n * C_ * p.H * p.W, ih0, nrows, WP);
+  __syncthreads();
+  // Pixel pix0 + 16 b + j of block b (past the image: pixel pix0, computed but not stored).
+  // Every staged offset read is below C * nrows * WP: (OW - 1) * SW + KW - 1 < W + 2 * PW.
+  int base[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int pix = min(pix0 + 16 * b + j, npix - 1);
+    const int oh = pix / p.OW;
+    base[b] = (oh - oh_first) * p.SH * WP + (pix - oh * p.OW) * p.SW;
+  }
+  float4_t acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int koff = sk[4 * s + q];
+    float a[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) a[b] = sx[base[b] + koff];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[b], wb[s], acc[b], 0, 0, 0);
+  }
+  const float sc = p.scale[ch], bi = p.bias[ch];
+  const bool fold = p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2;
+  const float dec = p.np.neuron == SENGINE_NEURON_IF ? 1.f : p.np.decay;
+  const int fw = p.F / 16;
+  const int64_t tstride = (int64_t)p.N * npix * fw;
+  // the word this lane stores (lanes 0-15): pixel 4 g + r of a block, g = j / 4, r = j % 4
+  const int rsel = j & 3, gsh = 16 * (j >> 2);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    float xo[4], v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      xo[r] = __builtin_fmaf(acc[b][r], sc, bi);
+      const int pix = pix0 + 16 * b + 4 * q + r;
+      if (p.out && pix < npix) p.out[((int64_t)n * npix + pix) * p.F + ch] = xo[r];
+      if (fold) xo[r] *= p.np.rtau;  // exact
+      v[r] = 0.f;
+    }
+    const int spix = pix0 + 16 * b + j;
+    uint16_t* so = p.spikes + ((int64_t)n * npix + spix) * fw + wv;
+    const bool st = q == 0 && spix < npix;
+    for (int t = 0; t < p.T; ++t) {
+      uint64_t mk[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float h = FASTN ? __builtin_fmaf(v[r], dec, xo[r]) : neuron_charge(p.np, v[r], xo[r]);
+        const bool spike = h >= p.np.vth;
+        v[r] = FASTN ? (spike ? p.np.vreset : h) : neuron_reset(p.np, h, spike);
+        mk[r] = __builtin_amdgcn_ballot_w64(spike);
+      }
+      const uint64_t m = rsel == 0 ? mk[0] : rsel == 1 ? mk[1] : rsel == 2 ? mk[2] : mk[3];
+      if (st) so[t * tstride] = (uint16_t)(m >> gsh);
+    }
   }
 }
 
@@ -645,6 +763,64 @@ int launch_head(const HeadParams& p, hipStream_t stream) {
 
 using namespace sengine;
 
+static bool env_stem_mfma() {  // read per call: tests compare both stem kernels
+  const char* e = getenv("SENGINE_AMD_STEM_MFMA");
+  return !(e && atoi(e) == 0);
+}
+
+// Staged input floats of one workgroup of `pix` output pixels (at most ceil(pix / OW) + 1 rows).
+static int64_t stem_staged(const StemParams& p, int pix) {
+  const int64_t orows = std::min<int64_t>(p.OH, (pix + p.OW - 1) / p.OW + 1);
+  return (int64_t)p.C * ((orows - 1) * p.SH + p.KH) * (p.W + 2 * p.PW);
+}
+
+// Launch geometry of stem_mfma_kernel<..., NB>: workgroups, the rounds the chip needs for
+// them at the occupancy the kernel reaches (resident workgroups per CU x CUs), and its LDS.
+template <int K_, int NWV, bool FASTN, int NB>
+static void stem_mfma_shape(const StemParams& p, int cus, int64_t& wgs, int64_t& rounds, size_t& lds) {
+  lds = (size_t)(stem_staged(p, 16 * NB) + 4 * ((3 * K_ * K_ + 3) / 4)) * sizeof(float);  // + tap offsets
+  wgs = (int64_t)p.N * ((p.OH * p.OW + 16 * NB - 1) / (16 * NB));
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(
+                                                       &stem_mfma_kernel<3, K_, K_, NWV, FASTN, NB>),
+                                                   64 * NWV, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int64_t slots = (int64_t)per_cu * cus;
+  rounds = (wgs + slots - 1) / slots;
+}
+
+// Pixels per workgroup (16 NB): the fewest pixel-block rounds over the chip, weighing a round
+// by its workgroup's pixels; at equal cost the larger block (less halo staging).
+template <int K_, int NWV, bool FASTN>
+static int launch_stem_mfma(const StemParams& p, hipStream_t stream) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess)
+    cus = 256;
+  int64_t w16, r16, w11, r11, w8, r8;
+  size_t l16, l11, l8;
+  stem_mfma_shape<K_, NWV, FASTN, 16>(p, cus, w16, r16, l16);
+  stem_mfma_shape<K_, NWV, FASTN, 11>(p, cus, w11, r11, l11);
+  stem_mfma_shape<K_, NWV, FASTN, 8>(p, cus, w8, r8, l8);
+  int nb = 16;
+  int64_t best = r16 * 16;
+  if (r11 * 11 < best) { nb = 11; best = r11 * 11; }
+  if (r8 * 8 < best) nb = 8;
+  if (const char* e = getenv("SENGINE_AMD_STEM_NB")) {
+    const int f = atoi(e);
+    if (f == 16 || f == 11 || f == 8) nb = f;
+  }
+  const dim3 block(64 * NWV);
+  if (nb == 16)
+    hipLaunchKernelGGL((stem_mfma_kernel<3, K_, K_, NWV, FASTN, 16>), dim3((unsigned)w16), block, l16, stream, p);
+  else if (nb == 11)
+    hipLaunchKernelGGL((stem_mfma_kernel<3, K_, K_, NWV, FASTN, 11>), dim3((unsigned)w11), block, l11, stream, p);
+  else
+    hipLaunchKernelGGL((stem_mfma_kernel<3, K_, K_, NWV, FASTN, 8>), dim3((unsigned)w8), block, l8, stream, p);
+  return (int)hipGetLastError();
+}
+
 extern "C" int sengine_amd_stem_conv_bn(const sengine_conv_lif_desc* d, const float* x, const float* weight,
                                         int32_t w_layout, const float* bn_scale, const float* bn_bias, float* out,
                                         hipStream_t stream) {
@@ -714,8 +890,20 @@ extern "C" int sengine_amd_stem_conv_bn_neuron(const sengine_conv_lif_desc* d, c
   p.spikes = reinterpret_cast<uint16_t*>(spikes);
   p.T = d->T;
   p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
-  const int64_t blocks = (int64_t)p.N * ((p.OH * p.OW + kStemPix - 1) / kStemPix) * (p.F / 16);
   const size_t lds = (size_t)staged * sizeof(float);
+  const int64_t pblocks = (int64_t)p.N * ((p.OH * p.OW + kStemPix - 1) / kStemPix);
+  // The matrix-core kernel for the 3-channel 7x7 and 3x3 stems of 32 or 64 channels (one
+  // wave per 16 channels); SENGINE_AMD_STEM_MFMA=0 keeps the FMA kernel.
+  if (p.C == 3 && p.KH == p.KW && (p.KW == 7 || p.KW == 3) && (p.F == 32 || p.F == 64) && env_stem_mfma()) {
+    const bool fast = p.np.hard_reset && (p.np.neuron == SENGINE_NEURON_IF ||
+                                          (p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2));
+    if (p.KW == 7)
+      return p.F == 64 ? (fast ? launch_stem_mfma<7, 4, true>(p, stream) : launch_stem_mfma<7, 4, false>(p, stream))
+                       : (fast ? launch_stem_mfma<7, 2, true>(p, stream) : launch_stem_mfma<7, 2, false>(p, stream));
+    return p.F == 64 ? (fast ? launch_stem_mfma<3, 4, true>(p, stream) : launch_stem_mfma<3, 4, false>(p, stream))
+                     : (fast ? launch_stem_mfma<3, 2, true>(p, stream) : launch_stem_mfma<3, 2, false>(p, stream));
+  }
+  const int64_t blocks = pblocks * (p.F / 16);
   if (p.KW == 7)
     hipLaunchKernelGGL((stem_conv_bn_lds_kernel<7, kStemSpikes, 16>), dim3((unsigned)blocks), dim3(kStemPix), lds,
                        stream, p);
