@@ -318,7 +318,11 @@ int sengine_amd_stem_conv_bn_lif_pool(const sengine_conv_lif_desc* d, const floa
  * folded BN as sengine_amd_stem_conv_bn (HWIO weights) into out (optional, may be NULL: NHWC
  * fp32 (B, OH, OW, C_out)), and the neuron of d (V0 = 0) on it repeated over d->T into
  * spikes (T, B, OH, OW) x C_out bits, the layout of sengine_amd_multistep_neuron_repeat on
- * that out.  Bit-identical to those two entry points.  Needs C_out % 32 == 0 and the input
+ * that out.  3-channel 7x7 or 3x3 stems of 32 or 64 channels run on the fp32 matrix cores:
+ * out then agrees with sengine_amd_stem_conv_bn to fp32 summation order, and the spikes are
+ * bit-identical to sengine_amd_multistep_neuron_repeat on this out; other stems (or the
+ * environment switch SENGINE_AMD_STEM_MFMA=0) are bit-identical to those two entry points
+ * with sengine_amd_stem_conv_bn's own out.  Needs C_out % 32 == 0 and the input
  * rows of 256 consecutive output pixels within LDS (3 channels of 224-wide images with a
  * 7x7/2 or 3x3/1 stem fit); returns -2 otherwise.
  */
