@@ -171,7 +171,8 @@ static int device_cus() {
 
 // The persistent 1x1 kernel (tile1ps.h) serves the token Linears when a layer is what it is
 // written for: stride 1, T = 4, 16 | M, an even chunk count, a fast stateless neuron, no trace,
-// state or bit-plane residual.  fp16 input with spike-bit output (q/k/v, fc1): 256-channel
+// state or bit-plane residual.  fp16 input with spike-bit or fp16 output (q/k/v and fc1; the
+// exported per-node call's fp16-in, fp16-out 1x1 layers), no fp16 residual: 256-channel
 // super-blocks (4 waves, phases of 2 chunks) or 384-channel ones (6 waves, phases of 3 chunks,
 // an even phase count).  Spike-bit input with fp16 output, optionally + the fp16 residual (proj,
 // fc2) or spike bits (1x1 layers of convolutional networks): 384-channel super-blocks with
@@ -186,7 +187,7 @@ static int tile1ps_config(const sengine_conv_lif_desc* d, const Geometry& geo, c
     return 0;
   if (a && (a->state || a->sew.res || a->sew.real_out || a->h_trace || a->x_trace)) return 0;
   if (d->in_enc == SENGINE_ENC_F16) {
-    if (d->out_enc != SENGINE_ENC_BITS || !c.pm || (a && a->sew.res16)) return 0;
+    if (!c.pm || (a && a->sew.res16)) return 0;
     if ((int64_t)d->T * geo.M * d->C_in * 2 > 0x7fffffff) return 0;  // piece offsets are 32-bit
     if (d->C_out % 256 == 0) return 4 * 16 + 2;
     if (d->C_out % 384 == 0 && nchunk % 6 == 0) return 6 * 16 + 3;
@@ -311,9 +312,13 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
       shortcut_only);
   if (d->in_enc == SENGINE_ENC_F16) {
     if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
-    if (const int ps = tile1ps_config(d, geo, c, mode, &a))
+    if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
+      if (d->out_enc == SENGINE_ENC_F16)  // fp16 in and out: the exported per-node call's form
+        return ps == 6 * 16 + 3 ? launch_tile1ps<6, 3, SENGINE_ENC_F16, SENGINE_ENC_F16>(p, mode, tile1ps_slots(6), stream)
+                                : launch_tile1ps<4, 2, SENGINE_ENC_F16, SENGINE_ENC_F16>(p, mode, tile1ps_slots(4), stream);
       return ps == 6 * 16 + 3 ? launch_tile1ps<6, 3, SENGINE_ENC_F16, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(6), stream)
                               : launch_tile1ps<4, 2, SENGINE_ENC_F16, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(4), stream);
+    }
     if (c.pm)
       return c.pmw == 6 ? launch_tile1pm<4, 1, 2, 6, SENGINE_ENC_F16>(p, d->out_enc, mode, stream)
                         : launch_tile1pm<4, 1, 2, 4, SENGINE_ENC_F16>(p, d->out_enc, mode, stream);

@@ -488,25 +488,28 @@ def test_tile3ps_walks(dev, shape, C_in, C_out, H, W, B, slots, neuron):
 @pytest.mark.parametrize("neuron", ["lif", "if"])
 @pytest.mark.parametrize("C_in,C_out,H,W,B", [(384, 512, 64, 40, 2), (128, 1024, 8, 16, 2), (128, 256, 4, 4, 1),
                                              (384, 384, 64, 40, 2), (384, 1152, 4, 8, 1)])
-def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron, slots):
-    """The persistent fp16-input 1x1 kernel (token Linears: stride 1, 16 | M, spike bits out,
-    stateless hard-reset neuron): 4-wave super-blocks with resident workgroups walking 1 or 2
-    position groups each (5,120 positions over 256 workgroups per super-block), a single group,
-    four super-blocks; 6-wave 384-channel super-blocks (phases of three chunks), one per CU
-    walking 1 or 2 groups, or three super-blocks; LIF and IF, against the oracle."""
+@pytest.mark.parametrize("out_enc", ["bits", "f16"])
+def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron, slots, out_enc):
+    """The persistent fp16-input 1x1 kernel (token Linears: stride 1, 16 | M, spike bits out;
+    the exported per-node call's fp16 spikes out; stateless hard-reset neuron): 4-wave
+    super-blocks with resident workgroups walking 1 or 2 position groups each (5,120 positions
+    over 256 workgroups per super-block), a single group, four super-blocks; 6-wave 384-channel
+    super-blocks (phases of three chunks), one per CU walking 1 or 2 groups, or three
+    super-blocks; LIF and IF, against the oracle."""
     if slots:  # few resident workgroups: every one walks many groups
         os.environ["SENGINE_AMD_PS_SLOTS"] = str(slots)
     try:
         spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
-                            neuron=neuron, in_enc=ops.ENC_F16)
+                            neuron=neuron, in_enc=ops.ENC_F16,
+                            out_enc=ops.ENC_F16 if out_enc == "f16" else ops.ENC_BITS)
         plan = ops.fused_plan(spec)
         nw, cg = (4, 2) if C_out % 256 == 0 else (6, 3)
-        assert plan.startswith(f"tile1ps<T=4,NW={nw},CG={cg},in=f16,out=bits,"), plan
+        assert plan.startswith(f"tile1ps<T=4,NW={nw},CG={cg},in=f16,out={out_enc},"), plan
         print(plan)
         case = ref.make_layer_case(260 + C_in // 64 + C_out // 64, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=1,
                                    padding=0, fp16_weights=True, p_spike=0.2)
         kw = dict(neuron="if", v_th=0.5, v_reset=0.0) if neuron == "if" else {}
-        rep, _, r, _ = run_case(dev, case, in_enc=ops.ENC_F16, traces=False, **kw)
+        rep, _, r, _ = run_case(dev, case, in_enc=ops.ENC_F16, out_enc=spec.out_enc, traces=False, **kw)
         print(rep, float(r.spikes.mean()))
         assert rep.ok, str(rep)
         assert float(r.spikes.mean()) > 0.002  # the comparison covers firing neurons
