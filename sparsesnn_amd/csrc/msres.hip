@@ -3,9 +3,10 @@
 // (BasicBlock18.shortcut = TDBNContainer(Conv2d 1x1 / stride s, BatchNorm3d),
 // models/msresnet.py:113-118,111; TDBNContainer.forward :79-87).  The spike convolutions
 // of the block run on the fused sparse kernels; this one multiplies fp32 activations, so it
-// is a plain fp32 GEMM over the strided pixels on the VALU:
+// is a plain fp32 GEMM over the strided pixels on the fp32 matrix cores:
 //   out[(t, b, oh, ow), f] = (sum_c x[(t, b, oh*S, ow*S), c] * w[c, f]) * scale[f] + bias[f]
-// Accumulation in increasing c, one fused multiply-add per term, fp32 throughout.  When the
+// fp32 throughout; the matrix cores sum four products per step, so the order of the terms
+// differs from a sequential sum (results agree to fp32 rounding).  When the
 // input carries one timestep and the output T (the stem output that the reference repeats
 // over T before the first block, models/msresnet.py:146-150), each value is computed once
 // and stored T times.
@@ -28,15 +29,16 @@ constexpr int kRcPos = 64;  // positions per workgroup
 constexpr int kRcCh = 64;   // output channels per workgroup
 constexpr int kRcK = 16;    // reduction chunk staged in LDS
 
-// Workgroup = 64 positions x 64 channels, 256 threads; thread (ty, tx) owns positions
-// 4ty..4ty+3 and channels 4tx..4tx+3 (16 accumulators).  Per 16-channel reduction chunk the
-// input pixels (transposed, c-major) and the weights are staged in LDS; each step then reads
-// one float4 of each and issues 16 FMAs.
+// Workgroup = 64 positions x 64 channels, 256 threads.  Per 16-channel reduction chunk the
+// input pixels (transposed, c-major) and the weights are staged in LDS; wave w then computes
+// positions 16w..16w+15 x the 64 channels on the fp32 matrix cores (v_mfma_f32_16x16x4_f32,
+// four 16-channel tiles, 4 taps of the reduction per instruction): lane l feeds weight
+// (tap 4s + l/16, channel l % 16 of the tile) and input (same tap, position l % 16) and ends
+// holding channels 4 (l/16)..4 (l/16) + 3 of each tile for position l % 16.
 __global__ __launch_bounds__(256) void real_conv1x1_bn_kernel(RealConvParams p) {
   __shared__ float xs[kRcK][kRcPos + 4];
-  __shared__ float ws[kRcK][kRcCh];
+  __shared__ float ws[kRcK][kRcCh + 4];
   const int tid = threadIdx.x;
-  const int tx = tid & 15, ty = tid >> 4;
   const int64_t m0 = (int64_t)blockIdx.x * kRcPos;
   const int f0 = blockIdx.y * kRcCh;
 
@@ -53,12 +55,11 @@ __global__ __launch_bounds__(256) void real_conv1x1_bn_kernel(RealConvParams p) 
     xrow = p.x + ((n * p.H + (int64_t)oh * p.S) * p.W + (int64_t)ow * p.S) * p.C;
   }
   const int wk = tid >> 4, wf = (tid & 15) * 4;  // weight staging: row wk, channels wf..wf+3
+  const int wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
 
-  float acc[4][4];
+  float4_t acc[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+  for (int nb = 0; nb < 4; ++nb) acc[nb] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int k0 = 0; k0 < p.C; k0 += kRcK) {
     const float4 xv = svalid ? *reinterpret_cast<const float4*>(xrow + k0 + 4 * lq) : float4{0.f, 0.f, 0.f, 0.f};
@@ -77,28 +78,24 @@ __global__ __launch_bounds__(256) void real_conv1x1_bn_kernel(RealConvParams p) 
     *reinterpret_cast<float4*>(&ws[wk][wf]) = wv;
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kRcK; ++k) {
-      const float4 a = *reinterpret_cast<const float4*>(&xs[k][4 * ty]);
-      const float4 b = *reinterpret_cast<const float4*>(&ws[k][4 * tx]);
-      const float av[4] = {a.x, a.y, a.z, a.w};
-      const float bv[4] = {b.x, b.y, b.z, b.w};
+    for (int s = 0; s < kRcK / 4; ++s) {
+      const float xb = xs[4 * s + q][16 * wave + j];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+      for (int nb = 0; nb < 4; ++nb)
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(ws[4 * s + q][16 * nb + j], xb, acc[nb], 0, 0, 0);
     }
   }
 
-  const int f = f0 + 4 * tx;
-  const float4 sc = *reinterpret_cast<const float4*>(p.scale + f);
-  const float4 bi = *reinterpret_cast<const float4*>(p.bias + f);
+  const int64_t m = m0 + 16 * wave + j;
+  if (m >= p.M) return;
   const int64_t rep_stride = p.M * p.F;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t m = m0 + 4 * ty + i;
-    if (m >= p.M) continue;
-    const float4 o{__builtin_fmaf(acc[i][0], sc.x, bi.x), __builtin_fmaf(acc[i][1], sc.y, bi.y),
-                   __builtin_fmaf(acc[i][2], sc.z, bi.z), __builtin_fmaf(acc[i][3], sc.w, bi.w)};
+  for (int nb = 0; nb < 4; ++nb) {
+    const int f = f0 + 16 * nb + 4 * q;
+    const float4 sc = *reinterpret_cast<const float4*>(p.scale + f);
+    const float4 bi = *reinterpret_cast<const float4*>(p.bias + f);
+    const float4 o{__builtin_fmaf(acc[nb][0], sc.x, bi.x), __builtin_fmaf(acc[nb][1], sc.y, bi.y),
+                   __builtin_fmaf(acc[nb][2], sc.z, bi.z), __builtin_fmaf(acc[nb][3], sc.w, bi.w)};
     float* dst = p.out + m * p.F + f;
     for (int r = 0; r < p.reps; ++r) *reinterpret_cast<float4*>(dst + r * rep_stride) = o;
   }
