@@ -38,6 +38,7 @@ constexpr int kRcK = 16;    // reduction chunk staged in LDS
 __global__ __launch_bounds__(256) void real_conv1x1_bn_kernel(RealConvParams p) {
   __shared__ float xs[kRcK][kRcPos + 4];
   __shared__ float ws[kRcK][kRcCh + 4];
+  __shared__ __align__(16) float sO[kRcPos][kRcCh + 4];  // output tile, wave w: rows 16w..16w+15
   const int tid = threadIdx.x;
   const int64_t m0 = (int64_t)blockIdx.x * kRcPos;
   const int f0 = blockIdx.y * kRcCh;
@@ -86,16 +87,24 @@ __global__ __launch_bounds__(256) void real_conv1x1_bn_kernel(RealConvParams p) 
     }
   }
 
-  const int64_t m = m0 + 16 * wave + j;
-  if (m >= p.M) return;
+  // The wave's 16 x 64 tile goes through LDS (its own rows only: no barrier) so that each
+  // store instruction writes four whole 256-byte position rows.
+  float* so = &sO[16 * wave][0];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+    *reinterpret_cast<float4_t*>(so + j * (kRcCh + 4) + 16 * nb + 4 * q) = acc[nb];
+  const int f = f0 + 4 * j;
+  const float4 sc = *reinterpret_cast<const float4*>(p.scale + f);
+  const float4 bi = *reinterpret_cast<const float4*>(p.bias + f);
   const int64_t rep_stride = p.M * p.F;
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const int f = f0 + 16 * nb + 4 * q;
-    const float4 sc = *reinterpret_cast<const float4*>(p.scale + f);
-    const float4 bi = *reinterpret_cast<const float4*>(p.bias + f);
-    const float4 o{__builtin_fmaf(acc[nb][0], sc.x, bi.x), __builtin_fmaf(acc[nb][1], sc.y, bi.y),
-                   __builtin_fmaf(acc[nb][2], sc.z, bi.z), __builtin_fmaf(acc[nb][3], sc.w, bi.w)};
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * i + q;  // position 16 wave + row, channels 4j..4j+3
+    const int64_t m = m0 + 16 * wave + row;
+    const float4_t a = *reinterpret_cast<const float4_t*>(so + row * (kRcCh + 4) + 4 * j);
+    if (m >= p.M) continue;
+    const float4 o{__builtin_fmaf(a[0], sc.x, bi.x), __builtin_fmaf(a[1], sc.y, bi.y),
+                   __builtin_fmaf(a[2], sc.z, bi.z), __builtin_fmaf(a[3], sc.w, bi.w)};
     float* dst = p.out + m * p.F + f;
     for (int r = 0; r < p.reps; ++r) *reinterpret_cast<float4*>(dst + r * rep_stride) = o;
   }
