@@ -449,7 +449,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU fused operator only; multi-GPU runs are not part of this "
-              "build (the operator shards by batch with no communication, see DESIGN.md)", file=sys.stderr)
+              "build (the operator shards by batch: each GPU runs the same launches on its images, with no "
+              "communication)", file=sys.stderr)
         sys.exit(2)
 
     import torch
