@@ -13,7 +13,9 @@ namespace sengine {
 // accumulation in (c_in, kh, kw) order in fp32 like the reference's CPU conv.
 // Fast path (HWIO, C_out % 16 == 0, the input rows of 256 output pixels fit in LDS): each
 // thread computes 8 or 16 output channels of one pixel from LDS-staged input, with the
-// weights in SGPRs.  Generic path: one output value per thread.
+// weights in SGPRs.  Generic path: one output value per thread.  The stem + neuron entry runs
+// 3-channel 7x7 / 3x3 stems of 32 or 64 channels on the fp32 matrix cores instead
+// (stem_mfma_kernel), summing the taps in a different order.
 struct StemParams {
   const float* x;
   const float* w;
