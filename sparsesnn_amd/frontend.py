@@ -27,15 +27,34 @@ def _state(model) -> dict:
 
 
 def _neuron_attrs(model, neuron, tau, v_threshold, v_reset):
-    """Neuron hyper-parameters: taken from the model's first neuron module when it exposes
-    them (LIFNeuron keeps tau / v_threshold / v_reset, models/neurons.py:85-146), else the
-    arguments."""
+    """Neuron kind and hyper-parameters of a module tree, else the arguments (a state dict
+    carries neither).
+
+    Kind: the model's `neuron_type` ("if" builds MultiStepIFNeuron, anything else
+    MultiStepLIFNeuron, models/sewresnet.py:124,138), else the class name of its first neuron.
+    Settings: the multi-step wrappers keep them on their single-step `neuron` member
+    (MultiStepLIFNeuron.neuron = LIFNeuron(tau, v_threshold, v_reset), MultiStepIFNeuron.neuron =
+    IFNeuron(v_threshold, v_reset), models/neurons.py:195-199,217-221); a module that holds them
+    itself is read directly.  v_reset None means soft reset.  tau / v_threshold may be
+    learnable parameters (0-d tensors)."""
     sn = getattr(model, "sn1", None)
+    kind = getattr(model, "neuron_type", None)
+    if kind is not None:
+        neuron = "if" if str(kind).lower() == "if" else "lif"
+    elif sn is not None:
+        cls = type(sn).__name__.upper()
+        if "LIF" in cls:
+            neuron = "lif"
+        elif "IF" in cls:
+            neuron = "if"
     if sn is not None:
-        tau = float(getattr(sn, "tau", tau))
-        v_threshold = float(getattr(sn, "v_threshold", v_threshold))
-        v_reset = getattr(sn, "v_reset", v_reset)
-        v_reset = None if v_reset is None else float(v_reset)
+        core = getattr(sn, "neuron", sn)
+        if neuron == "lif" and hasattr(core, "tau"):
+            tau = float(core.tau)
+        if hasattr(core, "v_threshold"):
+            v_threshold = float(core.v_threshold)
+        if hasattr(core, "v_reset"):
+            v_reset = None if core.v_reset is None else float(core.v_reset)
     return neuron, tau, v_threshold, v_reset
 
 

@@ -14,7 +14,8 @@ from tests.sew_modules import SEWResNet18Modules
 @pytest.fixture(scope="module")
 def ir_and_params():
     p = sr.make_params(3, num_classes=100, fp16_weights=True)
-    model = SEWResNet18Modules.from_params(p, neuron_kw=dict(tau=2.0, v_threshold=1.0, v_reset=0.0))
+    model = SEWResNet18Modules.from_params(p, neuron_type="lif",
+                                           neuron_kw=dict(tau=2.0, v_threshold=1.0, v_reset=0.0))
     ir = frontend.sew_resnet_ir(model, T=4, batch=2, in_hw=(32, 32))
     stats = passes.optimize_ir(ir)
     return ir, stats, p
@@ -112,3 +113,41 @@ def test_non_add_connection_rejected():
     m.connect_f = "IAND"
     with pytest.raises(ValueError, match="ADD"):
         frontend.sew_resnet_ir(m, T=4, batch=1)
+
+
+@pytest.mark.parametrize("neuron_type,kw,want", [
+    ("if", {}, ("IF", 1.0, 1.0, 0.0, True)),  # the reference default (models/sewresnet.py:124)
+    ("if", dict(v_threshold=0.75, v_reset=None), ("IF", 1.0, 0.75, 0.0, False)),
+    ("lif", dict(tau=3.0, v_threshold=0.5, v_reset=0.25), ("LIF", 3.0, 0.5, 0.25, True)),
+])
+def test_neuron_settings_from_the_nested_neuron(neuron_type, kw, want):
+    """The kind comes from the model's neuron_type and the settings from the multi-step
+    wrapper's single-step `neuron` member, as in the reference's module tree; the function's
+    own defaults (LIF, tau 2) must not leak into a model that says otherwise."""
+    p = sr.make_params(3, num_classes=10)
+    m = SEWResNet18Modules.from_params(p, neuron_type=neuron_type, neuron_kw=kw)
+    assert not hasattr(m.sn1, "tau") and not hasattr(m.sn1, "v_threshold")  # nested like the reference
+    ir = frontend.sew_resnet_ir(m, T=4, batch=1)
+    neurons = [n for n in ir.nodes.values() if n.op_type in (OpType.LIF, OpType.IF)]
+    assert len(neurons) == 20
+    kind, tau, vth, vreset, hard = want
+    for n in neurons:
+        assert n.op_type.name == kind
+        np_ = n.neuron_params
+        assert (np_.tau, np_.v_threshold, np_.v_reset, np_.hard_reset) == (tau, vth, vreset, hard), n.name
+    # the compiled kernel objects carry the same neuron
+    passes.optimize_ir(ir)
+    kernels = SparseKernelCompiler(ir, batch_size=1).compile_all()
+    fused = [k for k in kernels.values() if hasattr(k, "in_planes")]
+    assert fused and all(k.spec.neuron == kind.lower() and k.spec.v_threshold == vth for k in fused)
+    assert all(k.spec.tau == (tau if kind == "LIF" else 2.0) and k.spec.hard_reset == hard for k in fused)
+
+
+def test_neuron_class_names_without_neuron_type():
+    """A tree without neuron_type: the kind follows the first neuron's class."""
+    p = sr.make_params(3, num_classes=10)
+    m = SEWResNet18Modules.from_params(p, neuron_type="lif", neuron_kw=dict(tau=4.0))
+    del m.neuron_type
+    ir = frontend.sew_resnet_ir(m, T=4, batch=1, neuron="if")
+    n = next(n for n in ir.nodes.values() if n.name == "sn1")
+    assert n.op_type == OpType.LIF and n.neuron_params.tau == 4.0

@@ -28,7 +28,8 @@ def build_engine(model, B, dev):
 def test_generic_engine_runs_sew_resnet18(dev, B, bn_random):
     p = sr.make_params(11, bn_random=bn_random, fp16_weights=True)
     x = sr.make_images(12, B)
-    model = SEWResNet18Modules.from_params(p, neuron_kw=dict(tau=2.0, v_threshold=1.0, v_reset=0.0))
+    model = SEWResNet18Modules.from_params(p, neuron_type="lif",
+                                           neuron_kw=dict(tau=2.0, v_threshold=1.0, v_reset=0.0))
     eng = build_engine(model, B, dev)
     ref_eng = SEWResNet18Engine(p, batch=B, device=dev)
     assert eng.n_launches == ref_eng.launches == 18, (eng.n_launches, ref_eng.launches)
