@@ -1,13 +1,15 @@
 """Parity helpers shared by the GPU tests, smoke() and bench.py.
 
-Acceptance rule, applied per layer call:
-  * spikes bit-exact, except for at most floor(1e-4 * n_neuron_steps) mismatching
-    neuron-steps;
+Acceptance rule (output spikes bit-exact except for a fraction
+<= 1e-4 of neurons whose reference membrane lies within 1e-3 of threshold), applied per layer
+call:
+  * at most floor(1e-4 * n_neurons) distinct neurons may have any spike mismatch (a neuron is
+    one output element over its T steps);
   * a neuron's first mismatch (its spike history agreed with the reference up to the
-    previous step) must have a reference membrane within 1e-3 of V_th at that step.  Later
-    mismatches of the same neuron follow from that flip -- one side reset, the other did
-    not, so the two membrane trajectories differ from then on -- and are counted against
-    the budget above but not required to be near threshold;
+    previous step) must have a reference membrane within 1e-3 of V_th at that step;
+  * its later mismatches are consequences of that flip -- one side reset, the other did
+    not, so the two membrane trajectories differ from then on -- and are allowed at any
+    membrane distance: they belong to a neuron already counted in the budget;
   * charged membranes within 1e-3 * max(|v_ref|, V_th), compared wherever the spike
     history of the neuron agrees with the reference up to the previous step.
 """
@@ -30,17 +32,21 @@ class ParityReport:
     far_mismatch: int      # first flips of a neuron whose reference membrane is not near threshold
     membrane_max_rel: float
     membrane_compared: int
-    flips: int = 0         # first mismatches (neurons whose history diverged)
+    flips: int = 0         # first mismatches = distinct neurons whose spike history diverged
+    neurons: int = 0       # neurons compared (n / T)
+
+    @property
+    def allowed(self) -> int:
+        return int(np.floor(SPIKE_FLIP_FRACTION * self.neurons))
 
     @property
     def ok(self) -> bool:
-        allowed = int(np.floor(SPIKE_FLIP_FRACTION * self.n))
-        return self.far_mismatch == 0 and self.spike_mismatch <= allowed and self.membrane_max_rel <= MEMBRANE_RTOL
+        return self.far_mismatch == 0 and self.flips <= self.allowed and self.membrane_max_rel <= MEMBRANE_RTOL
 
     def __str__(self):
-        return (f"n={self.n} spike_mismatch={self.spike_mismatch} (first flips {self.flips}, "
-                f"{self.spike_mismatch - self.flips} after a flip) far={self.far_mismatch} "
-                f"membrane_max_rel={self.membrane_max_rel:.3e} over {self.membrane_compared}")
+        return (f"n={self.n} neurons={self.neurons} mismatching neurons={self.flips} (allowed {self.allowed}; "
+                f"{self.spike_mismatch} neuron-steps, {self.spike_mismatch - self.flips} after a flip) "
+                f"far={self.far_mismatch} membrane_max_rel={self.membrane_max_rel:.3e} over {self.membrane_compared}")
 
 
 def compare(spikes_gpu: np.ndarray, h_gpu, spikes_ref: np.ndarray, h_ref: np.ndarray, v_th: float) -> ParityReport:
@@ -61,7 +67,7 @@ def compare(spikes_gpu: np.ndarray, h_gpu, spikes_ref: np.ndarray, h_ref: np.nda
             rel = max(rel, float(err.max()))
             cnt += int(sel.sum())
         hist_ok = hist_ok & ~mism[t]
-    return ParityReport(int(s_g.size), int(mism.sum()), far, rel, cnt, flips)
+    return ParityReport(int(s_g.size), int(mism.sum()), far, rel, cnt, flips, int(s_g[0].size))
 
 
 def compare_final(v_gpu: np.ndarray, v_ref: np.ndarray, spikes_gpu: np.ndarray, spikes_ref: np.ndarray,

@@ -51,16 +51,32 @@ def test_far_first_flip_fails():
 
 
 def test_flip_budget():
-    """Near-threshold flips are allowed only up to 1e-4 of the neuron-steps."""
-    n = 20000  # 80,000 neuron-steps: 8 mismatches allowed
+    """Near-threshold flips are allowed in at most 1e-4 of the neurons (not of the neuron-steps:
+    T = 4 steps per neuron would allow four times as many)."""
+    n = 20000  # 20,000 neurons (80,000 neuron-steps): 2 mismatching neurons allowed
     x = np.full((4, n), 0.3, np.float32)
     x[0, :] = 1.9995  # h0 = 0.99975 at every neuron: near threshold, no reference spike
     s_r, h_r, _ = _lif(x)
-    for k, ok in ((8, True), (9, False)):
+    for k, ok in ((2, True), (3, False), (8, False)):
         s_g = s_r.copy()
         s_g[0, :k] = 1.0  # first flips only, near threshold; later steps kept equal
         rep = compare(s_g, None, s_r, h_r, 1.0)
         assert rep.flips == k and rep.far_mismatch == 0 and rep.ok == ok, (k, str(rep))
+
+
+def test_budget_counts_neurons_not_steps():
+    """Two neurons that each mismatch at several steps after a near-threshold first flip use two
+    units of the budget, not one per mismatching step."""
+    n = 20000  # 2 neurons allowed
+    x = np.full((4, n), 0.3, np.float32)
+    x[0, :] = 1.9995
+    s_r, h_r, _ = _lif(x)
+    s_g = s_r.copy()
+    s_g[:, :2] = 1.0  # neurons 0 and 1 differ at all four steps
+    rep = compare(s_g, None, s_r, h_r, 1.0)
+    assert rep.spike_mismatch == 8 and rep.flips == 2 and rep.ok, str(rep)
+    s_g[:, 2] = 1.0  # a third neuron: over budget
+    assert not compare(s_g, None, s_r, h_r, 1.0).ok
 
 
 def test_membrane_tolerance():
