@@ -411,11 +411,20 @@ int sengine_amd_unpack_spikes(const uint32_t* bits, int64_t n_pos, int32_t C, vo
  * The library keeps one 2:4 blob per (device, weight pointer, geometry): prepared on the first
  * call outside stream capture (allocation, compression, one synchronising check of the 2:4
  * pattern -- the reference executor runs three eager warm-ups before it captures,
- * cpp_executor.cu:1270-1276) and reused by every later call, captured ones included.  A weight
- * first seen during capture returns -4; a weight that is not 2:4 along C_in returns -5.
- * The blob is not refreshed when the weight memory changes: call sengine_amd_release_weights()
- * (no kernel of the library may be running) after updating weights in place.
- * sengine_amd_prepare_weight does the preparation step alone.
+ * cpp_executor.cu:1270-1276) and reused by later calls.  The reference reads the weight on
+ * every call, so a cached blob must follow the weight's bytes: every call outside stream
+ * capture reads the whole weight into a 64-bit fingerprint (one small kernel and one
+ * synchronisation) and, when it differs from the fingerprint recorded at the last build --
+ * the weight was updated in place, or freed and its address handed to a different weight --
+ * rebuilds the blob in place before launching.  Calls inside a capture cannot synchronise:
+ * they use the blob as of the last call outside capture, and a captured graph replays
+ * whatever that blob holds when it runs (an eager call after a weight update refreshes it
+ * for the graph too).  A weight first seen during capture returns -4; a weight that is not
+ * 2:4 along C_in returns -5 (and so do captured calls after an eager call found it so).
+ * sengine_amd_prepare_weight does the preparation / refresh step alone.
+ * sengine_amd_release_weights frees every blob: call it only when no kernel of the library
+ * is running and no captured graph that launched a raw-weight call will be replayed again
+ * (the graph holds the blob's address).
  */
 int sengine_amd_fused_call_raw_weight(const sengine_conv_lif_desc* d, const void* data, const void* weight,
                                       int32_t w_enc, int32_t w_layout, float* state, const float* bn_scale,

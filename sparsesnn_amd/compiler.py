@@ -60,6 +60,23 @@ class SparseWeight:
         return cls(spec, blob, vb)
 
 
+def _cached_blob(cache: dict, w: torch.Tensor, prepare):
+    """The prepared form of raw weight `w`, rebuilt when `w` is not the tensor (or a view of the
+    storage) it was built from, or was modified in place since.  The cache keeps a reference to
+    the tensor it was built from: while the entry lives, that memory cannot be freed and handed
+    to a different weight (the caching allocator reuses addresses routinely), so equal
+    (address, version, shape, strides, dtype) means the same bytes.  Views share their base's
+    version counter, so an in-place update through any view is seen.  One entry per kernel
+    object (the most recent weight)."""
+    key = (w.data_ptr(), w._version, tuple(w.shape), tuple(w.stride()), w.dtype)
+    hit = cache.get("entry")
+    if hit is not None and hit[0] == key and hit[1].untyped_storage().data_ptr() == w.untyped_storage().data_ptr():
+        return hit[2]
+    blob = prepare(w)
+    cache["entry"] = (key, w, blob)
+    return blob
+
+
 def _weight_layout(spec: ConvSpec, w: torch.Tensor) -> int:
     if tuple(w.shape) == (spec.C_out, spec.C_in, spec.KH, spec.KW):
         return ops.WLAYOUT_OIHW
@@ -97,12 +114,7 @@ class FusedSparseConvBNLIFKernel:
             return w
         if not isinstance(w, torch.Tensor):
             raise TypeError("weight must be a SparseWeight or a torch.Tensor")
-        k = (w.data_ptr(), w._version, tuple(w.shape), w.dtype)
-        sw = self._wcache.get(k)
-        if sw is None:
-            sw = self.prepare_weight(w)
-            self._wcache = {k: sw}
-        return sw
+        return _cached_blob(self._wcache, w, self.prepare_weight)
 
     def __call__(self, data: torch.Tensor, weight, *args, out_enc=None, out=None, h_trace=None, x_trace=None):
         if len(args) == 3:
@@ -184,11 +196,7 @@ class DenseConvBNKernel:
         if isinstance(weight, torch.Tensor) and weight.dtype == torch.int16:
             blob = weight
         else:
-            k = (weight.data_ptr(), weight._version, tuple(weight.shape))
-            blob = self._wcache.get(k)
-            if blob is None:
-                blob = self.prepare_weight(weight)
-                self._wcache = {k: blob}
+            blob = _cached_blob(self._wcache, weight, self.prepare_weight)
         return ops.dense_conv_bn(spec, data, blob, bn_scale, bn_bias, out=out)
 
 

@@ -183,3 +183,89 @@ def test_raw_weight_rejects_dense(dev):
     finally:
         torch.cuda.synchronize()
         assert _lib.load().sengine_amd_release_weights() == 0
+
+
+def test_raw_weight_follows_the_weight_bytes(dev, tmp_path):
+    """The raw-weight call() caches a 2:4 blob per weight address, but the reference reads the
+    weight on every call: a weight freed and replaced by a different one at the same address
+    (the caching allocator hands the block straight back), or updated in place, must give the
+    new weight's spikes on the next eager call -- and a graph captured before the update replays
+    the refreshed blob once an eager call has seen the new bytes."""
+    from sparsesnn_amd import _lib
+    ir, cid, conv, bn = build()
+    node = ir.nodes[cid]
+    kern = SparseKernelCompiler(ir, batch_size=B).compile_all()[cid]
+    so = ctypes.CDLL(export.export_all_kernels({cid: kern}, ir, str(tmp_path))[cid])
+    so.init.restype = ctypes.c_int
+    so.call.restype = ctypes.c_int
+    so.call.argtypes = [ctypes.c_void_p] * 7
+    assert so.init() == 0
+    w_oihw = torch.from_numpy(ir.weights[node.weight_info.name]).float()
+    sc = torch.tensor(node.bn_scale, dtype=torch.float32, device=dev)
+    bi = torch.tensor(node.bn_bias, dtype=torch.float32, device=dev)
+    x, data = inputs(dev, seed=5)
+    mem = torch.zeros(B * H * W, F, device=dev)
+    out = torch.empty(T * B, H, W, F, dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def hwio(w):
+        return w.permute(2, 3, 1, 0).contiguous().half().to(dev)
+
+    def call(w, s=stream):
+        mem.zero_()
+        return so.call(data.data_ptr(), w.data_ptr(), mem.data_ptr(), sc.data_ptr(), bi.data_ptr(), out.data_ptr(),
+                       s.cuda_stream)
+
+    def expect(w, what):
+        c = torch.nn.Conv2d(C, F, 3, padding=1, bias=False)
+        with torch.no_grad():
+            c.weight.copy_(w)
+        r = oracle(x, c, bn)
+        rep = compare(nhwc_seq(out.float().cpu(), T), None, r.spikes.numpy(), r.h.numpy(), 1.0)
+        assert rep.ok, f"{what}: {rep}"
+        assert torch.allclose(mem.view(B, H, W, F).permute(0, 3, 1, 2).cpu(), r.v_final, atol=1e-4), what
+        return r
+
+    # three different 2:4 weights with the same shape (same magnitudes, other signs / order)
+    w_a = w_oihw
+    w_b = -w_oihw
+    w_c = torch.roll(w_oihw, shifts=1, dims=0)  # output channels permuted
+    try:
+        wa = hwio(w_a)
+        addr = wa.data_ptr()
+        assert call(wa) == 0
+        torch.cuda.synchronize()
+        r_a = expect(w_a, "first weight")
+        del wa  # freed: the caching allocator keeps the block for the next request of this size
+        wb = hwio(w_b)
+        assert wb.data_ptr() == addr, "the allocator did not reuse the address (the case this test is about)"
+        assert call(wb) == 0
+        torch.cuda.synchronize()
+        r_b = expect(w_b, "different weight at a reused address")
+        assert float((r_a.v_final - r_b.v_final).abs().max()) > 0.1  # the two weights are told apart
+
+        # a graph captured over wb; then wb updated in place (same address, same tensor)
+        g = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            rc = so.call(data.data_ptr(), wb.data_ptr(), mem.data_ptr(), sc.data_ptr(), bi.data_ptr(),
+                         out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+        assert rc == 0
+        wb.copy_(hwio(w_c))
+        assert call(wb) == 0  # eager: sees the new bytes, rebuilds the blob in place
+        torch.cuda.synchronize()
+        expect(w_c, "weight updated in place")
+        for i in range(3):  # the captured graph replays the refreshed blob
+            out.fill_(7.0)
+            mem.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            expect(w_c, f"graph replay {i} after the in-place update")
+            _ = (torch.ones(1000, device=dev) * i).sum().item()
+        # a dense weight written over it is refused on the next eager call, and by captured ones
+        wb.copy_(torch.randn(3, 3, C, F, device=dev).half())
+        assert call(wb) == -5
+        assert "2:4" in _lib.load().sengine_amd_last_error().decode()
+    finally:
+        torch.cuda.synchronize()
+        assert _lib.load().sengine_amd_release_weights() == 0
