@@ -84,10 +84,41 @@ def build_workloads(dev, T, B, seed=1234):
     return work
 
 
-def run_layer(wk):
+def run_layer(wk, state=None):
     from sparsesnn_amd import ops
     ops.fused_sparse_conv_bn_lif(wk["spec"], wk["data"], wk["values"], wk["meta"], wk["scale"], wk["bias"],
-                                 out=wk["out"])
+                                 out=wk["out"], state=state)
+
+
+def state_launch_times(dev, work, warmup: int):
+    """The sweep launches with a live fp32 (B*OH*OW, C_out) membrane (V0 read, final membrane
+    written), as the reference executor binds one to every fused node: per-launch durations
+    from event-bracketed bursts, like the stateless ones, and the kernel instance each runs.
+    Reported beside the headline; not part of `value` (the roofline's bytes exclude the
+    membrane)."""
+    import torch
+    from sparsesnn_amd import ops
+    stream = torch.cuda.current_stream(dev)
+    per, plans = {}, {}
+    for wk in work:
+        s = wk["spec"]
+        _, _, M, _ = ops.geometry(s)
+        mem = torch.zeros(M, s.C_out, dtype=torch.float32, device=dev)
+        plans[wk["name"]] = ops.fused_plan(s, state=True)
+        for _ in range(max(1, warmup)):
+            run_layer(wk, mem)
+        ts = []
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(BURST):
+                run_layer(wk, mem)
+            b.record(stream)
+            torch.cuda.synchronize(dev)
+            ts.append(a.elapsed_time(b) * 1e-3 / BURST)
+        per[wk["name"]] = round(statistics.median(ts) * 1e6, 2)
+        del mem
+    return per, {k: v for i, (k, v) in enumerate(plans.items()) if i % len(DENSITIES) == 0}
 
 
 def abi_work(wk):
@@ -100,13 +131,19 @@ def abi_work(wk):
 
 
 def bench_abi(dev, work, warmup: int, steps: int):
-    """The 15 sweep launches through the reference's native ABI: one exported per-node .so per
-    shape (export.export_kernel_so), call(data, weight, state, bn_scale, bn_bias, spikes, stream)
-    with fp16 NHWC spikes in and out and the runtime's fp16 (KH, KW, C_in, C_out) weight (the
-    library builds the 2:4 blob on the first eager call).  Per-launch durations from event-
-    bracketed bursts, the step from a hipGraph of the 15 calls; the fp16 output is checked
-    against the bit path's output of the same inputs."""
+    """The 15 sweep launches through the reference's native ABI, called as its executor calls
+    them (sengine/csrc/cpp_executor.cu:704-718,909-913): one exported per-node .so per shape
+    (export.export_kernel_so), call(data, weight, state, bn_scale, bn_bias, spikes, stream) with
+    fp16 NHWC spikes in and out, the runtime's fp16 (KH, KW, C_in, C_out) weight (the library
+    builds the 2:4 blob on the first eager call) and a live fp32 (B*OH*OW, C_out) membrane per
+    node, zeroed before each call inside the captured graph as sengine_reset_membranes zeroes
+    them before every replay (:1196-1203).  The same calls with state = NULL are reported beside
+    it.  Per-launch durations from hipGraphs of BURST back-to-back calls of one node (eager
+    raw-weight calls re-check the weight's bytes and synchronise, so eager bursts would time
+    that check); the step from a hipGraph of the 15 (reset, call) pairs.  The fp16 output is
+    checked against the bit path's output of the same inputs, with and without state."""
     import ctypes
+    import dataclasses
     import tempfile
     import torch
     from sparsesnn_amd import _lib, export, ops
@@ -129,76 +166,105 @@ def bench_abi(dev, work, warmup: int, steps: int):
         x = ops.unpack_spikes(wk["data"], s.C_in)
         OH, OW, M, _ = ops.geometry(s)
         out = torch.empty(s.T * s.B, OH, OW, s.C_out, dtype=torch.float16, device=dev)
-        args = (x.data_ptr(), w.data_ptr(), None, wk["scale"].data_ptr(), wk["bias"].data_ptr(), out.data_ptr())
-        calls.append(dict(wk=wk, so=so, args=args, x=x, out=out, bytes=abi_work(wk)))
+        mem = torch.zeros(M, s.C_out, dtype=torch.float32, device=dev)
+        calls.append(dict(wk=wk, so=so, x=x, out=out, mem=mem, w=w, bytes=abi_work(wk),
+                          state_bytes=2 * mem.numel() * 4,
+                          plan=ops.fused_plan(dataclasses.replace(s, in_enc=ops.ENC_F16, out_enc=ops.ENC_F16),
+                                              state=True)))
 
-    def run(c, st):
-        rc = c["so"].call(*c["args"], st.cuda_stream)
+    def run(c, st, with_state):
+        rc = c["so"].call(c["x"].data_ptr(), c["w"].data_ptr(), c["mem"].data_ptr() if with_state else None,
+                          c["wk"]["scale"].data_ptr(), c["wk"]["bias"].data_ptr(), c["out"].data_ptr(),
+                          st.cuda_stream)
         if rc:
             raise RuntimeError(f"call() of {c['wk']['name']} returned {rc}: "
                                f"{_lib.load().sengine_amd_last_error().decode()}")
 
-    for _ in range(max(1, warmup)):
+    for _ in range(3):  # eager warm-up calls, as the reference executor's (cpp_executor.cu:1270-1276)
         for c in calls:
-            run(c, stream)
+            c["mem"].zero_()
+            run(c, stream, True)
     torch.cuda.synchronize(dev)
-    mismatch = 0
-    for c in calls:
-        run_layer(c["wk"])
-        ref = ops.unpack_spikes(c["wk"]["out"], c["wk"]["spec"].C_out)
-        mismatch += int((ref != c["out"]).sum().item())
-    per = {c["wk"]["name"]: [] for c in calls}
-    evs = []
-    for _ in range(3):
+    mismatch = {True: 0, False: 0}
+    for with_state in (True, False):
         for c in calls:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for _ in range(BURST):
-                run(c, stream)
-            b.record(stream)
-            evs.append((c["wk"]["name"], a, b))
-    torch.cuda.synchronize(dev)
-    for name, a, b in evs:
-        per[name].append(a.elapsed_time(b) * 1e-3 / BURST)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        cs = torch.cuda.current_stream(dev)
-        for c in calls:
-            run(c, cs)
-    for _ in range(max(1, warmup)):
-        graph.replay()
-    torch.cuda.synchronize(dev)
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for _ in range(steps):
-        graph.replay()
-    t1.record(stream)
-    torch.cuda.synchronize(dev)
-    step_s = t0.elapsed_time(t1) * 1e-3 / steps
-    ideal = sum(max(c["wk"]["flops"] / P_SPARSE, c["bytes"] / BW_HBM) for c in calls)
-    n = sum(len(v) for v in per.values())
-    avg = sum(sum(v) for v in per.values()) / n
-    hbm = [c for c in calls if c["bytes"] / BW_HBM > c["wk"]["flops"] / P_SPARSE]
-    res = {
-        "value": round(100.0 * ideal / step_s, 3),
-        "unit": "% of roofline (sum of per-layer max(F/5.0 PFLOP/s, B_fp16/8 TB/s) / step time)",
-        "ms_per_step": round(step_s * 1e3, 4),
-        "per_layer_us": {k: round(statistics.median(v) * 1e6, 2) for k, v in per.items()},
-        "spikes_differing_from_bit_path": mismatch,
+            c["mem"].zero_()
+            run(c, stream, with_state)
+            run_layer(c["wk"])
+            ref = ops.unpack_spikes(c["wk"]["out"], c["wk"]["spec"].C_out)
+            mismatch[with_state] += int((ref != c["out"]).sum().item())
+
+    def graph_of(fn):
+        g = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize(dev)
+        with torch.cuda.graph(g):
+            fn(torch.cuda.current_stream(dev))
+        return g
+
+    def timed(g, n):
+        for _ in range(max(1, warmup)):
+            g.replay()
+        torch.cuda.synchronize(dev)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(n):
+            g.replay()
+        b.record(stream)
+        torch.cuda.synchronize(dev)
+        return a.elapsed_time(b) * 1e-3 / n
+
+    res = {}
+    for with_state in (True, False):
+        per = {}
+        for c in calls:  # BURST calls of one node per graph (the membrane carries on: same work)
+            g = graph_of(lambda st, c=c: [run(c, st, with_state) for _ in range(BURST)])
+            per[c["wk"]["name"]] = [timed(g, 3) / BURST for _ in range(3)]
+            del g
+
+        def step(st):
+            for c in calls:
+                if with_state:
+                    c["mem"].zero_()  # the membrane reset, a fill kernel inside the graph
+                run(c, st, with_state)
+        g = graph_of(step)
+        step_s = timed(g, steps)
+        del g
+        ideal = sum(max(c["wk"]["flops"] / P_SPARSE, c["bytes"] / BW_HBM) for c in calls)
+        avg = sum(statistics.median(v) for v in per.values()) / len(per)
+        hbm = [c for c in calls if c["bytes"] / BW_HBM > c["wk"]["flops"] / P_SPARSE]
+        r = {
+            "value": round(100.0 * ideal / step_s, 3),
+            "unit": "% of roofline (sum of per-layer max(F/5.0 PFLOP/s, B_fp16/8 TB/s) / step time)",
+            "ms_per_step": round(step_s * 1e3, 4),
+            "per_layer_us": {k: round(statistics.median(v) * 1e6, 2) for k, v in per.items()},
+            "spikes_differing_from_bit_path": mismatch[with_state],
+            "roofline": {
+                "bound": "hbm" if len(hbm) * 2 > len(calls) else "mfma",
+                "achieved_tflops": round(sum(c["wk"]["flops"] for c in calls) / len(calls) / avg / 1e12, 2),
+                "achieved_gbps": round(sum(c["bytes"] for c in calls) / len(calls) / avg / 1e9, 1),
+                "avg_launch_us": round(avg * 1e6, 3),
+                "hbm_bound_layers": [c["wk"]["name"] for c in hbm],
+            },
+        }
+        if with_state:
+            r["state"] = ("live fp32 (B*OH*OW, C_out) membrane per node: V0 read, final membrane written; zeroed "
+                          "by a fill kernel before each call inside the step's graph")
+            r["state_bytes_per_step"] = sum(c["state_bytes"] for c in calls)
+            r["state_bytes_note"] = ("membrane read + write, not part of B_fp16 (the roofline's bytes); the step "
+                                     "also holds the 15 membrane fills")
+            r["plans"] = {c["wk"]["name"]: c["plan"] for c in calls[::len(DENSITIES)]}
+        res[with_state] = r
+    out = dict(res[True])
+    out.update({
         "launches_per_step": len(calls),
-        "step": "hipGraph replay of the 15 exported-.so call()s",
-        "io": "fp16 NHWC spikes in and out, fp16 HWIO weight (2:4 blob built once by the library)",
-        "roofline": {
-            "bound": "hbm" if len(hbm) * 2 > len(calls) else "mfma",
-            "achieved_tflops": round(sum(c["wk"]["flops"] for c in calls) / len(calls) / avg / 1e12, 2),
-            "achieved_gbps": round(sum(c["bytes"] for c in calls) / len(calls) / avg / 1e9, 1),
-            "avg_launch_us": round(avg * 1e6, 3),
-            "hbm_bound_layers": [c["wk"]["name"] for c in hbm],
-        },
-    }
+        "step": "hipGraph replay of the 15 exported-.so call()s, each after its membrane reset",
+        "io": "fp16 NHWC spikes in and out, fp16 HWIO weight (2:4 blob built once by the library), "
+              "fp32 membrane state",
+        "stateless": res[False],
+    })
     del calls
     torch.cuda.empty_cache()
-    return res
+    return out
 
 
 CPU_WARMUP, CPU_MIN_RUNS = 3, 10  # 3 warmups, median of >= 10 runs
@@ -580,6 +646,11 @@ def main():
             "frac_of_measured": round(avg_flops / avg_launch / (calib["smfmac_tflops_dense_equiv"] * 1e12), 4),
         },
     }
+    st_per, st_plans = state_launch_times(dev, work, args.warmup)
+    result["config"]["per_layer_us_state"] = st_per
+    result["config"]["state_plans"] = st_plans
+    result["config"]["state_note"] = ("the same launches with a live fp32 membrane (V0 read, final membrane written: "
+                                      "8 bytes per output neuron, not part of B_min)")
     if not args.no_abi:
         result["abi_f16"] = bench_abi(dev, work, warmup=args.warmup, steps=args.steps)
     if not args.no_cpu_baseline:

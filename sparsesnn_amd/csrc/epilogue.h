@@ -256,6 +256,56 @@ __device__ __forceinline__ void lean_epilogue_stateless(const float4_t (&acc)[4]
   }
 }
 
+// lean_epilogue_stateless with a membrane state, for the persistent kernels (the reference
+// executor always binds one, sengine/csrc/cpp_executor.cu:704-718,909-913): V0 is read from
+// state (fp32, F channels per position: the runtime's (B*OH*OW, C_out) membrane,
+// sengine/cuda_graph_runtime.py:385-390; the lane's 16 channels are 64 contiguous bytes), every
+// step charges from the carried membrane and resets, and the membrane after step T - 1 is
+// written back.  Same arithmetic as lif_epilogue's branch-free hard-reset loop.  Lanes with
+// `valid` false compute but load and store nothing.
+template <int MODE, int OUT_ENC>
+__device__ __forceinline__ void lean_epilogue_state(const float4_t (&acc)[4][4], bool valid, int m, int F, int cob,
+                                                    const NeuronParams& np, const float* fsc, const float* fbi,
+                                                    uint8_t* __restrict__ out, int M, const SewAdd& sa, float* state) {
+  constexpr int T = 4;
+  const SpikeDst sd = spike_dst(sa, out, F, cob);
+  float* st = state + (size_t)m * F + cob;
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 16; j += 4) {
+    const float4_t v4 = valid ? *reinterpret_cast<const float4_t*>(st + j) : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[j + e] = v4[e];
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j4 = 12; j4 >= 0; j4 -= 4) {
+      const float4_t s4 = *reinterpret_cast<const float4_t*>(fsc + j4);
+      const float4_t b4 = *reinterpret_cast<const float4_t*>(fbi + j4);
+#pragma unroll
+      for (int e = 3; e >= 0; --e) {
+        const int j = j4 + e;
+        const float xin = __builtin_fmaf(acc[t][j >> 2][j & 3], s4[e], b4[e]);
+        const float h = MODE == EPI_LIF_HARD ? __builtin_fmaf(v[j], np.decay, xin) : __fadd_rn(v[j], xin);
+        fire_hard(h, np.vth, np.vreset, v[j], word);
+      }
+    }
+    if (!valid) continue;
+    if (OUT_ENC == SENGINE_ENC_BITS) {
+      *reinterpret_cast<uint16_t*>(sd.out + ((((size_t)t * M + m) * sd.F + sd.cob) >> 3)) = (uint16_t)word;
+    } else {
+      const uint32_t zr[kResWords] = {};
+      store_spike_f16(word, ((size_t)t * M + m) * F + cob, out, sa, zr);
+    }
+  }
+  if (valid) {
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) *reinterpret_cast<float4_t*>(st + j) = float4_t{v[j], v[j + 1], v[j + 2], v[j + 3]};
+  }
+}
+
 // 4x4 transpose of 16-byte chunks across the four 16-lane rows of a wave: afterwards chunk q of
 // row r holds what chunk r of row q held (rows r = lane / 16).  Two v_permlane32_swap and two
 // v_permlane16_swap (gfx950) per dword position; every lane of the wave must execute it.

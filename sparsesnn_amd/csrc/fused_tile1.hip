@@ -170,14 +170,15 @@ static int device_cus() {
 }
 
 // The persistent 1x1 kernel (tile1ps.h) serves the token Linears when a layer is what it is
-// written for: stride 1, T = 4, 16 | M, an even chunk count, a fast stateless neuron, no trace,
-// state or bit-plane residual.  fp16 input with spike-bit or fp16 output (q/k/v and fc1; the
+// written for: stride 1, T = 4, 16 | M, an even chunk count, a fast hard-reset neuron, no trace
+// or bit-plane residual.  fp16 input with spike-bit or fp16 output (q/k/v and fc1; the
 // exported per-node call's fp16-in, fp16-out 1x1 layers), no fp16 residual: 256-channel
 // super-blocks (4 waves, phases of 2 chunks) or 384-channel ones (6 waves, phases of 3 chunks,
 // an even phase count).  Spike-bit input with fp16 output, optionally + the fp16 residual (proj,
 // fc2) or spike bits (1x1 layers of convolutional networks): 384-channel super-blocks with
-// phases of 6 chunks, or 256-channel ones with 4.  SENGINE_AMD_TILE1_PS=0 turns it off.
-// Returns waves * 16 + chunks per phase, or 0.
+// phases of 6 chunks, or 256-channel ones with 4.  A membrane state (the reference executor's
+// call) is served on the fp16-in, fp16-out and the bits-in, bits-out forms.
+// SENGINE_AMD_TILE1_PS=0 turns it off.  Returns waves * 16 + chunks per phase, or 0.
 static int tile1ps_config(const sengine_conv_lif_desc* d, const Geometry& geo, const TileChoice& c, int mode,
                           const FusedArgs* a) {
   const int nchunk = d->C_in / 64;
@@ -185,7 +186,8 @@ static int tile1ps_config(const sengine_conv_lif_desc* d, const Geometry& geo, c
   if (env == 0 || c.k3 || d->T != 4 || d->stride_h != 1 || d->stride_w != 1 || d->weight_planes != 1 ||
       geo.M % 16 != 0 || nchunk % 2 != 0 || (mode != EPI_LIF_HARD && mode != EPI_IF_HARD))
     return 0;
-  if (a && (a->state || a->sew.res || a->sew.real_out || a->h_trace || a->x_trace)) return 0;
+  if (a && (a->sew.res || a->sew.real_out || a->h_trace || a->x_trace)) return 0;
+  if (a && a->state && (d->in_enc != d->out_enc || a->sew.res16 || a->sew.split_c)) return 0;
   if (d->in_enc == SENGINE_ENC_F16) {
     if (!c.pm || (a && a->sew.res16)) return 0;
     if ((int64_t)d->T * geo.M * d->C_in * 2 > 0x7fffffff) return 0;  // piece offsets are 32-bit
@@ -209,8 +211,8 @@ static int tile1ps_slots(int nw) {
 
 // The persistent 3x3 kernel (tile3ps.h) takes the tile launches it is written for: T = 4, spike
 // bits in and out, one channel group per wave, no reduction split, one-tap prefetch, a fast
-// stateless neuron, no trace, state or residual, and at least two tiles per resident workgroup
-// (three per CU).  SENGINE_AMD_TILE3_PS=0 turns it off, =2 lifts the two-tile rule.
+// hard-reset neuron (with or without a membrane state), no trace or residual, and at least two
+// tiles per resident workgroup (three per CU).  SENGINE_AMD_TILE3_PS=0 turns it off, =2 lifts the two-tile rule.
 // SENGINE_AMD_PS_SLOTS=n launches the persistent kernels on n workgroups instead (tests use it
 // to make small layers walk several tiles or groups per workgroup).
 static int ps_slots_override() { return env_int_now("SENGINE_AMD_PS_SLOTS", 0); }
@@ -224,8 +226,7 @@ static bool tile3ps_eligible(const sengine_conv_lif_desc* d, const TileChoice& c
   const int env = env_int_now("SENGINE_AMD_TILE3_PS", -1);
   if (env == 0 || (env != 2 && (int64_t)c.ntiles * (d->C_out / 64) < 2LL * tile3ps_slots())) return false;
   // (its epilogue stores plain spike-bit rows: no SEW sum, no channel-split planes)
-  if (a && (a->state || a->sew.res || a->sew.res16 || a->sew.real_out || a->sew.split_c || a->h_trace ||
-            a->x_trace))
+  if (a && (a->sew.res || a->sew.res16 || a->sew.real_out || a->sew.split_c || a->h_trace || a->x_trace))
     return false;
   return true;
 }
@@ -245,8 +246,8 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
   if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
     const int nw = ps >> 4, npg = (int)(geo.M / 16), nsb = d->C_out / (64 * nw);
     const int per = tile1ps_per(npg, nsb, tile1ps_slots(nw));
-    return snprintf(buf, len, "tile1ps<T=4,NW=%d,CG=%d,in=%s,out=%s,epi=%s> grid=%d (persistent, %d groups)", nw,
-                    ps & 15, f16in ? "f16" : "bits", oe, kEpi[mode], per * nsb, npg);
+    return snprintf(buf, len, "tile1ps<T=4,NW=%d,CG=%d,in=%s,out=%s,epi=%s%s> grid=%d (persistent, %d groups)", nw,
+                    ps & 15, f16in ? "f16" : "bits", oe, kEpi[mode], a.state ? ",state" : "", per * nsb, npg);
   }
   if (f16in && c.pm)
     return snprintf(buf, len, "tile1pm<T=4,GPW=1,CG=2,NW=%d,in=f16,out=%s,epi=%s> grid=%lld", c.pmw, oe, epi,
@@ -264,8 +265,8 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
     const TileShape s = kShapes3[c.shape];
     const int ncb = d->C_out / 64;
     const int per = std::max(1, std::min(tile3ps_slots() / ncb, c.ntiles));
-    return snprintf(buf, len, "tile3ps<T=4,TR=%d,TC=%d,GR=%d,out=bits,epi=%s> grid=%d (persistent, %d tiles)", s.TR,
-                    s.TC, s.GR, kEpi[mode], per * ncb, c.ntiles);
+    return snprintf(buf, len, "tile3ps<T=4,TR=%d,TC=%d,GR=%d,out=bits,epi=%s%s> grid=%d (persistent, %d tiles)",
+                    s.TR, s.TC, s.GR, kEpi[mode], a.state ? ",state" : "", per * ncb, c.ntiles);
   }
   if (c.k3) {
     const TileShape s = kShapes3[c.shape];
@@ -313,9 +314,10 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
   if (d->in_enc == SENGINE_ENC_F16) {
     if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
     if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
-      if (d->out_enc == SENGINE_ENC_F16)  // fp16 in and out: the exported per-node call's form
-        return ps == 6 * 16 + 3 ? launch_tile1ps<6, 3, SENGINE_ENC_F16, SENGINE_ENC_F16>(p, mode, tile1ps_slots(6), stream)
-                                : launch_tile1ps<4, 2, SENGINE_ENC_F16, SENGINE_ENC_F16>(p, mode, tile1ps_slots(4), stream);
+      if (d->out_enc == SENGINE_ENC_F16)  // fp16 in and out: the exported per-node call's form (with state)
+        return ps == 6 * 16 + 3
+                   ? launch_tile1ps<6, 3, SENGINE_ENC_F16, SENGINE_ENC_F16, 0, true>(p, mode, tile1ps_slots(6), stream)
+                   : launch_tile1ps<4, 2, SENGINE_ENC_F16, SENGINE_ENC_F16, 0, true>(p, mode, tile1ps_slots(4), stream);
       return ps == 6 * 16 + 3 ? launch_tile1ps<6, 3, SENGINE_ENC_F16, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(6), stream)
                               : launch_tile1ps<4, 2, SENGINE_ENC_F16, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(4), stream);
     }
@@ -331,10 +333,12 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
     if (d->out_enc == SENGINE_ENC_F16)
       return nw == 6 ? launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_F16>(p, mode, tile1ps_slots(6), stream)
                      : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_F16>(p, mode, tile1ps_slots(4), stream);
-    if (nw == 6) return launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(6), stream);
+    if (nw == 6)
+      return launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_BITS, 0, true>(p, mode, tile1ps_slots(6), stream);
     // one 4-chunk phase (C_in = 256): the A operands stay resident
-    return p.nchunk == 4 ? launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_BITS, 1>(p, mode, tile1ps_slots(4), stream)
-                         : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_BITS>(p, mode, tile1ps_slots(4), stream);
+    return p.nchunk == 4
+               ? launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_BITS, 1, true>(p, mode, tile1ps_slots(4), stream)
+               : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_BITS, 0, true>(p, mode, tile1ps_slots(4), stream);
   }
   if (c.pm == 2) return c.cg == 4 ? launch_tile1pm<4, 2, 4>(p, d->out_enc, mode, stream)
                                   : launch_tile1pm<4, 2, 2>(p, d->out_enc, mode, stream);

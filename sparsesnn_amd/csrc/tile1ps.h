@@ -28,8 +28,10 @@
 // form, the transformer's residual).
 //
 // Restricted to what the token Linears need: T = 4, stride 1 (position m's input row is
-// t*M + m), M a multiple of 16, an even chunk count, a hard-reset LIF or IF without state or
-// traces, spike bits out or fp16 spikes (+ an fp16 residual) out.
+// t*M + m), M a multiple of 16, an even chunk count, a hard-reset LIF or IF without traces,
+// spike bits out or fp16 spikes (+ an fp16 residual) out.  STATE: the membrane state of the
+// reference's call (V0 read, final membrane written; lean_epilogue_state), else V0 = 0 and the
+// final membrane is not kept.
 #pragma once
 #include "tile1pm.h"
 
@@ -42,7 +44,7 @@ namespace sengine {
 // ARES = 1 (spike-bit input whose whole reduction is one phase, nchunk == CG == 4): the wave's
 // A operands for all chunks (80 registers) are loaded once and stay resident, since its channel
 // block never changes; the loop then issues no A-operand loads at all.
-template <int NW, int CG, int MODE, int IN_ENC, int OUT_ENC, int ARES = 0>
+template <int NW, int CG, int MODE, int IN_ENC, int OUT_ENC, int ARES = 0, bool STATE = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   constexpr int T = 4;
@@ -54,7 +56,7 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   constexpr int PPT = ITEMS / NTH;
   constexpr int CHB = F16IN ? 128 : 8;  // bytes of one 64-channel chunk in an input row
   using Item = std::conditional_t<F16IN, u32x4_t, uint2>;
-  static_assert(MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD, "fast stateless modes only");
+  static_assert(MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD, "fast hard-reset modes only");
   static_assert(ITEMS % NTH == 0, "every thread stages the same number of items");
   __shared__ uint2 sB[2][CG * CE];
   __shared__ float sCoef[2][NW * 64];
@@ -232,8 +234,12 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
     if (ph == nphase - 1) {  // the group's reduction is complete
       const int m = (j0 + blk * J) * 16 + col;
       const int cl = wave * 64 + g * 16;
-      lean_epilogue_stateless<MODE, OUT_ENC>(acc, true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl], &sCoef[1][cl],
-                                             p.out, p.M, p.sew);
+      if constexpr (STATE)
+        lean_epilogue_state<MODE, OUT_ENC>(acc, true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl], &sCoef[1][cl],
+                                           p.out, p.M, p.sew, p.state);
+      else
+        lean_epilogue_stateless<MODE, OUT_ENC>(acc, true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl],
+                                               &sCoef[1][cl], p.out, p.M, p.sew);
 #pragma unroll
       for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -251,13 +257,24 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
 inline int tile1ps_per(int npg, int nsb, int slots) { return std::max(1, std::min(slots / nsb, npg)); }
 
 // Launch on `slots` resident workgroups (a multiple of the super-block count, at most one per
-// (group, super-block) pair).
-template <int NW, int CG, int IN_ENC, int OUT_ENC, int ARES = 0>
+// (group, super-block) pair).  WITH_STATE: the instance also has a state form, taken when
+// p.state is set (the host routes state-carrying calls here only for such instances).
+template <int NW, int CG, int IN_ENC, int OUT_ENC, int ARES = 0, bool WITH_STATE = false>
 hipError_t launch_tile1ps(const TileParams& p, int mode, int slots, hipStream_t s) {
   const int npg = p.M / 16;
   const int nsb = p.F / (NW * 64);
   const int per = tile1ps_per(npg, nsb, slots);
   const dim3 grid((unsigned)(per * nsb)), block(64 * NW);
+  if (WITH_STATE && p.state) {
+    if (mode == EPI_LIF_HARD)
+      hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC, ARES, WITH_STATE>), grid, block,
+                         0, s, p, npg, nsb);
+    else
+      hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD, IN_ENC, OUT_ENC, ARES, WITH_STATE>), grid, block,
+                         0, s, p, npg, nsb);
+    return hipGetLastError();
+  }
+  if (p.state) return hipErrorInvalidValue;  // no state form of this instance
   if (mode == EPI_LIF_HARD)
     hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC, ARES>), grid, block, 0, s, p, npg,
                        nsb);

@@ -11,14 +11,15 @@
 // instead of opening every workgroup's life.
 //
 // Restricted to the fast launches: T = 4, one 64-channel group per wave, no reduction split,
-// one-tap operand prefetch, spike bits in and out, a hard-reset LIF or IF without state, traces
-// or residual.
+// one-tap operand prefetch, spike bits in and out, a hard-reset LIF or IF without traces or
+// residual.  STATE: the membrane state of the reference's call (V0 read, final membrane
+// written; lean_epilogue_state), else V0 = 0 and the final membrane is not kept.
 #pragma once
 #include "tile_kernel.h"
 
 namespace sengine {
 
-template <int TR, int TC, int GR, int MODE>
+template <int TR, int TC, int GR, int MODE, bool STATE>
 __global__ __launch_bounds__((TileGeom<3, TR, TC, GR>::NTHR)) __attribute__((amdgpu_waves_per_eu(3)))
 void fused_tile3ps_kernel(TileParams p, int ncb) {
   using Gm = TileGeom<3, TR, TC, GR>;
@@ -29,7 +30,7 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
   constexpr int UPT = (UNITS + NTHR - 1) / NTHR;  // per thread
   constexpr int PAD = Gm::PAD;
   constexpr int TS = Gm::TS;
-  static_assert(MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD, "fast stateless modes only");
+  static_assert(MODE == EPI_LIF_HARD || MODE == EPI_IF_HARD, "fast hard-reset modes only");
   __shared__ uint2 sB[T * TS];
   __shared__ float sCoef[4][64];
 
@@ -209,9 +210,14 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
       const bool valid = pin && oh < p.OH && ow < p.OW;
       const int m = valid ? (b * p.OH + oh) * p.OW + ow : 0;
       const int cl = g * 16;
-      const EpiCoeffs cf{&sCoef[0][cl], &sCoef[1][cl], &sCoef[2][cl], &sCoef[3][cl]};
-      fast_epilogue_stateless<T, SENGINE_ENC_BITS, MODE>(acc, valid, m, p.M, p.F, Gb * 64 + cl, np, cf, p.out, nosew,
-                                                         nullptr);
+      if constexpr (STATE) {
+        lean_epilogue_state<MODE, SENGINE_ENC_BITS>(acc, valid, m, p.F, Gb * 64 + cl, np, &sCoef[0][cl],
+                                                    &sCoef[1][cl], p.out, p.M, nosew, p.state);
+      } else {
+        const EpiCoeffs cf{&sCoef[0][cl], &sCoef[1][cl], &sCoef[2][cl], &sCoef[3][cl]};
+        fast_epilogue_stateless<T, SENGINE_ENC_BITS, MODE>(acc, valid, m, p.M, p.F, Gb * 64 + cl, np, cf, p.out,
+                                                           nosew, nullptr);
+      }
 #pragma unroll
       for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -232,10 +238,16 @@ hipError_t launch_tile3ps(const TileParams& p, int mode, int slots, hipStream_t 
   const int ncb = p.F / 64;
   const int per = std::max(1, std::min(slots / ncb, p.ntiles));
   const dim3 grid((unsigned)(per * ncb)), block(TileGeom<3, TR, TC, GR>::NTHR);
-  if (mode == EPI_LIF_HARD)
-    hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_LIF_HARD>), grid, block, 0, s, p, ncb);
-  else
-    hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_IF_HARD>), grid, block, 0, s, p, ncb);
+  if (p.state) {
+    if (mode == EPI_LIF_HARD)
+      hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_LIF_HARD, true>), grid, block, 0, s, p, ncb);
+    else
+      hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_IF_HARD, true>), grid, block, 0, s, p, ncb);
+  } else if (mode == EPI_LIF_HARD) {
+    hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_LIF_HARD, false>), grid, block, 0, s, p, ncb);
+  } else {
+    hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_IF_HARD, false>), grid, block, 0, s, p, ncb);
+  }
   return hipGetLastError();
 }
 
