@@ -1,7 +1,9 @@
 """GPU parity of Spikformer as a whole network: the SPS stages, every block
 teacher-forced on the oracle's own token stream, the whole forward from one hipGraph replay
-against the oracle's logits, and the config-4 shape (224x224, embed 384, 8 heads, 8 blocks)
-with SPS and the first block checked on one image."""
+against the oracle's logits, and the config-4 shape (224x224, embed 384, 8 heads, 8 blocks):
+at the benchmark's batch of 32 every SPS stage and all 8 blocks are checked on sampled images
+(images are independent through the network, so each launch's rows for an image are compared
+with the oracle run on that image's inputs), and on one and four images."""
 import numpy as np
 import pytest
 import torch
@@ -57,6 +59,14 @@ def _stream_of(eng, x, planes, dev):
     return _planes_of(x, planes, dev)
 
 
+def _rows(t, T, B, sel):
+    """Rows (T*B, ...) of a device tensor -> the rows of images `sel` (T*len(sel), ...)."""
+    if sel is None:
+        return t
+    v = t.reshape(T, B, *t.shape[1:])[:, list(sel)]
+    return v.reshape(T * len(sel), *t.shape[1:])
+
+
 def _stage(p, name, x_seq):
     bn = sf.bn_of(p, f"patch_embed.{name.replace('conv', 'bn')}")
     return ref.fused_layer(x_seq, p[f"patch_embed.{name}.weight"], bn, 1, 1, 1, "lif", 2.0, 1.0, 0.0)
@@ -68,35 +78,40 @@ def _pool(x):
     return y.view(T, -1, *y.shape[1:])
 
 
-def _check_sps(eng, p, x_img, T, B, embed):
-    """Each SPS stage of the engine against the oracle stage run on the engine's own input."""
+def _check_sps(eng, p, x_img, T, B, embed, sel=None):
+    """Each SPS stage of the engine against the oracle stage run on the engine's own input (of
+    images `sel` only, when given)."""
     H, W = eng.stem_spec.H, eng.stem_spec.W
     c8, c4, c2 = embed // 8, embed // 4, embed // 2
     P8, P4 = eng.stem_spec.C_out, eng.c1.spec.C_out
+    if sel is not None:
+        x_img = x_img[list(sel)]
+    Bs = B if sel is None else len(sel)
     r0 = _stage(p, "proj_conv", x_img.float().unsqueeze(0).repeat(T, 1, 1, 1, 1))
-    s0 = _img_bits(eng.s0, T, B, P8, H, W)
+    B = Bs
+    s0 = _img_bits(_rows(eng.s0, T, eng.B, sel), T, B, P8, H, W)
     assert float(s0[:, :, c8:].abs().sum()) == 0  # padded channels never fire
     rep = compare(s0[:, :, :c8].numpy(), None, r0.spikes.numpy(), r0.h.numpy(), 1.0)
     assert rep.ok, f"proj_conv {rep}"
     r1 = _stage(p, "proj_conv1", s0[:, :, :c8])
-    s1 = _img_bits(eng.s1, T, B, P4, H, W)
+    s1 = _img_bits(_rows(eng.s1, T, eng.B, sel), T, B, P4, H, W)
     assert float(s1[:, :, c4:].abs().sum()) == 0
     rep = compare(s1[:, :, :c4].numpy(), None, r1.spikes.numpy(), r1.h.numpy(), 1.0)
     assert rep.ok, f"proj_conv1 {rep}"
     r2 = _stage(p, "proj_conv2", s1[:, :, :c4])
-    s2 = _img_bits(eng.s2, T, B, c2, H, W)
+    s2 = _img_bits(_rows(eng.s2, T, eng.B, sel), T, B, c2, H, W)
     rep = compare(s2.numpy(), None, r2.spikes.numpy(), r2.h.numpy(), 1.0)
     assert rep.ok, f"proj_conv2 {rep}"
-    p2 = _img_bits(eng.p2, T, B, c2, eng.H2, eng.W2)
+    p2 = _img_bits(_rows(eng.p2, T, eng.B, sel), T, B, c2, eng.H2, eng.W2)
     assert torch.equal(p2, _pool(s2))
     r3 = _stage(p, "proj_conv3", p2)
-    s3 = _img_bits(eng.s3, T, B, embed, eng.H2, eng.W2)
+    s3 = _img_bits(_rows(eng.s3, T, eng.B, sel), T, B, embed, eng.H2, eng.W2)
     rep = compare(s3.numpy(), None, r3.spikes.numpy(), r3.h.numpy(), 1.0)
     assert rep.ok, f"proj_conv3 {rep}"
-    p3 = _img_bits(eng.p3, T, B, embed, eng.H4, eng.W4)
+    p3 = _img_bits(_rows(eng.p3, T, eng.B, sel), T, B, embed, eng.H4, eng.W4)
     assert torch.equal(p3, _pool(s3))
     rr = _stage(p, "rpe_conv", p3)
-    x0 = _tok_stream(eng, eng.x0, 2, T, B, eng.N, embed)
+    x0 = _tok_stream(eng, _rows(eng.x0, T, eng.B, sel), 2, T, B, eng.N, embed)
     srpe = x0 - p3.flatten(-2).transpose(-1, -2)
     assert set(np.unique(srpe.numpy())) <= {0.0, 1.0}
     rep = compare(srpe.transpose(-1, -2).reshape(rr.spikes.shape).numpy(), None, rr.spikes.numpy(), rr.h.numpy(),
@@ -105,16 +120,23 @@ def _check_sps(eng, p, x_img, T, B, embed):
     return [float(r.spikes.mean()) for r in (r0, r1, r2, r3, rr)]
 
 
-def _check_block(dev, eng, p, i, x, T, B, heads):
-    """Block i on the oracle token stream x (T, B, N, C): q/k/v and fc1 spikes under the
-    parity rule on the engine's own inputs, SSA bit-exact on the engine's q/k/v, the two
-    residual adds exact.  Returns the oracle block output."""
+def _check_block(dev, eng, p, i, x, T, B, heads, sel=None):
+    """Block i on the token stream x (T, B, N, C): q/k/v and fc1 spikes under the parity rule
+    on the engine's own inputs, SSA bit-exact on the engine's q/k/v, the two residual adds
+    exact.  x given: the block is re-run on it (teacher forcing); x None: the block's buffers
+    from the engine's last forward are checked against its own input stream, on images `sel`.
+    Returns the mean attention spike rate."""
     blk = eng.blocks[i]
-    N, C = x.shape[2], x.shape[3]
     pre = blk.name
-    eng.run_block(i, x=_stream_of(eng, x, blk.planes_in, dev))
-    torch.cuda.synchronize()
-    b = blk.bufs
+    if x is not None:
+        eng.run_block(i, x=_stream_of(eng, x, blk.planes_in, dev))
+        torch.cuda.synchronize()
+    else:
+        xin, planes = eng.block_input(i)
+        x = _tok_stream(eng, _rows(xin, T, B, sel), planes, T, len(sel), eng.N, eng.embed)
+        B = len(sel)
+    N, C = x.shape[2], x.shape[3]
+    b = {k: _rows(v, T, eng.B, sel) if k != "qkv" else None for k, v in blk.bufs.items()}
 
     def lin(name, inp, got, v_th=1.0):
         s, h, _ = sf.linear_bn_lif(inp, p[f"{pre}.{name}_linear.weight"], p[f"{pre}.{name}_linear.bias"],
@@ -186,8 +208,7 @@ def test_engine_end_to_end_graph(dev, sf_case, stream):
 @pytest.mark.parametrize("batch,nblocks,stream", [(1, 1, "f16"), (4, 2, "f16"), (1, 1, "planes")])
 def test_engine_cfg4_shape(dev, batch, nblocks, stream):
     """BASELINE config 4's shape: 3x224x224 pixels ~N(0,1), T=4, embed 384, 8 heads, MLP ratio
-    4, 8 blocks (3,136 tokens), 1000 classes, on one image and on four (whose token layers
-    take the same tile-kernel instances as the benchmark's batch of 32); the SPS stages and
+    4, 8 blocks (3,136 tokens), 1000 classes, on one image and on four; the SPS stages and
     the first `nblocks` blocks teacher-forced against the oracle, graph replays equal to the
     eager run."""
     p = sf.make_params(41, embed=384, depth=8, num_classes=1000)
@@ -207,3 +228,35 @@ def test_engine_cfg4_shape(dev, batch, nblocks, stream):
         _check_block(dev, eng, p, i, xi, 4, batch, 8)
         blk = eng.blocks[i]
         xi = _tok_stream(eng, blk.bufs["x2"], blk.planes_out, 4, batch, eng.N, 384)  # checked block output
+
+
+def test_engine_cfg4_bench_batch(dev):
+    """BASELINE config 4 at the benchmark's own shape and batch (B = 32, fp16 stream, 8 blocks):
+    every launch the bench times runs here.  After one eager forward every SPS stage and all 8
+    blocks are checked against the oracle on the engine's own inputs for images 0, 13 and 31
+    (images are independent through SPS, the token Linears and the per-image attention), the
+    fused-kernel instances are asserted to be the ones named for B = 32, and a graph replay
+    reproduces the eager logits."""
+    from sparsesnn_amd import ops
+    B, sel = 32, (0, 13, 31)
+    p = sf.make_params(43, embed=384, depth=8, num_classes=1000)
+    x = torch.randn(B, 3, 224, 224, generator=torch.Generator().manual_seed(44))
+    eng = SpikformerEngine(p, batch=B, T=4, embed=384, heads=8, depth=8, in_hw=(224, 224), device=dev)
+    assert eng.N == 3136 and eng.stream == "f16"
+    for f in [eng.c1, eng.c2, eng.c3, eng.rpe] + [l for blk in eng.blocks for l in (blk.qkv, blk.proj, blk.fc1,
+                                                                                     blk.fc2)]:
+        assert f.spec.B == B
+        print(f"{f.spec.C_in}->{f.spec.C_out} {f.spec.H}x{f.spec.W} k{f.spec.KH}: {ops.fused_plan(f.spec)}",
+              flush=True)
+    eager = eng.forward(x.to(dev)).clone()
+    torch.cuda.synchronize()
+    rates = _check_sps(eng, p, x, 4, B, 384, sel=sel)
+    print("SPS spike rates", [round(r, 4) for r in rates], flush=True)
+    assert all(0.005 < r < 0.9 for r in rates), rates
+    for i in range(8):
+        ra = _check_block(dev, eng, p, i, None, 4, B, 8, sel=sel)
+        print(f"block {i}: attention spike rate {ra:.4f}", flush=True)
+    eng.capture()
+    y = eng.forward(x.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(y, eager)
