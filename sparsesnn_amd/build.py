@@ -23,7 +23,8 @@ LIB_PATH = os.path.join(LIB_DIR, "libsengine_amd.so")
 ARCH = "gfx950"
 
 SOURCES = ["capi.hip", "fused_sparse.hip", "fused_sparse_lds.hip", "fused_tile1.hip", "fused_tile3.hip",
-           "compress.hip", "fallback.hip", "sew.hip", "ssa.hip", "msres.hip", "calib.hip", "weights.hip"]
+           "fused_tile3s.hip", "compress.hip", "fallback.hip", "sew.hip", "ssa.hip", "msres.hip", "calib.hip",
+           "weights.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -400,8 +400,9 @@ struct FusedPlan {
 // Checks a descriptor and its pointers and picks the kernel.  Small outputs run in the flat
 // layout (their weight blob is built that way): the split-K small-M kernel for bit inputs,
 // the direct kernel on the flat view otherwise.  Other bit inputs: tile kernel for 3x3 /
-// stride 1 / pad 1 and 1x1 / pad 0, else the LDS-staged kernel (its per-thread tap mask holds
-// up to 64 taps), else the direct-gather kernel.
+// stride 1 / pad 1 and 1x1 / pad 0, the strided halo-tiled kernel for 3x3 / stride 2 / pad 1
+// at T = 4, else the LDS-staged kernel (its per-thread tap mask holds up to 64 taps), else the
+// direct-gather kernel.
 static int plan_fused(const sengine_conv_lif_desc* d, const void* data, const void* blob_values,
                       const void* blob_meta, float* state, const float* bn_scale, const float* bn_bias, void* spikes,
                       float* h_trace, float* x_trace, const SewAdd& sew, FusedPlan& plan) {
@@ -489,6 +490,8 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
     const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace, sew};
     const int choice = fused_kernel_choice();
     if ((choice == 0 || choice == 3) && tile_eligible(d)) return (int)launch_fused_bits_tile(d, plan.geo, args, stream);
+    if ((choice == 0 || choice == 3) && tile3s_eligible(d))
+      return (int)launch_fused_bits_tile3s(d, plan.geo, args, stream);
     return (int)launch_fused_bits_lds(d, plan.geo, args, stream);
   }
   const FusedParams& p = plan.p;
@@ -533,8 +536,12 @@ extern "C" int sengine_amd_fused_plan(const sengine_conv_lif_desc* d, int32_t fl
     const int choice = fused_kernel_choice();
     const bool shortcut_only = shortcut && !traces && !(flags & SENGINE_PLAN_SEW_ADD);
     const FusedArgs fa{nz, nz, nz, state ? fz : nullptr, fz, fz, fz, traces ? fz : nullptr, traces ? fz : nullptr, sew};
-    n = (choice == 0 || choice == 3) && tile_eligible(d) ? describe_tile(d, plan.geo, mode, shortcut_only, fa, buf, len)
-                                                         : describe_lds(d, plan.geo, mode, buf, len);
+    if ((choice == 0 || choice == 3) && tile_eligible(d))
+      n = describe_tile(d, plan.geo, mode, shortcut_only, fa, buf, len);
+    else if ((choice == 0 || choice == 3) && tile3s_eligible(d))
+      n = describe_tile3s(d, plan.geo, mode, buf, len);
+    else
+      n = describe_lds(d, plan.geo, mode, buf, len);
   } else if (plan.route == kRouteSmall) {
     n = snprintf(buf, len, "smallm<T=%d,planes=%d,out=%s,epi=%s,flat=%d>", d->T, d->weight_planes,
                  d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16", kEpi[plan.mode], flat_layout(d, plan.geo) ? 1 : 0);

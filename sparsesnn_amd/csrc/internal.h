@@ -76,6 +76,13 @@ struct TileChoice {
 };
 bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice& c);
 
+// Halo-tiled kernel for spike-bit 3x3 / stride 2 / pad 1 convolutions with one weight plane and
+// T = 4 (tile3s.h, fused_tile3s.hip).
+bool tile3s_eligible(const sengine_conv_lif_desc* d);
+hipError_t launch_fused_bits_tile3s(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+                                    hipStream_t stream);
+int describe_tile3s(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len);
+
 // Human-readable names of the kernel instance a launch would run (snprintf semantics); `a`
 // carries which optional buffers (state, traces, residuals) the launch passes.
 int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool shortcut_only,
