@@ -430,8 +430,10 @@ static int plan_fused(const sengine_conv_lif_desc* d, const void* data, const vo
     return 0;
   }
   // fp16 activations (the reference's call() ABI): the tile kernel copies fp16 rows into its
-  // LDS layout; other geometries take the direct-gather kernel
-  if (!flat && d->in_enc == SENGINE_ENC_F16 && (choice == 0 || choice == 3) && tile_eligible(d)) {
+  // LDS layout, as halo tiles (3x3 / s1 / p1), position tiles (1x1 / p0) or, for any other
+  // geometry at T = 4, one tap per chunk (the gather form); the rest take the direct-gather kernel
+  if (!flat && d->in_enc == SENGINE_ENC_F16 && (choice == 0 || choice == 3) &&
+      (tile_eligible(d) || tile_gather_eligible(d))) {
     plan.route = kRouteTiled;
     return 0;
   }
@@ -490,6 +492,7 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
     const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace, sew};
     const int choice = fused_kernel_choice();
     if ((choice == 0 || choice == 3) && tile_eligible(d)) return (int)launch_fused_bits_tile(d, plan.geo, args, stream);
+    if (d->in_enc == SENGINE_ENC_F16) return (int)launch_fused_f16_gather(d, plan.geo, args, stream);
     if ((choice == 0 || choice == 3) && tile3s_eligible(d))
       return (int)launch_fused_bits_tile3s(d, plan.geo, args, stream);
     return (int)launch_fused_bits_lds(d, plan.geo, args, stream);
@@ -538,6 +541,8 @@ extern "C" int sengine_amd_fused_plan(const sengine_conv_lif_desc* d, int32_t fl
     const FusedArgs fa{nz, nz, nz, state ? fz : nullptr, fz, fz, fz, traces ? fz : nullptr, traces ? fz : nullptr, sew};
     if ((choice == 0 || choice == 3) && tile_eligible(d))
       n = describe_tile(d, plan.geo, mode, shortcut_only, fa, buf, len);
+    else if (d->in_enc == SENGINE_ENC_F16)
+      n = describe_gather(d, plan.geo, mode, buf, len);
     else if ((choice == 0 || choice == 3) && tile3s_eligible(d))
       n = describe_tile3s(d, plan.geo, mode, buf, len);
     else

@@ -281,6 +281,47 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
                   (long long)c.ntiles * (d->C_out / (64 * c.gpw)));
 }
 
+bool tile_gather_eligible(const sengine_conv_lif_desc* d) {
+  if (d->in_enc != SENGINE_ENC_F16 || d->T != 4 || d->weight_planes != 1 || tile_eligible(d)) return false;
+  if (env_int_now("SENGINE_AMD_GATHER", 1) == 0) return false;  // =0: the direct-gather kernel instead
+  // 32-bit byte offsets of the fp16 rows; 16-bit receptive-field origins
+  return (int64_t)d->T * d->B * d->H * d->W * d->C_in * 2 < ((int64_t)1 << 31) && d->H < 16384 && d->W < 16384;
+}
+
+int describe_gather(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len) {
+  static const char* const kEpi[] = {"generic", "lif_hard", "if_hard"};
+  return snprintf(buf, len, "tile<T=4,KS=0(gather %dx%d/%d),GPW=1,in=f16,out=%s,epi=%s> grid=%lld", d->KH, d->KW,
+                  d->stride_h, d->out_enc == SENGINE_ENC_BITS ? "bits" : "f16", kEpi[mode],
+                  (long long)((geo.M + 63) / 64) * (d->C_out / 64));
+}
+
+hipError_t launch_fused_f16_gather(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+                                   hipStream_t stream) {
+  TileParams p{};
+  p.in = static_cast<const uint8_t*>(a.data);
+  p.wvals = static_cast<const u32x4_t*>(a.wvals);
+  p.wmeta = static_cast<const uint32_t*>(a.wmeta);
+  p.state = a.state;
+  p.scale = a.scale;
+  p.bias = a.bias;
+  p.out = static_cast<uint8_t*>(a.out);
+  p.h_trace = a.h_trace;
+  p.x_trace = a.x_trace;
+  p.B = d->B; p.C = d->C_in; p.H = d->H; p.W = d->W; p.F = d->C_out;
+  p.OH = geo.OH; p.OW = geo.OW; p.S = d->stride_h;
+  p.KW = d->KW; p.SH = d->stride_h; p.SW = d->stride_w; p.PH = d->pad_h; p.PW = d->pad_w;
+  p.DH = d->dil_h; p.DW = d->dil_w;
+  p.M = (int)geo.M;
+  p.nchunk = d->C_in / 64;
+  p.nq = d->KH * d->KW * p.nchunk;
+  p.np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
+  p.enc_scale = 1.0f;
+  p.sew = a.sew;
+  p.ntiles = (int)((geo.M + 63) / 64);
+  const int mode = epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr || a.sew.real_out != nullptr);
+  return launch_tile_f16in<0, 0, 0, 1>(p, d->out_enc, mode, stream);
+}
+
 hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
                                   hipStream_t stream) {
   TileChoice c;

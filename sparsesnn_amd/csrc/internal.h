@@ -76,6 +76,13 @@ struct TileChoice {
 };
 bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice& c);
 
+// fp16 activations (T = 4, one weight plane) on geometries the tile forms do not cover: the
+// gather form of the tile kernel (tile_kernel.h, KS = 0; fused_tile1.hip).
+bool tile_gather_eligible(const sengine_conv_lif_desc* d);
+hipError_t launch_fused_f16_gather(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+                                   hipStream_t stream);
+int describe_gather(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, char* buf, size_t len);
+
 // Halo-tiled kernel for spike-bit 3x3 / stride 2 / pad 1 convolutions with one weight plane and
 // T = 4 (tile3s.h, fused_tile3s.hip).
 bool tile3s_eligible(const sengine_conv_lif_desc* d);

@@ -20,6 +20,11 @@
 //    not 9 times.  Each wave owns a GR-row x 2-column block of the tile (lane column l is
 //    block pixel (l/2, l%2)); with a halo row length HC = 2 (mod 4) (or GR = 7, HC = 9)
 //    the 16 pixels of a block land in 16 distinct 16-byte bank groups for every tap.
+//  * KS == 0 (fp16 input, any kernel size / stride / padding / dilation: the reference ABI's
+//    activations on geometries the other forms do not cover): like KS == 1, but the reduction
+//    runs over the KH*KW*C_in/64 chunks of the blob, and chunk q stages, for each (t, position),
+//    the 64 fp16 channels of the input pixel under tap q / (C_in/64) (zero in the padding):
+//    an implicit im2col, one tap per chunk, with the same LDS layout and loop.
 //  * KS == 1 (1x1, any stride, pad 0): a workgroup owns 64 consecutive output positions
 //    (flattened b, oh, ow); LDS holds their input pixels, double-buffered across the
 //    64-channel reduction chunks (one barrier per chunk).
@@ -59,9 +64,10 @@ struct TileParams {
   float* h_trace;
   float* x_trace;
   int B, C, H, W, F, OH, OW, S;  // S: stride (KS == 1 only)
+  int KW, SH, SW, PH, PW, DH, DW;  // KS == 0: kernel width, strides, paddings, dilations
   int M;                         // B*OH*OW positions per timestep
   int nchunk;                    // C / 64
-  int nq;                        // KS*KS*nchunk reduction chunks in the blob
+  int nq;                        // KH*KW*nchunk reduction chunks in the blob
   int tiles_w, tiles_per_image;  // KS == 3: spatial tiles
   int ntiles;                    // tiles per channel block
   NeuronParams np;
@@ -76,7 +82,7 @@ struct TileGeom {
   static constexpr int NCP = KS == 3 ? (TC + 1) / 2 : 1;
   static constexpr int NWAVE = KS == 3 ? NCP * ((TR + GR - 1) / GR) : 4;
   static constexpr int NTHR = 64 * NWAVE;
-  static constexpr int NTAP = KS * KS;
+  static constexpr int NTAP = KS == 0 ? 1 : KS * KS;  // taps per chunk
   static constexpr int NBUF = KS == 3 ? 1 : 2;
   // odd half-piece region shift (entries) that makes every fragment read conflict-free
   static constexpr int PAD = (KS == 3 && TR == 7 && TC == 7) ? 8 : 16;
@@ -128,6 +134,7 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
                                        : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
   using Gm = TileGeom<KS, TR, TC, GR>;
   static_assert(PF == 1 || (PF == 2 && KS == 3), "two-deep prefetch needs the unrolled 9-tap loop");
+  static_assert(KS != 0 || (IN_ENC == SENGINE_ENC_F16 && KSP == 1), "the gather form stages fp16 rows");
   constexpr int NA = PF + 1;  // A operand sets in flight (ring over taps; 9 % 3 == 0)
   constexpr int NB = PF + 1;  // B fragment sets in flight (ring over (tap, t) steps)
   constexpr int NPIX = Gm::NPIX;
@@ -238,9 +245,12 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
     }
     return inb ? (((t * p.B + ib) * p.H + ih) * p.W + iw) * (p.C * 2) : -1;
   };
-  // byte offsets of this thread's pieces' fp16 rows (fixed over the chunks; -1 = zero piece)
+  // byte offsets of this thread's pieces' fp16 rows (fixed over the chunks; -1 = zero piece).
+  // KS == 0: instead the (t, image) row block of the piece's position (-1: past M) and the
+  // top-left input pixel of its receptive field, ih0 in the high and iw0 in the low 16 bits.
   int off16[IN_ENC == SENGINE_ENC_F16 ? PPT : 1];
-  if (IN_ENC == SENGINE_ENC_F16) {
+  int gpix[KS == 0 ? PPT : 1];
+  if (IN_ENC == SENGINE_ENC_F16 && KS != 0) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int pc = tid + j * NTHR;
@@ -248,10 +258,40 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
       off16[j] = o < 0 ? -1 : o + (pc & 7) * 16;
     }
   }
-  auto load_pieces = [&](u32x4_t (&v)[PPT], int c) {
+  if (KS == 0) {
 #pragma unroll
-    for (int j = 0; j < PPT; ++j)
-      v[j] = off16[j] >= 0 ? *reinterpret_cast<const u32x4_t*>(p.in + off16[j] + c * 128) : u32x4_t{0u, 0u, 0u, 0u};
+    for (int j = 0; j < PPT; ++j) {
+      const int u = (tid + j * NTHR) >> 3;
+      const int t = u / NPIX;
+      const int m = m0 + (u - t * NPIX);
+      const bool inb = u < UNITS && m < p.M;
+      const int ohw = p.OH * p.OW;
+      const int ib = inb ? m / ohw : 0;
+      const int r = m - ib * ohw;
+      const int oh = inb ? r / p.OW : 0;
+      const int ow = r - oh * p.OW;
+      off16[j] = inb ? t * p.B + ib : -1;
+      gpix[j] = ((oh * p.SH - p.PH) << 16) | ((ow * p.SW - p.PW) & 0xffff);
+    }
+  }
+  auto load_pieces = [&](u32x4_t (&v)[PPT], int c) {
+    if constexpr (KS == 0) {  // chunk c: tap c / nchunk, channels 64 (c % nchunk) ..
+      const int tap = c / p.nchunk, cc = c - tap * p.nchunk;
+      const int kh = tap / p.KW, kw = tap - kh * p.KW;
+      const int piece = (tid & 7) * 16 + cc * 128;  // NTHR % 8 == 0: a thread's pieces share their index
+#pragma unroll
+      for (int j = 0; j < PPT; ++j) {
+        const int ih = (gpix[j] >> 16) + kh * p.DH, iw = (int)(int16_t)(gpix[j] & 0xffff) + kw * p.DW;
+        const bool inb = off16[j] >= 0 && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+        v[j] = inb ? *reinterpret_cast<const u32x4_t*>(p.in + ((off16[j] * p.H + ih) * p.W + iw) * (p.C * 2) + piece)
+                   : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < PPT; ++j)
+        v[j] = off16[j] >= 0 ? *reinterpret_cast<const u32x4_t*>(p.in + off16[j] + c * 128)
+                             : u32x4_t{0u, 0u, 0u, 0u};
+    }
   };
   auto store_pieces = [&](int buf, const u32x4_t (&v)[PPT]) {
 #pragma unroll
@@ -373,8 +413,9 @@ __attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EP
     store_units(set * NBUF, stg);
   }
   __syncthreads();
-  for (int c = set; c < p.nchunk; c += KSP) {  // host: nchunk % KSP == 0 (sets stay in step)
-    const bool more = c + KSP < p.nchunk;
+  const int nloop = KS == 0 ? p.nq : p.nchunk;  // KS == 0: every chunk of every tap
+  for (int c = set; c < nloop; c += KSP) {  // host: nloop % KSP == 0 (sets stay in step)
+    const bool more = c + KSP < nloop;
     const int buf = NBUF == 2 ? ((c / KSP) & 1) : 0;
     if (IN_ENC == SENGINE_ENC_F16 && more) load_pieces(pnext, c + KSP);
     // B fragments: four ds_read_b64 per (tap, t), issued PF steps ahead of their SMFMACs
