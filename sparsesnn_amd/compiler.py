@@ -200,6 +200,28 @@ class DenseConvBNKernel:
         return ops.dense_conv_bn(spec, data, blob, bn_scale, bn_bias, out=out)
 
 
+class RealConvBNKernel:
+    """fp32 1x1 Conv + folded BN on a real-valued NHWC tensor (MS-ResNet's TDBN shortcut;
+    TileLangConv1x1BN with a real input): kern(x, weight, bn_scale, bn_bias, in_T=..., out=...).
+    in_T = 1: the input holds one timestep (a stem's output), every output is stored T times."""
+
+    def __init__(self, spec: ConvSpec, key: str):
+        self.spec = spec
+        self.key = key
+
+    def prepare_weight(self, w, device=None) -> torch.Tensor:
+        if isinstance(w, np.ndarray):
+            w = torch.from_numpy(np.ascontiguousarray(w))
+        device = device or (w.device if w.is_cuda else torch.device("cuda"))
+        w = w.to(device).float()
+        if _weight_layout(self.spec, w) == ops.WLAYOUT_OIHW:
+            w = w.permute(2, 3, 1, 0)
+        return w.contiguous()  # HWIO (1, 1, C_in, C_out)
+
+    def __call__(self, x, weight, bn_scale, bn_bias, in_T=None, out=None):
+        return ops.real_conv_bn(self.spec, x, weight, bn_scale, bn_bias, in_T=in_T, out=out, layout=ops.WLAYOUT_HWIO)
+
+
 class NeuronExt:
     """Standalone temporal neuron with the torch-extension API the reference JIT-builds
     (if_neuron / lif_neuron, sengine/csrc/green_context/if_neuron.cu:75-126):
@@ -269,13 +291,14 @@ class SparseKernelCompiler:
             raise SEngineError(f"node {node.name}: input batch {N} != T*B = {self.T * self.B}")
         if cp.stride_h != cp.stride_w or cp.pad_h != cp.pad_w or cp.dilation_h != cp.dilation_w or cp.groups != 1:
             raise SEngineError(f"node {node.name}: only square stride/pad/dilation and groups=1 are supported")
-        is_lif = neuron_kind == "LIF"
+        neuron = {"LIF": "lif", "IF": "if", "MS": "ms"}.get(neuron_kind, "if")
         hard = True if np_ is None else bool(np_.hard_reset)
         planes = int(node.extra_attrs.get("in_planes", 1))
+        # LIF: tau; MS: the decay (models/msresnet.py:28-56; kept in tau, as NeuronParams does)
         return ConvSpec(T=self.T, B=self.B, C_in=cp.in_channels * planes, H=H, W=W, C_out=cp.out_channels,
                         KH=cp.kernel_h, KW=cp.kernel_w, stride=cp.stride_h, padding=cp.pad_h,
-                        dilation=cp.dilation_h, neuron="lif" if is_lif else "if", hard_reset=hard,
-                        tau=float(np_.tau) if (np_ is not None and is_lif) else 2.0,
+                        dilation=cp.dilation_h, neuron=neuron, hard_reset=hard,
+                        tau=float(np_.tau) if (np_ is not None and neuron != "if") else 2.0,
                         v_threshold=float(np_.v_threshold) if np_ is not None else 1.0,
                         v_reset=float(np_.v_reset) if np_ is not None else 0.0,
                         weight_planes=1 if self.precision == "fp16" else 2)
@@ -302,6 +325,14 @@ class SparseKernelCompiler:
                 node.tilelang_config = {"kernel": "fused_sparse_conv_bn_lif", "T": self.T, "waves": 4,
                                         "tile_channels": 64, "tile_positions": 64}
                 kernels[nid] = kern
+            elif name in DENSE_VARIANTS and node.extra_attrs.get("real_input"):
+                spec = self._spec(node, "IF", None)
+                key = f"real_{spec}"
+                kern = self._kernel_cache.get(key)
+                if kern is None:
+                    kern = RealConvBNKernel(spec, key)
+                    self._kernel_cache[key] = kern
+                kernels[nid] = kern
             elif name in DENSE_VARIANTS:
                 spec = self._spec(node, "IF", None)
                 key = f"dense_{spec}_{self.precision}"
@@ -315,8 +346,8 @@ class SparseKernelCompiler:
             elif name in STEM_VARIANTS:
                 kernels[nid] = self._stem(node)
             elif name in HEAD_VARIANTS:
-                gap = self.ir.nodes[node.extra_attrs["absorbed_nids"][-1]]
-                N, C, H, W = gap.input_shapes[0]
+                first = self.ir.nodes[node.extra_attrs["absorbed_nids"][-1]]  # the chain's first op
+                N, C, H, W = first.input_shapes[0]
                 key = f"head_{self.T}_{self.B}_{H * W}_{C}_{node.extra_attrs.get('in_planes', 1)}"
                 kernels[nid] = SpikeHeadKernel(self.T, self.B, H * W, C, int(node.extra_attrs.get("in_planes", 1)),
                                                key)
@@ -331,10 +362,10 @@ class SparseKernelCompiler:
             raise SEngineError(f"node {node.name}: only square stride/pad and groups=1 are supported")
         neuron = self.ir.nodes[node.extra_attrs["neuron_nid"]]
         np_ = neuron.neuron_params
-        is_lif = neuron.op_type.name == "LIF"
+        kind = {"LIF": "lif", "IF": "if", "MS": "ms"}[neuron.op_type.name]
         spec = ConvSpec(T=self.T, B=self.B, C_in=C, H=H, W=W, C_out=cp.out_channels, KH=cp.kernel_h,
-                        KW=cp.kernel_w, stride=cp.stride_h, padding=cp.pad_h, neuron="lif" if is_lif else "if",
-                        hard_reset=bool(np_.hard_reset), tau=float(np_.tau) if is_lif else 2.0,
+                        KW=cp.kernel_w, stride=cp.stride_h, padding=cp.pad_h, neuron=kind,
+                        hard_reset=bool(np_.hard_reset), tau=float(np_.tau) if kind != "if" else 2.0,
                         v_threshold=float(np_.v_threshold), v_reset=float(np_.v_reset))
         pool = None
         for a in node.extra_attrs["absorbed_nids"]:

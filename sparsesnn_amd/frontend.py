@@ -163,3 +163,69 @@ def sew_resnet_ir(model, T: int = 4, batch: int = 1, in_hw=(32, 32), neuron: str
                  output_shapes=[(batch, fw.shape[0])], gemm_params={"transB": 1},
                  weight_info=WeightInfo("fc.weight", tuple(fw.shape)), bias_info=WeightInfo("fc.bias", tuple(fb.shape))))
     return ir
+
+
+def ms_resnet_ir(model, T: int = 4, batch: int = 1, in_hw=(224, 224), depth: int = 34, neuron: str = "ms",
+                 tau=None, v_threshold=None) -> EngineIR:
+    """EngineIR of an MS-ResNet-18/34 (models/msresnet.py:87-161, 318-319) for `batch` images.
+
+    Structure, as the reference's forward runs it: conv1 = TDBN(Conv2d 7x7/2, BN) on the image
+    repeated over T (computed here once per image, then the Tile: the T copies are equal), then
+    per block (BasicBlock18.forward): x -> sn1 -> conv_bn1 -> sn2 -> conv_bn2, plus the shortcut
+    (a TDBN 1x1 conv of the real-valued x where the stride or width changes, else x itself),
+    out = conv_bn2 + shortcut; after the last block sn_out, mean over T, average pool, fc.
+    TDBNContainer's BatchNorm3d in eval mode is the same per-channel affine as BatchNorm2d.
+    `model`: a module tree (its state_dict) or a state dict with the reference's key names
+    (conv1.module.{0,1}, conv{2..5}_x.{i}.conv_bn{1,2}.module.{0,1}, ...shortcut.module.{0,1},
+    fc).  neuron 'ms' builds the reference's MSNeuron (decay `tau`, default 0.25; threshold
+    default 0.5) as OpType.MS; 'lif' a LIF (tau default 2, threshold 1, hard reset to 0)."""
+    from .ms_resnet import MS_DECAY, MS_THRESH, block_names
+    if neuron not in ("ms", "lif"):
+        raise ValueError("neuron must be 'ms' or 'lif'")
+    sd = _state(model)
+    ir = EngineIR()
+    ir.T = T
+    is_ms = neuron == "ms"
+    tau = float(tau if tau is not None else (MS_DECAY if is_ms else 2.0))
+    vth = float(v_threshold if v_threshold is not None else (MS_THRESH if is_ms else 1.0))
+    bld = _Builder(ir, sd, T, "lif", tau, vth, 0.0)
+    if is_ms:
+        bld.op = OpType.MS
+        bld.np = NeuronParams(NeuronType.MS, T, tau, vth, 0.0, True)
+    H, W = in_hw
+    cin = sd["conv1.module.0.weight"].shape[1]
+
+    # stem: conv + BN once per image, then the repeat over T
+    x, shp = bld.conv("conv1.module.0", "x", (batch, cin, H, W), 2, 3)
+    x = bld.bn("conv1.module.1", x, shp)
+    shp = (T * batch,) + shp[1:]
+    x = bld.simple("conv1.repeat", OpType.Tile, x, (batch,) + shp[1:], shp, extra_attrs={"repeats": T})
+
+    for pre, _, cout, s, has_sc in block_names(depth):
+        a = bld.neuron(pre + ".sn1", x, shp)
+        a, ashp = bld.conv(pre + ".conv_bn1.module.0", a, shp, s, 1)
+        a = bld.bn(pre + ".conv_bn1.module.1", a, ashp)
+        a = bld.neuron(pre + ".sn2", a, ashp)
+        b, bshp = bld.conv(pre + ".conv_bn2.module.0", a, ashp, 1, 1)
+        b = bld.bn(pre + ".conv_bn2.module.1", b, bshp)
+        sc = x
+        if has_sc:
+            if (pre + ".shortcut.module.0.weight") not in sd:
+                raise ValueError(f"{pre}: stride/width change without a shortcut conv")
+            sc, sshp = bld.conv(pre + ".shortcut.module.0", x, shp, s, 0)
+            sc = bld.bn(pre + ".shortcut.module.1", sc, sshp)
+        x = bld.simple(pre + ".add", OpType.Add, [b, sc], bshp, bshp)
+        shp = bshp
+
+    # head: sn_out, mean over T, average pool, flatten, fc
+    x = bld.neuron("sn_out", x, shp)
+    N, C, h, w = shp
+    x = bld.simple("mean", OpType.TemporalMean, x, shp, (batch, C, h, w))
+    x = bld.simple("avgpool", OpType.GlobalAvgPool, x, (batch, C, h, w), (batch, C, 1, 1))
+    x = bld.simple("flatten", OpType.Flatten, x, (batch, C, 1, 1), (batch, C))
+    fw, fb = sd["fc.weight"], sd["fc.bias"]
+    ir.weights["fc.weight"], ir.weights["fc.bias"] = fw, fb
+    bld.add(Node(0, "fc", OpType.Gemm, input_names=[x], output_names=["logits"], input_shapes=[(batch, C)],
+                 output_shapes=[(batch, fw.shape[0])], gemm_params={"transB": 1},
+                 weight_info=WeightInfo("fc.weight", tuple(fw.shape)), bias_info=WeightInfo("fc.bias", tuple(fb.shape))))
+    return ir

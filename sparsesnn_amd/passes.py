@@ -4,9 +4,10 @@ nodes straight from torch modules (ONNX is not available to this build).
 
 Pass order (optimize_ir, sengine/optimizer.py:24-59, restricted to this path):
   fold_batchnorm -> detect_fusion_groups -> mark_sparsity -> assign_kernels
-  -> fuse_stem -> absorb_residual_add -> fuse_head -> assign_pools -> annotate_planes
-(the last five play the role of the reference's slicer for the network-level nodes,
-sengine/fusion_strategy.py:28-193 / graph_slicer.py:43-182).
+  -> fuse_stem -> absorb_residual_add -> absorb_membrane_shortcut -> assign_real_convs
+  -> fuse_head -> assign_pools -> annotate_planes
+(the passes after assign_kernels play the role of the reference's slicer for the
+network-level nodes, sengine/fusion_strategy.py:28-193 / graph_slicer.py:43-182).
 """
 from __future__ import annotations
 
@@ -18,7 +19,7 @@ from .sparsity import fold_batchnorm as _fold_vectors
 from .sparsity import validate_2_4_pattern
 
 _TRANSPARENT = {OpType.Reshape, OpType.Transpose, OpType.Identity, OpType.Flatten}
-_NEURONS = {OpType.LIF, OpType.IF}
+_NEURONS = {OpType.LIF, OpType.IF, OpType.MS}
 
 
 def fold_batchnorm(ir: EngineIR) -> int:
@@ -127,7 +128,7 @@ def assign_kernels(ir: EngineIR) -> dict:
             conv.bound_type = BoundType.COMPUTE
             neuron.assigned_kernel = KernelVariant.ZeroCost
             neuron.bound_type = BoundType.ZERO
-            conv.extra_attrs["fusion_slice"] = "Conv2d+" + ("LIF" if neuron.op_type == OpType.LIF else "IF")
+            conv.extra_attrs["fusion_slice"] = "Conv2d+" + neuron.op_type.name
             conv.extra_attrs["absorbed_nids"] = [neuron.id]
             stats["fused"] += 1
         elif dense_eligible(conv, T):
@@ -155,11 +156,13 @@ def _single_consumer(ir: EngineIR, nid: int):
 
 def fuse_stem(ir: EngineIR) -> int:
     """Dense stem convs (C_in < 4: never 2:4 along C_in, optimizer.py:540-543) feeding
-    Tile (repeat over T) -> LIF/IF [-> MaxPool] run as one TileLangStemConvBN launch: the conv
+    Tile (repeat over T) -> LIF/IF/MS [-> MaxPool] run as one TileLangStemConvBN launch: the conv
     + BN once per image, the neuron over the T repeats and the spike max-pool from the same
     workgroup (the reference computes conv1/bn1 before repeating, models/sewresnet.py:199-201).
     The absorbed nodes become ZeroCost; extra_attrs: fusion_slice, absorbed_nids,
-    fused_output (the tensor the launch writes)."""
+    fused_output (the tensor the launch writes).  When the repeated real-valued output has other
+    readers besides the neuron (MS-ResNet's first shortcut, models/msresnet.py:111), the launch
+    also stores it, once per image: extra_attrs real_output (that tensor)."""
     n = 0
     for nid in list(ir.topo_order):
         conv = ir.nodes[nid]
@@ -170,15 +173,20 @@ def fuse_stem(ir: EngineIR) -> int:
         tile = _single_consumer(ir, nid)
         if tile is None or tile.op_type != OpType.Tile:
             continue
-        neuron = _single_consumer(ir, tile.id)
-        if neuron is None or neuron.op_type not in _NEURONS:
+        readers = [ir.nodes[c] for c in ir.successors(tile.id)]
+        neurons = [r for r in readers if r.op_type in _NEURONS]
+        if len(neurons) != 1:
             continue
+        neuron = neurons[0]
+        real_out = tile.output_names[0] if len(readers) > 1 else None
         absorbed, pattern, out = [tile.id, neuron.id], ["Conv2d", "Tile", neuron.op_type.name], neuron.output_names[0]
         pool = _single_consumer(ir, neuron.id)
-        if pool is not None and pool.op_type == OpType.MaxPool:
+        if pool is not None and pool.op_type == OpType.MaxPool and real_out is None:
             absorbed.append(pool.id)
             pattern.append("MaxPool")
             out = pool.output_names[0]
+        if real_out is not None:
+            conv.extra_attrs["real_output"] = real_out
         conv.assigned_kernel = KernelVariant.TileLangStemConvBN
         conv.bound_type = BoundType.COMPUTE
         conv.layout = TensorLayout.NHWC
@@ -241,9 +249,11 @@ def absorb_residual_add(ir: EngineIR) -> int:
 
 def fuse_head(ir: EngineIR) -> int:
     """GlobalAvgPool -> Flatten -> TemporalMean -> Gemm (avgpool, flatten, x.mean(0), fc;
-    models/sewresnet.py:206-210) as one CuBLASGemm launch on the spike counts: the pooled
-    means are integer counts times 1/(HW*T), so the pool and mean run exactly on integers
-    before the Linear.  The Gemm node anchors it (fusion_slice, absorbed_nids, head_input)."""
+    models/sewresnet.py:206-210) or TemporalMean -> GlobalAvgPool -> Flatten -> Gemm
+    (models/msresnet.py:153-161) as one CuBLASGemm launch on the spike counts: the pooled
+    means are integer counts times 1/(HW*T) in either order, so the pool and mean run exactly
+    on integers before the Linear.  The Gemm node anchors it (fusion_slice, absorbed_nids --
+    the chain from the Gemm back, its first op last -- and head_input)."""
     n = 0
     for nid in list(ir.topo_order):
         gemm = ir.nodes[nid]
@@ -258,21 +268,88 @@ def fuse_head(ir: EngineIR) -> int:
             if p.op_type in (OpType.TemporalMean, OpType.Flatten, OpType.Reshape, OpType.GlobalAvgPool):
                 chain.append(p)
                 cur = p
-                if p.op_type == OpType.GlobalAvgPool:
-                    break
             else:
                 break
         kinds = {c.op_type for c in chain}
         if OpType.GlobalAvgPool not in kinds or OpType.TemporalMean not in kinds:
             continue
-        gap = chain[-1]
+        first = chain[-1]
         gemm.assigned_kernel = KernelVariant.CuBLASGemm
         gemm.bound_type = BoundType.MEMORY
         gemm.extra_attrs.update(fusion_slice="+".join([c.op_type.name for c in reversed(chain)] + ["Gemm"]),
-                                absorbed_nids=[c.id for c in chain], head_input=gap.input_names[0])
+                                absorbed_nids=[c.id for c in chain], head_input=first.input_names[0])
         for c in chain:
             c.assigned_kernel = KernelVariant.ZeroCost
             c.bound_type = BoundType.ZERO
+        n += 1
+    return n
+
+
+def absorb_membrane_shortcut(ir: EngineIR) -> int:
+    """MS-ResNet's block output out = conv_bn2 + shortcut (models/msresnet.py:107-112) with the
+    next neuron on it (the next block's sn1, or sn_out) into one launch: the 2:4 conv + folded
+    BN whose output feeds only the Add becomes a FusedSparseConvBNLIF anchor that adds the
+    real-valued shortcut, stores the sum (the next block's real-valued input) and fires the
+    neuron -- the reference engine's Add+LIF fusion (TileLangFusedAddLIF,
+    sengine/kernels/add_lif_fused.py:20-75) with the conv in front of it.  extra_attrs:
+    shortcut_input (the Add's other input), real_output (the Add's output), fused_output (the
+    neuron's spikes), absorbed_nids [Add, neuron]."""
+    n = 0
+    for nid in list(ir.topo_order):
+        add = ir.nodes[nid]
+        if add.op_type != OpType.Add or len(add.input_names) != 2 or add.assigned_kernel != KernelVariant.ZeroCost:
+            continue
+        if any(add.id in a.extra_attrs.get("absorbed_nids", []) for a in ir.nodes.values()):
+            continue
+        y = add.output_names[0]
+        neurons = [ir.nodes[c] for c in ir._consumers.get(y, []) if ir.nodes[c].op_type in _NEURONS]
+        if len(neurons) != 1:
+            continue
+        neuron = neurons[0]
+        for k in (0, 1):
+            pid = ir._producer.get(add.input_names[k])
+            conv = ir.nodes.get(pid) if pid is not None else None
+            if (conv is None or conv.op_type != OpType.Conv2d or conv.fusion_group_id >= 0 or conv.bn_scale is None
+                    or not conv.sparse_weight or conv.assigned_kernel != KernelVariant.ZeroCost
+                    or not fused_eligible(conv, ir.T) or len(ir._consumers.get(add.input_names[k], [])) != 1):
+                continue
+            conv.assigned_kernel = KernelVariant.FusedSparseConvBNLIF
+            conv.bound_type = BoundType.COMPUTE
+            conv.layout = TensorLayout.NHWC
+            conv.extra_attrs.update(fusion_slice="Conv2d+Add+" + neuron.op_type.name, absorbed_nids=[add.id, neuron.id],
+                                    shortcut_input=add.input_names[1 - k], real_output=y,
+                                    fused_output=neuron.output_names[0], neuron_nid=neuron.id)
+            for a in (add, neuron):
+                a.assigned_kernel = KernelVariant.ZeroCost
+                a.bound_type = BoundType.ZERO
+            n += 1
+            break
+    return n
+
+
+def _real_tensors(ir: EngineIR) -> set:
+    """Real-valued (fp32) tensors the launches write: stems' kept outputs and membrane-shortcut sums."""
+    return {n.extra_attrs["real_output"] for n in ir.nodes.values() if "real_output" in n.extra_attrs}
+
+
+def assign_real_convs(ir: EngineIR) -> int:
+    """1x1 convs + folded BN on a real-valued tensor (MS-ResNet's TDBN shortcut of the block
+    input, models/msresnet.py:100-105) run as fp32 1x1 Conv+BN launches: TileLangConv1x1BN with
+    extra_attrs real_input (the products of real activations are not exact in fp16, so the
+    spike kernels do not apply)."""
+    real = _real_tensors(ir)
+    n = 0
+    for node in ir.nodes.values():
+        cp = node.conv_params
+        if node.op_type != OpType.Conv2d or node.assigned_kernel != KernelVariant.ZeroCost or cp is None:
+            continue
+        if node.bn_scale is None or node.input_names[0] not in real or cp.kernel_h != 1 or cp.kernel_w != 1 or \
+                cp.pad_h != 0 or cp.pad_w != 0 or cp.groups != 1:
+            continue
+        node.assigned_kernel = KernelVariant.TileLangConv1x1BN
+        node.bound_type = BoundType.MEMORY
+        node.layout = TensorLayout.NHWC
+        node.extra_attrs["real_input"] = True
         n += 1
     return n
 
@@ -333,10 +410,13 @@ def optimize_ir(ir: EngineIR) -> dict:
     stats = assign_kernels(ir)
     stems = fuse_stem(ir)
     adds = absorb_residual_add(ir)
+    shortcuts = absorb_membrane_shortcut(ir)
+    real_convs = assign_real_convs(ir)
     heads = fuse_head(ir)
     pools = assign_pools(ir)
     annotate_planes(ir)
-    stats.update(folded=folded, groups=groups, sparse=sparse, stems=stems, adds=adds, heads=heads, pools=pools)
+    stats.update(folded=folded, groups=groups, sparse=sparse, stems=stems, adds=adds, heads=heads, pools=pools,
+                 shortcuts=shortcuts, real_convs=real_convs)
     return stats
 
 

@@ -21,10 +21,16 @@ this path needs):
   * FusedSparseConvBNLIF (and the reference's TileLangFused* names), neuron absorbed, with
     the SEW 'ADD' absorbed into its epilogue when the passes recorded a residual_input; two
     fused convs reading the same input with no residual run as one paired launch;
+  * FusedSparseConvBNLIF with a real-valued shortcut_input (MS-ResNet's membrane shortcut):
+    the conv + BN + shortcut add + next neuron in one launch, writing the next neuron's spikes
+    and the fp32 sum (real_output, the next block's real-valued input);
   * TileLangConvBN / TileLangConv1x1BN (dense fallback, fp32 out) + CUDAVec4LIF / CUDAVec4IF;
-  * TileLangStemConvBN: the dense image stem with its repeat, neuron and max-pool absorbed;
+    TileLangConv1x1BN with real_input: the fp32 1x1 conv + BN of a real-valued tensor;
+  * TileLangStemConvBN: the dense image stem with its repeat, neuron and max-pool absorbed
+    (and its fp32 output kept, once per image, when the passes recorded a real_output);
   * CuDNNPool: spike max-pool; CuBLASGemm: the head (pool + mean over T + Linear absorbed);
   * ZeroCost: views.  An unabsorbed Add / Tile / TemporalMean / GlobalAvgPool raises.
+Spike tensors live as bits, real-valued tensors as fp32 NHWC.
 """
 from __future__ import annotations
 
@@ -96,10 +102,15 @@ _VIEW_OPS = {"Reshape", "Transpose", "Identity", "Flatten"}
 class _Launch:
     """One kernel launch of the schedule: the anchor node, what it reads and writes."""
 
-    def __init__(self, nid: int, kind: str, inputs: list, output: str):
+    def __init__(self, nid: int, kind: str, inputs: list, output: str, real_output: Optional[str] = None):
         self.nid, self.kind, self.inputs, self.output = nid, kind, inputs, output
+        self.real_output = real_output        # a second, fp32 output (membrane-shortcut sums, a kept stem output)
         self.pair_with: Optional[int] = None  # nid of a fused conv launched together with this one
         self.skip = False                     # launched as the second half of a pair
+
+    @property
+    def outputs(self) -> list:
+        return [self.output] + ([self.real_output] if self.real_output else [])
 
 
 class CUDAGraphEngine:
@@ -127,15 +138,20 @@ class CUDAGraphEngine:
     def _launch_of(self, node) -> Optional[_Launch]:
         name = _kname(node)
         ea = node.extra_attrs
+        if name in FUSED_VARIANTS and "shortcut_input" in ea:
+            return _Launch(node.id, "fused_sc", [node.input_names[0], ea["shortcut_input"]], ea["fused_output"],
+                           ea["real_output"])
         if name in FUSED_VARIANTS:
             ins = [node.input_names[0]] + ([ea["residual_input"]] if "residual_input" in ea else [])
             return _Launch(node.id, "fused", ins, ea.get("fused_output", node.output_names[0]))
+        if name in DENSE_VARIANTS and ea.get("real_input"):
+            return _Launch(node.id, "real_conv", [node.input_names[0]], node.output_names[0])
         if name in DENSE_VARIANTS:
             return _Launch(node.id, "dense", [node.input_names[0]], node.output_names[0])
         if name in NEURON_VARIANTS:
             return _Launch(node.id, "neuron", [node.input_names[0]], node.output_names[0])
         if name in STEM_VARIANTS:
-            return _Launch(node.id, "stem", [node.input_names[0]], ea["fused_output"])
+            return _Launch(node.id, "stem", [node.input_names[0]], ea["fused_output"], ea.get("real_output"))
         if name in HEAD_VARIANTS:
             return _Launch(node.id, "head", [ea["head_input"]], node.output_names[0])
         if name in POOL_VARIANTS:
@@ -162,7 +178,7 @@ class CUDAGraphEngine:
             ln = self._launch_of(node)
             if ln is not None:
                 launches.append(ln)
-                written.add(ln.output)
+                written.update(ln.outputs)
         for nid in order:  # views (and absorbed single-input nodes) alias their input
             node = ir.nodes[nid]
             if _kname(node) != "ZeroCost":
@@ -183,7 +199,7 @@ class CUDAGraphEngine:
     def _order(self, launches, aliases, schedule):
         """Launches in a dependency order (Kahn over what each reads and writes); the given
         schedule (or the IR's topological order) breaks ties."""
-        prod = {self._root(l.output, aliases): l for l in launches}
+        prod = {self._root(o, aliases): l for l in launches for o in l.outputs}
         rank = {nid: i for i, nid in enumerate(schedule)}
         deps = {l.nid: {prod[self._root(t, aliases)].nid for t in l.inputs if self._root(t, aliases) in prod}
                 for l in launches}
@@ -214,7 +230,7 @@ class CUDAGraphEngine:
         launches, aliases, shapes = self._analyse(ir, self.schedule)
         launches = self._order(launches, aliases, self.schedule)
         root = lambda t: self._root(t, aliases)  # noqa: E731
-        produced = {root(l.output) for l in launches}
+        produced = {root(o) for l in launches for o in l.outputs}
         inputs = {root(t) for l in launches for t in l.inputs if root(t) not in produced}
         if len(inputs) != 1:
             raise SEngineError(f"expected one graph input tensor, found {sorted(inputs)}")
@@ -261,13 +277,19 @@ class CUDAGraphEngine:
             launches = ordered
         self.launches = launches
 
-        # buffers: spike bits (x planes), fp32 dense outputs, logits; graph input / output kept
+        # buffers: spike bits (x planes), fp32 dense / real-valued outputs, logits; graph input and
+        # output kept
+        self.real = {root(l.real_output) for l in launches if l.real_output} | \
+                    {root(l.output) for l in launches if l.kind == "real_conv"}
+        # real tensors that hold one timestep (a stem's output, stored once per image)
+        self.real_one_t = {root(l.real_output) for l in launches if l.kind == "stem" and l.real_output}
+
         def cls(t):
             r = root(t)
             shp = shapes[r]
             kind = next((l.kind for l in launches if root(l.output) == r), None)
             n = int(np.prod(shp))
-            if kind == "dense" or kind == "head":
+            if kind == "dense" or kind == "head" or r in self.real:
                 return ("f32", n)
             if r == self.input_name and self.image_input:
                 return ("f32", n)
@@ -276,9 +298,9 @@ class CUDAGraphEngine:
                 raise SEngineError(f"tensor {t}: {C} channels is not a multiple of 32 (spike bits)")
             return ("bits", n * self.planes.get(r, 1) // 32)
 
-        produces = {l.nid: [root(l.output)] for l in launches}
+        produces = {l.nid: [root(o) for o in l.outputs] for l in launches}
         consumes = {l.nid: [root(t) for t in l.inputs] for l in launches}
-        live = {root(t) for l in launches for t in l.inputs + [l.output]}
+        live = {root(t) for l in launches for t in l.inputs + l.outputs}
         sizes = {t: cls(t) for t in live}
         plan = plan_buffers([l.nid for l in launches], produces, consumes, {}, sizes,
                             {self.input_name, root(self.output_name)})
@@ -308,12 +330,12 @@ class CUDAGraphEngine:
         # weights, BN vectors, membranes
         for l in launches:
             node = ir.nodes[l.nid]
-            if l.kind in ("fused", "dense", "stem"):
+            if l.kind in ("fused", "fused_sc", "dense", "stem", "real_conv"):
                 w = torch.from_numpy(np.ascontiguousarray(ir.weights[node.weight_info.name]))
                 self.weights[l.nid] = self.kernels[l.nid].prepare_weight(w.to(self.dev), device=self.dev)
                 self.bn[l.nid] = (torch.tensor(node.bn_scale, dtype=torch.float32, device=self.dev),
                                   torch.tensor(node.bn_bias, dtype=torch.float32, device=self.dev))
-                if keep_membranes and l.kind == "fused":
+                if keep_membranes and l.kind in ("fused", "fused_sc"):
                     N, C, H, W = node.output_shapes[0]
                     self.membranes[l.nid] = torch.zeros(N // self.T * H * W, C, device=self.dev)
             elif l.kind == "neuron" and keep_membranes:
@@ -368,6 +390,27 @@ class CUDAGraphEngine:
         args = (x, sw, mem, sc, bi) if mem is not None else (x, sw, sc, bi)
         kern(*args, out_enc=ENC_BITS, out=y)
 
+    def _real(self, t):
+        """A real-valued tensor as fp32 NHWC (N, H, W, C); one-timestep tensors (a stem's kept
+        output) as their first N / T rows."""
+        r = self._root_fn(t)
+        N, C, H, W = self._shapes[r]
+        if r in self.real_one_t:
+            N //= self.T
+        return self.tensors[r][:N * H * W * C].view(N, H, W, C)
+
+    def _run_fused_sc(self, l):
+        kern = self.kernels[l.nid]
+        sc, bi = self.bn[l.nid]
+        sw = self.weights[l.nid]
+        res = self._root_fn(l.inputs[1])
+        if res in self.real_one_t:
+            raise SEngineError(f"node {self.ir.nodes[l.nid].name}: an identity shortcut needs a T-step real input")
+        ops.fused_sparse_conv_bn_add_neuron(kern.spec_for(ENC_BITS, ENC_BITS), self._bits(l.inputs[0]).view(-1),
+                                            sw.values, sw.meta, sc, bi, residual=self._real(res),
+                                            state=self.membranes.get(l.nid), real_out=self._real(l.real_output),
+                                            out=self._bits(l.output))
+
     def _execute_schedule(self):
         if not self.image_input:  # first op of the graph
             ops.pack_spikes(self._graph_input, out=self._bits(self.input_name))
@@ -377,6 +420,13 @@ class CUDAGraphEngine:
             node = self.ir.nodes[l.nid]
             if l.kind == "fused":
                 self._run_fused(l)
+            elif l.kind == "fused_sc":
+                self._run_fused_sc(l)
+            elif l.kind == "real_conv":
+                sc, bi = self.bn[l.nid]
+                x = self._root_fn(l.inputs[0])
+                self.kernels[l.nid](self._real(x), self.weights[l.nid], sc, bi,
+                                    in_T=1 if x in self.real_one_t else self.T, out=self._real(l.output))
             elif l.kind == "dense":
                 sc, bi = self.bn[l.nid]
                 r = self._root_fn(l.output)
@@ -397,7 +447,8 @@ class CUDAGraphEngine:
                 if kern.pool is not None:
                     kern(self._graph_input, self.weights[l.nid], sc, bi, pooled=y)
                 else:
-                    kern(self._graph_input, self.weights[l.nid], sc, bi, spikes=y)
+                    kern(self._graph_input, self.weights[l.nid], sc, bi, spikes=y,
+                         out=self._real(l.real_output) if l.real_output else None)
             elif l.kind == "pool":
                 r = self._root_fn(l.inputs[0])
                 N, C, H, W = self._shapes[r]
@@ -480,7 +531,7 @@ class CUDAGraphEngine:
         lut = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.int64, device=self.dev)
         out = {}
         for l in self.launches:
-            if l.kind in ("dense", "head"):
+            if l.kind in ("dense", "head", "real_conv"):
                 continue
             r = self._root_fn(l.output)
             N, C, H, W = self._shapes[r]
