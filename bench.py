@@ -402,33 +402,6 @@ def cpu_e2e(params, x, budget_s=6.0, min_runs=CPU_MIN_RUNS):
 CFG34_BATCH, CFG34_HW, CFG34_CLASSES = 32, 224, 1000
 
 
-def bench_graph_engine(eng, x, warmup: int, iters: int, eager: bool = False) -> float:
-    """Seconds per batch of a captured engine: HIP events around `iters` hipGraph replays.
-    eager=True times eager forwards instead (no graph: the counter-collection pass)."""
-    import torch
-    eng.forward(x)
-    if eager:
-        torch.cuda.synchronize(x.device)
-        t0 = time.perf_counter()
-        for _ in range(iters):
-            eng.forward(x)
-        torch.cuda.synchronize(x.device)
-        return (time.perf_counter() - t0) / iters
-    eng.capture()
-    for _ in range(warmup):
-        eng.forward(x)
-    torch.cuda.synchronize(x.device)
-    stream = torch.cuda.current_stream(x.device)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    eng.x_buf.copy_(x)
-    a.record(stream)
-    for _ in range(iters):
-        eng.graph.replay()
-    b.record(stream)
-    torch.cuda.synchronize(x.device)
-    return a.elapsed_time(b) * 1e-3 / iters
-
-
 def bench_generic_engine(eng, x, warmup: int, iters: int, eager: bool = False) -> float:
     """Seconds per batch of a CUDAGraphEngine: HIP events around `iters` hipGraph replays
     (CUDAGraphEngine.benchmark), or eager forwards (the counter-collection pass)."""
@@ -469,15 +442,23 @@ def bench_msresnet34(dev, warmup: int, iters: int, eager: bool = False):
 def bench_spikformer(dev, warmup: int, iters: int, eager: bool = False):
     """Spikformer, 8 blocks, embed 384, 8 heads, MLP ratio 4, SPS stem on
     3x224x224 pixels ~N(0,1) (3,136 tokens), T=4, batch 32, 1000 classes, the stem convs after
-    the first and every block Linear 2:4 with fused BN+LIF, the model's own initialisation."""
+    the first and every block Linear 2:4 with fused BN+LIF, the model's own initialisation, run
+    the way the reference runs a network: state dict -> EngineIR (front end) -> optimize_ir
+    (the residual stream as fp16 integers) -> compile_all -> CUDAGraphEngine, one hipGraph
+    replay per batch."""
     import torch
-    from sparsesnn_amd.spikformer import SpikformerEngine, random_params
+    from sparsesnn_amd import frontend, passes
+    from sparsesnn_amd.compiler import SparseKernelCompiler
+    from sparsesnn_amd.runtime import CUDAGraphEngine
+    from sparsesnn_amd.spikformer import random_params
     params = random_params(2026, embed=384, depth=8, num_classes=CFG34_CLASSES)
-    eng = SpikformerEngine(params, batch=CFG34_BATCH, T=T_STEPS, embed=384, heads=8, depth=8,
-                           in_hw=(CFG34_HW, CFG34_HW), device=dev)
+    ir = frontend.spikformer_ir(params, T=T_STEPS, batch=CFG34_BATCH, in_hw=(CFG34_HW, CFG34_HW), heads=8)
+    passes.optimize_ir(ir, int_stream="f16")
+    kernels = SparseKernelCompiler(ir, batch_size=CFG34_BATCH).compile_all()
+    eng = CUDAGraphEngine().build(ir, kernels, T=T_STEPS, batch_size=CFG34_BATCH, device=dev)
     x = torch.randn((CFG34_BATCH, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(9))
-    s = bench_graph_engine(eng, x.to(dev), warmup, iters, eager)
-    return dict(params=params, x=x, batch_s=s, launches=eng.launches)
+    s = bench_generic_engine(eng, x.to(dev), warmup, iters, eager)
+    return dict(params=params, x=x, batch_s=s, launches=eng.n_launches)
 
 
 def cpu_sample(fn, budget_s: float, min_runs: int = CPU_MIN_RUNS):
@@ -732,7 +713,9 @@ def main():
             "metric": "images/sec", "model": "Spikformer-8-384 (8 heads, MLP x4, 3136 tokens, 2:4 Linears/convs, fused BN+LIF)",
             "value": round(CFG34_BATCH / f["batch_s"], 1), "batch": CFG34_BATCH, "timesteps": T_STEPS,
             "input": f"3x{CFG34_HW}x{CFG34_HW} ~N(0,1)", "ms_per_batch": round(f["batch_s"] * 1e3, 4),
-            "launches_per_batch": f["launches"], "step": "one hipGraph replay per batch",
+            "launches_per_batch": f["launches"],
+            "step": "one hipGraph replay per batch of the generic engine (EngineIR -> optimize_ir, fp16 residual "
+                    "stream -> compile_all -> CUDAGraphEngine)",
             "data": "synthetic images, the model's own random init (models/spikformer.py:238-245)"}
         if not args.no_cpu_baseline:  # the oracle networks on the host cores (CPU baseline leg only)
             from oracle import ms_resnet as msr

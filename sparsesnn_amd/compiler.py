@@ -29,6 +29,7 @@ NEURON_VARIANTS = {"CUDAVec4LIF", "CUDAVec4IF"}
 STEM_VARIANTS = {"TileLangStemConvBN"}
 HEAD_VARIANTS = {"CuBLASGemm"}
 POOL_VARIANTS = {"CuDNNPool"}
+ATTENTION_VARIANTS = {"FusedSpikformerAttn"}
 
 
 class SparseWeight:
@@ -164,13 +165,43 @@ class StemConvBNKernel:
 
 class SpikeHeadKernel:
     """GlobalAvgPool -> Flatten -> TemporalMean -> Gemm on (integer) spike activations
-    (CuBLASGemm with the pool and mean absorbed): kern(x_bits, fc_weight, fc_bias, out=...)."""
+    (CuBLASGemm with the pool and mean absorbed): kern(x, fc_weight, fc_bias, out=..., workspace=...).
+    planes 0: x is an integer-valued fp16 stream; a `workspace` of workspace_numel int32 then
+    splits its sums over many workgroups per image."""
 
     def __init__(self, T: int, B: int, HW: int, C: int, planes: int, key: str):
         self.T, self.B, self.HW, self.C, self.planes, self.key = T, B, HW, C, planes, key
 
-    def __call__(self, x, fc_weight, fc_bias, out=None):
-        return ops.sew_head(x, self.T, self.B, self.HW, self.C, self.planes, fc_weight, fc_bias, out=out)
+    @property
+    def workspace_numel(self) -> int:
+        return self.B * ops.HEAD_WS_SPLIT * self.C if self.planes == 0 else 0
+
+    def __call__(self, x, fc_weight, fc_bias, out=None, workspace=None):
+        return ops.sew_head(x, self.T, self.B, self.HW, self.C, self.planes, fc_weight, fc_bias, out=out,
+                            workspace=workspace)
+
+
+class SpikingSelfAttentionKernel:
+    """The Spikformer attention core (FusedSpikformerAttn; sengine/tdl/attention_ops.py:48-98):
+    kern(q, k, v, kv=..., out=...) on spike bits (T*B, N, C/32) -> the attention LIF's spike bits.
+    kv: an int32 workspace of kv_numel elements (K^T V per head)."""
+
+    def __init__(self, T: int, B: int, N: int, C: int, ap, key: str):
+        self.T, self.B, self.N, self.C, self.key = T, B, N, C, key
+        self.heads, self.scale = int(ap.num_heads), float(ap.scale)
+        self.tau, self.v_threshold = float(ap.attn_lif_tau), float(ap.attn_lif_v_threshold)
+        if self.heads * int(ap.head_dim) != C:
+            raise SEngineError(f"attention: {self.heads} heads x {ap.head_dim} != {C} channels")
+
+    @property
+    def kv_numel(self) -> int:
+        d = self.C // self.heads
+        return self.T * self.B * self.heads * d * d
+
+    def __call__(self, q, k, v, kv=None, out=None):
+        return ops.spiking_self_attention(q, k, v, self.T, self.B, self.N, self.C, self.heads, scale=self.scale,
+                                          neuron="lif", tau=self.tau, v_threshold=self.v_threshold, v_reset=0.0,
+                                          kv=kv, out=out)
 
 
 class DenseConvBNKernel:
@@ -293,9 +324,10 @@ class SparseKernelCompiler:
             raise SEngineError(f"node {node.name}: only square stride/pad/dilation and groups=1 are supported")
         neuron = {"LIF": "lif", "IF": "if", "MS": "ms"}.get(neuron_kind, "if")
         hard = True if np_ is None else bool(np_.hard_reset)
-        planes = int(node.extra_attrs.get("in_planes", 1))
+        planes = int(node.extra_attrs.get("in_planes", 1))  # 0: an fp16 input
+        c_out = int(node.extra_attrs.get("merged_out_channels", cp.out_channels))
         # LIF: tau; MS: the decay (models/msresnet.py:28-56; kept in tau, as NeuronParams does)
-        return ConvSpec(T=self.T, B=self.B, C_in=cp.in_channels * planes, H=H, W=W, C_out=cp.out_channels,
+        return ConvSpec(T=self.T, B=self.B, C_in=cp.in_channels * max(planes, 1), H=H, W=W, C_out=c_out,
                         KH=cp.kernel_h, KW=cp.kernel_w, stride=cp.stride_h, padding=cp.pad_h,
                         dilation=cp.dilation_h, neuron=neuron, hard_reset=hard,
                         tau=float(np_.tau) if (np_ is not None and neuron != "if") else 2.0,
@@ -345,6 +377,15 @@ class SparseKernelCompiler:
                 kernels[nid] = get_cuda_if()
             elif name in STEM_VARIANTS:
                 kernels[nid] = self._stem(node)
+            elif name in ATTENTION_VARIANTS:
+                TB, C, H, W = node.input_shapes[0]
+                ap = node.attention_params
+                key = f"attn_{self.T}_{self.B}_{H * W}_{C}_{ap}"
+                kern = self._kernel_cache.get(key)
+                if kern is None:
+                    kern = SpikingSelfAttentionKernel(self.T, self.B, H * W, C, ap, key)
+                    self._kernel_cache[key] = kern
+                kernels[nid] = kern
             elif name in HEAD_VARIANTS:
                 first = self.ir.nodes[node.extra_attrs["absorbed_nids"][-1]]  # the chain's first op
                 N, C, H, W = first.input_shapes[0]

@@ -1,5 +1,5 @@
-"""Front end: EngineIR straight from a SEW-ResNet module tree (ONNX, the reference's route via
-sengine/parser.py:77-368, is not available to this build).
+"""Front ends: EngineIR straight from a SEW-ResNet, MS-ResNet or Spikformer module tree or state
+dict (ONNX, the reference's route via sengine/parser.py:77-368, is not available to this build).
 
 `sew_resnet_ir` walks the structure of the reference's `sew_resnet18` (models/sewresnet.py:
 123-210): stem conv1 / bn1, the image repeated over T, sn1, maxpool, layer1..layer4 of
@@ -15,7 +15,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from .ir import ConvParams, EngineIR, Node, NeuronParams, NeuronType, OpType, WeightInfo
+from .ir import (AttentionParams, ConvParams, EngineIR, KernelVariant, Node, NeuronParams, NeuronType, OpType,
+                 WeightInfo)
 
 STAGES = ((64, 1), (128, 2), (256, 2), (512, 2))
 
@@ -228,4 +229,119 @@ def ms_resnet_ir(model, T: int = 4, batch: int = 1, in_hw=(224, 224), depth: int
     bld.add(Node(0, "fc", OpType.Gemm, input_names=[x], output_names=["logits"], input_shapes=[(batch, C)],
                  output_shapes=[(batch, fw.shape[0])], gemm_params={"transB": 1},
                  weight_info=WeightInfo("fc.weight", tuple(fw.shape)), bias_info=WeightInfo("fc.bias", tuple(fb.shape))))
+    return ir
+
+
+def spikformer_ir(model, T: int = 4, batch: int = 1, in_hw=(224, 224), heads: int = 8, tau: float = 2.0,
+                  v_threshold: float = 1.0, attn_v_threshold: float = 0.5) -> EngineIR:
+    """EngineIR of a Spikformer (models/spikformer.py:153-288) for `batch` images of in_hw pixels.
+
+    SPS (:153-209): proj_conv + proj_bn on the images, computed once per image (the forward
+    repeats the image over T first, :283-285, so the T copies are equal), then the Tile and
+    proj_lif; proj_conv1..3 + BN + LIF with a 3x3/2 max-pool after the third and fourth; the
+    relative-position conv rpe_conv + rpe_bn + rpe_lif on the pooled features x_feat, added to
+    them; the feature map viewed as T*B x N tokens (flatten(-2).transpose(-1, -2)).  Tokens are
+    an (N, 1) grid here, NCHW (T*B, C, N, 1), which in the runtime's NHWC memory is the same
+    bytes as the (H/4, W/4) feature map: the view is free, and every token Linear is a Linear
+    node over that grid.  Blocks (:59-150): q, k, v = Linear + BatchNorm1d + LIF of x, the
+    attention core as one FusedAttention node (the reference's FusedSpikformerAttention op,
+    sengine/tdl/attention_ops.py:48-98: (Q K^T * 0.125) V per head, then attn_lif with
+    V_th = attn_v_threshold), proj = Linear + BN + LIF, x1 = x + proj; fc1, fc2 = Linear + BN +
+    LIF, x2 = x1 + fc2.  Head (:273-288): mean over the tokens, mean over T, Linear.
+
+    `model`: a module tree (its state_dict; heads from block[0].attn.num_heads) or a state dict
+    with the reference's key names (patch_embed.proj_conv, .proj_bn, .proj_conv1..3,
+    .proj_bn1..3, .rpe_conv, .rpe_bn; block.{i}.attn.{q,k,v,proj}_{linear,bn};
+    block.{i}.mlp.fc{1,2}_{linear,bn}; head).  Every neuron but attn_lif is a LIF with `tau`,
+    `v_threshold` and hard reset to 0 (MultiStepLIFNeuron(tau=2.0), :26,93-104)."""
+    blocks = getattr(model, "block", None)
+    if blocks is not None and len(blocks) and hasattr(blocks[0], "attn"):
+        heads = int(getattr(blocks[0].attn, "num_heads", heads))
+    sd = _state(model)
+    depth = 0
+    while f"block.{depth}.attn.q_linear.weight" in sd:
+        depth += 1
+    ir = EngineIR()
+    ir.T = T
+    bld = _Builder(ir, sd, T, "lif", tau, v_threshold, 0.0)
+    H, W = in_hw
+    cin = sd["patch_embed.proj_conv.weight"].shape[1]
+    pool = {"kernel_size": 3, "stride": 2, "padding": 1}
+
+    def maxpool(name, x, shp):
+        out = shp[:2] + ((shp[2] - 1) // 2 + 1, (shp[3] - 1) // 2 + 1)
+        return bld.simple(name, OpType.MaxPool, x, shp, out, pool_params=dict(pool)), out
+
+    def conv_bn_lif(idx, x, shp):
+        x, shp = bld.conv(f"patch_embed.proj_conv{idx}", x, shp, 1, 1)
+        x = bld.bn(f"patch_embed.proj_bn{idx}", x, shp)
+        return bld.neuron(f"patch_embed.proj_lif{idx}", x, shp), shp
+
+    # ---- SPS
+    x, shp = bld.conv("patch_embed.proj_conv", "x", (batch, cin, H, W), 1, 1)
+    x = bld.bn("patch_embed.proj_bn", x, shp)
+    shp = (T * batch,) + shp[1:]
+    x = bld.simple("patch_embed.repeat", OpType.Tile, x, (batch,) + shp[1:], shp, extra_attrs={"repeats": T})
+    x = bld.neuron("patch_embed.proj_lif", x, shp)
+    x, shp = conv_bn_lif(1, x, shp)
+    x, shp = conv_bn_lif(2, x, shp)
+    x, shp = maxpool("patch_embed.maxpool2", x, shp)
+    x, shp = conv_bn_lif(3, x, shp)
+    feat, shp = maxpool("patch_embed.maxpool3", x, shp)
+    r, _ = bld.conv("patch_embed.rpe_conv", feat, shp, 1, 1)
+    r = bld.bn("patch_embed.rpe_bn", r, shp)
+    r = bld.neuron("patch_embed.rpe_lif", r, shp)
+    x = bld.simple("patch_embed.add", OpType.Add, [r, feat], shp, shp)
+    TB, C, h4, w4 = shp
+    N = h4 * w4
+    tok = (TB, C, N, 1)
+    x = bld.simple("patch_embed.tokens", OpType.Reshape, x, shp, tok)
+    if C % heads:
+        raise ValueError(f"embed {C} is not a multiple of {heads} heads")
+
+    def linear_bn_lif(pre, x, cin_, cout_, neuron=True):
+        wk, bk = pre + "_linear.weight", pre + "_linear.bias"
+        w = sd[wk]
+        if tuple(w.shape) != (cout_, cin_):
+            raise ValueError(f"{wk}: expected shape {(cout_, cin_)}, got {tuple(w.shape)}")
+        ir.weights[wk] = w
+        bias = None
+        if bk in sd:
+            ir.weights[bk] = sd[bk]
+            bias = WeightInfo(bk, tuple(sd[bk].shape))
+        oshp = (TB, cout_, N, 1)
+        y = bld.add(Node(0, pre + "_linear", OpType.Linear, input_names=[x], output_names=[pre + "_linear.out"],
+                         input_shapes=[(TB, cin_, N, 1)], output_shapes=[oshp], gemm_params={"N": cout_},
+                         weight_info=WeightInfo(wk, tuple(w.shape)), bias_info=bias))
+        y = bld.bn(pre + "_bn", y, oshp)
+        return bld.neuron(pre + "_lif", y, oshp)
+
+    # ---- blocks
+    attn_np = NeuronParams(NeuronType.LIF, T, float(tau), float(attn_v_threshold), 0.0, True)
+    for i in range(depth):
+        pre = f"block.{i}"
+        hidden = sd[f"{pre}.mlp.fc1_linear.weight"].shape[0]
+        q, k, v = (linear_bn_lif(f"{pre}.attn.{n}", x, C, C) for n in ("q", "k", "v"))
+        a = bld.add(Node(0, f"{pre}.attn.core", OpType.FusedAttention, is_stateful=True, input_names=[q, k, v],
+                         output_names=[f"{pre}.attn.core.out"], input_shapes=[tok] * 3, output_shapes=[tok],
+                         neuron_params=attn_np,
+                         attention_params=AttentionParams("spikformer", heads, C // heads, 0.125, h4, w4,
+                                                          float(tau), float(attn_v_threshold)),
+                         assigned_kernel=KernelVariant.FusedSpikformerAttn))
+        p_ = linear_bn_lif(f"{pre}.attn.proj", a, C, C)
+        x = bld.simple(f"{pre}.add1", OpType.Add, [x, p_], tok, tok)
+        f1 = linear_bn_lif(f"{pre}.mlp.fc1", x, C, hidden)
+        f2 = linear_bn_lif(f"{pre}.mlp.fc2", f1, hidden, C)
+        x = bld.simple(f"{pre}.add2", OpType.Add, [x, f2], tok, tok)
+
+    # ---- head: mean over tokens, mean over T, Linear
+    x = bld.simple("avgpool", OpType.GlobalAvgPool, x, tok, (TB, C, 1, 1))
+    x = bld.simple("flatten", OpType.Flatten, x, (TB, C, 1, 1), (TB, C))
+    x = bld.simple("mean", OpType.TemporalMean, x, (TB, C), (batch, C))
+    fw, fb = sd["head.weight"], sd["head.bias"]
+    ir.weights["head.weight"], ir.weights["head.bias"] = fw, fb
+    bld.add(Node(0, "head", OpType.Gemm, input_names=[x], output_names=["logits"], input_shapes=[(batch, C)],
+                 output_shapes=[(batch, fw.shape[0])], gemm_params={"transB": 1},
+                 weight_info=WeightInfo("head.weight", tuple(fw.shape)),
+                 bias_info=WeightInfo("head.bias", tuple(fb.shape))))
     return ir

@@ -32,6 +32,7 @@ class OpType(Enum):
     Tile = auto()            # repeat over T (the static image fed to every timestep)
     TemporalMean = auto()
     Gemm = auto()            # classifier Linear
+    FusedAttention = auto()  # attention core (q, k, v spikes -> attention neuron spikes), one custom node
 
 
 class NeuronType(Enum):
@@ -70,6 +71,7 @@ class KernelVariant(Enum):
     TemporalMean = auto()
     TileRepeat = auto()
     CuBLASGemm = auto()           # classifier
+    FusedSpikformerAttn = auto()  # Spikformer SSA core: (Q K^T * scale) V per head -> attention LIF
 
 
 class BoundType(Enum):
@@ -109,6 +111,7 @@ KERNEL_CONTRACTS = {
     KernelVariant.TemporalMean: None,
     KernelVariant.TileRepeat: None,
     KernelVariant.CuBLASGemm: KernelLayoutContract(TensorLayout.ND, TensorLayout.ND),
+    KernelVariant.FusedSpikformerAttn: KernelLayoutContract(TensorLayout.NHWC, TensorLayout.NHWC),
 }
 
 
@@ -138,6 +141,20 @@ class NeuronParams:
 
 
 @dataclass
+class AttentionParams:
+    """Attention-core node parameters (sengine/ir.py:205-215): the variant, head geometry, the
+    product's scale and the attention neuron (a LIF, hard reset to 0)."""
+    variant: str = ""
+    num_heads: int = 1
+    head_dim: int = 64
+    scale: float = 1.0
+    H: int = 0
+    W: int = 0
+    attn_lif_tau: float = 2.0
+    attn_lif_v_threshold: float = 1.0
+
+
+@dataclass
 class WeightInfo:
     name: str = ""
     shape: tuple = ()
@@ -159,6 +176,7 @@ class Node:
     neuron_params: Optional[NeuronParams] = None
     pool_params: Optional[dict] = None    # kernel_size / stride / padding (MaxPool)
     gemm_params: Optional[dict] = None
+    attention_params: Optional[AttentionParams] = None
     extra_attrs: dict = field(default_factory=dict)
     assigned_kernel: KernelVariant = KernelVariant.ZeroCost
     layout: TensorLayout = TensorLayout.NCHW

@@ -3,9 +3,10 @@ and sengine/fusion_strategy.py), plus a small front end that builds Conv->BN->ne
 nodes straight from torch modules (ONNX is not available to this build).
 
 Pass order (optimize_ir, sengine/optimizer.py:24-59, restricted to this path):
-  fold_batchnorm -> detect_fusion_groups -> mark_sparsity -> assign_kernels
-  -> fuse_stem -> absorb_residual_add -> absorb_membrane_shortcut -> assign_real_convs
-  -> fuse_head -> assign_pools -> annotate_planes
+  lower_linears -> fold_batchnorm -> detect_fusion_groups -> mark_sparsity -> pad_channels
+  -> assign_kernels -> fuse_stem -> absorb_residual_add -> absorb_membrane_shortcut
+  -> assign_real_convs -> merge_sibling_convs -> assign_attention -> fuse_head -> assign_pools
+  -> annotate_planes
 (the passes after assign_kernels play the role of the reference's slicer for the
 network-level nodes, sengine/fusion_strategy.py:28-193 / graph_slicer.py:43-182).
 """
@@ -20,6 +21,32 @@ from .sparsity import validate_2_4_pattern
 
 _TRANSPARENT = {OpType.Reshape, OpType.Transpose, OpType.Identity, OpType.Flatten}
 _NEURONS = {OpType.LIF, OpType.IF, OpType.MS}
+
+
+def lower_linears(ir: EngineIR) -> int:
+    """Token Linears (OpType.Linear, weight (out, in) as nn.Linear holds it, optional bias) over a
+    (T*B, C, N, 1) token grid become 1x1 Conv2d nodes over that grid: y[t, :, n] = W x[t, :, n] + b
+    is the 1x1 convolution with weight W[:, :, None, None] and that bias (the reference fuses
+    Linear + BatchNorm1d + LIF the same way, TileLangLinearBNLIF, sengine/ir.py:72-74).  The
+    BatchNorm1d that follows is the per-channel affine fold_batchnorm folds; the Linear bias
+    goes into it as the conv bias.  Returns the number of nodes lowered."""
+    n = 0
+    for node in ir.nodes.values():
+        if node.op_type != OpType.Linear or node.weight_info is None:
+            continue
+        w = np.asarray(ir.weights[node.weight_info.name])
+        shp = tuple(node.input_shapes[0]) if node.input_shapes else ()
+        if w.ndim != 2 or len(shp) != 4 or shp[3] != 1 or shp[1] != w.shape[1]:
+            raise ValueError(f"node {node.name}: a Linear over a (T*B, C, N, 1) token grid with a 2-D weight "
+                             f"is served, got input {shp} and weight {w.shape}")
+        w4 = w[:, :, None, None]
+        ir.weights[node.weight_info.name] = w4
+        node.weight_info.shape = tuple(w4.shape)
+        node.op_type = OpType.Conv2d
+        node.conv_params = ConvParams(int(w.shape[1]), int(w.shape[0]), 1, 1, 1, 1, 0, 0)
+        node.extra_attrs["lowered_from"] = "Linear"
+        n += 1
+    return n
 
 
 def fold_batchnorm(ir: EngineIR) -> int:
@@ -96,6 +123,87 @@ def mark_sparsity(ir: EngineIR) -> int:
             node.sparse_weight = True
             node.weight_info.is_sparse = True
             n += 1
+    return n
+
+
+def _pad_to(c: int, multiple: int) -> int:
+    return -(-c // multiple) * multiple
+
+
+def _pad_weight(ir: EngineIR, node: Node, axis: int, size: int):
+    """Zero-pad the node's weight along `axis` (0 = C_out, 1 = C_in) to `size`, stored under a
+    name of its own (the original array is left alone)."""
+    w = np.asarray(ir.weights[node.weight_info.name])
+    pad = [(0, 0)] * w.ndim
+    pad[axis] = (0, size - w.shape[axis])
+    name = node.weight_info.name if node.weight_info.name.endswith("#padded") else node.weight_info.name + "#padded"
+    ir.weights[name] = np.pad(w, pad)
+    node.weight_info = WeightInfo(name, tuple(ir.weights[name].shape), node.weight_info.is_sparse)
+
+
+def _with_channels(shape, c):
+    return (shape[0], c) + tuple(shape[2:])
+
+
+def pad_channels(ir: EngineIR, multiple: int = 64) -> int:
+    """Pad the output channels of a Conv -> BN [-> Tile] -> neuron chain to a multiple of 64
+    (the fused kernels' channel blocking; Spikformer's SPS has embed/8 = 48 and embed/4 = 96
+    channels, models/spikformer.py:159-165) with zero weights and a zero BN affine: the padded
+    channels' input is 0 every step, so a neuron with V_th > max(0, V_reset) never fires there.
+    Their spikes flow through max-pools into convs only, whose input channels get matching zero
+    weight columns (a group of four zeros keeps the
+    kernels' rule of at most two nonzeros per group).  Chains whose spikes reach anything else
+    are left alone.  Shapes along the way are updated.  Returns the number of convs padded."""
+    n = 0
+    for nid in list(ir.topo_order):
+        conv = ir.nodes[nid]
+        cp = conv.conv_params
+        if conv.op_type != OpType.Conv2d or cp is None or cp.groups != 1 or conv.bn_scale is None or \
+                conv.weight_info is None or cp.out_channels % multiple == 0:
+            continue
+        path = []
+        nxt = _single_consumer(ir, nid)
+        if nxt is not None and nxt.op_type == OpType.Tile:
+            path.append(nxt)
+            nxt = _single_consumer(ir, nxt.id)
+        if nxt is None or nxt.op_type not in _NEURONS or nxt.neuron_params is None:
+            continue
+        npar = nxt.neuron_params
+        if not npar.v_threshold > max(0.0, npar.v_reset if npar.hard_reset else 0.0):
+            continue
+        path.append(nxt)
+        carriers, readers, frontier, ok = [], [], [nxt.id], True
+        while frontier and ok:
+            cur = frontier.pop()
+            for sid in ir.successors(cur):
+                sn = ir.nodes[sid]
+                if sn.op_type in (OpType.MaxPool, OpType.Identity):
+                    carriers.append(sn)
+                    frontier.append(sid)
+                elif sn.op_type == OpType.Conv2d and sn.conv_params is not None and sn.conv_params.groups == 1 \
+                        and sn.weight_info is not None and len(sn.input_names) == 1:
+                    readers.append(sn)
+                else:
+                    ok = False
+                    break
+        if not ok or not readers:
+            continue
+        P = _pad_to(cp.out_channels, multiple)
+        _pad_weight(ir, conv, 0, P)
+        extra = [0.0] * (P - cp.out_channels)
+        conv.bn_scale = list(conv.bn_scale) + extra
+        conv.bn_bias = list(conv.bn_bias) + extra
+        cp.out_channels = P
+        conv.output_shapes = [_with_channels(conv.output_shapes[0], P)]
+        for m in path + carriers:
+            m.input_shapes = [_with_channels(s, P) for s in m.input_shapes]
+            m.output_shapes = [_with_channels(s, P) for s in m.output_shapes]
+        for r in readers:
+            _pad_weight(ir, r, 1, P)
+            r.conv_params.in_channels = P
+            r.input_shapes = [_with_channels(r.input_shapes[0], P)] + list(r.input_shapes[1:])
+        conv.extra_attrs["padded_from"] = int(P - len(extra))
+        n += 1
     return n
 
 
@@ -367,28 +475,123 @@ def assign_pools(ir: EngineIR) -> int:
     return n
 
 
-def annotate_planes(ir: EngineIR) -> int:
+def merge_sibling_convs(ir: EngineIR, round_to: int = 256) -> int:
+    """Fused 1x1 convs that read the same tensor with the same shape and neuron and no residual
+    (Spikformer's q, k and v Linears, models/spikformer.py:103-125) run as one launch over their
+    weights concatenated along C_out -- the input is read once instead of once per conv -- with
+    the spike bits split back into one plane per conv (sengine_amd_fused_sparse_conv_bn_lif_split).
+    The concatenation is zero-padded to a multiple of `round_to` output channels (zero weights
+    and a zero BN affine: never fire; 256 = the persistent 1x1 kernel's four-wave super-block).
+    The first conv anchors the launch: extra_attrs merged_nids (the convs, in order),
+    merged_weight (the concatenated weight's name in ir.weights), merged_bn (scale, bias lists),
+    merged_outputs (each conv's spike tensor) and split_channels; the other convs and their
+    neurons are absorbed (ZeroCost).  Returns the number of merged launches."""
+    groups: dict = {}
+    for nid in ir.topo_order:
+        n = ir.nodes[nid]
+        ea = n.extra_attrs
+        cp = n.conv_params
+        if n.assigned_kernel != KernelVariant.FusedSparseConvBNLIF or cp is None or \
+                any(k in ea for k in ("residual_input", "shortcut_input", "merged_nids")):
+            continue
+        if (cp.kernel_h, cp.kernel_w, cp.stride_h, cp.stride_w, cp.pad_h, cp.pad_w) != (1, 1, 1, 1, 0, 0) or \
+                cp.out_channels % 64:
+            continue
+        absorbed = ea.get("absorbed_nids", [])
+        if len(absorbed) != 1:
+            continue
+        neuron = ir.nodes[absorbed[0]]
+        np_ = neuron.neuron_params
+        key = (n.input_names[0], cp.in_channels, cp.out_channels, tuple(n.input_shapes[0]), neuron.op_type,
+               None if np_ is None else (np_.tau, np_.v_threshold, np_.v_reset, np_.hard_reset))
+        groups.setdefault(key, []).append((n, neuron))
+    merged = 0
+    for key, members in groups.items():
+        if len(members) < 2:
+            continue
+        anchor = members[0][0]
+        cout = anchor.conv_params.out_channels
+        total = _pad_to(len(members) * cout, round_to)
+        ws = [np.asarray(ir.weights[c.weight_info.name], dtype=np.float32) for c, _ in members]
+        w = np.zeros((total,) + ws[0].shape[1:], np.float32)
+        w[:len(members) * cout] = np.concatenate(ws)
+        zeros = [0.0] * (total - len(members) * cout)
+        wname = anchor.name + ".merged.weight"
+        ir.weights[wname] = w
+        absorbed = [members[0][1].id]
+        for c, nr in members[1:]:
+            absorbed += [c.id, nr.id]
+            for x in (c, nr):
+                x.assigned_kernel = KernelVariant.ZeroCost
+                x.bound_type = BoundType.ZERO
+        anchor.extra_attrs.update(
+            merged_nids=[c.id for c, _ in members], merged_weight=wname, split_channels=cout,
+            merged_bn=(sum((list(c.bn_scale) for c, _ in members), []) + zeros,
+                       sum((list(c.bn_bias) for c, _ in members), []) + zeros),
+            merged_outputs=[nr.output_names[0] for _, nr in members], merged_out_channels=total,
+            absorbed_nids=absorbed,
+            fusion_slice="Split(" + ",".join("Conv2d+" + nr.op_type.name for _, nr in members) + ")")
+        merged += 1
+    return merged
+
+
+def assign_attention(ir: EngineIR) -> int:
+    """FusedAttention nodes of the Spikformer variant run as FusedSpikformerAttn (the SSA core on
+    spike bits: K^T V per head, then Q (K^T V) * scale and the attention LIF in one more launch);
+    other variants are not served here and raise."""
+    n = 0
+    for node in ir.nodes.values():
+        if node.op_type != OpType.FusedAttention:
+            continue
+        ap = node.attention_params
+        if ap is None or ap.variant != "spikformer" or len(node.input_names) != 3:
+            raise ValueError(f"node {node.name}: only the Spikformer attention core (q, k, v) is served")
+        node.assigned_kernel = KernelVariant.FusedSpikformerAttn
+        node.bound_type = BoundType.COMPUTE
+        node.layout = TensorLayout.NHWC
+        n += 1
+    return n
+
+
+def annotate_planes(ir: EngineIR, int_stream: str = "planes") -> int:
     """Integer range of every activation: spikes are 0/1, a fused SEW add yields
     max(residual) + 1, max-pool keeps its input's range.  Fused convs record in_planes (the
     bit planes of their input, which multiply the reduction, sparsity.expand_planes) and
-    out_planes; residual sums above 31 (5 planes) are rejected."""
+    out_planes; residual sums above 31 (5 planes) are rejected.
+
+    int_stream 'f16': integer activations (ranges above 1) are stored as fp16 integers instead
+    -- the reference's own representation of the residual stream -- exact up to 2048.  Their
+    readers record in_planes 0 (an fp16 input, K = C_in) and res_planes 0; their writers
+    out_planes 0 (fp16 output)."""
+    if int_stream not in ("planes", "f16"):
+        raise ValueError("int_stream must be 'planes' or 'f16'")
+    f16 = int_stream == "f16"
+    ir.int_stream = int_stream
     vmax: dict = {}
+
+    def planes_of(t):
+        m = int(vmax.get(t, 1))
+        return 0 if (f16 and m > 1) else max(1, m.bit_length())
+
     for nid in ir.topo_order:
         node = ir.nodes[nid]
         kv = node.assigned_kernel
-        if node.op_type in _NEURONS:
+        if node.op_type in _NEURONS or node.op_type == OpType.FusedAttention:
             for o in node.output_names:
                 vmax[o] = 1
         if kv == KernelVariant.FusedSparseConvBNLIF:
             inp = node.input_names[0]
-            node.extra_attrs["in_planes"] = max(1, int(vmax.get(inp, 1)).bit_length())
+            node.extra_attrs["in_planes"] = planes_of(inp)
             if "residual_input" in node.extra_attrs:
-                m = int(vmax.get(node.extra_attrs["residual_input"], 1)) + 1
-                if m > 31:
+                res = node.extra_attrs["residual_input"]
+                m = int(vmax.get(res, 1)) + 1
+                if f16 and m >= 2048:
+                    raise ValueError(f"{node.name}: residual sums up to {m} exceed fp16's exact integers")
+                if not f16 and m > 31:
                     raise ValueError(f"{node.name}: residual sums up to {m} need more than 5 bit planes")
                 vmax[node.extra_attrs["fused_output"]] = m
-                node.extra_attrs["res_planes"] = max(1, int(m - 1).bit_length())
-                node.extra_attrs["out_planes"] = m.bit_length()
+                node.extra_attrs["res_planes"] = planes_of(res)
+                node.extra_attrs["out_planes"] = 0 if f16 else m.bit_length()
             else:
                 node.extra_attrs["out_planes"] = 1
         elif node.op_type in (OpType.MaxPool, OpType.Flatten, OpType.Reshape, OpType.Identity):
@@ -397,26 +600,32 @@ def annotate_planes(ir: EngineIR) -> int:
         elif kv == KernelVariant.TileLangStemConvBN:
             vmax[node.extra_attrs["fused_output"]] = 1
         elif kv == KernelVariant.CuBLASGemm and "head_input" in node.extra_attrs:
-            node.extra_attrs["in_planes"] = max(1, int(vmax.get(node.extra_attrs["head_input"], 1)).bit_length())
+            node.extra_attrs["in_planes"] = planes_of(node.extra_attrs["head_input"])
     return len(vmax)
 
 
-def optimize_ir(ir: EngineIR) -> dict:
+def optimize_ir(ir: EngineIR, int_stream: str = "planes") -> dict:
     """The hot-path subset of sengine's optimize_ir pipeline, plus the network-level fusions
-    the generic runtime serves (stem, SEW add, head, pools)."""
+    the generic runtime serves (stem, SEW add, membrane shortcut, merged siblings, attention,
+    head, pools).  int_stream: how integer activations (residual sums) are stored, annotate_planes."""
+    linears = lower_linears(ir)
     folded = fold_batchnorm(ir)
     groups = detect_fusion_groups(ir)
     sparse = mark_sparsity(ir)
+    padded = pad_channels(ir)
     stats = assign_kernels(ir)
     stems = fuse_stem(ir)
     adds = absorb_residual_add(ir)
     shortcuts = absorb_membrane_shortcut(ir)
     real_convs = assign_real_convs(ir)
+    merged = merge_sibling_convs(ir)
+    attention = assign_attention(ir)
     heads = fuse_head(ir)
     pools = assign_pools(ir)
-    annotate_planes(ir)
+    annotate_planes(ir, int_stream)
     stats.update(folded=folded, groups=groups, sparse=sparse, stems=stems, adds=adds, heads=heads, pools=pools,
-                 shortcuts=shortcuts, real_convs=real_convs)
+                 shortcuts=shortcuts, real_convs=real_convs, linears=linears, padded=padded, merged=merged,
+                 attention=attention)
     return stats
 
 

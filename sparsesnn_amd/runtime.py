@@ -28,9 +28,16 @@ this path needs):
     TileLangConv1x1BN with real_input: the fp32 1x1 conv + BN of a real-valued tensor;
   * TileLangStemConvBN: the dense image stem with its repeat, neuron and max-pool absorbed
     (and its fp32 output kept, once per image, when the passes recorded a real_output);
+  * FusedSparseConvBNLIF anchoring merged siblings (merged_nids: Spikformer's q, k, v): one
+    launch over the concatenated weights, its spike bits split into one plane per conv -- the
+    planes of one buffer, each conv's spike tensor a view of its plane;
+  * FusedSpikformerAttn: the SSA core on spike bits (K^T V, then Q (K^T V) and the attention
+    LIF: two kernels), its K^T V workspace allocated in build();
   * CuDNNPool: spike max-pool; CuBLASGemm: the head (pool + mean over T + Linear absorbed);
   * ZeroCost: views.  An unabsorbed Add / Tile / TemporalMean / GlobalAvgPool raises.
-Spike tensors live as bits, real-valued tensors as fp32 NHWC.
+Spike tensors live as bits, real-valued tensors as fp32 NHWC, integer activations (residual
+sums) as bit planes or, when the passes chose an fp16 stream (annotate_planes int_stream
+'f16'), as fp16 integers NHWC.
 """
 from __future__ import annotations
 
@@ -40,9 +47,9 @@ import numpy as np
 import torch
 
 from . import ops
-from .compiler import (DENSE_VARIANTS, FUSED_VARIANTS, HEAD_VARIANTS, NEURON_VARIANTS, POOL_VARIANTS, STEM_VARIANTS,
-                       _kname)
-from .ops import ENC_BITS, SEngineError
+from .compiler import (ATTENTION_VARIANTS, DENSE_VARIANTS, FUSED_VARIANTS, HEAD_VARIANTS, NEURON_VARIANTS,
+                       POOL_VARIANTS, STEM_VARIANTS, _kname)
+from .ops import ENC_BITS, ENC_F16, SEngineError
 
 
 def plan_buffers(schedule: list, produces: dict, consumes: dict, aliases: dict, sizes: dict, keep: set) -> dict:
@@ -102,9 +109,11 @@ _VIEW_OPS = {"Reshape", "Transpose", "Identity", "Flatten"}
 class _Launch:
     """One kernel launch of the schedule: the anchor node, what it reads and writes."""
 
-    def __init__(self, nid: int, kind: str, inputs: list, output: str, real_output: Optional[str] = None):
+    def __init__(self, nid: int, kind: str, inputs: list, output: str, real_output: Optional[str] = None,
+                 subs: Optional[list] = None):
         self.nid, self.kind, self.inputs, self.output = nid, kind, inputs, output
         self.real_output = real_output        # a second, fp32 output (membrane-shortcut sums, a kept stem output)
+        self.subs = subs or []                # split launch: the tensors held by the planes of `output`
         self.pair_with: Optional[int] = None  # nid of a fused conv launched together with this one
         self.skip = False                     # launched as the second half of a pair
 
@@ -133,11 +142,19 @@ class CUDAGraphEngine:
         self._graph_output: Optional[torch.Tensor] = None
         self.image_input = False
         self.logits_output = False
+        self.enc: dict = {}
+        self.sub: dict = {}
+        self.attn_ws: Optional[torch.Tensor] = None
+        self.head_ws: Optional[torch.Tensor] = None
 
     # ------------------------------------------------------------------ graph analysis
     def _launch_of(self, node) -> Optional[_Launch]:
         name = _kname(node)
         ea = node.extra_attrs
+        if name in FUSED_VARIANTS and "merged_nids" in ea:
+            return _Launch(node.id, "split", [node.input_names[0]], node.name + ".split", subs=list(ea["merged_outputs"]))
+        if name in ATTENTION_VARIANTS:
+            return _Launch(node.id, "attn", list(node.input_names), node.output_names[0])
         if name in FUSED_VARIANTS and "shortcut_input" in ea:
             return _Launch(node.id, "fused_sc", [node.input_names[0], ea["shortcut_input"]], ea["fused_output"],
                            ea["real_output"])
@@ -163,6 +180,7 @@ class CUDAGraphEngine:
         raise SEngineError(f"node {node.name}: kernel {name} is not served by this build")
 
     def _analyse(self, ir, order):
+        self.sub = {}
         absorbed = set()
         for node in ir.nodes.values():
             absorbed.update(node.extra_attrs.get("absorbed_nids", []))
@@ -178,7 +196,16 @@ class CUDAGraphEngine:
             ln = self._launch_of(node)
             if ln is not None:
                 launches.append(ln)
-                written.update(ln.outputs)
+                written.update(ln.outputs + ln.subs)
+                if ln.kind == "split":  # the merged buffer: one plane of split_channels per conv
+                    ea = node.extra_attrs
+                    split = int(ea["split_channels"])
+                    nplanes = -(-int(ea["merged_out_channels"]) // split)
+                    N, _, H, W = node.output_shapes[0]
+                    shapes[ln.output] = (N, nplanes * split, H, W)
+                    for j, t in enumerate(ln.subs):
+                        aliases[t] = ln.output
+                        self.sub[t] = (j, nplanes)
         for nid in order:  # views (and absorbed single-input nodes) alias their input
             node = ir.nodes[nid]
             if _kname(node) != "ZeroCost":
@@ -246,21 +273,26 @@ class CUDAGraphEngine:
             raise SEngineError("the image input must feed the stem only")
         self.logits_output = launches[-1].kind == "head" and launches[-1].output == self.output_name
 
-        # activation ranges: bit planes per tensor
-        self.planes = {}
+        # activation ranges: bit planes per tensor; out_planes 0 = an fp16 integer stream
+        self.planes, self.enc = {}, {}
         for l in launches:
             node = ir.nodes[l.nid]
-            self.planes[root(l.output)] = int(node.extra_attrs.get("out_planes", 1)) if l.kind == "fused" else 1
+            p = int(node.extra_attrs.get("out_planes", 1)) if l.kind == "fused" else 1
+            self.planes[root(l.output)] = max(p, 1)
+            self.enc[root(l.output)] = "f16" if p == 0 else "bits"
         self.planes.setdefault(self.input_name, 1)
+        if keep_membranes and any(l.kind in ("split", "attn") for l in launches):
+            raise SEngineError("keep_membranes is not served for merged sibling convs or attention cores")
 
         # pair two fused convs on the same input (a block's conv1 and downsample): one launch
         if pair_launches and not keep_membranes:
             for i, a in enumerate(launches):
-                if a.kind != "fused" or a.skip or a.pair_with is not None or len(a.inputs) != 1:
+                if a.kind != "fused" or a.skip or a.pair_with is not None or len(a.inputs) != 1 or \
+                        self.enc.get(root(a.inputs[0]), "bits") != "bits" or self.enc[root(a.output)] != "bits":
                     continue
                 for b in launches[i + 1:]:
                     if b.kind == "fused" and not b.skip and b.pair_with is None and len(b.inputs) == 1 and \
-                            root(b.inputs[0]) == root(a.inputs[0]):
+                            root(b.inputs[0]) == root(a.inputs[0]) and self.enc[root(b.output)] == "bits":
                         a.pair_with, b.skip = b.nid, True
                         break
             # the partner is written by its pair's launch: schedule it right after, so buffer
@@ -293,6 +325,8 @@ class CUDAGraphEngine:
                 return ("f32", n)
             if r == self.input_name and self.image_input:
                 return ("f32", n)
+            if self.enc.get(r) == "f16":
+                return ("f16", n)
             N, C = shp[0], shp[1]
             if (C * self.planes.get(r, 1)) % 32:
                 raise SEngineError(f"tensor {t}: {C} channels is not a multiple of 32 (spike bits)")
@@ -306,7 +340,8 @@ class CUDAGraphEngine:
                             {self.input_name, root(self.output_name)})
         n_buf = 1 + max(b for b in plan.values() if b is not None)
         bufcls = {plan[t]: sizes[t] for t in sizes}
-        self.buffers = [torch.empty(n, dtype=torch.float32 if k == "f32" else torch.int32, device=self.dev)
+        dtypes = {"f32": torch.float32, "bits": torch.int32, "f16": torch.float16}
+        self.buffers = [torch.empty(n, dtype=dtypes[k], device=self.dev)
                         for k, n in (bufcls[i] for i in range(n_buf))]
         self.tensors = {}
         for t in live:
@@ -341,17 +376,32 @@ class CUDAGraphEngine:
             elif l.kind == "neuron" and keep_membranes:
                 N, C, H, W = node.output_shapes[0]
                 self.membranes[l.nid] = torch.zeros(N // self.T * H * W * C, device=self.dev)
+            elif l.kind == "split":  # the concatenated weights and BN vectors of the merged convs
+                ea = node.extra_attrs
+                w = torch.from_numpy(np.ascontiguousarray(ir.weights[ea["merged_weight"]]))
+                self.weights[l.nid] = self.kernels[l.nid].prepare_weight(w.to(self.dev), device=self.dev)
+                sc, bi = ea["merged_bn"]
+                self.bn[l.nid] = (torch.tensor(sc, dtype=torch.float32, device=self.dev),
+                                  torch.tensor(bi, dtype=torch.float32, device=self.dev))
             elif l.kind == "head":
                 self.weights[l.nid] = (
                     torch.from_numpy(np.ascontiguousarray(ir.weights[node.weight_info.name])).float().to(self.dev),
                     torch.from_numpy(np.ascontiguousarray(ir.weights[node.bias_info.name])).float().to(self.dev))
+        # workspaces, shared by the launches that need one (they run one after another on one stream)
+        n_kv = max([self.kernels[l.nid].kv_numel for l in launches if l.kind == "attn"], default=0)
+        self.attn_ws = torch.empty(n_kv, dtype=torch.int32, device=self.dev) if n_kv else None
+        n_hw = max([self.kernels[l.nid].workspace_numel for l in launches if l.kind == "head"], default=0)
+        self.head_ws = torch.empty(n_hw, dtype=torch.int32, device=self.dev) if n_hw else None
         self.graph = None
         return self
 
     @property
     def n_launches(self) -> int:
-        """Kernel launches per forward (pack / unpack of a spike-input graph included)."""
+        """Kernel launches per forward (pack / unpack of a spike-input graph included; an
+        attention core is two, and so is a head whose sums are split over a workspace)."""
         n = sum(1 for l in self.launches if not l.skip)
+        n += sum(1 for l in self.launches if l.kind == "attn")
+        n += sum(1 for l in self.launches if l.kind == "head" and self.kernels[l.nid].workspace_numel)
         if not self.image_input:
             n += 1
         if not self.logits_output:
@@ -360,9 +410,19 @@ class CUDAGraphEngine:
 
     # ------------------------------------------------------------------ execution
     def _bits(self, t):
+        """An activation tensor as NHWC: int32 spike bits (N, H, W, C * planes / 32), or fp16
+        (N, H, W, C) for an fp16 stream; a merged launch's per-conv tensor is its plane."""
         r = self._root_fn(t)
         N, C, H, W = self._shapes[r]
+        if t in self.sub:
+            j, nplanes = self.sub[t]
+            return self.tensors[r].view(nplanes, N, H, W, C // nplanes // 32)[j]
+        if self.enc.get(r) == "f16":
+            return self.tensors[r].view(N, H, W, C)
         return self.tensors[r].view(N, H, W, C * self.planes.get(r, 1) // 32)
+
+    def _enc_of(self, t) -> int:
+        return ENC_F16 if self.enc.get(self._root_fn(t)) == "f16" else ENC_BITS
 
     def _run_fused(self, l):
         node = self.ir.nodes[l.nid]
@@ -370,13 +430,15 @@ class CUDAGraphEngine:
         x, y = self._bits(l.inputs[0]), self._bits(l.output)
         sc, bi = self.bn[l.nid]
         sw = self.weights[l.nid]
-        spec = kern.spec_for(ENC_BITS, ENC_BITS)
-        if len(l.inputs) == 2:  # SEW add absorbed
+        in_enc, out_enc = self._enc_of(l.inputs[0]), self._enc_of(l.output)
+        spec = kern.spec_for(in_enc, out_enc)
+        if len(l.inputs) == 2:  # SEW add absorbed; an fp16 residual / output is the fp16 stream
             ea = node.extra_attrs
-            res = self._bits(l.inputs[1])
-            ops.fused_sparse_conv_bn_lif_add(spec, x.view(-1), sw.values, sw.meta, sc, bi, res,
-                                             int(self.planes.get(self._root_fn(l.inputs[1]), 1)),
-                                             int(ea.get("out_planes", 1)), state=self.membranes.get(l.nid), out=y)
+            r = self._root_fn(l.inputs[1])
+            res_planes = 0 if self.enc.get(r) == "f16" else int(self.planes.get(r, 1))
+            ops.fused_sparse_conv_bn_lif_add(spec, x.view(-1), sw.values, sw.meta, sc, bi, self._bits(l.inputs[1]),
+                                             res_planes, int(ea.get("out_planes", 1)),
+                                             state=self.membranes.get(l.nid), out=y)
             return
         if l.pair_with is not None:
             o = next(m for m in self.launches if m.nid == l.pair_with)
@@ -388,7 +450,17 @@ class CUDAGraphEngine:
             return
         mem = self.membranes.get(l.nid)
         args = (x, sw, mem, sc, bi) if mem is not None else (x, sw, sc, bi)
-        kern(*args, out_enc=ENC_BITS, out=y)
+        kern(*args, out_enc=out_enc, out=y)
+
+    def _run_split(self, l):
+        kern = self.kernels[l.nid]
+        sc, bi = self.bn[l.nid]
+        sw = self.weights[l.nid]
+        split = int(self.ir.nodes[l.nid].extra_attrs["split_channels"])
+        r = self._root_fn(l.output)
+        ops.fused_sparse_conv_bn_lif_split(kern.spec_for(self._enc_of(l.inputs[0]), ENC_BITS),
+                                           self._bits(l.inputs[0]).view(-1), sw.values, sw.meta, sc, bi, split,
+                                           out=self.tensors[r])
 
     def _real(self, t):
         """A real-valued tensor as fp32 NHWC (N, H, W, C); one-timestep tensors (a stem's kept
@@ -415,53 +487,64 @@ class CUDAGraphEngine:
         if not self.image_input:  # first op of the graph
             ops.pack_spikes(self._graph_input, out=self._bits(self.input_name))
         for l in self.launches:
-            if l.skip:
-                continue
-            node = self.ir.nodes[l.nid]
-            if l.kind == "fused":
-                self._run_fused(l)
-            elif l.kind == "fused_sc":
-                self._run_fused_sc(l)
-            elif l.kind == "real_conv":
-                sc, bi = self.bn[l.nid]
-                x = self._root_fn(l.inputs[0])
-                self.kernels[l.nid](self._real(x), self.weights[l.nid], sc, bi,
-                                    in_T=1 if x in self.real_one_t else self.T, out=self._real(l.output))
-            elif l.kind == "dense":
-                sc, bi = self.bn[l.nid]
-                r = self._root_fn(l.output)
-                N, C, H, W = self._shapes[r]
-                self.kernels[l.nid](self._bits(l.inputs[0]), self.weights[l.nid], sc, bi,
-                                    out=self.tensors[r].view(N, H, W, C))
-            elif l.kind == "neuron":  # standalone neuron on a dense conv's fp32 output
-                p = node.neuron_params
-                kind = "lif" if node.op_type.name == "LIF" else "if"
-                v_reset = float(p.v_reset) if p.hard_reset else None
-                ops.multistep_neuron(self.tensors[self._root_fn(l.inputs[0])], self.T, kind, float(p.tau),
-                                     float(p.v_threshold), v_reset, state=self.membranes.get(l.nid), out_enc=ENC_BITS,
-                                     out=self._bits(l.output).view(-1))
-            elif l.kind == "stem":
-                sc, bi = self.bn[l.nid]
-                kern = self.kernels[l.nid]
-                y = self._bits(l.output)
-                if kern.pool is not None:
-                    kern(self._graph_input, self.weights[l.nid], sc, bi, pooled=y)
-                else:
-                    kern(self._graph_input, self.weights[l.nid], sc, bi, spikes=y,
-                         out=self._real(l.real_output) if l.real_output else None)
-            elif l.kind == "pool":
-                r = self._root_fn(l.inputs[0])
-                N, C, H, W = self._shapes[r]
-                if self.planes.get(r, 1) != 1:
-                    raise SEngineError(f"node {node.name}: max-pool of integer activations is not served")
-                pp = node.pool_params or {}
-                ops.maxpool_spikes(self._bits(l.inputs[0]), N, H, W, C, int(pp.get("kernel_size", 3)),
-                                   int(pp.get("stride", 2)), int(pp.get("padding", 1)), out=self._bits(l.output))
-            elif l.kind == "head":
-                fw, fb = self.weights[l.nid]
-                self.kernels[l.nid](self._bits(l.inputs[0]).view(-1), fw, fb, out=self._graph_output)
+            if not l.skip:
+                self._run_launch(l)
         if not self.logits_output:
             ops.unpack_spikes(self._bits(self.output_name), self._graph_output.shape[-1], out=self._graph_output)
+
+    def _run_launch(self, l):
+        """One launch of the schedule (the second half of a pair runs with its first)."""
+        node = self.ir.nodes[l.nid]
+        if l.kind == "fused":
+            self._run_fused(l)
+        elif l.kind == "fused_sc":
+            self._run_fused_sc(l)
+        elif l.kind == "split":
+            self._run_split(l)
+        elif l.kind == "attn":
+            kern = self.kernels[l.nid]
+            q, k, v = (self._bits(t) for t in l.inputs)
+            kern(q, k, v, kv=self.attn_ws[:kern.kv_numel], out=self._bits(l.output))
+        elif l.kind == "real_conv":
+            sc, bi = self.bn[l.nid]
+            x = self._root_fn(l.inputs[0])
+            self.kernels[l.nid](self._real(x), self.weights[l.nid], sc, bi,
+                                in_T=1 if x in self.real_one_t else self.T, out=self._real(l.output))
+        elif l.kind == "dense":
+            sc, bi = self.bn[l.nid]
+            r = self._root_fn(l.output)
+            N, C, H, W = self._shapes[r]
+            self.kernels[l.nid](self._bits(l.inputs[0]), self.weights[l.nid], sc, bi,
+                                out=self.tensors[r].view(N, H, W, C))
+        elif l.kind == "neuron":  # standalone neuron on a dense conv's fp32 output
+            p = node.neuron_params
+            kind = "lif" if node.op_type.name == "LIF" else "if"
+            v_reset = float(p.v_reset) if p.hard_reset else None
+            ops.multistep_neuron(self.tensors[self._root_fn(l.inputs[0])], self.T, kind, float(p.tau),
+                                 float(p.v_threshold), v_reset, state=self.membranes.get(l.nid), out_enc=ENC_BITS,
+                                 out=self._bits(l.output).view(-1))
+        elif l.kind == "stem":
+            sc, bi = self.bn[l.nid]
+            kern = self.kernels[l.nid]
+            y = self._bits(l.output)
+            if kern.pool is not None:
+                kern(self._graph_input, self.weights[l.nid], sc, bi, pooled=y)
+            else:
+                kern(self._graph_input, self.weights[l.nid], sc, bi, spikes=y,
+                     out=self._real(l.real_output) if l.real_output else None)
+        elif l.kind == "pool":
+            r = self._root_fn(l.inputs[0])
+            N, C, H, W = self._shapes[r]
+            if self.planes.get(r, 1) != 1:
+                raise SEngineError(f"node {node.name}: max-pool of integer activations is not served")
+            pp = node.pool_params or {}
+            ops.maxpool_spikes(self._bits(l.inputs[0]), N, H, W, C, int(pp.get("kernel_size", 3)),
+                               int(pp.get("stride", 2)), int(pp.get("padding", 1)), out=self._bits(l.output))
+        elif l.kind == "head":
+            fw, fb = self.weights[l.nid]
+            kern = self.kernels[l.nid]
+            ws = self.head_ws[:kern.workspace_numel] if kern.workspace_numel else None
+            kern(self._bits(l.inputs[0]).view(-1), fw, fb, out=self._graph_output, workspace=ws)
 
     def capture_graph(self):
         """Warm up on a side stream, then capture the whole schedule into one hipGraph."""
@@ -526,23 +609,43 @@ class CUDAGraphEngine:
         return a.elapsed_time(b) / n_iters
 
     def spike_density(self) -> dict:
-        """Activity of every spike tensor of the last forward: fraction of set bits per
-        activation (for integer activations, of nonzero values).  Off the timed path."""
+        """Activity of every spike tensor of the last forward's input: fraction of set bits per
+        activation (for integer activations, of nonzero values).  The forward is run again
+        eagerly, launch by launch, and each tensor measured right after its launch wrote it (the
+        buffer planner recycles a tensor's memory once its readers have run); kept membranes advance
+        as in a forward.  Off the timed path."""
         lut = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.int64, device=self.dev)
         out = {}
+        if not self.image_input:
+            ops.pack_spikes(self._graph_input, out=self._bits(self.input_name))
         for l in self.launches:
-            if l.kind in ("dense", "head", "real_conv"):
+            if l.skip:
                 continue
-            r = self._root_fn(l.output)
+            self._run_launch(l)
+            done = [l] + ([m for m in self.launches if m.nid == l.pair_with] if l.pair_with is not None else [])
+            for m in done:
+                if m.kind not in ("dense", "head", "real_conv"):
+                    self._density(m, lut, out)
+        return out
+
+    def _density(self, l, lut, out):
+        for t in (l.subs or [l.output]):
+            r = self._root_fn(t)
+            v = self._bits(t)
+            name = self.ir.nodes[l.nid].name + (f"[{t}]" if l.subs else "")
+            if self.enc.get(r) == "f16":
+                out[name] = float((v != 0).sum()) / v.numel()
+                continue
             N, C, H, W = self._shapes[r]
             P = self.planes.get(r, 1)
-            words = self._bits(l.output).reshape(N * H * W, P, C // 32)
+            if t in self.sub:
+                C //= self.sub[t][1]
+            words = v.reshape(N * H * W, P, C // 32)
             nz = words[:, 0]
             for p in range(1, P):
                 nz = nz | words[:, p]
             cnt = int(lut[nz.contiguous().view(torch.uint8).long()].sum())
-            out[self.ir.nodes[l.nid].name] = cnt / float(N * H * W * C)
-        return out
+            out[name] = cnt / float(N * H * W * C)
 
 
 HipGraphEngine = CUDAGraphEngine

@@ -145,7 +145,7 @@ def test_passes_route_sparse_conv_to_fused_variant():
     ir, out, conv, bn = build_block()
     stats = passes.optimize_ir(ir)
     assert stats == dict(fused=1, dense=0, unsupported=0, folded=1, groups=1, sparse=1, stems=0, adds=0, heads=0,
-                         pools=0, shortcuts=0, real_convs=0)
+                         pools=0, shortcuts=0, real_convs=0, linears=0, padded=0, merged=0, attention=0)
     convs = [n for n in ir.nodes.values() if n.op_type == OpType.Conv2d]
     lifs = [n for n in ir.nodes.values() if n.op_type == OpType.LIF]
     assert not [n for n in ir.nodes.values() if n.op_type == OpType.BatchNorm]
