@@ -22,9 +22,9 @@ LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libsengine_amd.so")
 ARCH = "gfx950"
 
-SOURCES = ["capi.hip", "fused_sparse.hip", "fused_sparse_lds.hip", "fused_tile1.hip", "fused_tile3.hip",
-           "fused_tile3s.hip", "compress.hip", "fallback.hip", "sew.hip", "ssa.hip", "msres.hip", "calib.hip",
-           "weights.hip"]
+SOURCES = ["capi.hip", "fused_sparse.hip", "fused_sparse_lds.hip", "fused_tile1.hip", "fused_tile1ds.hip",
+           "fused_tile3.hip", "fused_tile3s.hip", "compress.hip", "fallback.hip", "sew.hip", "ssa.hip", "msres.hip",
+           "calib.hip", "weights.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

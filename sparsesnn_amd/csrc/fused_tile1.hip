@@ -243,6 +243,9 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
   // tile instances (every mode)
   const bool fast_f16out = f16in ? c.pm == 0 : (!c.k3 && d->T == 4 && c.pm == 0 && mode == EPI_LIF_HARD);
   const char* epi = d->out_enc == SENGINE_ENC_BITS || fast_f16out ? kEpi[mode] : "generic";
+  if (!c.k3)
+    if (const int nw = tile1ds_config(d, geo.M, mode, &a))
+      return describe_tile1ds(d, geo.M, nw, mode, a.state != nullptr, buf, len);
   if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
     const int nw = ps >> 4, npg = (int)(geo.M / 16), nsb = d->C_out / (64 * nw);
     const int per = tile1ps_per(npg, nsb, tile1ps_slots(nw));
@@ -354,6 +357,7 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
       shortcut_only);
   if (d->in_enc == SENGINE_ENC_F16) {
     if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
+    if (const int nw = tile1ds_config(d, geo.M, mode, &a)) return launch_fused_f16_tile1ds(p, d, nw, mode, stream);
     if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
       if (d->out_enc == SENGINE_ENC_F16)  // fp16 in and out: the exported per-node call's form (with state)
         return ps == 6 * 16 + 3

@@ -76,6 +76,15 @@ struct TileChoice {
 };
 bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice& c);
 
+// Direct-staged fp16-input 1x1 kernel (tile1ds.h, fused_tile1ds.hip): tile1ds_config returns its
+// waves per workgroup (0: not eligible); the launch takes the tile route's TileParams.
+struct TileParams;
+int tile1ds_config(const sengine_conv_lif_desc* d, int64_t M, int mode, const FusedArgs* a);
+int describe_tile1ds(const sengine_conv_lif_desc* d, int64_t M, int nw, int mode, bool state, char* buf,
+                     size_t len);
+hipError_t launch_fused_f16_tile1ds(const TileParams& p, const sengine_conv_lif_desc* d, int nw, int mode,
+                                    hipStream_t stream);
+
 // fp16 activations (T = 4, one weight plane) on geometries the tile forms do not cover: the
 // gather form of the tile kernel (tile_kernel.h, KS = 0; fused_tile1.hip).
 bool tile_gather_eligible(const sengine_conv_lif_desc* d);

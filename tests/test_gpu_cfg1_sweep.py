@@ -87,8 +87,8 @@ def test_cfg1_layer_full_size(dev, abi_so, C_in, C_out, H, W, k, p_spike):
     spec_abi = dataclasses.replace(spec, in_enc=ops.ENC_F16, out_enc=ops.ENC_F16)
     plan_abi = ops.fused_plan(spec_abi, state=True)
     print(f"  reference call(): {plan_abi}", flush=True)
-    if k == 1:  # fp16 in and out with a membrane: the persistent 1x1 kernel's state form
-        assert plan_abi.startswith("tile1ps<T=4,") and "in=f16,out=f16" in plan_abi and ",state>" in plan_abi
+    if k == 1:  # fp16 in and out with a membrane: the direct-staged 1x1 kernel's state form
+        assert plan_abi.startswith("tile1ds<T=4,") and "in=f16,out=f16" in plan_abi and ",state>" in plan_abi
     else:
         assert plan_abi.startswith("tile<T=4,KS=3,") and "in=f16,out=f16" in plan_abi
 

@@ -495,9 +495,12 @@ def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron, slots, out_enc):
     super-blocks with resident workgroups walking 1 or 2 position groups each (5,120 positions
     over 256 workgroups per super-block), a single group, four super-blocks; 6-wave 384-channel
     super-blocks (phases of three chunks), one per CU walking 1 or 2 groups, or three
-    super-blocks; LIF and IF, against the oracle."""
+    super-blocks; LIF and IF, against the oracle.  The direct-staged kernel (tile1ds.h), which
+    takes 4- and 6-chunk layers of 256 | C_out by default, is switched off here; it has its own
+    tests (tests/test_gpu_tile1ds.py)."""
     if slots:  # few resident workgroups: every one walks many groups
         os.environ["SENGINE_AMD_PS_SLOTS"] = str(slots)
+    os.environ["SENGINE_AMD_TILE1_DS"] = "0"
     try:
         spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
                             neuron=neuron, in_enc=ops.ENC_F16,
@@ -515,6 +518,7 @@ def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron, slots, out_enc):
         assert float(r.spikes.mean()) > 0.002  # the comparison covers firing neurons
     finally:
         os.environ.pop("SENGINE_AMD_PS_SLOTS", None)
+        os.environ.pop("SENGINE_AMD_TILE1_DS", None)
 
 
 @pytest.mark.parametrize("C_in,C_out,H,W,B,mode", [(768, 384, 64, 40, 2, "res16"), (256, 512, 32, 32, 2, "f16"),
