@@ -203,14 +203,15 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
       const int c = ph * CG + cc;
       // chunk c uses set c & 1 (ring), or set cc (resident)
       const int ra = ARES ? cc : (CG % 2 == 0 ? cc : PAR + cc) & 1;
-      if (!ARES) {
-        if (c + 1 < p.nchunk) load_a(c + 1, av[ra ^ 1], ix[ra ^ 1]);
-        else if (f + 1 < nf) load_a(0, av[ra ^ 1], ix[ra ^ 1]);  // nchunk even: set 0, the next group
-      }
+      // Both loads below are unconditional (the operands of an existing chunk or phase when
+      // there is no next one: loaded again, then unused).  Under a branch, the compiler's wait
+      // counts after the join would have to cover the path with fewer loads in flight, and it
+      // falls back to waiting for every outstanding load (this chunk's prefetch included).
+      if (!ARES) load_a(c + 1 < p.nchunk ? c + 1 : 0, av[ra ^ 1], ix[ra ^ 1]);  // nchunk even: set 0, the next group
       // Phase f + 2's items go out after this phase's last A-operand load: vector memory counts
       // complete in issue order, so a wait for a later-issued A operand would also wait for
       // these.  Set PAR is free: phase f's own items were stored at the end of phase f - 1.
-      if (cc == CG - 1 && f + 2 < nf) load_pieces(pst[PAR], f + 2);
+      if (cc == CG - 1) load_pieces(pst[PAR], f + 2 < nf ? f + 2 : nf - 1);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int step = cc * T + t;
