@@ -436,7 +436,7 @@ def bench_msresnet34(dev, warmup: int, iters: int, eager: bool = False):
     eng = CUDAGraphEngine().build(ir, kernels, T=T_STEPS, batch_size=CFG34_BATCH, device=dev)
     x = torch.randn((CFG34_BATCH, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(8))
     s = bench_generic_engine(eng, x.to(dev), warmup, iters, eager)
-    return dict(params=params, x=x, batch_s=s, launches=eng.n_launches)
+    return dict(params=params, x=x, batch_s=s, launches=eng.n_launches, names=eng.launch_names())
 
 
 def bench_spikformer(dev, warmup: int, iters: int, eager: bool = False):
@@ -458,7 +458,7 @@ def bench_spikformer(dev, warmup: int, iters: int, eager: bool = False):
     eng = CUDAGraphEngine().build(ir, kernels, T=T_STEPS, batch_size=CFG34_BATCH, device=dev)
     x = torch.randn((CFG34_BATCH, 3, CFG34_HW, CFG34_HW), generator=torch.Generator().manual_seed(9))
     s = bench_generic_engine(eng, x.to(dev), warmup, iters, eager)
-    return dict(params=params, x=x, batch_s=s, launches=eng.n_launches)
+    return dict(params=params, x=x, batch_s=s, launches=eng.n_launches, names=eng.launch_names())
 
 
 def cpu_sample(fn, budget_s: float, min_runs: int = CPU_MIN_RUNS):
@@ -537,6 +537,8 @@ def main():
             e2e, batch = bench_msresnet34(dev, warmup=args.warmup, iters=args.steps, eager=eager), CFG34_BATCH
         else:
             e2e, batch = bench_spikformer(dev, warmup=args.warmup, iters=args.steps, eager=eager), CFG34_BATCH
+        for i, name in enumerate(e2e.get("names", [])):  # kernel launches of one forward, in order
+            print(f"launch {i}: {name}", file=sys.stderr)
         if eager:
             copy_calibration(dev)  # the counters' scale: a copy of known size
         print(json.dumps({"metric": "images/sec", "model": args.e2e_model, "value": round(batch / e2e["batch_s"], 1),

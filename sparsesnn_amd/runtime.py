@@ -408,6 +408,29 @@ class CUDAGraphEngine:
             n += 1
         return n
 
+    def launch_names(self) -> list:
+        """One label per kernel launch of a forward, in launch order (len == n_launches): the
+        anchor node's name and launch kind; a pair names both convs, an attention core and a
+        split-sum head give one label per kernel."""
+        names = [] if self.image_input else ["pack_spikes"]
+        for l in self.launches:
+            if l.skip:
+                continue
+            name = self.ir.nodes[l.nid].name
+            if l.kind == "split":
+                name = " + ".join(self.ir.nodes[i].name for i in self.ir.nodes[l.nid].extra_attrs["merged_nids"])
+            if l.pair_with is not None:
+                name += " + " + self.ir.nodes[l.pair_with].name
+            if l.kind == "attn":
+                names += [f"{name} (attn: key-value sums)", f"{name} (attn: attend)"]
+            elif l.kind == "head" and self.kernels[l.nid].workspace_numel:
+                names += [f"{name} (head: partial sums)", f"{name} (head: classifier)"]
+            else:
+                names.append(f"{name} ({l.kind})")
+        if not self.logits_output:
+            names.append("unpack_spikes")
+        return names
+
     # ------------------------------------------------------------------ execution
     def _bits(self, t):
         """An activation tensor as NHWC: int32 spike bits (N, H, W, C * planes / 32), or fp16

@@ -29,6 +29,7 @@ def test_generic_engine_runs_ms_resnet(dev, depth, neuron, B, hw):
     eng = build_generic(p, B, depth, neuron, hw, dev)
     ref_eng = MSResNetEngine(p, batch=B, T=4, depth=depth, neuron=neuron, in_hw=hw, device=dev)
     assert eng.n_launches == ref_eng.launches, (eng.n_launches, ref_eng.launches)
+    assert len(eng.launch_names()) == eng.n_launches
     want = ref_eng.forward(x.to(dev)).clone()
     eager = eng(x.to(dev))
     torch.cuda.synchronize()

@@ -38,6 +38,8 @@ def test_generic_engine_runs_spikformer(dev, stream, embed, heads, depth, B, hw)
     ref_eng = SpikformerEngine(p, batch=B, T=4, embed=embed, heads=heads, depth=depth, in_hw=hw, device=dev,
                                stream=stream)
     assert eng.n_launches == ref_eng.launches, (eng.n_launches, ref_eng.launches)
+    names = eng.launch_names()
+    assert len(names) == eng.n_launches and any("(attn: attend)" in n for n in names), names
     want = ref_eng.forward(x.to(dev)).clone()
     eager = eng(x.to(dev))
     torch.cuda.synchronize()
