@@ -7,10 +7,11 @@
 // N^2 d to N d^2 per head, and the result is bit-identical.
 //
 //   ssa_kv_kernel:     KV[t, b, h] = K^T V (int32 d x d).  A workgroup of 16 waves per
-//                      (t*B + b, h): each wave turns 64 tokens' head slices into
-//                      per-channel 64-token masks with ballots (bit transposition; lane i
-//                      collects mask i, one wave-wide LDS store per group), then threads
-//                      sum popcount(K_i & V_j) over the token masks.
+//                      (t*B + b, head pair), walking the tokens in chunks of 16 x 64: each
+//                      wave turns 64 tokens' head slices into per-channel 64-token masks
+//                      with a butterfly bit transpose across the wave (lane i ends with
+//                      mask i), then threads add popcount(K_i & V_j) over the chunk's token
+//                      masks to registers.
 //   ssa_attend_kernel: X = Q KV on MFMA (v_mfma_f32_16x16x32_f16: A = KV^T as two exact
 //                      6-bit fp16 pieces pre-scaled by a power of two, B = Q expanded
 //                      from bits, one fp32 accumulator), the neuron over T in
@@ -24,7 +25,7 @@
 
 namespace sengine {
 
-constexpr int kSsaMaxN = 8192;   // tokens (the KV kernel keeps 2 x d x N/64 token masks in LDS)
+constexpr int kSsaMaxN = 8192;   // tokens (the attend kernel stages a workgroup's Q slices in LDS)
 constexpr int kSsaMaxD = 64;
 constexpr size_t kSsaMaxLds = 163840;  // attend kernel: KV pieces of every t and the staged Q slices
 
@@ -50,82 +51,174 @@ __device__ __forceinline__ uint64_t head_slice(const uint32_t* row, int words, i
 
 constexpr int kSsaKvWaves = 16;
 
+// 64 x 64 bit-matrix transpose across a wave: lane l holds row l (64 bits); afterwards lane c
+// holds column c (bit l = row l's bit c).  Six butterfly stages swap the off-diagonal blocks of
+// every 2d x 2d block: at stage d, a lane with bit d clear keeps the low d bits of each 2d-bit
+// field and takes its partner's low d bits above them, a lane with bit d set keeps the high d
+// bits and takes its partner's high d bits below them.
+__device__ __forceinline__ uint64_t transpose64(uint64_t x, int lane) {
+  uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+  {  // d = 32: whole words
+    const bool up = lane & 32;
+    const uint32_t r = (uint32_t)__shfl_xor((int)(up ? lo : hi), 32, 64);
+    if (up) lo = r;
+    else hi = r;
+  }
+  constexpr uint32_t kMask[5] = {0x0000ffffu, 0x00ff00ffu, 0x0f0f0f0fu, 0x33333333u, 0x55555555u};
+#pragma unroll
+  for (int st = 0; st < 5; ++st) {
+    const int d = 16 >> st;
+    const uint32_t m = kMask[st];
+    const bool clear = (lane & d) == 0;
+    const uint32_t plo = (uint32_t)__shfl_xor((int)lo, d, 64), phi = (uint32_t)__shfl_xor((int)hi, d, 64);
+    lo = clear ? ((lo & m) | ((plo << d) & ~m)) : ((lo & ~m) | ((plo >> d) & m));
+    hi = clear ? ((hi & m) | ((phi << d) & ~m)) : ((hi & ~m) | ((phi >> d) & m));
+  }
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// A row slice of up to 256 bits (bit 0 = the slice's first bit) and the D bits at `bit`.
+struct RowSlice {
+  unsigned __int128 a, b;  // bits 0..127, 128..255
+};
 template <int D>
-__global__ __launch_bounds__(64 * kSsaKvWaves) void ssa_kv_kernel(SsaParams p) {
-  // K masks [G][D], then V masks [G][VS] (mask j at j + j/32: a read of masks j0+u by lane
-  // groups j0 = 0, 16, 32, 48 hits four different bank pairs), then the KV sums
-  extern __shared__ uint64_t masks[];
-  constexpr int VS = D + 2;
+__device__ __forceinline__ uint64_t bits_at(const RowSlice& w, int bit) {
+  uint64_t x;
+  if (bit >= 128) {
+    x = (uint64_t)(w.b >> (bit - 128));
+  } else {
+    x = (uint64_t)(w.a >> bit);
+    if (bit + D > 128) x |= (uint64_t)(w.b << (128 - bit));
+  }
+  return D == 64 ? x : (x & ((1ull << D) - 1));
+}
+
+// Workgroup = (t*B + b, HP consecutive heads).  The tokens are walked in chunks of one 64-token
+// group per wave: each wave loads its group's HP head slices (one contiguous run of the token
+// row: HP heads share every cache line fetched), transposes each into per-channel token masks
+// (the next chunk's rows are already in flight), and after a barrier every thread adds the
+// popcounts of its (head, IB i, 16 j) item over a residue class of the chunk's groups to
+// registers; the residues meet in LDS by integer atomics at the end (exact, order-free).
+template <int D, int HP>
+__global__ __launch_bounds__(64 * kSsaKvWaves) __attribute__((amdgpu_waves_per_eu(HP >= 4 ? 4 : 8))) void ssa_kv_kernel(SsaParams p) {
+  constexpr int VS = D + 2;  // V mask j at j + j/32: reads of masks j0+u by the j0 = 0, 16, 32, 48 lane groups spread over bank pairs
+  constexpr int NWS = (HP * D + 31) / 32 + (HP * D % 32 != 0 || HP == 1 ? 1 : 0);  // words of a row slice
+  static_assert(NWS <= 8, "a row slice fits 256 bits");
+  constexpr int JC = D / 16;
+  constexpr int IB = 1;  // K channels per item (each V mask read feeds IB popcounts; 2 measured no faster)
+  constexpr int ITEMS = HP * (D / IB) * JC;
+  constexpr int R = kSsaKvWaves * 64 / ITEMS > 0 ? kSsaKvWaves * 64 / ITEMS : 1;
+  // the chunk's K masks [HP][wave][D] and V masks [HP][wave][VS]; after the last chunk the same
+  // memory holds the (head, i, j) sums
+  constexpr int KM = HP * kSsaKvWaves * D, MW = KM + HP * kSsaKvWaves * VS, SW = (HP * D * D + 1) / 2;
+  __shared__ uint64_t smem[MW > SW ? MW : SW];
+  uint64_t* sKm = smem;       // [(e * kSsaKvWaves + g) * D + c]
+  uint64_t* sVm = smem + KM;  // [(e * kSsaKvWaves + g) * VS + c]
+  uint32_t* sum = reinterpret_cast<uint32_t*>(smem);  // [(e * D + i) * D + j]
   const int G = (p.N + 63) >> 6;
-  uint64_t* Km = masks;
-  uint64_t* Vm = masks + (size_t)D * G;
-  uint32_t* sum = reinterpret_cast<uint32_t*>(masks + (size_t)(D + VS) * G);  // [D][D]
-  for (int idx = threadIdx.x; idx < D * D; idx += blockDim.x) sum[idx] = 0u;
-  const int tb = blockIdx.x / p.H;
-  const int h = blockIdx.x - tb * p.H;
+  const int nhb = p.H / HP;
+  const int tb = blockIdx.x / nhb;
+  const int h0 = (blockIdx.x - tb * nhb) * HP;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int words = p.C >> 5;
-  // this lane's token slices, loaded one token group ahead of the ballots
-  auto load = [&](int g, uint64_t& ks, uint64_t& vs) {
+  const int w0 = (h0 * D) >> 5;                                  // first word of the slice
+  const int sh = (HP * D) % 32 == 0 && HP > 1 ? 0 : ((h0 * D) & 31);  // its first bit within that word
+
+  // this lane's token row slice (the HP heads' bits from word w0 on) of group g, k and v
+  auto load = [&](int g, RowSlice& kw, RowSlice& vw) {
     const int n = (g << 6) + lane;
-    ks = vs = 0;
-    if (g < G && n < p.N) {
-      const size_t row = ((size_t)tb * p.N + n) * words;
-      ks = head_slice(p.k + row, words, h * D, D);
-      vs = head_slice(p.v + row, words, h * D, D);
+    const bool in = g < G && n < p.N;
+    const size_t row = ((size_t)tb * p.N + (in ? n : 0)) * words + w0;
+    uint32_t kx[NWS], vx[NWS];
+    if constexpr (HP > 1) {  // the slice is whole words inside the row: one vector load each
+      typedef uint32_t slice_t __attribute__((ext_vector_type(NWS), aligned(4)));
+      const slice_t ka = *reinterpret_cast<const slice_t*>(p.k + row);
+      const slice_t va = *reinterpret_cast<const slice_t*>(p.v + row);
+#pragma unroll
+      for (int u = 0; u < NWS; ++u) {
+        kx[u] = in ? ka[u] : 0u;
+        vx[u] = in ? va[u] : 0u;
+      }
+    } else {  // a head's bits may end in the row's last word
+#pragma unroll
+      for (int u = 0; u < NWS; ++u) {
+        const bool ok = in && w0 + u < words;
+        kx[u] = ok ? p.k[row + u] : 0u;
+        vx[u] = ok ? p.v[row + u] : 0u;
+      }
+    }
+    kw = vw = RowSlice{0, 0};
+#pragma unroll
+    for (int u = 0; u < NWS; ++u) {
+      if (u < 4) {
+        kw.a |= (unsigned __int128)kx[u] << (32 * u);
+        vw.a |= (unsigned __int128)vx[u] << (32 * u);
+      } else {
+        kw.b |= (unsigned __int128)kx[u] << (32 * (u - 4));
+        vw.b |= (unsigned __int128)vx[u] << (32 * (u - 4));
+      }
     }
   };
-  uint64_t ksn, vsn;
-  load(wave, ksn, vsn);
-  for (int g = wave; g < G; g += kSsaKvWaves) {
-    const uint32_t k0 = (uint32_t)ksn, k1 = (uint32_t)(ksn >> 32);
-    const uint32_t v0 = (uint32_t)vsn, v1 = (uint32_t)(vsn >> 32);
-    load(g + kSsaKvWaves, ksn, vsn);
-    // compile-time bit masks: one test and one ballot per bit; lane i keeps mask i, so the
-    // group's masks go to LDS as two wave-wide stores instead of 2*D single-lane ones
-    int km0 = 0, km1 = 0, vm0 = 0, vm1 = 0;  // lane i: mask i (low, high word)
+  // this thread's item: head hh, channels i0 .. i0 + IB - 1 of K, channels j0 .. j0 + 15 of V, residue r
+  const int r = (int)threadIdx.x / ITEMS;
+  const int ij = (int)threadIdx.x - r * ITEMS;
+  const int hh = ij / ((D / IB) * JC);
+  const int i0 = (ij - hh * (D / IB) * JC) / JC * IB;
+  const int j0 = (ij - hh * (D / IB) * JC - (i0 / IB) * JC) << 4;
+  const bool active = r < R;
+  uint32_t acc[IB][16];
 #pragma unroll
-    for (int i = 0; i < D; ++i) {
-      const uint64_t mk = __ballot(((i < 32 ? k0 : k1) >> (i & 31)) & 1u);
-      const uint64_t mv = __ballot(((i < 32 ? v0 : v1) >> (i & 31)) & 1u);
-      // the ballot's SGPRs come from a VALU compare: wait states before v_writelane reads
-      // them (the compiler's hazard recognizer does not look inside inline asm)
-      asm("s_nop 4\n\tv_writelane_b32 %0, %1, %2" : "+v"(km0) : "s"((uint32_t)mk), "i"(i));
-      asm("v_writelane_b32 %0, %1, %2" : "+v"(km1) : "s"((uint32_t)(mk >> 32)), "i"(i));
-      asm("s_nop 4\n\tv_writelane_b32 %0, %1, %2" : "+v"(vm0) : "s"((uint32_t)mv), "i"(i));
-      asm("v_writelane_b32 %0, %1, %2" : "+v"(vm1) : "s"((uint32_t)(mv >> 32)), "i"(i));
+  for (int a = 0; a < IB; ++a)
+#pragma unroll
+    for (int u = 0; u < 16; ++u) acc[a][u] = 0;
+
+  RowSlice kn, vn;
+  load(wave, kn, vn);
+  for (int c0 = 0; c0 < G; c0 += kSsaKvWaves) {
+    const RowSlice kw = kn, vw = vn;
+    load(c0 + kSsaKvWaves + wave, kn, vn);
+#pragma unroll
+    for (int e = 0; e < HP; ++e) {
+      // lane c: the token mask of channel c of head h0 + e (bit l = token l's bit c)
+      const uint64_t km = transpose64(bits_at<D>(kw, e * D + sh), lane);
+      const uint64_t vm = transpose64(bits_at<D>(vw, e * D + sh), lane);
+      if (lane < D) {
+        sKm[(e * kSsaKvWaves + wave) * D + lane] = km;
+        sVm[(e * kSsaKvWaves + wave) * VS + lane + (lane >> 5)] = vm;
+      }
     }
-    if (lane < D) {
-      Km[(size_t)g * D + lane] = ((uint64_t)(uint32_t)km1 << 32) | (uint32_t)km0;
-      Vm[(size_t)g * VS + lane + (lane >> 5)] = ((uint64_t)(uint32_t)vm1 << 32) | (uint32_t)vm0;
+    __syncthreads();
+    const int ng = min(kSsaKvWaves, G - c0);
+    if (active) {
+      for (int gg = r; gg < ng; gg += R) {
+        uint64_t ki[IB];
+#pragma unroll
+        for (int a = 0; a < IB; ++a) ki[a] = sKm[(hh * kSsaKvWaves + gg) * D + i0 + a];
+        const uint64_t* vj = sVm + (hh * kSsaKvWaves + gg) * VS + j0 + (j0 >> 5);  // j0 % 32 + 16 <= 32: one shift for all u
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const uint64_t vm = vj[u];
+#pragma unroll
+          for (int a = 0; a < IB; ++a) acc[a][u] += (uint32_t)__popcll(ki[a] & vm);
+        }
+      }
     }
+    __syncthreads();
+  }
+  for (int idx = threadIdx.x; idx < HP * D * D; idx += blockDim.x) sum[idx] = 0u;
+  __syncthreads();
+  if (active) {
+#pragma unroll
+    for (int a = 0; a < IB; ++a)
+#pragma unroll
+      for (int u = 0; u < 16; ++u) atomicAdd(&sum[(hh * D + i0 + a) * D + j0 + u], acc[a][u]);
   }
   __syncthreads();
-  // work item = (i, 16 consecutive j, token-group residue r): K_i masks read once per
-  // token group; the residues' partial counts meet in LDS by integer atomics (exact, order-free)
-  constexpr int JC = D / 16;
-  constexpr int R = kSsaKvWaves * 64 / (D * JC) > 0 ? kSsaKvWaves * 64 / (D * JC) : 1;
-  for (int item = threadIdx.x; item < D * JC * R; item += blockDim.x) {
-    const int r = item / (D * JC);
-    const int ij = item - r * (D * JC);
-    const int i = ij / JC;
-    const int j0 = (ij - i * JC) << 4;
-    uint32_t acc[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) acc[u] = 0;
-    for (int g = r; g < G; g += R) {
-      const uint64_t ki = Km[(size_t)g * D + i];
-      const uint64_t* vj = Vm + (size_t)g * VS + j0 + (j0 >> 5);  // j0 % 32 + 16 <= 32: one shift for all u
-#pragma unroll
-      for (int u = 0; u < 16; ++u) acc[u] += (uint32_t)__popcll(ki & vj[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < 16; ++u) atomicAdd(&sum[i * D + j0 + u], acc[u]);
+  for (int idx = threadIdx.x; idx < HP * D * D; idx += blockDim.x) {
+    const int e = idx / (D * D);
+    p.kv[((size_t)tb * p.H + h0 + e) * D * D + (idx - e * D * D)] = (int32_t)sum[idx];
   }
-  __syncthreads();
-  int32_t* kv = p.kv + (size_t)blockIdx.x * D * D;
-  for (int idx = threadIdx.x; idx < D * D; idx += blockDim.x) kv[idx] = (int32_t)sum[idx];
 }
 
 // Workgroup = (b, h, one of `splits` token ranges): KV of every t is staged once in LDS
@@ -151,16 +244,44 @@ __global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits
   const int words = p.C >> 5;
   const bool fold = p.np.neuron == SENGINE_NEURON_LIF && p.np.pow2;
 
-  // stage: a wave per (t, i) row, lanes over j (coalesced reads), transposed fp16 pieces
+  // stage: K^T V of every t as transposed fp16 pieces [t][piece][j][i].  The entries move as
+  // 16-byte rows (4 consecutive j of one i), up to 8 per thread in flight before any is stored,
+  // so the workgroup waits for a few round trips, not one per row.  Pieces are pre-scaled by
+  // xscale (a power of two): lo * xs and hi * 64 * xs stay exact in fp16, and both MFMAs
+  // accumulate x itself into one fp32 accumulator.
   _Float16* s = reinterpret_cast<_Float16*>(skv);
-  for (int ti = wave; ti < T * 64; ti += 4) {
-    const int t = ti >> 6, i = ti & 63;
-    if (lane < D) {
-      // pieces pre-scaled by xscale (a power of two): lo * xs and hi * 64 * xs stay exact in
-      // fp16, and both MFMAs accumulate x itself into one fp32 accumulator
-      const int32_t x = i < D ? p.kv[((size_t)(t * p.B + b) * p.H + h) * D * D + i * D + lane] : 0;
-      s[((size_t)(t * 2 + 0) * D + lane) * kSsaRow + i] = (_Float16)((float)(x & 63) * p.xscale);
-      s[((size_t)(t * 2 + 1) * D + lane) * kSsaRow + i] = (_Float16)((float)((x >> 6) << 6) * p.xscale);
+  constexpr int NV4 = T * D * D / 4;  // 16-byte rows
+  constexpr int QB = 8;               // rows in flight per thread
+  for (int base = threadIdx.x; base < NV4; base += 256 * QB) {
+    int4 xv[QB];
+#pragma unroll
+    for (int r = 0; r < QB; ++r) {
+      const int q4 = base + r * 256;
+      if (q4 < NV4) {
+        const int t = q4 / (D * D / 4);
+        xv[r] = *reinterpret_cast<const int4*>(p.kv + ((size_t)(t * p.B + b) * p.H + h) * D * D +
+                                                (size_t)(q4 - t * (D * D / 4)) * 4);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < QB; ++r) {
+      const int q4 = base + r * 256;
+      if (q4 < NV4) {
+        const int t = q4 / (D * D / 4), rem = q4 - t * (D * D / 4);
+        const int i = rem / (D / 4), j0 = (rem - i * (D / 4)) * 4;
+        const int xs[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          s[((size_t)(t * 2 + 0) * D + j0 + u) * kSsaRow + i] = (_Float16)((float)(xs[u] & 63) * p.xscale);
+          s[((size_t)(t * 2 + 1) * D + j0 + u) * kSsaRow + i] = (_Float16)((float)((xs[u] >> 6) << 6) * p.xscale);
+        }
+      }
+    }
+  }
+  if (D < 64) {  // rows i = D .. 63 of the last k step read as zero
+    for (int idx = threadIdx.x; idx < T * 2 * D * (64 - D); idx += 256) {
+      const int row = idx / (64 - D);
+      s[(size_t)row * kSsaRow + D + (idx - row * (64 - D))] = (_Float16)0.f;
     }
   }
   __syncthreads();
@@ -174,10 +295,19 @@ __global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits
   // wait for those stores too.
   uint64_t* sq = reinterpret_cast<uint64_t*>(skv + (size_t)T * 2 * D * RV);  // [t][token]
   const int ntok = (tile_end - tile0) * 16;
-  for (int idx = threadIdx.x; idx < T * ntok; idx += blockDim.x) {
-    const int t = idx / ntok, k = idx - (idx / ntok) * ntok;
-    const int n = tile0 * 16 + k;
-    sq[idx] = n < p.N ? head_slice(p.q + ((size_t)(t * p.B + b) * p.N + n) * words, words, h * D, D) : 0ull;
+  for (int base = threadIdx.x; base < T * ntok; base += 256 * QB) {  // QB slices in flight per thread
+    uint64_t qs[QB];
+#pragma unroll
+    for (int r = 0; r < QB; ++r) {
+      const int idx = base + r * 256;
+      const int t = idx / ntok, n = tile0 * 16 + idx - t * ntok;
+      qs[r] = idx < T * ntok && n < p.N
+                  ? head_slice(p.q + ((size_t)(t * p.B + b) * p.N + n) * words, words, h * D, D)
+                  : 0ull;
+    }
+#pragma unroll
+    for (int r = 0; r < QB; ++r)
+      if (base + r * 256 < T * ntok) sq[base + r * 256] = qs[r];
   }
   __syncthreads();
   for (int tile = tile0 + wave; tile < tile_end; tile += 4) {
@@ -272,7 +402,7 @@ namespace {
 
 struct KvLaunch {
   SsaParams p;
-  size_t lds;
+  int hp;  // heads per workgroup
 };
 
 int kv_setup(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, const uint32_t* k_bits,
@@ -283,21 +413,32 @@ int kv_setup(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, const ui
   p = SsaParams{};
   p.k = k_bits; p.v = v_bits; p.kv = kv;
   p.T = T; p.B = B; p.N = N; p.C = C; p.H = heads; p.d = C / heads;
-  L.lds = (2 * (size_t)p.d + 2) * ((N + 63) / 64) * sizeof(uint64_t) + (size_t)p.d * p.d * sizeof(uint32_t);
-  if (L.lds > 65536) return set_error(-2, "ssa_kv: (C/heads) * ceil(N/64) too large for the token masks in LDS");
+  // heads per workgroup: the heads of one workgroup share the cache lines of their token rows
+  // (a line request per lane and row serves all of them); four while the chunk's masks fit LDS
+  L.hp = heads % 4 == 0 && p.d <= 48 ? 4 : heads % 2 == 0 ? 2 : 1;
   return 0;
+}
+
+template <int HP>
+int kv_launch_hp(const SsaParams& p, dim3 grid, hipStream_t stream) {
+  const dim3 block(64 * kSsaKvWaves);
+  switch (p.d) {
+    case 16: hipLaunchKernelGGL((ssa_kv_kernel<16, HP>), grid, block, 0, stream, p); break;
+    case 32: hipLaunchKernelGGL((ssa_kv_kernel<32, HP>), grid, block, 0, stream, p); break;
+    case 48: hipLaunchKernelGGL((ssa_kv_kernel<48, HP>), grid, block, 0, stream, p); break;
+    default:
+      if constexpr (HP == 4) return set_error(-2, "ssa_kv: four heads per workgroup need head dim <= 48");
+      else hipLaunchKernelGGL((ssa_kv_kernel<64, HP>), grid, block, 0, stream, p);
+  }
+  return (int)hipGetLastError();
 }
 
 int kv_launch(const KvLaunch& L, hipStream_t stream) {
   const SsaParams& p = L.p;
-  const dim3 grid((unsigned)(p.T * p.B * p.H)), block(64 * kSsaKvWaves);
-  switch (p.d) {
-    case 16: hipLaunchKernelGGL(ssa_kv_kernel<16>, grid, block, L.lds, stream, p); break;
-    case 32: hipLaunchKernelGGL(ssa_kv_kernel<32>, grid, block, L.lds, stream, p); break;
-    case 48: hipLaunchKernelGGL(ssa_kv_kernel<48>, grid, block, L.lds, stream, p); break;
-    default: hipLaunchKernelGGL(ssa_kv_kernel<64>, grid, block, L.lds, stream, p); break;
-  }
-  return (int)hipGetLastError();
+  const dim3 grid((unsigned)(p.T * p.B * p.H / L.hp));
+  if (L.hp == 4) return kv_launch_hp<4>(p, grid, stream);
+  if (L.hp == 2) return kv_launch_hp<2>(p, grid, stream);
+  return kv_launch_hp<1>(p, grid, stream);
 }
 
 struct AttendLaunch {

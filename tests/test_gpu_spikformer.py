@@ -31,7 +31,9 @@ def _unbits(w, T, B, N, C):
 
 @pytest.mark.parametrize("T,B,N,C,heads,p", [(4, 2, 200, 384, 8, 0.15), (4, 1, 3136, 384, 8, 0.2),
                                              (2, 3, 70, 256, 8, 0.3), (4, 2, 130, 128, 2, 0.25),
-                                             (2, 2, 65, 64, 4, 0.4), (8, 1, 100, 128, 2, 0.3), (1, 2, 90, 384, 12, 0.3)])
+                                             (2, 2, 65, 64, 4, 0.4), (8, 1, 100, 128, 2, 0.3), (1, 2, 90, 384, 12, 0.3),
+                                             # an odd head count (one head per K^T V workgroup)
+                                             (2, 2, 150, 160, 5, 0.3), (4, 1, 100, 64, 1, 0.3)])
 def test_ssa_bit_exact(dev, T, B, N, C, heads, p):
     q, k, v = (_spikes((T, B, N, C), p, s) for s in (11, 12, 13))
     out = ops.spiking_self_attention(_bits(q).to(dev), _bits(k).to(dev), _bits(v).to(dev), T, B, N, C, heads)
