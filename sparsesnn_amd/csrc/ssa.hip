@@ -13,11 +13,13 @@
 //                      mask i), then threads add popcount(K_i & V_j) over the chunk's token
 //                      masks to registers.
 //   ssa_attend_kernel: X = Q KV on MFMA (v_mfma_f32_16x16x32_f16: A = KV^T as two exact
-//                      6-bit fp16 pieces pre-scaled by a power of two, B = Q expanded
+//                      fp16 pieces pre-scaled by a power of two -- the second only when
+//                      some entry reaches 2048 --, B = Q expanded
 //                      from bits, one fp32 accumulator), the neuron over T in
 //                      registers, 16 output channels of a token assembled across lanes
 //                      and stored as one u16.
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "epilogue.h"
@@ -27,7 +29,8 @@ namespace sengine {
 
 constexpr int kSsaMaxN = 8192;   // tokens (the attend kernel stages a workgroup's Q slices in LDS)
 constexpr int kSsaMaxD = 64;
-constexpr size_t kSsaMaxLds = 163840;  // attend kernel: KV pieces of every t and the staged Q slices
+constexpr size_t kSsaMaxLds = 163840 - 256;  // attend kernel: KV pieces of every t and the staged Q slices (the
+                                              // rest: the kernel's own workgroup reduction)
 
 struct SsaParams {
   const uint32_t* q;
@@ -222,7 +225,7 @@ __global__ __launch_bounds__(64 * kSsaKvWaves) __attribute__((amdgpu_waves_per_e
 }
 
 // Workgroup = (b, h, one of `splits` token ranges): KV of every t is staged once in LDS
-// (fp16 hi/lo 6-bit pieces, exact, transposed to [j][i]); each wave then walks 16-token
+// (fp16 pieces: the low 11 bits and the rest, exact, transposed to [j][i]); each wave then walks 16-token
 // tiles, t inner, membrane in registers.  MFMA roles: D[j][token] = sum_i KV^T[j][i] *
 // Q^T[i][token].
 constexpr int kSsaRow = 72;  // fp16 per staged KV row: i padded to 64 plus 8 (bank spread)
@@ -247,11 +250,15 @@ __global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits
   // stage: K^T V of every t as transposed fp16 pieces [t][piece][j][i].  The entries move as
   // 16-byte rows (4 consecutive j of one i), up to 8 per thread in flight before any is stored,
   // so the workgroup waits for a few round trips, not one per row.  Pieces are pre-scaled by
-  // xscale (a power of two): lo * xs and hi * 64 * xs stay exact in fp16, and both MFMAs
-  // accumulate x itself into one fp32 accumulator.
+  // xscale (a power of two): the low 11 bits (x & 2047) and the rest (a multiple of 2048, at
+  // most N) both stay exact in fp16, and both MFMAs accumulate x itself into one fp32
+  // accumulator.  Entries below 2048 -- every entry unless some channel pair is set together in
+  // 2048 tokens -- leave the high pieces zero, and a workgroup whose high pieces are all zero
+  // skips their MFMAs (the same sums, exactly).
   _Float16* s = reinterpret_cast<_Float16*>(skv);
   constexpr int NV4 = T * D * D / 4;  // 16-byte rows
   constexpr int QB = 8;               // rows in flight per thread
+  int high = 0;                       // any high piece of this thread's entries
   for (int base = threadIdx.x; base < NV4; base += 256 * QB) {
     int4 xv[QB];
 #pragma unroll
@@ -272,8 +279,9 @@ __global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits
         const int xs[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          s[((size_t)(t * 2 + 0) * D + j0 + u) * kSsaRow + i] = (_Float16)((float)(xs[u] & 63) * p.xscale);
-          s[((size_t)(t * 2 + 1) * D + j0 + u) * kSsaRow + i] = (_Float16)((float)((xs[u] >> 6) << 6) * p.xscale);
+          s[((size_t)(t * 2 + 0) * D + j0 + u) * kSsaRow + i] = (_Float16)((float)(xs[u] & 2047) * p.xscale);
+          s[((size_t)(t * 2 + 1) * D + j0 + u) * kSsaRow + i] = (_Float16)((float)(xs[u] & ~2047) * p.xscale);
+          high |= xs[u] & ~2047;
         }
       }
     }
@@ -284,7 +292,7 @@ __global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits
       s[(size_t)row * kSsaRow + D + (idx - row * (64 - D))] = (_Float16)0.f;
     }
   }
-  __syncthreads();
+  const bool big = __syncthreads_or(high != 0);  // some high piece is nonzero (workgroup-uniform)
 
   const int tiles = (p.N + 15) >> 4;
   const int per = (tiles + splits - 1) / splits;
@@ -327,17 +335,23 @@ __global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits
       float4_t acc[JT];
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) acc[jt] = float4_t{0.f, 0.f, 0.f, 0.f};
+      auto mma = [&](auto with_high) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const half8_t bq = expand_bits8((uint32_t)(qcur[t] >> (32 * ks + 8 * g)) & 0xffu);
+        for (int ks = 0; ks < KS; ++ks) {
+          const half8_t bq = expand_bits8((uint32_t)(qcur[t] >> (32 * ks + 8 * g)) & 0xffu);
 #pragma unroll
-        for (int jt = 0; jt < JT; ++jt) {
-          const half8_t a0 = st[(size_t)(jt * 16 + c) * RV + ks * 4 + g];
-          const half8_t a1 = st[(size_t)(D + jt * 16 + c) * RV + ks * 4 + g];
-          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bq, acc[jt], 0, 0, 0);
-          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bq, acc[jt], 0, 0, 0);
+          for (int jt = 0; jt < JT; ++jt) {
+            const half8_t a0 = st[(size_t)(jt * 16 + c) * RV + ks * 4 + g];
+            acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bq, acc[jt], 0, 0, 0);
+            if constexpr (decltype(with_high)::value) {
+              const half8_t a1 = st[(size_t)(D + jt * 16 + c) * RV + ks * 4 + g];
+              acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bq, acc[jt], 0, 0, 0);
+            }
+          }
         }
-      }
+      };
+      if (big) mma(std::true_type{});
+      else mma(std::false_type{});
       // neuron on x[token][j = 16 jt + 4 g + e]; 16 spikes of a token gathered from 4 lanes
       uint32_t word[JT];
 #pragma unroll
@@ -464,9 +478,9 @@ int attend_setup(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, floa
   p.T = T; p.B = B; p.N = N; p.C = C; p.H = heads; p.d = C / heads;
   p.xscale = scale * 0.5f;
   p.np = make_neuron_params(neuron, hard_reset, tau, v_threshold, v_reset);
-  // token ranges per (b, head): enough workgroups for every CU several times over
+  // token ranges per (b, head): about 1024 workgroups (four rounds of one per CU), at least 4 tiles each
   const int tiles = (N + 15) / 16;
-  L.splits = std::max(1, std::min((tiles + 3) / 4, (2048 + B * heads - 1) / (B * heads)));
+  L.splits = std::max(1, std::min((tiles + 3) / 4, (1024 + B * heads - 1) / (B * heads)));
   const int per = (tiles + L.splits - 1) / L.splits;
   L.lds = (size_t)T * 2 * p.d * kSsaRow * sizeof(_Float16) + (size_t)T * per * 16 * sizeof(uint64_t);
   if (L.lds > kSsaMaxLds)
@@ -476,7 +490,7 @@ int attend_setup(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, floa
   L.fn = p.d == 16 ? attend_fn<16>(T, fast) : p.d == 32 ? attend_fn<32>(T, fast)
                                              : p.d == 48 ? attend_fn<48>(T, fast) : attend_fn<64>(T, fast);
   if (fast) p.xscale *= p.np.rtau;  // exact: both powers of two
-  // the K^T V entries (integers <= N) go to fp16 as (x & 63) * xscale and ((x >> 6) << 6) *
+  // the K^T V entries (integers <= N) go to fp16 as (x & 2047) * xscale and (x & ~2047) *
   // xscale: exact only while the larger stays finite and the smaller's unit is representable
   if ((double)N * p.xscale > 65504.0 || p.xscale < 0x1p-24f)
     return set_error(-2, "ssa_attend_neuron: scale out of range for exact fp16 attention pieces (needs "
@@ -486,7 +500,7 @@ int attend_setup(int32_t T, int32_t B, int32_t N, int32_t C, int32_t heads, floa
 
 int attend_launch(AttendLaunch& L, hipStream_t stream) {
   if (L.lds > 65536) {  // opt in to more than 64 KB of dynamic LDS (a host-side attribute)
-    const hipError_t e2 = hipFuncSetAttribute(L.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSsaMaxLds);
+    const hipError_t e2 = hipFuncSetAttribute(L.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.lds);
     if (e2 != hipSuccess) return (int)e2;
   }
   void* args[] = {&L.p, &L.splits};

@@ -44,6 +44,21 @@ def test_ssa_bit_exact(dev, T, B, N, C, heads, p):
     assert np.array_equal(got, s_ref.numpy()), int((got != s_ref.numpy()).sum())
 
 
+def test_ssa_large_kv_entries(dev):
+    """K^T V entries of 2048 and more (channels set together in over 2048 tokens) take the
+    attend kernel's two-piece path; entries below 2048 the one-piece path.  Both bit-exact."""
+    T, B, N, C, heads = 2, 1, 2200, 128, 2
+    q, k, v = (_spikes((T, B, N, C), 0.3, s) for s in (31, 32, 33))
+    k[:, :, :, :4] = 1.0
+    v[:, :, :, 2:6] = 1.0  # head 0: KV[0..3][2..5] = 2200; head 1 keeps entries below 2048
+    out = ops.spiking_self_attention(_bits(q).to(dev), _bits(k).to(dev), _bits(v).to(dev), T, B, N, C, heads)
+    torch.cuda.synchronize()
+    s_ref, _, x = sf.ssa(q, k, v, heads)
+    got = _unbits(out, T, B, N, C)
+    assert float(s_ref.mean()) > 0.01
+    assert np.array_equal(got, s_ref.numpy()), int((got != s_ref.numpy()).sum())
+
+
 def test_ssa_kv_workspace_matches_kt_v(dev):
     T, B, N, C, H = 2, 2, 333, 384, 8
     q, k, v = (_spikes((T, B, N, C), 0.2, s) for s in (21, 22, 23))
