@@ -177,8 +177,11 @@ static int device_cus() {
 // an even phase count).  Spike-bit input with fp16 output, optionally + the fp16 residual (proj,
 // fc2) or spike bits (1x1 layers of convolutional networks): 384-channel super-blocks with
 // phases of 6 chunks, or 256-channel ones with 4.  A membrane state (the reference executor's
-// call) is served on the fp16-in, fp16-out and the bits-in, bits-out forms.
-// SENGINE_AMD_TILE1_PS=0 turns it off.  Returns waves * 16 + chunks per phase, or 0.
+// call) is served on the fp16-in, fp16-out and the bits-in, bits-out forms.  Stateless spike-bit
+// input on 384-channel super-blocks with 32 | M takes 32-position groups (phases of 3 chunks:
+// each A operand feeds twice the SMFMACs); SENGINE_AMD_TILE1_NPG=1 keeps 16-position groups.
+// SENGINE_AMD_TILE1_PS=0 turns it off.  Returns 256 * (position groups per group - 1) + waves *
+// 16 + chunks per phase, or 0.
 static int tile1ps_config(const sengine_conv_lif_desc* d, const Geometry& geo, const TileChoice& c, int mode,
                           const FusedArgs* a) {
   const int nchunk = d->C_in / 64;
@@ -197,7 +200,10 @@ static int tile1ps_config(const sengine_conv_lif_desc* d, const Geometry& geo, c
   }
   if (d->in_enc != SENGINE_ENC_BITS) return 0;
   if (d->out_enc == SENGINE_ENC_BITS && a && a->sew.res16) return 0;
-  if (d->C_out % 384 == 0 && nchunk % 6 == 0) return 6 * 16 + 6;
+  if (d->C_out % 384 == 0 && nchunk % 6 == 0) {
+    if (geo.M % 32 == 0 && !(a && a->state) && env_int_now("SENGINE_AMD_TILE1_NPG", 2) == 2) return 256 + 6 * 16 + 3;
+    return 6 * 16 + 6;
+  }
   if (d->C_out % 256 == 0 && nchunk % 4 == 0) return 4 * 16 + 4;
   return 0;
 }
@@ -247,10 +253,11 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
     if (const int nw = tile1ds_config(d, geo.M, mode, &a))
       return describe_tile1ds(d, geo.M, nw, mode, a.state != nullptr, buf, len);
   if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
-    const int nw = ps >> 4, npg = (int)(geo.M / 16), nsb = d->C_out / (64 * nw);
+    const int nw = (ps >> 4) & 15, gp = 16 * (1 + (ps >> 8)), npg = (int)(geo.M / gp), nsb = d->C_out / (64 * nw);
     const int per = tile1ps_per(npg, nsb, tile1ps_slots(nw));
-    return snprintf(buf, len, "tile1ps<T=4,NW=%d,CG=%d,in=%s,out=%s,epi=%s%s> grid=%d (persistent, %d groups)", nw,
-                    ps & 15, f16in ? "f16" : "bits", oe, kEpi[mode], a.state ? ",state" : "", per * nsb, npg);
+    return snprintf(buf, len, "tile1ps<T=4,NW=%d,CG=%d,in=%s,out=%s,epi=%s%s%s> grid=%d (persistent, %d groups)", nw,
+                    ps & 15, f16in ? "f16" : "bits", oe, kEpi[mode], a.state ? ",state" : "", gp == 32 ? ",pos=32" : "",
+                    per * nsb, npg);
   }
   if (f16in && c.pm)
     return snprintf(buf, len, "tile1pm<T=4,GPW=1,CG=2,NW=%d,in=f16,out=%s,epi=%s> grid=%lld", c.pmw, oe, epi,
@@ -374,7 +381,11 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
   if (c.k3 && tile3ps_eligible(d, c, mode, &a)) return launch_tile3_persistent(p, c.shape, mode, tile3ps_slots(), stream);
   if (c.k3) return launch_tile3(p, d->T, c.shape, c.gpw, c.ksplit, c.pf, d->out_enc, mode, stream);
   if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
-    const int nw = ps >> 4;
+    const int nw = (ps >> 4) & 15;
+    if (ps >> 8)  // 32-position groups, 384-channel super-blocks
+      return d->out_enc == SENGINE_ENC_F16
+                 ? launch_tile1ps<6, 3, SENGINE_ENC_BITS, SENGINE_ENC_F16, 0, false, 2>(p, mode, tile1ps_slots(6), stream)
+                 : launch_tile1ps<6, 3, SENGINE_ENC_BITS, SENGINE_ENC_BITS, 0, false, 2>(p, mode, tile1ps_slots(6), stream);
     if (d->out_enc == SENGINE_ENC_F16)
       return nw == 6 ? launch_tile1ps<6, 6, SENGINE_ENC_BITS, SENGINE_ENC_F16>(p, mode, tile1ps_slots(6), stream)
                      : launch_tile1ps<4, 4, SENGINE_ENC_BITS, SENGINE_ENC_F16>(p, mode, tile1ps_slots(4), stream);

@@ -44,15 +44,23 @@ namespace sengine {
 // ARES = 1 (spike-bit input whose whole reduction is one phase, nchunk == CG == 4): the wave's
 // A operands for all chunks (80 registers) are loaded once and stay resident, since its channel
 // block never changes; the loop then issues no A-operand loads at all.
-template <int NW, int CG, int MODE, int IN_ENC, int OUT_ENC, int ARES = 0, bool STATE = false>
+//
+// NPG = 2: a group is 32 positions, two 16-position halves whose B fragments each feed the
+// wave's four A tiles: every A operand loaded feeds 8 SMFMACs instead of 4 (twice the
+// accumulators), which halves the A-operand traffic per SMFMAC -- for long reductions, whose A
+// operands stream from L2 for every group.
+template <int NW, int CG, int MODE, int IN_ENC, int OUT_ENC, int ARES = 0, bool STATE = false, int NPG = 1>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   constexpr int T = 4;
   constexpr int NTH = 64 * NW;
-  constexpr int CE = T * 16 * 16;  // LDS entries (8 bytes) per staged chunk
+  constexpr int GP = 16 * NPG;     // positions per group
+  constexpr int LGP = NPG == 2 ? 5 : 4;
+  constexpr int CE = T * GP * 16;  // LDS entries (8 bytes) per staged chunk
   constexpr bool F16IN = IN_ENC == SENGINE_ENC_F16;
   // staged items per phase: 16-byte fp16 pieces, or 8-byte spike words of (chunk, t, position)
-  constexpr int ITEMS = F16IN ? CG * T * 16 * 8 : CG * T * 16;
+  constexpr int ITEMS = F16IN ? CG * T * GP * 8 : CG * T * GP;
+  static_assert(NPG == 1 || (NPG == 2 && ARES == 0 && !STATE), "two position groups: streamed A operands, no state");
   constexpr int PPT = ITEMS / NTH;
   constexpr int CHB = F16IN ? 128 : 8;  // bytes of one 64-channel chunk in an input row
   using Item = std::conditional_t<F16IN, u32x4_t, uint2>;
@@ -92,11 +100,12 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   for (int j = 0; j < PPT; ++j) {
     const int q = tid + j * NTH;
     const int u = F16IN ? q >> 3 : q, i = F16IN ? q & 7 : 0;
-    const int pos = u & 15;
-    const int t = (u >> 4) & (T - 1);
-    const int cc = u >> 6;
+    const int pos = u & (GP - 1);
+    const int t = (u >> LGP) & (T - 1);
+    const int cc = u >> (LGP + 2);
     rel[j] = (int)(((int64_t)t * p.M + pos) * rowb) + cc * CHB + i * 16;
-    poff[j] = (cc * T + t) * 256 + pos + i * 16;
+    // 256-entry blocks per (chunk, t, 16-position half); half-piece h at +16 h
+    poff[j] = ((cc * T + t) * NPG + (pos >> 4)) * 256 + (pos & 15) + i * 16;
   }
   const int nphase = p.nchunk / CG;
   const int nf = nblk * nphase;
@@ -104,7 +113,7 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
   auto phase_base = [&](int f) -> int64_t {
     const int blk = f / nphase;
     const int ph = f - blk * nphase;
-    return (int64_t)(j0 + blk * J) * 16 * rowb + ph * CG * CHB;
+    return (int64_t)(j0 + blk * J) * GP * rowb + ph * CG * CHB;
   };
   // through a buffer resource based at the phase's data: the lane offset is one 32-bit VGPR
   auto load_pieces = [&](Item (&v)[PPT], int f) {
@@ -155,11 +164,13 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
     for (int a = 0; a < 4; ++a) ix[a] = m4[a];
   };
 
-  float4_t acc[T][4];
+  float4_t acc[NPG][T][4];
 #pragma unroll
-  for (int t = 0; t < T; ++t)
+  for (int h = 0; h < NPG; ++h)
 #pragma unroll
-    for (int a = 0; a < 4; ++a) acc[t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) acc[h][t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   static_assert(ARES == 0 || (CG == 4 && !F16IN), "resident A operands: one 4-chunk phase of spike bits");
   constexpr int NAS = ARES ? CG : 2;  // A-operand sets: resident chunks, or the two-set ring
@@ -189,13 +200,17 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
     const int ph = f - blk * nphase;
     const uint32_t lbase = lds0 + (uint32_t)PAR * (uint32_t)(CG * CE * 8);
     constexpr int NSTEP = CG * T;
-    uint2 fr[2][4];
-    auto issue = [&](int step, uint2 (&fq)[4]) {
-      const int o = step * 256 * 8;
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[0]) : "v"(lbase), "i"(o));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[1]) : "v"(lbase), "i"(o + 8 * 16 * 8));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[2]) : "v"(lbase), "i"(o + 4 * 16 * 8));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[3]) : "v"(lbase), "i"(o + 12 * 16 * 8));
+    uint2 fr[2][NPG][4];
+    auto issue = [&](int step, uint2 (&fs)[NPG][4]) {
+#pragma unroll
+      for (int h = 0; h < NPG; ++h) {
+        uint2(&fq)[4] = fs[h];
+        const int o = (step * NPG + h) * 256 * 8;
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[0]) : "v"(lbase), "i"(o));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[1]) : "v"(lbase), "i"(o + 8 * 16 * 8));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[2]) : "v"(lbase), "i"(o + 4 * 16 * 8));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[3]) : "v"(lbase), "i"(o + 12 * 16 * 8));
+      }
     };
     issue(0, fr[0]);
 #pragma unroll
@@ -215,36 +230,54 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int step = cc * T + t;
-        uint2(&fq)[4] = fr[step & 1];
+        uint2(&fs)[NPG][4] = fr[step & 1];
         if (step + 1 < NSTEP) {
           issue(step + 1, fr[(step + 1) & 1]);
-          asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(fq[0]), "+v"(fq[1]), "+v"(fq[2]), "+v"(fq[3]) :: "memory");
+          // the wait names the fragment registers as operands, so every use is ordered after it
+          if (NPG == 2)
+            asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(fs[0][0]), "+v"(fs[0][1]), "+v"(fs[0][2]), "+v"(fs[0][3]),
+                         "+v"(fs[NPG - 1][0]), "+v"(fs[NPG - 1][1]), "+v"(fs[NPG - 1][2]), "+v"(fs[NPG - 1][3])::"memory");
+          else
+            asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(fs[0][0]), "+v"(fs[0][1]), "+v"(fs[0][2]), "+v"(fs[0][3])::"memory");
         } else {
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fq[0]), "+v"(fq[1]), "+v"(fq[2]), "+v"(fq[3]) :: "memory");
+          if (NPG == 2)
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fs[0][0]), "+v"(fs[0][1]), "+v"(fs[0][2]), "+v"(fs[0][3]),
+                         "+v"(fs[NPG - 1][0]), "+v"(fs[NPG - 1][1]), "+v"(fs[NPG - 1][2]), "+v"(fs[NPG - 1][3])::"memory");
+          else
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fs[0][0]), "+v"(fs[0][1]), "+v"(fs[0][2]), "+v"(fs[0][3])::"memory");
         }
-        const half16_t bf = __builtin_bit_cast(
-            half16_t, u32x8_t{fq[0].x, fq[0].y, fq[1].x, fq[1].y, fq[2].x, fq[2].y, fq[3].x, fq[3].y});
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
-          acc[t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(half8_t, av[ra][a]), bf, acc[t][a],
-                                                               (int)ix[ra][a], 0, 0);
+        for (int h = 0; h < NPG; ++h) {
+          const uint2(&fq)[4] = fs[h];
+          const half16_t bf = __builtin_bit_cast(
+              half16_t, u32x8_t{fq[0].x, fq[0].y, fq[1].x, fq[1].y, fq[2].x, fq[2].y, fq[3].x, fq[3].y});
+#pragma unroll
+          for (int a = 0; a < 4; ++a)
+            acc[h][t][a] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(half8_t, av[ra][a]), bf,
+                                                                    acc[h][t][a], (int)ix[ra][a], 0, 0);
+        }
       }
     }
     if (f + 1 < nf) store_pieces(PAR ^ 1, pst[PAR ^ 1]);
     __syncthreads();
     if (ph == nphase - 1) {  // the group's reduction is complete
-      const int m = (j0 + blk * J) * 16 + col;
       const int cl = wave * 64 + g * 16;
-      if constexpr (STATE)
-        lean_epilogue_state<MODE, OUT_ENC>(acc, true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl], &sCoef[1][cl],
-                                           p.out, p.M, p.sew, p.state);
-      else
-        lean_epilogue_stateless<MODE, OUT_ENC>(acc, true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl],
-                                               &sCoef[1][cl], p.out, p.M, p.sew);
 #pragma unroll
-      for (int t = 0; t < T; ++t)
+      for (int h = 0; h < NPG; ++h) {
+        const int m = (j0 + blk * J) * GP + h * 16 + col;
+        if constexpr (STATE)
+          lean_epilogue_state<MODE, OUT_ENC>(acc[h], true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl],
+                                             &sCoef[1][cl], p.out, p.M, p.sew, p.state);
+        else
+          lean_epilogue_stateless<MODE, OUT_ENC>(acc[h], true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl],
+                                                 &sCoef[1][cl], p.out, p.M, p.sew);
+      }
 #pragma unroll
-        for (int a = 0; a < 4; ++a) acc[t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int h = 0; h < NPG; ++h)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int a = 0; a < 4; ++a) acc[h][t][a] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
   };
   for (int f = 0; f < nf; f += 2) {
@@ -259,29 +292,32 @@ inline int tile1ps_per(int npg, int nsb, int slots) { return std::max(1, std::mi
 
 // Launch on `slots` resident workgroups (a multiple of the super-block count, at most one per
 // (group, super-block) pair).  WITH_STATE: the instance also has a state form, taken when
-// p.state is set (the host routes state-carrying calls here only for such instances).
-template <int NW, int CG, int IN_ENC, int OUT_ENC, int ARES = 0, bool WITH_STATE = false>
+// p.state is set (the host routes state-carrying calls here only for such instances).  NPG = 2:
+// 32-position groups (host: 32 | M).
+template <int NW, int CG, int IN_ENC, int OUT_ENC, int ARES = 0, bool WITH_STATE = false, int NPG = 1>
 hipError_t launch_tile1ps(const TileParams& p, int mode, int slots, hipStream_t s) {
-  const int npg = p.M / 16;
+  const int npg = p.M / (16 * NPG);
   const int nsb = p.F / (NW * 64);
   const int per = tile1ps_per(npg, nsb, slots);
   const dim3 grid((unsigned)(per * nsb)), block(64 * NW);
-  if (WITH_STATE && p.state) {
-    if (mode == EPI_LIF_HARD)
-      hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC, ARES, WITH_STATE>), grid, block,
-                         0, s, p, npg, nsb);
-    else
-      hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD, IN_ENC, OUT_ENC, ARES, WITH_STATE>), grid, block,
-                         0, s, p, npg, nsb);
-    return hipGetLastError();
+  if constexpr (WITH_STATE) {
+    if (p.state) {
+      if (mode == EPI_LIF_HARD)
+        hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC, ARES, true, NPG>), grid, block,
+                           0, s, p, npg, nsb);
+      else
+        hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD, IN_ENC, OUT_ENC, ARES, true, NPG>), grid, block,
+                           0, s, p, npg, nsb);
+      return hipGetLastError();
+    }
   }
   if (p.state) return hipErrorInvalidValue;  // no state form of this instance
   if (mode == EPI_LIF_HARD)
-    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC, ARES>), grid, block, 0, s, p, npg,
-                       nsb);
+    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_LIF_HARD, IN_ENC, OUT_ENC, ARES, false, NPG>), grid, block, 0,
+                       s, p, npg, nsb);
   else
-    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD, IN_ENC, OUT_ENC, ARES>), grid, block, 0, s, p, npg,
-                       nsb);
+    hipLaunchKernelGGL((fused_tile1ps_kernel<NW, CG, EPI_IF_HARD, IN_ENC, OUT_ENC, ARES, false, NPG>), grid, block, 0,
+                       s, p, npg, nsb);
   return hipGetLastError();
 }
 

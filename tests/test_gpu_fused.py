@@ -521,24 +521,31 @@ def test_tile1ps_f16_input(dev, C_in, C_out, H, W, B, neuron, slots, out_enc):
         os.environ.pop("SENGINE_AMD_TILE1_DS", None)
 
 
+@pytest.mark.parametrize("npg", [1, 2])
 @pytest.mark.parametrize("C_in,C_out,H,W,B,mode", [(768, 384, 64, 40, 2, "res16"), (256, 512, 32, 32, 2, "f16"),
-                                                    (384, 384, 48, 32, 1, "res16"), (256, 1024, 16, 16, 2, "bits")])
-def test_tile1ps_bits_input(dev, C_in, C_out, H, W, B, mode):
+                                                    (384, 384, 48, 32, 1, "res16"), (256, 1024, 16, 16, 2, "bits"),
+                                                    (1536, 384, 28, 52, 1, "res16"), (384, 384, 32, 48, 1, "bits")])
+def test_tile1ps_bits_input(dev, C_in, C_out, H, W, B, mode, npg):
     """The persistent 1x1 kernel on spike bits (the token Linears fed by spikes: proj, fc2):
-    fp16 spikes + the fp16 residual stream out (6-wave 384-channel super-blocks with phases of
-    six chunks, one per CU walking 1 or 2 of 320 position groups, or one group each), plain fp16
-    spikes (4-wave super-blocks, phases of four chunks), and spike bits out (the opt-in
-    SENGINE_AMD_TILE1_PS=2), against the oracle."""
+    fp16 spikes + the fp16 residual stream out (6-wave 384-channel super-blocks: 32-position
+    groups with phases of three chunks, or with SENGINE_AMD_TILE1_NPG=1 -- and always when
+    32 does not divide M -- 16-position groups with phases of six; one workgroup per CU walking
+    a few of hundreds of groups, or one group each), plain fp16 spikes (4-wave super-blocks,
+    phases of four chunks), and spike bits out (the opt-in SENGINE_AMD_TILE1_PS=2), against the
+    oracle."""
     T = 4
     out_enc = ops.ENC_BITS if mode == "bits" else ops.ENC_F16
     spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
                         out_enc=out_enc)
     if mode == "bits":
         os.environ["SENGINE_AMD_TILE1_PS"] = "2"
+    os.environ["SENGINE_AMD_TILE1_NPG"] = str(npg)
     try:
         plan = ops.fused_plan(spec)
-        nw, cg = (6, 6) if C_out % 384 == 0 else (4, 4)
+        pos32 = C_out % 384 == 0 and npg == 2 and (B * H * W) % 32 == 0
+        nw, cg = ((6, 3) if pos32 else (6, 6)) if C_out % 384 == 0 else (4, 4)
         assert plan.startswith(f"tile1ps<T=4,NW={nw},CG={cg},in=bits,out={'bits' if mode == 'bits' else 'f16'},"), plan
+        assert (",pos=32>" in plan) == pos32, plan
         print(plan)
         case = ref.make_layer_case(270 + C_in // 64 + C_out // 64, T=T, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=1,
                                    padding=0, fp16_weights=True, p_spike=0.15)
@@ -568,6 +575,41 @@ def test_tile1ps_bits_input(dev, C_in, C_out, H, W, B, mode):
         assert float(r.spikes.mean()) > 0.002
     finally:
         os.environ.pop("SENGINE_AMD_TILE1_PS", None)
+        os.environ.pop("SENGINE_AMD_TILE1_NPG", None)
+
+
+@pytest.mark.parametrize("slots", [1, 3, 5])
+def test_tile1ps_pos32_walks_many_groups(dev, slots):
+    """32-position groups on a few resident workgroups, each walking dozens of groups (the
+    A-operand ring and the phase buffers wrap many times, across group boundaries): spikes and
+    the fp16 stream identical to the 16-position-group kernel's."""
+    T, B, C_in, C_out, H, W = 4, 1, 1536, 384, 64, 40
+    spec = ops.ConvSpec(T=T, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0,
+                        out_enc=ops.ENC_F16)
+    case = ref.make_layer_case(290 + slots, T=T, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=1, padding=0,
+                               fp16_weights=True, p_spike=0.15)
+    values, meta, _ = ops.compress_2_4(spec, case.w.to(dev))
+    sc, bi = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
+    sc_d, bi_d = torch.from_numpy(sc).to(dev), torch.from_numpy(bi).to(dev)
+    data = torch.from_numpy(pk.seq_to_nhwc_bits(case.x_seq.numpy()).view(np.int32)).to(dev)
+    res = torch.randint(0, 18, (T * B, H, W, C_out), generator=torch.Generator().manual_seed(slots)).half().to(dev)
+    outs = []
+    try:
+        os.environ["SENGINE_AMD_PS_SLOTS"] = str(slots)
+        for npg in (2, 1):
+            os.environ["SENGINE_AMD_TILE1_NPG"] = str(npg)
+            plan = ops.fused_plan(spec)
+            assert (",pos=32>" in plan) == (npg == 2), plan
+            outs.append(ops.fused_sparse_conv_bn_lif_add(spec, data, values, meta, sc_d, bi_d, res, 0, 0))
+        torch.cuda.synchronize()
+    finally:
+        os.environ.pop("SENGINE_AMD_PS_SLOTS", None)
+        os.environ.pop("SENGINE_AMD_TILE1_NPG", None)
+    assert torch.equal(outs[0], outs[1])
+    r = ref.fused_layer(case.x_seq, case.w, case.bn, 1, 0, 1, "lif", 2.0, 1.0, 0.0)
+    spk = outs[0].float().cpu() - res.float().cpu()
+    rep = compare(nhwc_seq(spk, T), None, r.spikes.numpy(), r.h.numpy(), 1.0)
+    assert rep.ok, str(rep)
 
 
 @pytest.mark.parametrize("C_out", [384, 128])
