@@ -247,7 +247,7 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
   const bool f16in = d->in_enc == SENGINE_ENC_F16;
   // fp16 output runs the generic epilogue except in launch_tile's 1x1 fast case and the fp16-input
   // tile instances (every mode)
-  const bool fast_f16out = f16in ? c.pm == 0 : (!c.k3 && d->T == 4 && c.pm == 0 && mode == EPI_LIF_HARD);
+  const bool fast_f16out = f16in ? c.pm == 0 : (d->T == 4 && c.pm == 0 && mode == EPI_LIF_HARD);
   const char* epi = d->out_enc == SENGINE_ENC_BITS || fast_f16out ? kEpi[mode] : "generic";
   if (!c.k3)
     if (const int nw = tile1ds_config(d, geo.M, mode, &a))

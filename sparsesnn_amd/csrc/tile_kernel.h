@@ -129,7 +129,8 @@ __device__ __forceinline__ void expand_word64(uint2 w, u32x4_t (&pc)[8]) {
 template <int T, int KS, int TR, int TC, int GR, int GPW, int OUT_ENC, int MODE, int KSP, int PF = 1,
           int IN_ENC = SENGINE_ENC_BITS>
 __global__ __launch_bounds__((TileGeom<KS, TR, TC, GR>::NTHR * KSP))
-__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EPI_GENERIC && IN_ENC == SENGINE_ENC_BITS
+__attribute__((amdgpu_waves_per_eu(GPW == 1 && KSP == 1 && PF == 1 && MODE != EPI_GENERIC && IN_ENC == SENGINE_ENC_BITS &&
+                                           !(KS == 3 && OUT_ENC == SENGINE_ENC_F16)
                                        ? 3
                                        : (GPW == 2 && KS == 3 ? 1 : 2)))) void fused_tile_kernel(TileParams p) {
   using Gm = TileGeom<KS, TR, TC, GR>;
@@ -577,10 +578,11 @@ hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s
     else
       hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_BITS, EPI_GENERIC, KSP, PF>), grid,
                          dim3(NTHR), 0, s, p);
-  } else if (KS == 1 && T == 4 && mode == EPI_LIF_HARD) {
-    // fp16 output of 1x1 layers (token Linears writing the fp16 residual stream): fast epilogue
+  } else if ((KS == 1 || KS == 3) && T == 4 && mode == EPI_LIF_HARD) {
+    // fp16 output (token Linears and a transformer stem's last conv writing the fp16 residual
+    // stream): fast epilogue
     hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16,
-                                          (KS == 1 && T == 4) ? EPI_LIF_HARD : EPI_GENERIC, KSP, PF>),
+                                          ((KS == 1 || KS == 3) && T == 4) ? EPI_LIF_HARD : EPI_GENERIC, KSP, PF>),
                        grid, dim3(NTHR), 0, s, p);
   } else {
     hipLaunchKernelGGL((fused_tile_kernel<T, KS, TR, TC, GR, GPW, SENGINE_ENC_F16, EPI_GENERIC, KSP, PF>), grid,

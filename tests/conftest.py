@@ -22,3 +22,21 @@ def dev():
 
     _lib.load()  # fail loudly when the HIP library is not built
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def env():
+    """Set environment variables for one test (the library reads its routing switches per call);
+    restored afterwards."""
+    saved = {}
+
+    def set_(k, v):
+        saved.setdefault(k, os.environ.get(k))
+        os.environ[k] = str(v)
+
+    yield set_
+    for k, v in saved.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = v

@@ -612,6 +612,47 @@ def test_tile1ps_pos32_walks_many_groups(dev, slots):
     assert rep.ok, str(rep)
 
 
+@pytest.mark.parametrize("res", ["none", "f16", "bits"])
+@pytest.mark.parametrize("C,H,W,B", [(64, 56, 56, 4), (128, 28, 28, 8), (256, 14, 14, 16), (384, 14, 14, 8)])
+def test_tile3_f16_output_fast_epilogue(dev, C, H, W, B, res):
+    """3x3 spike-bit convolutions writing fp16 spikes (a transformer stem's last conv, whose
+    spikes start the fp16 residual stream) run the fast hard-reset epilogue, alone and adding an
+    fp16 residual of integers or a one-plane spike-bit residual (Spikformer's rpe conv plus the
+    pooled patch features), on every tile shape, against the oracle."""
+    T = 4
+    spec = ops.ConvSpec(T=T, B=B, C_in=C, H=H, W=W, C_out=C, KH=3, KW=3, stride=1, padding=1, out_enc=ops.ENC_F16)
+    plan = ops.fused_plan(spec)
+    assert plan.startswith("tile<T=4,KS=3,") and "out=f16,epi=lif_hard" in plan, plan
+    print(plan)
+    case = ref.make_layer_case(330 + C // 64 + H, T=T, B=B, C_in=C, C_out=C, H=H, W=W, k=3, padding=1,
+                               fp16_weights=True, p_spike=0.2)
+    values, meta, _ = ops.compress_2_4(spec, case.w.to(dev))
+    sc, bi = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
+    sc_d, bi_d = torch.from_numpy(sc).to(dev), torch.from_numpy(bi).to(dev)
+    data = torch.from_numpy(pk.seq_to_nhwc_bits(case.x_seq.numpy()).view(np.int32)).to(dev)
+    r = ref.fused_layer(case.x_seq, case.w, case.bn, 1, 1, 1, "lif", 2.0, 1.0, 0.0)
+    if res == "f16":
+        res_int = torch.randint(0, 6, (T * B, H, W, C), generator=torch.Generator().manual_seed(C + H))
+        out = ops.fused_sparse_conv_bn_lif_add(spec, data, values, meta, sc_d, bi_d, res_int.half().to(dev), 0, 0)
+        torch.cuda.synchronize()
+        spk = out.float().cpu() - res_int.float()
+    elif res == "bits":
+        res_int = (torch.rand((T * B, H, W, C), generator=torch.Generator().manual_seed(C + W)) < 0.3).half()
+        out = ops.fused_sparse_conv_bn_lif_add(spec, data, values, meta, sc_d, bi_d,
+                                               ops.pack_spikes(res_int.to(dev)), 1, 0)
+        torch.cuda.synchronize()
+        spk = out.float().cpu() - res_int.float()
+    else:
+        out = ops.fused_sparse_conv_bn_lif(spec, data, values, meta, sc_d, bi_d)
+        torch.cuda.synchronize()
+        spk = out.float().cpu()
+    assert set(np.unique(spk.numpy())) <= {0.0, 1.0}
+    rep = compare(nhwc_seq(spk, T), None, r.spikes.numpy(), r.h.numpy(), 1.0)
+    print(rep, float(r.spikes.mean()))
+    assert rep.ok, str(rep)
+    assert float(r.spikes.mean()) > 0.002
+
+
 @pytest.mark.parametrize("C_out", [384, 128])
 def test_fp16_residual_stream_add(dev, C_out):
     """out = spike + residual as fp16 (the reference add kernel's form) with an fp16 residual

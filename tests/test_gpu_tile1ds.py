@@ -25,23 +25,6 @@ from tests.test_gpu_fused import run_case
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture
-def env():
-    """Set environment variables for one test; restored afterwards."""
-    saved = {}
-
-    def set_(k, v):
-        saved.setdefault(k, os.environ.get(k))
-        os.environ[k] = str(v)
-
-    yield set_
-    for k, v in saved.items():
-        if v is None:
-            os.environ.pop(k, None)
-        else:
-            os.environ[k] = v
-
-
 def _spec(C_in, C_out, H, W, B, neuron="lif", out_enc=ops.ENC_BITS):
     return ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=1, KW=1, stride=1, padding=0, neuron=neuron,
                         in_enc=ops.ENC_F16, out_enc=out_enc)
