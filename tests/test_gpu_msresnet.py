@@ -103,13 +103,12 @@ def test_membrane_shortcut_options(dev, with_res, with_state, T):
 @pytest.mark.parametrize("neuron,tau,v_th", [("ms", DECAY, THRESH), ("lif", 2.0, 1.0)])
 @pytest.mark.parametrize("H,W,C_in,C_out,B,shape", [(8, 8, 64, 128, 3, "0"), (13, 11, 128, 64, 2, "0"),
                                                     (14, 8, 64, 64, 2, "1"), (9, 10, 256, 128, 2, "2")])
-def test_shortcut_mode_tile(dev, with_res, with_state, neuron, tau, v_th, H, W, C_in, C_out, B, shape):
+def test_shortcut_mode_tile(dev, env, with_res, with_state, neuron, tau, v_th, H, W, C_in, C_out, B, shape):
     """The lean membrane-shortcut epilogue of the 3x3 tile kernel (epi=shortcut: next timestep's
     residual rows prefetched, rows moved as whole lines through the cross-row transpose) with
     each tile shape, ragged tiles, with and without residual and membrane state: y, spikes and
     the final membrane against the oracle."""
-    import os
-    os.environ["SENGINE_AMD_TILE_SHAPE"] = shape
+    env("SENGINE_AMD_TILE_SHAPE", shape)
     ops.set_fused_kernel("tile")
     try:
         T = 4
@@ -132,7 +131,6 @@ def test_shortcut_mode_tile(dev, with_res, with_state, neuron, tau, v_th, H, W, 
         torch.cuda.synchronize()
     finally:
         ops.set_fused_kernel("auto")
-        del os.environ["SENGINE_AMD_TILE_SHAPE"]
     r = ref.shortcut_layer(case.x_seq, case.w, case.bn, res, 1, 1, neuron, tau, v_th, 0.0, v0)
     s_gpu = pk.unpack_bits(spk.cpu().numpy().view(np.uint32).reshape(-1, C_out // 32), C_out)
     s_gpu = nhwc_seq(torch.from_numpy(s_gpu.reshape(T * B, H, W, C_out)), T)
