@@ -259,8 +259,10 @@ int sengine_amd_real_conv_bn(const sengine_conv_lif_desc* d, const float* x, int
  * `scale` (a power of two), exact in fp32 in any order; this library evaluates
  * Q (K^T V) * scale, which is bit-identical and costs N*d^2 instead of N^2*d per head.
  * q/k/v/out: spike bits (T*B, N, C), head h = channels [h*d, h*d + d), d = C/heads
- * (d % 16 == 0, d <= 64, N <= 8192, 16*d*ceil(N/64) + 4*d*d <= 65536 bytes of token masks and
- * sums, T in {1, 2, 4, 8}).  Two steps:
+ * (d % 16 == 0, d <= 64, N <= 8192, T in {1, 2, 4, 8}; a workgroup of the attend step keeps
+ * K^T V of every t, 288*T*d bytes, and the Q slices of its token range, 8*T bytes per token --
+ * ranges of at least 64 tokens, about 1024*N/(B*heads) when B*heads < 1024 -- in LDS, together
+ * at most 160 KB, else -2).  Two steps:
  *   sengine_amd_ssa_kv:             kv (T*B, heads, d, d) int32 = K^T V   (caller's workspace)
  *   sengine_amd_ssa_attend_neuron:  out = neuron over T of (Q kv * scale)
  */
