@@ -121,9 +121,9 @@ bool choose_tile(const sengine_conv_lif_desc* d, const Geometry& geo, TileChoice
   c.cg = 0;
   const int nchunk = d->C_in / 64;
   c.cg = nchunk % 4 == 0 ? 4 : (nchunk % 2 == 0 ? 2 : 0);
-  if (d->in_enc == SENGINE_ENC_F16) {  // fp16 input: one channel group per wave, no reduction split
+  if (d->in_enc == SENGINE_ENC_F16) {  // fp16 input: one channel group per wave, one-tap prefetch
     c.gpw = 1;
-    c.ksplit = 1;
+    if (!c.k3) c.ksplit = 1;  // 3x3: the reduction split above (even chunk count, small grids)
     c.pf = 1;
     // 1x1: the position-major kernel stages each fp16 value once per 384 or 256 output
     // channels (6 or 4 waves), phases of 2 chunks (4 chunks hold too many prefetch registers)
@@ -265,8 +265,8 @@ int describe_tile(const sengine_conv_lif_desc* d, const Geometry& geo, int mode,
   if (f16in) {
     if (c.k3) {
       const TileShape s = kShapes3[c.shape];
-      return snprintf(buf, len, "tile<T=4,KS=3,TR=%d,TC=%d,GR=%d,GPW=1,KSP=1,PF=1,in=f16,out=%s,epi=%s> grid=%lld",
-                      s.TR, s.TC, s.GR, oe, epi, (long long)c.ntiles * (d->C_out / 64));
+      return snprintf(buf, len, "tile<T=4,KS=3,TR=%d,TC=%d,GR=%d,GPW=1,KSP=%d,PF=1,in=f16,out=%s,epi=%s> grid=%lld",
+                      s.TR, s.TC, s.GR, c.ksplit, oe, epi, (long long)c.ntiles * (d->C_out / 64));
     }
     return snprintf(buf, len, "tile<T=4,KS=1,GPW=1,in=f16,out=%s,epi=%s> grid=%lld", oe, epi,
                     (long long)c.ntiles * (d->C_out / 64));
@@ -363,7 +363,7 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
       d, c, epilogue_mode(p.np, a.h_trace != nullptr || a.x_trace != nullptr || a.sew.real_out != nullptr),
       shortcut_only);
   if (d->in_enc == SENGINE_ENC_F16) {
-    if (c.k3) return launch_tile3_f16in(p, c.shape, d->out_enc, mode, stream);
+    if (c.k3) return launch_tile3_f16in(p, c.shape, c.ksplit, d->out_enc, mode, stream);
     if (const int nw = tile1ds_config(d, geo.M, mode, &a)) return launch_fused_f16_tile1ds(p, d, nw, mode, stream);
     if (const int ps = tile1ps_config(d, geo, c, mode, &a)) {
       if (d->out_enc == SENGINE_ENC_F16)  // fp16 in and out: the exported per-node call's form (with state)

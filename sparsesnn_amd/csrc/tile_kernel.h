@@ -538,15 +538,16 @@ struct TileShape {
   int KS, TR, TC, GR;
 };
 
-// fp16-input instances: T = 4, one channel group per wave, no reduction split (the reference
-// ABI's fp16 activations), bit or fp16 output, every epilogue mode.
-template <int KS, int TR, int TC, int GR, int PF = 1>
+// fp16-input instances: T = 4, one channel group per wave (the reference ABI's fp16
+// activations), bit or fp16 output, every epilogue mode; KSP = 2 (3x3, an even chunk count)
+// splits the reduction over two wave sets for grids of at most one workgroup per CU.
+template <int KS, int TR, int TC, int GR, int PF = 1, int KSP = 1>
 hipError_t launch_tile_f16in(const TileParams& p, int out_enc, int mode, hipStream_t s) {
-  constexpr int NTHR = TileGeom<KS, TR, TC, GR>::NTHR;
+  constexpr int NTHR = TileGeom<KS, TR, TC, GR>::NTHR * KSP;
   const dim3 grid((unsigned)(p.ntiles * (p.F / 64)));
   constexpr int F16 = SENGINE_ENC_F16;
 #define SENGINE_TILE_F16(OE, MODE_)                                                                                 \
-  hipLaunchKernelGGL((fused_tile_kernel<4, KS, TR, TC, GR, 1, OE, MODE_, 1, PF, F16>), grid, dim3(NTHR), 0, s, p)
+  hipLaunchKernelGGL((fused_tile_kernel<4, KS, TR, TC, GR, 1, OE, MODE_, KSP, PF, F16>), grid, dim3(NTHR), 0, s, p)
   if (out_enc == SENGINE_ENC_BITS) {
     if (mode == EPI_LIF_HARD) SENGINE_TILE_F16(SENGINE_ENC_BITS, EPI_LIF_HARD);
     else if (mode == EPI_IF_HARD) SENGINE_TILE_F16(SENGINE_ENC_BITS, EPI_IF_HARD);
@@ -596,8 +597,9 @@ hipError_t launch_tile(const TileParams& p, int out_enc, int mode, hipStream_t s
 hipError_t launch_tile3(const TileParams& p, int T, int shape, int gpw, int ksplit, int pf, int out_enc, int mode,
                         hipStream_t s);
 hipError_t launch_tile1(const TileParams& p, int T, int gpw, int out_enc, int mode, hipStream_t s);
-// fp16 input (T = 4): the 3x3 tile shapes (fused_tile3.hip), the 1x1 tile kernel (fused_tile1.hip)
-hipError_t launch_tile3_f16in(const TileParams& p, int shape, int out_enc, int mode, hipStream_t s);
+// fp16 input (T = 4): the 3x3 tile shapes (fused_tile3.hip; ksplit 1 or 2), the 1x1 tile kernel
+// (fused_tile1.hip)
+hipError_t launch_tile3_f16in(const TileParams& p, int shape, int ksplit, int out_enc, int mode, hipStream_t s);
 // The persistent 3x3 form (tile3ps.h) of a tile shape, on `slots` resident workgroups.
 hipError_t launch_tile3_persistent(const TileParams& p, int shape, int mode, int slots, hipStream_t s);
 

@@ -368,6 +368,37 @@ F16_TILE_CASES = [(3, 1, "0", 13, 11, 128, 64, 2), (3, 1, "1", 16, 9, 64, 128, 1
                   (1, 1, None, 7, 9, 256, 128, 3), (1, 2, None, 11, 10, 128, 192, 2)]
 
 
+@pytest.mark.parametrize("state", [False, True])
+@pytest.mark.parametrize("out_enc", [ops.ENC_BITS, ops.ENC_F16])
+@pytest.mark.parametrize("C,H,W,B,shape", [(256, 7, 7, 4, "2"), (128, 16, 16, 2, "0"), (128, 14, 8, 2, "1")])
+def test_tile_f16_input_reduction_split(dev, env, C, H, W, B, shape, out_enc, state):
+    """fp16-input 3x3 layers on grids of at most one workgroup per CU (the exported per-node
+    call's 7x7 layer) split the reduction over two wave sets: each tile shape, both outputs,
+    with and without the membrane state, against the oracle and identical to the unsplit kernel."""
+    env("SENGINE_AMD_TILE_SHAPE", shape)
+    spec = ops.ConvSpec(T=4, B=B, C_in=C, H=H, W=W, C_out=C, KH=3, KW=3, stride=1, padding=1,
+                        in_enc=ops.ENC_F16, out_enc=out_enc)
+    ops.set_fused_kernel("tile")  # small shapes would otherwise take the small-M kernel
+    try:
+        plan = ops.fused_plan(spec, state=state)
+        assert plan.startswith("tile<T=4,KS=3,") and ",KSP=2," in plan and "in=f16" in plan, plan
+        case = ref.make_layer_case(380 + C // 64 + H, T=4, B=B, C_in=C, C_out=C, H=H, W=W, k=3, padding=1,
+                                   fp16_weights=True, p_spike=0.2)
+        v0 = torch.rand((B, C, H, W), generator=torch.Generator().manual_seed(9)) * 0.4 if state else None
+        rep, _, r, v_fin = run_case(dev, case, in_enc=ops.ENC_F16, out_enc=out_enc, v0=v0, traces=False)
+        assert rep.ok, str(rep)
+        if state:
+            assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
+        env("SENGINE_AMD_TILE_KSPLIT", 1)
+        assert ",KSP=1," in ops.fused_plan(spec, state=state)
+        rep1, _, _, v_fin1 = run_case(dev, case, in_enc=ops.ENC_F16, out_enc=out_enc, v0=v0, traces=False)
+        assert rep1.ok, str(rep1)
+        if state:
+            assert torch.allclose(v_fin, v_fin1, rtol=1e-5, atol=1e-6)
+    finally:
+        ops.set_fused_kernel("auto")
+
+
 @pytest.mark.parametrize("traces", [True, False])
 @pytest.mark.parametrize("out_enc", [ops.ENC_BITS, ops.ENC_F16])
 @pytest.mark.parametrize("k,stride,shape,H,W,C_in,C_out,B", F16_TILE_CASES)
