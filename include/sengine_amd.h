@@ -444,9 +444,13 @@ int sengine_amd_release_weights(void);
  *     each) and writes one float per thread to sink (blocks * 256 floats).
  *   calibrate_copy: streams `bytes` (a multiple of 16, 16-byte aligned buffers) from src to
  *     dst with 16-byte accesses (bytes read + bytes written of HBM traffic).
+ *   calibrate_stream: the same stream in `mode` 0 (that copy), 1 (the copy with non-temporal
+ *     loads and stores) or 2 (read only: bytes read; dst receives one 32-bit checksum per
+ *     thread of the launch, at most bytes / 4 of it).
  */
 int sengine_amd_calibrate_smfmac(int32_t blocks, int32_t iters, float* sink, hipStream_t stream);
 int sengine_amd_calibrate_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream);
+int sengine_amd_calibrate_stream(const void* src, void* dst, int64_t bytes, int32_t mode, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -56,6 +56,7 @@ SIGNATURES = {
     "sengine_amd_prepare_weight": (ctypes.c_int, [_DP, _P, _I32, _I32, _P]),
     "sengine_amd_release_weights": (ctypes.c_int, []),
     "sengine_amd_calibrate_copy": (ctypes.c_int, [_P, _P, _I64, _P]),
+    "sengine_amd_calibrate_stream": (ctypes.c_int, [_P, _P, _I64, _I32, _P]),
     "sengine_amd_fused_sparse_conv_bn_lif_pair": (ctypes.c_int, [_DP, _DP, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                                                   _P, _P]),
     "sengine_amd_fused_sparse_conv_bn_lif_add": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32,

@@ -5,7 +5,9 @@
 //    independent accumulators with register operands (no memory traffic), so the launch
 //    measures the sparse matrix-core issue rate the fused kernels are priced against.
 //  * calib_copy_kernel: a 16-byte-per-lane streaming copy over a caller buffer (read + write),
-//    the HBM bound of the memory-bound layers.
+//    the HBM bound of the memory-bound layers; calib_copy_nt_kernel the same copy with
+//    non-temporal loads and stores (no cache allocation), calib_read_kernel a read-only
+//    stream folded into one word per thread (the read ceiling with no write traffic).
 #include "common.h"
 #include "internal.h"
 
@@ -40,6 +42,41 @@ __global__ __launch_bounds__(256) void calib_copy_kernel(const u32x4_t* __restri
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
+// Four 16-byte pieces in flight per lane per trip (strided by the grid), the rest one by one.
+__global__ __launch_bounds__(256) void calib_copy_nt_kernel(const u32x4_t* __restrict__ src,
+                                                            u32x4_t* __restrict__ dst, int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = __builtin_nontemporal_load(src + i + k * stride);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) __builtin_nontemporal_store(v[k], dst + i + k * stride);
+  }
+  for (; i < n16; i += stride) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+__global__ __launch_bounds__(256) void calib_read_kernel(const u32x4_t* __restrict__ src, uint32_t* __restrict__ sink,
+                                                         int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t s = 0;
+  int64_t i = tid;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = src[i + k * stride];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s ^= v[k][0] ^ v[k][1] ^ v[k][2] ^ v[k][3];
+  }
+  for (; i < n16; i += stride) {
+    const u32x4_t v = src[i];
+    s ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  sink[tid] = s;
+}
+
 }  // namespace sengine
 
 using namespace sengine;
@@ -62,5 +99,25 @@ extern "C" int sengine_amd_calibrate_copy(const void* src, void* dst, int64_t by
   const unsigned grid = (unsigned)(want < 4096 ? want : 4096);
   hipLaunchKernelGGL(calib_copy_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4_t*>(src),
                      static_cast<u32x4_t*>(dst), n16);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sengine_amd_calibrate_stream(const void* src, void* dst, int64_t bytes, int32_t mode,
+                                            hipStream_t stream) {
+  if (!src || !dst) return set_error(-1, "calibrate_stream: null buffer");
+  if (mode < 0 || mode > 2) return set_error(-2, "calibrate_stream: mode must be 0 (copy), 1 (non-temporal copy) or 2 (read)");
+  if (bytes <= 0 || bytes % 16 != 0) return set_error(-2, "calibrate_stream: bytes must be a positive multiple of 16");
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15)
+    return set_error(-2, "calibrate_stream: buffers must be 16-byte aligned");
+  if (mode == 0) return sengine_amd_calibrate_copy(src, dst, bytes, stream);
+  const int64_t n16 = bytes / 16;
+  const int64_t want = (n16 + 255) / 256;
+  const unsigned grid = (unsigned)(want < 4096 ? want : 4096);
+  if (mode == 1)
+    hipLaunchKernelGGL(calib_copy_nt_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4_t*>(src),
+                       static_cast<u32x4_t*>(dst), n16);
+  else  // one 32-bit word per thread: grid * 256 * 4 <= bytes / 4 <= the buffer
+    hipLaunchKernelGGL(calib_read_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4_t*>(src),
+                       static_cast<uint32_t*>(dst), n16);
   return (int)hipGetLastError();
 }

@@ -269,3 +269,30 @@ def test_raw_weight_follows_the_weight_bytes(dev, tmp_path):
     finally:
         torch.cuda.synchronize()
         assert _lib.load().sengine_amd_release_weights() == 0
+
+
+@pytest.mark.gpu
+def test_calibrate_stream_modes(dev):
+    """The bandwidth probes move what they claim: the copy and the non-temporal copy reproduce
+    the source, and the read-only stream's per-thread checksums fold to the XOR of every source
+    word (the rest of the destination untouched); bad modes and misaligned buffers are refused."""
+    from sparsesnn_amd import _lib
+    lib = _lib.load()
+    n = (1 << 20) + 48  # 16-byte pieces that do not fill the last trip of the grid
+    src = torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    for mode in (0, 1, 2):
+        dst = torch.zeros_like(src)
+        assert lib.sengine_amd_calibrate_stream(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                                                4 * n, mode, stream) == 0
+        torch.cuda.synchronize(dev)
+        if mode < 2:
+            assert torch.equal(dst, src), mode
+        else:
+            h = src.cpu().numpy().view(np.uint32)
+            assert np.bitwise_xor.reduce(dst.cpu().numpy().view(np.uint32)) == np.bitwise_xor.reduce(h)
+    dst = torch.zeros_like(src)
+    assert lib.sengine_amd_calibrate_stream(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                                            4 * n, 3, stream) == -2
+    assert lib.sengine_amd_calibrate_stream(ctypes.c_void_p(src.data_ptr() + 4), ctypes.c_void_p(dst.data_ptr()),
+                                            4 * n - 16, 1, stream) == -2
