@@ -184,7 +184,35 @@ int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc* d, const v
 #define SENGINE_PLAN_STATE 2
 #define SENGINE_PLAN_SEW_ADD 4
 #define SENGINE_PLAN_SHORTCUT 8
+#define SENGINE_PLAN_TAIL 16 /* the paired-tail call, sengine_amd_fused_sparse_conv_bn_lif_tail */
 int sengine_amd_fused_plan(const sengine_conv_lif_desc* d, int32_t flags, char* buf, size_t len);
+
+/*
+ * Paired-tail form of the fused 3x3 call, for a conv whose input channels were padded up to a
+ * multiple of 64 by 32 zero channels (Spikformer's SPS proj_conv2 reads embed/4 = 96 channels,
+ * models/spikformer.py:159-165; the same operator as conv2d_bn_if_interleaved_kernel,
+ * sengine/kernels/conv2d_bn_if_t4.py:918-1022).  The descriptor is the padded conv (C_in a
+ * multiple of 64); its input's channels C_in - 32 .. C_in - 1 are never read, and their weights
+ * must be zero.  Each 64-deep reduction step of the last chunk takes the 32 real channels of
+ * two taps, so that chunk costs 5 steps instead of 9 (9 * (C_in / 64 - 1) + 5 in all).
+ * 3x3, stride 1, pad 1, no dilation, T = 4, spike bits in and out, one weight plane, a
+ * hard-reset IF or LIF (power-of-two tau); no traces.  state as in the fused call.
+ *   tail_blob_bytes : blob sizes of this form (fewer chunks than sparse_blob_bytes)
+ *   compress_2_4_tail: its 2:4 compressor (arguments as compress_2_4; violations also flags
+ *                      every group of four of the last 32 channels holding a weight with
+ *                      |w| >= 1e-10)
+ *   fused_sparse_conv_bn_lif_tail: the call; same values as the fused call on the padded
+ *                      conv and blob up to the order of the fp32 sums (within the parity
+ *                      tolerance, not bit for bit)
+ */
+int sengine_amd_tail_blob_bytes(const sengine_conv_lif_desc* d, size_t* value_bytes, size_t* meta_bytes);
+int sengine_amd_compress_2_4_tail(const sengine_conv_lif_desc* d, const void* weight, int32_t w_enc,
+                                  int32_t w_layout, void* blob_values, void* blob_meta, int32_t* violations,
+                                  hipStream_t stream);
+int sengine_amd_fused_sparse_conv_bn_lif_tail(const sengine_conv_lif_desc* d, const void* data,
+                                              const void* blob_values, const void* blob_meta, float* state,
+                                              const float* bn_scale, const float* bn_bias, void* spikes,
+                                              hipStream_t stream);
 
 /*
  * Two fused Conv + BN + neuron nodes that read the same input `data` -- a residual block's

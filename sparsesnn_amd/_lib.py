@@ -46,6 +46,9 @@ SIGNATURES = {
     "sengine_amd_sparse_blob_bytes": (ctypes.c_int, [_DP, _SZP, _SZP]),
     "sengine_amd_dense_blob_bytes": (ctypes.c_int, [_DP, _SZP]),
     "sengine_amd_compress_2_4": (ctypes.c_int, [_DP, _P, _I32, _I32, _P, _P, _P, _P]),
+    "sengine_amd_tail_blob_bytes": (ctypes.c_int, [_DP, _SZP, _SZP]),
+    "sengine_amd_compress_2_4_tail": (ctypes.c_int, [_DP, _P, _I32, _I32, _P, _P, _P, _P]),
+    "sengine_amd_fused_sparse_conv_bn_lif_tail": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sengine_amd_num_groups": (ctypes.c_int64, [_DP]),
     "sengine_amd_pack_dense_weights": (ctypes.c_int, [_DP, _P, _I32, _I32, _P, _P]),
     "sengine_amd_fused_sparse_conv_bn_lif": (ctypes.c_int, [_DP, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),

@@ -21,7 +21,7 @@ import numpy as np
 import torch
 
 from . import ops
-from .ops import ENC_BITS, ENC_F16, ConvSpec, SEngineError
+from .ops import ENC_BITS, ENC_F16, ConvSpec, SEngineError, tail_eligible
 
 FUSED_VARIANTS = {"FusedSparseConvBNLIF", "TileLangFusedConvBNIF", "TileLangFusedConv1x1BNIF"}
 DENSE_VARIANTS = {"TileLangConvBN", "TileLangConv1x1BN"}
@@ -47,13 +47,14 @@ class SparseWeight:
         return self.blob.data_ptr()
 
     @classmethod
-    def from_weight(cls, spec: ConvSpec, w: torch.Tensor, device=None, check_pattern=True) -> "SparseWeight":
+    def from_weight(cls, spec: ConvSpec, w: torch.Tensor, device=None, check_pattern=True,
+                    tail=False) -> "SparseWeight":
         if isinstance(w, np.ndarray):
             w = torch.from_numpy(np.ascontiguousarray(w))
         device = device or (w.device if w.is_cuda else torch.device("cuda"))
         w = w.to(device).contiguous()
         layout = _weight_layout(spec, w)
-        values, meta, _ = ops.compress_2_4(spec, w, layout, check_pattern=check_pattern)
+        values, meta, _ = ops.compress_2_4(spec, w, layout, check_pattern=check_pattern, tail=tail)
         vb = values.numel() * 2
         blob = torch.empty(vb + meta.numel() * 4, dtype=torch.uint8, device=device)
         blob[:vb].copy_(values.view(torch.uint8))
@@ -89,12 +90,15 @@ def _weight_layout(spec: ConvSpec, w: torch.Tensor) -> int:
 class FusedSparseConvBNLIFKernel:
     """The fused 2:4 Conv+BN+neuron node (one HIP launch per call).  in_planes > 1: the input
     is an integer activation stored as that many bit planes (spec.C_in counts plane
-    channels); a raw weight of the conv's own C_in is expanded to planes here."""
+    channels); a raw weight of the conv's own C_in is expanded to planes here.  tail: the
+    input's last 32 channels are zero padding and the node runs the paired-tail call (spike
+    bits in and out, no traces)."""
 
-    def __init__(self, spec: ConvSpec, key: str, in_planes: int = 1):
+    def __init__(self, spec: ConvSpec, key: str, in_planes: int = 1, tail: bool = False):
         self.spec = spec  # in_enc/out_enc of `spec` are ignored; chosen per call
         self.key = key
         self.in_planes = in_planes
+        self.tail = tail
         self._wcache: dict = {}
         self.OH, self.OW, self.M, self.K_red = ops.geometry(spec)
 
@@ -108,7 +112,7 @@ class FusedSparseConvBNLIFKernel:
                 w = torch.from_numpy(np.ascontiguousarray(w))
             if tuple(w.shape) == (self.spec.C_out, self.spec.C_in // self.in_planes, self.spec.KH, self.spec.KW):
                 w = expand_planes(w.float(), self.in_planes)
-        return SparseWeight.from_weight(self.spec, w, device)
+        return SparseWeight.from_weight(self.spec, w, device, tail=self.tail)
 
     def _weight(self, w) -> SparseWeight:
         if isinstance(w, SparseWeight):
@@ -129,6 +133,11 @@ class FusedSparseConvBNLIFKernel:
             raise SEngineError("data must be fp16 NHWC or int32 spike bits")
         spec = self.spec_for(in_enc, in_enc if out_enc is None else out_enc)
         sw = self._weight(weight)
+        if self.tail:
+            if h_trace is not None or x_trace is not None:
+                raise SEngineError("a paired-tail node records no traces")
+            return ops.fused_sparse_conv_bn_lif_tail(spec, data, sw.values, sw.meta, bn_scale, bn_bias, state=state,
+                                                     out=out)
         return ops.fused_sparse_conv_bn_lif(spec, data, sw.values, sw.meta, bn_scale, bn_bias, state=state, out=out,
                                             h_trace=h_trace, x_trace=x_trace)
 
@@ -349,10 +358,13 @@ class SparseKernelCompiler:
                                        "(dense weights take the TileLangConvBN + neuron fallback)")
                 kind, np_ = _neuron_params(self.ir, node)
                 spec = self._spec(node, kind or "IF", np_)
-                key = f"sparse_{spec}_{self.precision}"
+                planes = int(node.extra_attrs.get("in_planes", 1))
+                tail = planes == 1 and len(node.input_names) == 1 and \
+                    tail_eligible(spec, node.extra_attrs.get("in_channels_real"))
+                key = f"sparse_{spec}_{self.precision}" + ("_tail" if tail else "")
                 kern = self._kernel_cache.get(key)
                 if kern is None:
-                    kern = FusedSparseConvBNLIFKernel(spec, key, int(node.extra_attrs.get("in_planes", 1)))
+                    kern = FusedSparseConvBNLIFKernel(spec, key, planes, tail=tail)
                     self._kernel_cache[key] = kern
                 node.tilelang_config = {"kernel": "fused_sparse_conv_bn_lif", "T": self.T, "waves": 4,
                                         "tile_channels": 64, "tile_positions": 64}

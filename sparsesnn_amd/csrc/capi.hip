@@ -39,6 +39,25 @@ int check_desc(const sengine_conv_lif_desc* d, Geometry* geo, bool sparse) {
   return 0;
 }
 
+int check_tail_desc(const sengine_conv_lif_desc* d, const char* who) {
+  static thread_local char msg[192];
+  const char* why = nullptr;
+  if (d->KH != 3 || d->KW != 3 || d->stride_h != 1 || d->stride_w != 1 || d->pad_h != 1 || d->pad_w != 1 ||
+      d->dil_h != 1 || d->dil_w != 1)
+    why = "needs a 3x3 kernel, stride 1, padding 1, no dilation";
+  else if (d->T != 4)
+    why = "needs T = 4";
+  else if (d->in_enc != SENGINE_ENC_BITS || d->out_enc != SENGINE_ENC_BITS)
+    why = "needs spike bits in and out";
+  else if (d->weight_planes != 1)
+    why = "needs one weight plane";
+  else if ((int64_t)d->T * d->B * d->H * d->W * (d->C_in / 8) >= ((int64_t)1 << 31))
+    why = "input too large for 32-bit offsets";
+  if (!why) return 0;
+  snprintf(msg, sizeof msg, "%s: %s", who, why);
+  return set_error(-2, msg);
+}
+
 bool flat_layout(const sengine_conv_lif_desc* d, const Geometry& geo) {
   const int64_t npix = (int64_t)geo.OH * geo.OW;
   const int64_t kf = (int64_t)d->H * d->W * d->C_in;
@@ -163,6 +182,17 @@ extern "C" int sengine_amd_sparse_blob_bytes(const sengine_conv_lif_desc* d, siz
   const size_t nq = (size_t)((flat ? (int64_t)d->H * d->W * d->C_in : geo.K_red) / 64);
   // per (group, chunk, plane, tile): 64 lanes x 8 fp16; per (group, chunk, tile): 64 lanes x u32
   if (value_bytes) *value_bytes = groups * nq * d->weight_planes * 4 * 64 * 16;
+  if (meta_bytes) *meta_bytes = groups * nq * 4 * 64 * 4;
+  return 0;
+}
+
+extern "C" int sengine_amd_tail_blob_bytes(const sengine_conv_lif_desc* d, size_t* value_bytes, size_t* meta_bytes) {
+  Geometry geo;
+  int rc = check_desc(d, &geo, true);
+  if (rc) return rc;
+  if ((rc = check_tail_desc(d, "tail_blob_bytes"))) return rc;
+  const size_t groups = (size_t)d->C_out / 64, nq = (size_t)tail_chunks(d);
+  if (value_bytes) *value_bytes = groups * nq * 4 * 64 * 16;
   if (meta_bytes) *meta_bytes = groups * nq * 4 * 64 * 4;
   return 0;
 }

@@ -40,6 +40,7 @@ struct WeightParams {
   // flat layout (sparse blob only): rows (opix, c_out), reduction (ipix, c_in)
   int flat, W, OW, SH, SW, PH, PW, DH, DW;
   int rows;  // blob rows: C_out, or OH*OW*C_out in the flat layout
+  int tail;  // 3x3 paired-tail form: the last 64-channel chunk holds 32 real channels
 };
 
 // Flat layout: the conv tap that input pixel ipix contributes to output pixel opix
@@ -70,10 +71,23 @@ __global__ __launch_bounds__(256) void compress_2_4_kernel(WeightParams p, half8
   const int r = lane & 15;
   const int row = G * 64 + 16 * (r >> 2) + 4 * a + (r & 3);
   const int kbase = q * 64 + 16 * (lane >> 4);
-  const int tap = kbase / p.C_in;  // flat layout: the input pixel
-  const int cin0 = kbase - tap * p.C_in;
-  int co = row, kh = tap / p.KW, kw = tap - (tap / p.KW) * p.KW;
+  int tap = kbase / p.C_in;  // flat layout: the input pixel
+  int cin0 = kbase - tap * p.C_in;
   bool inside = true;
+  if (p.tail) {
+    // 9 * nfull full chunks in (tap, chunk) order, then 5 chunks pairing taps 2i, 2i + 1 over
+    // the last chunk's 32 real channels: lane groups 0, 1 the first tap, 2, 3 the second
+    const int nfull = p.C_in / 64 - 1, g = lane >> 4;
+    if (q < 9 * nfull) {
+      tap = q / nfull;
+      cin0 = (q - tap * nfull) * 64 + 16 * g;
+    } else {
+      tap = 2 * (q - 9 * nfull) + (g >> 1);
+      cin0 = nfull * 64 + 16 * (g & 1);
+      if (tap > 8) inside = false, tap = 8;  // tap 8 has no partner: zero weights
+    }
+  }
+  int co = row, kh = tap / p.KW, kw = tap - (tap / p.KW) * p.KW;
   if (p.flat) {
     const int opix = row / p.C_out;
     co = row - opix * p.C_out;
@@ -127,6 +141,24 @@ __global__ __launch_bounds__(256) void compress_2_4_kernel(WeightParams p, half8
   vals[base] = v0;
   if (p.planes == 2) vals[base + 4 * 64] = v1;
   meta[(size_t)gq * 4 * 64 + (size_t)lane * 4 + a] = bits;
+}
+
+// Paired-tail form: the last 32 input channels are not in the blob; a group of four of them
+// holding any entry with |w| >= 1e-10 is reported as a violation.
+__global__ __launch_bounds__(256) void tail_zero_check_kernel(WeightParams p, int32_t* violations) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.C_out * 9 * 8;  // (c_out, tap, group of the last 32 channels)
+  if (tid >= total) return;
+  const int gi = (int)(tid & 7);
+  const int tap = (int)((tid >> 3) % 9);
+  const int co = (int)(tid / 72);
+  const int kh = tap / 3, kw = tap - (tap / 3) * 3;
+  const int c0 = p.C_in - 32 + 4 * gi;
+  int n = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    n += is_kept(load_weight(p.w, p.w_enc, p.w_layout, co, c0 + e, kh, kw, p.C_out, p.C_in, 3, 3)) ? 1 : 0;
+  violations[(((int64_t)co * 3 + kh) * 3 + kw) * (p.C_in / 4) + c0 / 4] = n > 0 ? 1 : 0;
 }
 
 // Dense blob: values[G][q32][plane][tile a][lane][8 x fp16], A operand of
@@ -186,6 +218,31 @@ extern "C" int sengine_amd_compress_2_4(const sengine_conv_lif_desc* d, const vo
   const int64_t total = (int64_t)(p.rows / 64) * p.nq * 256;
   hipLaunchKernelGGL(compress_2_4_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, p,
                      static_cast<half8_t*>(blob_values), static_cast<uint32_t*>(blob_meta), violations);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sengine_amd_compress_2_4_tail(const sengine_conv_lif_desc* d, const void* weight, int32_t w_enc,
+                                             int32_t w_layout, void* blob_values, void* blob_meta,
+                                             int32_t* violations, hipStream_t stream) {
+  Geometry geo;
+  int rc = check_desc(d, &geo, true);
+  if (rc) return rc;
+  if ((rc = check_tail_desc(d, "compress_2_4_tail"))) return rc;
+  if (!weight || !blob_values || !blob_meta) return set_error(-1, "compress_2_4_tail: null pointer");
+  if (w_enc != SENGINE_ENC_F32 && w_enc != SENGINE_ENC_F16)
+    return set_error(-2, "compress_2_4_tail: weight encoding must be F32 or F16");
+  if (w_layout != SENGINE_WLAYOUT_OIHW && w_layout != SENGINE_WLAYOUT_HWIO)
+    return set_error(-2, "compress_2_4_tail: unknown weight layout");
+  WeightParams p{weight, w_enc, w_layout, d->C_out, d->C_in, 3, 3, tail_chunks(d), d->weight_planes,
+                 0, d->W, geo.OW, 1, 1, 1, 1, 1, 1, d->C_out, 1};
+  const int64_t total = (int64_t)(p.rows / 64) * p.nq * 256;
+  hipLaunchKernelGGL(compress_2_4_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, p,
+                     static_cast<half8_t*>(blob_values), static_cast<uint32_t*>(blob_meta), violations);
+  if (violations) {
+    const int64_t nz = (int64_t)d->C_out * 72;
+    hipLaunchKernelGGL(tail_zero_check_kernel, dim3((unsigned)((nz + 255) / 256)), dim3(256), 0, stream, p,
+                       violations);
+  }
   return (int)hipGetLastError();
 }
 

@@ -517,11 +517,34 @@ static int fused_entry(const sengine_conv_lif_desc* d, const void* data, const v
   return (int)e;
 }
 
+// The paired-tail call's checks (shared by the call and its plan): 0, or an error.
+static int tail_check(const sengine_conv_lif_desc* d, Geometry& geo, bool traces_or_residual, int& mode,
+                      const char* who) {
+  int rc = check_desc(d, &geo, true);
+  if (rc) return rc;
+  if ((rc = check_tail_desc(d, who))) return rc;
+  if (traces_or_residual) return set_error(-2, "paired-tail call: no traces, SEW sum or shortcut");
+  const NeuronParams np = make_neuron_params(d->neuron, d->hard_reset, d->tau, d->v_threshold, d->v_reset);
+  mode = epilogue_mode(np, false);
+  if (mode != EPI_LIF_HARD && mode != EPI_IF_HARD)
+    return set_error(-2, "paired-tail call: needs a hard-reset IF, or a hard-reset LIF with a power-of-two tau");
+  return 0;
+}
+
 extern "C" int sengine_amd_fused_plan(const sengine_conv_lif_desc* d, int32_t flags, char* buf, size_t len) {
   if (!d || !buf || len == 0) return set_error(-1, "fused_plan: null descriptor or buffer");
   const bool traces = flags & SENGINE_PLAN_TRACES;
   const bool state = flags & SENGINE_PLAN_STATE;
   const bool shortcut = flags & SENGINE_PLAN_SHORTCUT;
+  if (flags & SENGINE_PLAN_TAIL) {
+    Geometry geo;
+    int mode = 0;
+    const bool extra = traces || shortcut || (flags & SENGINE_PLAN_SEW_ADD);
+    if (const int rc = tail_check(d, geo, extra, mode, "fused_plan (paired tail)")) return rc;
+    const int n = describe_tail(d, geo, mode, state, buf, len);
+    if (n < 0 || (size_t)n >= len) return set_error(-2, "fused_plan: buffer too small");
+    return 0;
+  }
   // never dereferenced: the plan only checks that the pointers are present
   const void* nz = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
   float* fz = reinterpret_cast<float*>(static_cast<uintptr_t>(256));
@@ -566,6 +589,20 @@ extern "C" int sengine_amd_fused_sparse_conv_bn_lif(const sengine_conv_lif_desc*
                                                     hipStream_t stream) {
   return fused_entry(d, data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, h_trace, x_trace,
                      SewAdd{nullptr, 0, 0, 0, nullptr, nullptr}, stream);
+}
+
+extern "C" int sengine_amd_fused_sparse_conv_bn_lif_tail(const sengine_conv_lif_desc* d, const void* data,
+                                                         const void* blob_values, const void* blob_meta, float* state,
+                                                         const float* bn_scale, const float* bn_bias, void* spikes,
+                                                         hipStream_t stream) {
+  Geometry geo;
+  int mode = 0;
+  if (const int rc = tail_check(d, geo, false, mode, "fused_sparse_conv_bn_lif_tail")) return rc;
+  if (!data || !blob_values || !blob_meta || !bn_scale || !bn_bias || !spikes)
+    return set_error(-1, "fused_sparse_conv_bn_lif_tail: null pointer");
+  const FusedArgs args{data, blob_values, blob_meta, state, bn_scale, bn_bias, spikes, nullptr, nullptr,
+                       SewAdd{nullptr, 0, 0, 0, nullptr, nullptr}};
+  return (int)launch_fused_bits_tail(d, geo, args, mode, stream);
 }
 
 extern "C" int sengine_amd_fused_sparse_conv_bn_lif_split(const sengine_conv_lif_desc* d, const void* data,

@@ -332,10 +332,8 @@ hipError_t launch_fused_f16_gather(const sengine_conv_lif_desc* d, const Geometr
   return launch_tile_f16in<0, 0, 0, 1>(p, d->out_enc, mode, stream);
 }
 
-hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
-                                  hipStream_t stream) {
-  TileChoice c;
-  if (!choose_tile(d, geo, c)) return hipErrorInvalidValue;
+static TileParams tile_params(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+                              const TileChoice& c) {
   TileParams p;
   p.in = static_cast<const uint8_t*>(a.data);
   p.wvals = static_cast<const u32x4_t*>(a.wvals);
@@ -357,6 +355,35 @@ hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry
   p.tiles_w = c.tiles_w;
   p.tiles_per_image = c.tiles_per_image;
   p.ntiles = c.ntiles;
+  return p;
+}
+
+hipError_t launch_fused_bits_tail(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a, int mode,
+                                  hipStream_t stream) {
+  TileChoice c;
+  if (!choose_tile(d, geo, c) || !c.k3) return hipErrorInvalidValue;
+  TileParams p = tile_params(d, geo, a, c);
+  p.nq = tail_chunks(d);
+  return launch_tile3_persistent_pair(p, c.shape, mode, tile3ps_slots(), stream);
+}
+
+int describe_tail(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool state, char* buf, size_t len) {
+  TileChoice c;
+  if (!choose_tile(d, geo, c) || !c.k3) return snprintf(buf, len, "none (grid too large)");
+  static const char* const kEpi[] = {"generic", "lif_hard", "if_hard"};
+  const TileShape s = kShapes3[c.shape];
+  const int ncb = d->C_out / 64;
+  const int per = std::max(1, std::min(tile3ps_slots() / ncb, c.ntiles));
+  return snprintf(buf, len, "tile3ps<T=4,TR=%d,TC=%d,GR=%d,out=bits,epi=%s%s,pair> grid=%d (persistent, %d tiles, "
+                  "%d reduction chunks)", s.TR, s.TC, s.GR, kEpi[mode], state ? ",state" : "", per * ncb, c.ntiles,
+                  tail_chunks(d));
+}
+
+hipError_t launch_fused_bits_tile(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,
+                                  hipStream_t stream) {
+  TileChoice c;
+  if (!choose_tile(d, geo, c)) return hipErrorInvalidValue;
+  TileParams p = tile_params(d, geo, a, c);
   const bool shortcut_only = a.sew.real_out != nullptr && a.h_trace == nullptr && a.x_trace == nullptr &&
                              a.sew.res == nullptr;
   const int mode = tile_epilogue_mode(

@@ -45,6 +45,12 @@ hipError_t launch_tile3_persistent(const TileParams& p, int shape, int mode, int
   return launch_tile3ps<8, 8, 8>(p, mode, slots, s);
 }
 
+hipError_t launch_tile3_persistent_pair(const TileParams& p, int shape, int mode, int slots, hipStream_t s) {
+  if (shape == 1) return launch_tile3ps<14, 4, 8, true>(p, mode, slots, s);
+  if (shape == 2) return launch_tile3ps<7, 7, 7, true>(p, mode, slots, s);
+  return launch_tile3ps<8, 8, 8, true>(p, mode, slots, s);
+}
+
 hipError_t launch_tile3_f16in(const TileParams& p, int shape, int ksplit, int out_enc, int mode, hipStream_t s) {
   if (ksplit == 2) {
     if (shape == 1) return launch_tile_f16in<3, 14, 4, 8, 1, 2>(p, out_enc, mode, s);

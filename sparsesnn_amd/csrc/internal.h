@@ -34,6 +34,13 @@ constexpr int64_t kFlatMaxWaste = 2;             // H*W <= 2*KH*KW (MACs vs the 
 constexpr int64_t kFlatMaxInflate = 4;           // OH*OW*H*W <= 4*KH*KW (weight entries vs the conv's)
 bool flat_layout(const sengine_conv_lif_desc* d, const Geometry& geo);
 
+// Paired-tail form of a 3x3 conv (the input's last 64-channel chunk holds 32 real channels):
+// 0 if the descriptor takes it (3x3, stride 1, pad 1, no dilation, T = 4, spike bits in and
+// out, one weight plane; checked after check_desc), else an error recorded under `who`.
+int check_tail_desc(const sengine_conv_lif_desc* d, const char* who);
+// Reduction chunks of its blob: 9 per full 64-channel chunk, then 5 tap pairs.
+inline int tail_chunks(const sengine_conv_lif_desc* d) { return 9 * (d->C_in / 64 - 1) + 5; }
+
 // Null if (neuron, tau) is a valid neuron description, else the reason.
 const char* neuron_invalid(int neuron, float tau);
 
@@ -54,6 +61,12 @@ struct FusedArgs {
   float* x_trace;
   SewAdd sew;  // fused SEW residual add (sew.res == nullptr: none)
 };
+
+// The paired-tail form on the persistent 3x3 kernel (fused_tile1.hip); describe_tail names
+// its instance.
+hipError_t launch_fused_bits_tail(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a, int mode,
+                                  hipStream_t stream);
+int describe_tail(const sengine_conv_lif_desc* d, const Geometry& geo, int mode, bool state, char* buf, size_t len);
 
 // LDS-staged kernel for spike-bit inputs (fused_sparse_lds.hip).
 hipError_t launch_fused_bits_lds(const sengine_conv_lif_desc* d, const Geometry& geo, const FusedArgs& a,

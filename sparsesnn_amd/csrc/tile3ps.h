@@ -14,12 +14,19 @@
 // one-tap operand prefetch, spike bits in and out, a hard-reset LIF or IF without traces or
 // residual.  STATE: the membrane state of the reference's call (V0 read, final membrane
 // written; lean_epilogue_state), else V0 = 0 and the final membrane is not kept.
+//
+// PAIR: the input's last 64-channel chunk holds 32 real channels (a 96- or 160-channel layer
+// padded to a multiple of 64; the upper 32 are zero and have no weights).  That chunk runs 5
+// reduction steps instead of 9: step i takes the 32 real channels of taps 2i and 2i + 1 (tap 8
+// alone, its upper half against zero weights), the lower 32 reduction slots from the first
+// tap's pixel and the upper 32 from the second's.  The blob (compress_2_4_kernel, tail form)
+// holds 9 * (nchunk - 1) full chunks in (tap, chunk) order, then the 5 paired chunks.
 #pragma once
 #include "tile_kernel.h"
 
 namespace sengine {
 
-template <int TR, int TC, int GR, int MODE, bool STATE>
+template <int TR, int TC, int GR, int MODE, bool STATE, bool PAIR = false>
 __global__ __launch_bounds__((TileGeom<3, TR, TC, GR>::NTHR)) __attribute__((amdgpu_waves_per_eu(3)))
 void fused_tile3ps_kernel(TileParams p, int ncb) {
   using Gm = TileGeom<3, TR, TC, GR>;
@@ -127,8 +134,10 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
   const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(p.wmeta + (size_t)Gb * wgroup), 0, (int)(wgroup * sizeof(uint32_t)), kBufferDword3);
   const int lv = lane * (int)sizeof(u32x4_t), lm = lane * 16;
-  auto load_a = [&](int c, int tap, u32x4_t (&av)[4], uint32_t (&ix)[4]) {
-    const int e = (tap * p.nchunk + c) * 4 * 64;
+  const int nfull = PAIR ? p.nchunk - 1 : p.nchunk;  // chunks of 64 real channels
+  // A operands of chunk c's reduction step i (a tap, or in the paired chunk a tap pair)
+  auto load_a = [&](int c, int i, u32x4_t (&av)[4], uint32_t (&ix)[4]) {
+    const int e = ((PAIR && c == nfull) ? 9 * nfull + i : i * nfull + c) * 4 * 64;
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       av[a] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
@@ -162,28 +171,44 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
     const int c = f - k * p.nchunk;
     const bool more = f + 1 < nf;
     const int cn = c + 1 < p.nchunk ? c + 1 : 0;  // chunk of step f + 1
+    // 9 reduction steps over this chunk (taps), or in the paired chunk 5 (tap pairs: the loop
+    // leaves after step 4).  The last step uses A set 0 (9 and 5 are odd) and loads step
+    // f + 1's first operands into set 1.
+    const bool pc = PAIR && c == nfull;
     uint2 fr[2][4];
-    auto issue = [&](int step, uint2 (&fq)[4]) {
-      const int tp = step / T, t = step - (step / T) * T;
-      const int o = (t * TS + (tp / 3) * Gm::HC + (tp % 3)) * 8;
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[0]) : "v"(lds0), "i"(o));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[1]) : "v"(lds0), "i"(o + 4 * NPIX * 8));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[2]) : "v"(lds0), "i"(o + 2 * NPIX * 8));
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[3]) : "v"(lds0), "i"(o + 6 * NPIX * 8));
+    // (the LDS base is an argument: asm operands do not capture through the lambda)
+    auto issue = [](int step, uint2 (&fq)[4], uint32_t l0, bool pr) __attribute__((always_inline)) {
+      const int i = step / T, t = step - (step / T) * T;
+      const int oa = (t * TS + (i / 3) * Gm::HC + (i % 3)) * 8;
+      if (PAIR && pr) {
+        const int ta = 2 * i < 9 ? 2 * i : 8, tb = 2 * i + 1 < 9 ? 2 * i + 1 : 8;
+        const int pa = (t * TS + (ta / 3) * Gm::HC + (ta % 3)) * 8;
+        const int pb = (t * TS + (tb / 3) * Gm::HC + (tb % 3)) * 8;
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[0]) : "v"(l0), "i"(pa));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[1]) : "v"(l0), "i"(pa + 4 * NPIX * 8));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[2]) : "v"(l0), "i"(pb));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[3]) : "v"(l0), "i"(pb + 4 * NPIX * 8));
+      } else {
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[0]) : "v"(l0), "i"(oa));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[1]) : "v"(l0), "i"(oa + 4 * NPIX * 8));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[2]) : "v"(l0), "i"(oa + 2 * NPIX * 8));
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(fq[3]) : "v"(l0), "i"(oa + 6 * NPIX * 8));
+      }
     };
-    constexpr int NSTEP = 9 * T;
-    issue(0, fr[0]);
+    issue(0, fr[0], lds0, pc);
 #pragma unroll
-    for (int tap = 0; tap < 9; ++tap) {
-      const int ra = tap & 1, rn = ra ^ 1;  // ring over taps; 9 is odd, so step f + 1 starts in set 0 again
-      if (tap + 1 < 9) load_a(c, tap + 1, av[rn], ix[rn]);
+    for (int i = 0; i < 9; ++i) {
+      if (PAIR && i >= 5 && pc) continue;
+      const bool last = i == 8 || (PAIR && i == 4 && pc);
+      const int ra = i & 1, rn = ra ^ 1;
+      if (!last) load_a(c, i + 1, av[rn], ix[rn]);
       else if (more) load_a(cn, 0, av[rn], ix[rn]);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const int step = tap * T + t;
+        const int step = i * T + t;
         uint2(&fq)[4] = fr[step & 1];
-        if (step + 1 < NSTEP) {
-          issue(step + 1, fr[(step + 1) & 1]);
+        if (!(last && t == T - 1)) {
+          issue(step + 1, fr[(step + 1) & 1], lds0, pc);
           asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(fq[0]), "+v"(fq[1]), "+v"(fq[2]), "+v"(fq[3]) :: "memory");
         } else {
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fq[0]), "+v"(fq[1]), "+v"(fq[2]), "+v"(fq[3]) :: "memory");
@@ -197,7 +222,7 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
       }
     }
     if (more) load_units(stg, f + 1);
-    // tap 8 used set 0 and loaded step f + 1's first tap into set 1: move it to set 0
+    // the last step used set 0 and loaded step f + 1's first operands into set 1: move them to set 0
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       av[0][a] = av[1][a];
@@ -233,20 +258,20 @@ void fused_tile3ps_kernel(TileParams p, int ncb) {
 
 // Launch on `slots` resident workgroups (all of them: with fewer, the CUs left with an extra
 // workgroup would carry more tiles than any CU does now).
-template <int TR, int TC, int GR>
+template <int TR, int TC, int GR, bool PAIR = false>
 hipError_t launch_tile3ps(const TileParams& p, int mode, int slots, hipStream_t s) {
   const int ncb = p.F / 64;
   const int per = std::max(1, std::min(slots / ncb, p.ntiles));
   const dim3 grid((unsigned)(per * ncb)), block(TileGeom<3, TR, TC, GR>::NTHR);
   if (p.state) {
     if (mode == EPI_LIF_HARD)
-      hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_LIF_HARD, true>), grid, block, 0, s, p, ncb);
+      hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_LIF_HARD, true, PAIR>), grid, block, 0, s, p, ncb);
     else
-      hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_IF_HARD, true>), grid, block, 0, s, p, ncb);
+      hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_IF_HARD, true, PAIR>), grid, block, 0, s, p, ncb);
   } else if (mode == EPI_LIF_HARD) {
-    hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_LIF_HARD, false>), grid, block, 0, s, p, ncb);
+    hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_LIF_HARD, false, PAIR>), grid, block, 0, s, p, ncb);
   } else {
-    hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_IF_HARD, false>), grid, block, 0, s, p, ncb);
+    hipLaunchKernelGGL((fused_tile3ps_kernel<TR, TC, GR, EPI_IF_HARD, false, PAIR>), grid, block, 0, s, p, ncb);
   }
   return hipGetLastError();
 }

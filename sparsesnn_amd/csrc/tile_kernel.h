@@ -602,5 +602,7 @@ hipError_t launch_tile1(const TileParams& p, int T, int gpw, int out_enc, int mo
 hipError_t launch_tile3_f16in(const TileParams& p, int shape, int ksplit, int out_enc, int mode, hipStream_t s);
 // The persistent 3x3 form (tile3ps.h) of a tile shape, on `slots` resident workgroups.
 hipError_t launch_tile3_persistent(const TileParams& p, int shape, int mode, int slots, hipStream_t s);
+// ... its paired-tail form (the blob of compress_2_4_tail; p.nq its chunk count).
+hipError_t launch_tile3_persistent_pair(const TileParams& p, int shape, int mode, int slots, hipStream_t s);
 
 }  // namespace sengine

@@ -8,6 +8,8 @@ pointers and cannot check buffer sizes itself).
 from __future__ import annotations
 
 import ctypes
+import math
+import os
 from dataclasses import dataclass
 from typing import Optional
 
@@ -23,7 +25,8 @@ __all__ = [
     "multistep_neuron_repeat", "maxpool_spikes", "sew_head", "dense_conv_bn", "multistep_neuron", "SEngineError",
     "ENC_BITS", "ENC_F16", "ENC_F32", "NEURON_LIF", "NEURON_IF", "NEURON_MS", "WLAYOUT_OIHW", "WLAYOUT_HWIO",
     "neuron_code", "fused_sparse_conv_bn_add_neuron", "spiking_self_attention", "stem_conv_bn_neuron",
-    "fused_sparse_conv_bn_lif_pair", "fused_sparse_conv_bn_lif_split", "fused_plan",
+    "fused_sparse_conv_bn_lif_pair", "fused_sparse_conv_bn_lif_split", "fused_sparse_conv_bn_lif_tail", "tail_eligible",
+    "fused_plan",
 ]
 
 
@@ -109,17 +112,18 @@ def set_fused_kernel(choice: str) -> None:
           "set_fused_kernel")
 
 
-PLAN_TRACES, PLAN_STATE, PLAN_SEW_ADD, PLAN_SHORTCUT = 1, 2, 4, 8
+PLAN_TRACES, PLAN_STATE, PLAN_SEW_ADD, PLAN_SHORTCUT, PLAN_TAIL = 1, 2, 4, 8, 16
 
 
 def fused_plan(s: ConvSpec, traces: bool = False, state: bool = False, sew_add: bool = False,
-               shortcut: bool = False) -> str:
+               shortcut: bool = False, tail: bool = False) -> str:
     """Name of the kernel instance a fused call with these optional buffers would launch
-    (route and compile-time specialisation); host-only, launches nothing."""
+    (route and compile-time specialisation); tail: the paired-tail call
+    (fused_sparse_conv_bn_lif_tail).  Host-only, launches nothing."""
     lib = _lib.load()
     d = make_desc(s)
     flags = ((PLAN_TRACES if traces else 0) | (PLAN_STATE if state else 0) | (PLAN_SEW_ADD if sew_add else 0)
-             | (PLAN_SHORTCUT if shortcut else 0))
+             | (PLAN_SHORTCUT if shortcut else 0) | (PLAN_TAIL if tail else 0))
     buf = ctypes.create_string_buffer(256)
     check(lib.sengine_amd_fused_plan(ctypes.byref(d), flags, buf, len(buf)), "fused_plan")
     return buf.value.decode()
@@ -164,28 +168,42 @@ def _check_weight(s: ConvSpec, w: torch.Tensor, layout: int):
         raise SEngineError(f"weight: expected shape {shape}, got {tuple(w.shape)}")
 
 
-def compress_2_4(s: ConvSpec, weight: torch.Tensor, layout: int = WLAYOUT_OIHW, check_pattern: bool = True):
+def _blob_bytes(lib, d, tail: bool):
+    vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
+    if tail:
+        check(lib.sengine_amd_tail_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)), "tail_blob_bytes")
+    else:
+        check(lib.sengine_amd_sparse_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)),
+              "sparse_blob_bytes")
+    return vb, mb
+
+
+def compress_2_4(s: ConvSpec, weight: torch.Tensor, layout: int = WLAYOUT_OIHW, check_pattern: bool = True,
+                 tail: bool = False):
     """2:4-compress a conv weight on the GPU -> (values int16 tensor, meta int32 tensor, violations).
 
     Raises if check_pattern and any 4-group along C_in holds more than two entries with
-    |w| >= 1e-10 (such weights belong on the dense fallback, sengine/optimizer.py:845-853)."""
+    |w| >= 1e-10 (such weights belong on the dense fallback, sengine/optimizer.py:845-853).
+    tail: the blob of the paired-tail call (fused_sparse_conv_bn_lif_tail), for a 3x3 conv
+    whose last 32 input channels are zero padding; a nonzero weight there is a violation."""
     lib = _lib.load()
     _check_weight(s, weight, layout)
     d = make_desc(s)
-    vb, mb = ctypes.c_size_t(), ctypes.c_size_t()
-    check(lib.sengine_amd_sparse_blob_bytes(ctypes.byref(d), ctypes.byref(vb), ctypes.byref(mb)), "sparse_blob_bytes")
+    vb, mb = _blob_bytes(lib, d, tail)
     dev = weight.device
     values = torch.empty(vb.value // 2, dtype=torch.int16, device=dev)
     meta = torch.empty(mb.value // 4, dtype=torch.int32, device=dev)
     n_groups = lib.sengine_amd_num_groups(ctypes.byref(d))
     # zeroed: in the flat (small-output) layout taps that never touch the image are not visited
     viol = torch.zeros(n_groups, dtype=torch.int32, device=dev)
-    check(lib.sengine_amd_compress_2_4(ctypes.byref(d), _ptr(weight), _weight_enc(weight), layout,
-                                       _ptr(values), _ptr(meta), _ptr(viol), _stream(dev)), "compress_2_4")
+    fn = lib.sengine_amd_compress_2_4_tail if tail else lib.sengine_amd_compress_2_4
+    check(fn(ctypes.byref(d), _ptr(weight), _weight_enc(weight), layout, _ptr(values), _ptr(meta), _ptr(viol),
+             _stream(dev)), "compress_2_4")
     if check_pattern:
         n_bad = int(viol.sum().item())
         if n_bad:
-            raise SEngineError(f"compress_2_4: {n_bad} 4-groups have more than two non-zero weights")
+            raise SEngineError(f"compress_2_4: {n_bad} 4-groups have more than two non-zero weights"
+                               + (" or a nonzero weight in the last 32 (padding) input channels" if tail else ""))
     return values, meta, viol
 
 
@@ -277,6 +295,50 @@ def fused_sparse_conv_bn_lif(s: ConvSpec, data: torch.Tensor, values: torch.Tens
         ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta), _ptr(state), _ptr(bn_scale), _ptr(bn_bias),
         _ptr(out), _ptr(h_trace), _ptr(x_trace), _stream(dev))
     check(rc, "fused_sparse_conv_bn_lif")
+    return out
+
+
+def tail_eligible(spec: ConvSpec, in_channels_real) -> bool:
+    """A fused 3x3 node whose last 32 input channels are zero padding runs the paired-tail call
+    (fused_sparse_conv_bn_lif_tail: the last chunk's 32 real channels of two taps per
+    reduction step) when its shape and neuron allow it.  SENGINE_AMD_TAIL=0 (read when an
+    engine is built) keeps such nodes on the ordinary call over the padded blob."""
+    return (os.environ.get("SENGINE_AMD_TAIL", "1") != "0" and in_channels_real is not None and int(in_channels_real) == spec.C_in - 32 and spec.KH == 3
+            and spec.KW == 3 and spec.stride == 1 and spec.padding == 1 and spec.dilation == 1 and spec.T == 4
+            and spec.weight_planes == 1 and spec.hard_reset and spec.v_reset == 0.0
+            and (spec.neuron == "if" or (spec.neuron == "lif" and math.log2(spec.tau).is_integer())))
+
+
+def fused_sparse_conv_bn_lif_tail(s: ConvSpec, data: torch.Tensor, values: torch.Tensor, meta: torch.Tensor,
+                                  bn_scale: torch.Tensor, bn_bias: torch.Tensor, state: Optional[torch.Tensor] = None,
+                                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The paired-tail fused call: a 3x3 conv whose last 32 input channels are zero padding, with
+    the blob of compress_2_4(..., tail=True); spike bits in and out, T = 4, no traces.  Returns
+    the spike bits int32 (T*B, OH, OW, C_out/32)."""
+    lib = _lib.load()
+    OH, OW, M, _ = geometry(s)
+    d = make_desc(s)
+    vb, mb = _blob_bytes(lib, d, True)
+    for t, n in ((data, "data"), (values, "values"), (meta, "meta"), (bn_scale, "bn_scale"), (bn_bias, "bn_bias")):
+        _require_cuda(t, n)
+    dt, n_in = _enc_numel(s.in_enc, s.T * s.B * s.H * s.W * s.C_in)
+    _require_numel(data, n_in, dt, "data")
+    if values.numel() * values.element_size() != vb.value or meta.numel() * meta.element_size() != mb.value:
+        raise SEngineError("fused_sparse_conv_bn_lif_tail: weight blob does not match the descriptor")
+    _require_numel(bn_scale, s.C_out, torch.float32, "bn_scale")
+    _require_numel(bn_bias, s.C_out, torch.float32, "bn_bias")
+    if state is not None:
+        _require_cuda(state, "state")
+        _require_numel(state, M * s.C_out, torch.float32, "state")
+    odt, n_out = _enc_numel(s.out_enc, s.T * M * s.C_out)
+    if out is None:
+        out = torch.empty(s.T * s.B, OH, OW, s.C_out // 32, dtype=odt, device=data.device)
+    else:
+        _require_cuda(out, "out")
+        _require_numel(out, n_out, odt, "out")
+    check(lib.sengine_amd_fused_sparse_conv_bn_lif_tail(ctypes.byref(d), _ptr(data), _ptr(values), _ptr(meta),
+                                                        _ptr(state), _ptr(bn_scale), _ptr(bn_bias), _ptr(out),
+                                                        _stream(data.device)), "fused_sparse_conv_bn_lif_tail")
     return out
 
 

@@ -153,7 +153,8 @@ def pad_channels(ir: EngineIR, multiple: int = 64) -> int:
     Their spikes flow through max-pools into convs only, whose input channels get matching zero
     weight columns (a group of four zeros keeps the
     kernels' rule of at most two nonzeros per group).  Chains whose spikes reach anything else
-    are left alone.  Shapes along the way are updated.  Returns the number of convs padded."""
+    are left alone.  Shapes along the way are updated, and each reader records its real input
+    channel count (extra_attrs["in_channels_real"]).  Returns the number of convs padded."""
     n = 0
     for nid in list(ir.topo_order):
         conv = ir.nodes[nid]
@@ -188,7 +189,8 @@ def pad_channels(ir: EngineIR, multiple: int = 64) -> int:
                     break
         if not ok or not readers:
             continue
-        P = _pad_to(cp.out_channels, multiple)
+        real = cp.out_channels
+        P = _pad_to(real, multiple)
         _pad_weight(ir, conv, 0, P)
         extra = [0.0] * (P - cp.out_channels)
         conv.bn_scale = list(conv.bn_scale) + extra
@@ -202,6 +204,7 @@ def pad_channels(ir: EngineIR, multiple: int = 64) -> int:
             _pad_weight(ir, r, 1, P)
             r.conv_params.in_channels = P
             r.input_shapes = [_with_channels(r.input_shapes[0], P)] + list(r.input_shapes[1:])
+            r.extra_attrs["in_channels_real"] = real  # the rest are zero padding (paired-tail form)
         conv.extra_attrs["padded_from"] = int(P - len(extra))
         n += 1
     return n

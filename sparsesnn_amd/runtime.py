@@ -288,11 +288,13 @@ class CUDAGraphEngine:
         if pair_launches and not keep_membranes:
             for i, a in enumerate(launches):
                 if a.kind != "fused" or a.skip or a.pair_with is not None or len(a.inputs) != 1 or \
-                        self.enc.get(root(a.inputs[0]), "bits") != "bits" or self.enc[root(a.output)] != "bits":
+                        self.enc.get(root(a.inputs[0]), "bits") != "bits" or self.enc[root(a.output)] != "bits" or \
+                        getattr(self.kernels.get(a.nid), "tail", False):
                     continue
                 for b in launches[i + 1:]:
                     if b.kind == "fused" and not b.skip and b.pair_with is None and len(b.inputs) == 1 and \
-                            root(b.inputs[0]) == root(a.inputs[0]) and self.enc[root(b.output)] == "bits":
+                            root(b.inputs[0]) == root(a.inputs[0]) and self.enc[root(b.output)] == "bits" and \
+                            not getattr(self.kernels.get(b.nid), "tail", False):
                         a.pair_with, b.skip = b.nid, True
                         break
             # the partner is written by its pair's launch: schedule it right after, so buffer

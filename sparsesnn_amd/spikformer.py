@@ -37,7 +37,7 @@ from dataclasses import dataclass
 import torch
 
 from . import ops
-from .ops import ConvSpec, SEngineError
+from .ops import ConvSpec, SEngineError, tail_eligible
 from .sparsity import expand_planes, fold_batchnorm, validate_2_4_pattern
 
 ATTN_VTH = 0.5  # attn_lif threshold, models/spikformer.py:96
@@ -94,6 +94,7 @@ class Fused:
     meta: torch.Tensor
     scale: torch.Tensor
     bias: torch.Tensor
+    tail: bool = False  # the input's last 32 channels are zero padding: the paired-tail call
 
 
 @dataclass
@@ -227,9 +228,9 @@ class SpikformerEngine:
         return ConvSpec(T=self.T, B=self.B, C_in=cin, H=h, W=w, C_out=cout, KH=k, KW=k, stride=1, padding=pad,
                         neuron="lif", hard_reset=True, tau=2.0, v_threshold=1.0, v_reset=0.0)
 
-    def _prepare(self, spec: ConvSpec, w4: torch.Tensor, sc, bi) -> Fused:
-        values, meta, _ = ops.compress_2_4(spec, w4.contiguous().to(self.dev).half())
-        return Fused(spec, values, meta, sc.to(self.dev), bi.to(self.dev))
+    def _prepare(self, spec: ConvSpec, w4: torch.Tensor, sc, bi, tail: bool = False) -> Fused:
+        values, meta, _ = ops.compress_2_4(spec, w4.contiguous().to(self.dev).half(), tail=tail)
+        return Fused(spec, values, meta, sc.to(self.dev), bi.to(self.dev), tail)
 
     def _conv(self, p, name, cin, cout, cin_p, cout_p, h, w) -> Fused:
         wk = f"patch_embed.{name}.weight"
@@ -241,7 +242,8 @@ class SpikformerEngine:
         wp = torch.zeros(cout_p, cin_p, 3, 3)
         wp[:cout, :cin] = w_
         sc, bi = self._bn(p, f"patch_embed.{name.replace('conv', 'bn')}", pad_to=cout_p)
-        return self._prepare(self._spec(cin_p, cout_p, 3, h, w, 1), wp, sc, bi)
+        spec = self._spec(cin_p, cout_p, 3, h, w, 1)
+        return self._prepare(spec, wp, sc, bi, tail=tail_eligible(spec, cin))
 
     def _concat_qkv(self, p, pre, cin, planes) -> Fused:
         """attn.q, .k and .v concatenated along C_out, padded with zero rows (and a zero BN
@@ -283,7 +285,10 @@ class SpikformerEngine:
 
     # ------------------------------------------------------------------ execution
     def _fused(self, f: Fused, data, out):
-        ops.fused_sparse_conv_bn_lif(f.spec, data.view(-1), f.values, f.meta, f.scale, f.bias, out=out)
+        if f.tail:
+            ops.fused_sparse_conv_bn_lif_tail(f.spec, data.view(-1), f.values, f.meta, f.scale, f.bias, out=out)
+        else:
+            ops.fused_sparse_conv_bn_lif(f.spec, data.view(-1), f.values, f.meta, f.scale, f.bias, out=out)
 
     def _fused_add(self, f: Fused, data, residual, res_planes, out, out_planes):
         ops.fused_sparse_conv_bn_lif_add(f.spec, data.view(-1), f.values, f.meta, f.scale, f.bias, residual,

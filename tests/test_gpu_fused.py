@@ -4,6 +4,7 @@ Every case runs the reference PyTorch path (oracle.reference_path) on the CPU an
 HIP kernel through the C ABI on the same seeded inputs, then applies the acceptance
 rule of tests/parity.py.
 """
+import dataclasses
 import os
 
 import numpy as np
@@ -19,11 +20,12 @@ pytestmark = pytest.mark.gpu
 
 
 def run_case(dev, case: ref.LayerCase, neuron="lif", tau=2.0, v_th=1.0, v_reset=0.0, planes=1,
-             in_enc=ops.ENC_BITS, out_enc=ops.ENC_BITS, v0=None, layout=ops.WLAYOUT_OIHW, traces=True):
+             in_enc=ops.ENC_BITS, out_enc=ops.ENC_BITS, v0=None, layout=ops.WLAYOUT_OIHW, traces=True, tail=False):
     """One fused call against the oracle.  traces=True also records the per-step membrane and
     BN output (which selects the generic epilogue); traces=False runs the call as an engine
     does (the fast epilogue where the neuron allows it) and compares spikes and, with v0, the
-    final membrane.  Returns (report, BN-output error or None, oracle result, final state)."""
+    final membrane.  tail: the paired-tail call (the case's last 32 input channels must have
+    zero weights).  Returns (report, BN-output error or None, oracle result, final state)."""
     T, B, C_in, H, W = case.x_seq.shape
     C_out, _, KH, KW = case.w.shape
     hard = v_reset is not None
@@ -32,7 +34,7 @@ def run_case(dev, case: ref.LayerCase, neuron="lif", tau=2.0, v_th=1.0, v_reset=
                         v_reset=v_reset if hard else 0.0, in_enc=in_enc, out_enc=out_enc, weight_planes=planes)
     OH, OW, M, _ = ops.geometry(spec)
     w_dev = case.w.to(dev) if layout == ops.WLAYOUT_OIHW else case.w.permute(2, 3, 1, 0).contiguous().to(dev)
-    values, meta, _ = ops.compress_2_4(spec, w_dev, layout)
+    values, meta, _ = ops.compress_2_4(spec, w_dev, layout, tail=tail)
     scale, bias = ref.fold_batchnorm(case.bn.gamma, case.bn.beta, case.bn.mean, case.bn.var, case.bn.eps)
     scale_d = torch.from_numpy(scale).to(dev)
     bias_d = torch.from_numpy(bias).to(dev)
@@ -46,8 +48,12 @@ def run_case(dev, case: ref.LayerCase, neuron="lif", tau=2.0, v_th=1.0, v_reset=
         state = v0.permute(0, 2, 3, 1).reshape(M, C_out).contiguous().to(dev)
     h_tr = torch.empty(T, M, C_out, dtype=torch.float32, device=dev) if traces else None
     x_tr = torch.empty(T, M, C_out, dtype=torch.float32, device=dev) if traces else None
-    out = ops.fused_sparse_conv_bn_lif(spec, data, values, meta, scale_d, bias_d, state=state,
-                                       h_trace=h_tr, x_trace=x_tr)
+    if tail:
+        assert not traces
+        out = ops.fused_sparse_conv_bn_lif_tail(spec, data, values, meta, scale_d, bias_d, state=state)
+    else:
+        out = ops.fused_sparse_conv_bn_lif(spec, data, values, meta, scale_d, bias_d, state=state,
+                                           h_trace=h_tr, x_trace=x_tr)
     torch.cuda.synchronize()
     if out_enc == ops.ENC_BITS:
         s_gpu = pk.unpack_bits(out.cpu().numpy().view(np.uint32).reshape(-1, C_out // 32), C_out)
@@ -753,3 +759,64 @@ def test_fused_split_output(dev, C_in, C_out, split, H, W, B, in_enc, monkeypatc
     for j in range(-(-C_out // split)):
         n = min(split, C_out - j * split) // 32
         assert torch.equal(planes[j].reshape(T * B * H * W, split // 32)[:, :n], full[:, j * split // 32:j * split // 32 + n])
+
+
+def _tail_case(seed, B, C_in, C_out, H, W, p_spike=0.2):
+    """A 3x3 layer whose last 32 input channels are padding: zero weights there (the input
+    spikes in those channels stay random: the paired-tail call must not depend on them)."""
+    case = ref.make_layer_case(seed, T=4, B=B, C_in=C_in, C_out=C_out, H=H, W=W, k=3, padding=1,
+                               fp16_weights=True, p_spike=p_spike)
+    case.w[:, C_in - 32:] = 0.0
+    return case
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("neuron", ["lif", "if"])
+@pytest.mark.parametrize("state", [False, True])
+@pytest.mark.parametrize("shape", ["0", "1", "2"])
+@pytest.mark.parametrize("C_in,C_out,H,W,B", [(128, 64, 16, 16, 2), (64, 128, 13, 11, 3), (192, 64, 14, 9, 2)])
+def test_tail_pairs_taps(dev, env, C_in, C_out, H, W, B, shape, state, neuron):
+    """The paired-tail call (the last chunk's 32 real channels of two taps per reduction step) on
+    every tile shape, one to three channel chunks, ragged images, both neurons, with and without
+    the membrane state, against the oracle of the padded conv; and the same spikes as the
+    ordinary call on the padded blob up to the parity rule."""
+    env("SENGINE_AMD_TILE_SHAPE", shape)
+    case = _tail_case(400 + C_in + H + int(shape), B, C_in, C_out, H, W)
+    spec = ops.ConvSpec(T=4, B=B, C_in=C_in, H=H, W=W, C_out=C_out, KH=3, KW=3, stride=1, padding=1,
+                        neuron=neuron, hard_reset=True, tau=2.0, v_threshold=1.0, v_reset=0.0)
+    plan = ops.fused_plan(spec, state=state, tail=True)
+    assert plan.startswith("tile3ps<") and ",pair>" in plan and f"{9 * (C_in // 64 - 1) + 5} reduction chunks" in plan
+    assert ("state" in plan) == state, plan
+    v0 = (torch.rand((B, C_out, H, W), generator=torch.Generator().manual_seed(3)) * 0.6) if state else None
+    v_th = 1.0 if neuron == "lif" else 0.5
+    rep, _, r, v_fin = run_case(dev, case, neuron=neuron, v_th=v_th, v0=v0, traces=False, tail=True)
+    assert rep.ok, str(rep)
+    if state:
+        assert torch.allclose(v_fin, r.v_final, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("slots", [1, 3, 7])
+def test_tail_walks_many_tiles(dev, env, slots):
+    """Few resident workgroups walking many tiles: the paired chunk's operand lookahead into the
+    next tile's first full chunk, and tiles that start with the paired chunk (C_in = 64)."""
+    env("SENGINE_AMD_PS_SLOTS", slots * 2)
+    for C_in in (128, 64):
+        case = _tail_case(470 + slots + C_in, 3, C_in, 128, 20, 18)
+        rep, _, _, _ = run_case(dev, case, traces=False, tail=True)
+        assert rep.ok, (C_in, str(rep))
+
+
+@pytest.mark.gpu
+def test_tail_refuses(dev):
+    """A nonzero weight in the padding channels is a violation; strided, fp16 and T != 4
+    descriptors are refused with a reason."""
+    case = _tail_case(490, 1, 128, 64, 8, 8)
+    case.w[3, 100, 1, 1] = 0.5
+    spec = ops.ConvSpec(T=4, B=1, C_in=128, H=8, W=8, C_out=64, KH=3, KW=3, stride=1, padding=1)
+    with pytest.raises(ops.SEngineError, match="padding"):
+        ops.compress_2_4(spec, case.w.to(dev), tail=True)
+    for bad in (dataclasses.replace(spec, stride=2), dataclasses.replace(spec, in_enc=ops.ENC_F16),
+                dataclasses.replace(spec, T=2)):
+        with pytest.raises(ops.SEngineError, match="tail"):
+            ops.fused_plan(bad, tail=True)
