@@ -228,9 +228,13 @@ static bool tile3ps_eligible(const sengine_conv_lif_desc* d, const TileChoice& c
       c.ksplit != 1 || c.pf != 1 || (mode != EPI_LIF_HARD && mode != EPI_IF_HARD))
     return false;
   // at least two tiles per resident workgroup: with fewer, the hardware's dispatch of a partial
-  // second round of one-tile workgroups balances the CUs better than a fixed assignment (measured)
+  // second round of one-tile workgroups balances the CUs better than a fixed assignment
+  // (measured); and one input chunk: with two or three the halo-tiled kernel measured faster
+  // (Spikformer's 128 -> 192 224^2 and 192 -> 384 112^2 convs, 1,192 against 1,243 us and 842
+  // against 890).  SENGINE_AMD_TILE3_PS=2 waives both rules.
   const int env = env_int_now("SENGINE_AMD_TILE3_PS", -1);
-  if (env == 0 || (env != 2 && (int64_t)c.ntiles * (d->C_out / 64) < 2LL * tile3ps_slots())) return false;
+  if (env == 0) return false;
+  if (env != 2 && ((int64_t)c.ntiles * (d->C_out / 64) < 2LL * tile3ps_slots() || d->C_in != 64)) return false;
   // (its epilogue stores plain spike-bit rows: no SEW sum, no channel-split planes)
   if (a && (a->sew.res || a->sew.res16 || a->sew.real_out || a->sew.split_c || a->h_trace || a->x_trace))
     return false;

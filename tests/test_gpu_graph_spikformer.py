@@ -24,19 +24,24 @@ def build_generic(p, B, heads, hw, dev, int_stream="f16"):
     return CUDAGraphEngine().build(ir, kernels, T=4, batch_size=B, device=dev)
 
 
-@pytest.mark.parametrize("stream,embed,heads,depth,B,hw", [
-    ("f16", 128, 2, 4, 2, (32, 32)),
-    ("planes", 128, 2, 4, 2, (32, 32)),
-    ("f16", 256, 4, 2, 3, (64, 48)),
-    ("f16", 384, 8, 8, 32, (224, 224)),
+@pytest.mark.parametrize("stream,embed,heads,depth,B,hw,tail", [
+    ("f16", 128, 2, 4, 2, (32, 32), False),
+    ("planes", 128, 2, 4, 2, (32, 32), False),
+    ("f16", 128, 2, 4, 2, (32, 32), True),
+    ("f16", 256, 4, 2, 3, (64, 48), False),
+    ("f16", 384, 8, 8, 32, (224, 224), False),
 ])
-def test_generic_engine_runs_spikformer(dev, stream, embed, heads, depth, B, hw):
-    print(f"stream {stream} embed {embed} heads {heads} depth {depth} B {B} {hw}", flush=True)
+def test_generic_engine_runs_spikformer(dev, env, stream, embed, heads, depth, B, hw, tail):
+    """tail: both engines run proj_conv2 (embed/4 channels padded to 64) on the opt-in
+    paired-tail call."""
+    print(f"stream {stream} embed {embed} heads {heads} depth {depth} B {B} {hw} tail {tail}", flush=True)
+    env("SENGINE_AMD_TAIL", int(tail))
     p = sf.make_params(80 + depth, embed=embed, depth=depth, num_classes=1000 if hw[0] == 224 else 10)
     x = torch.randn((B, 3) + hw, generator=torch.Generator().manual_seed(81))
     eng = build_generic(p, B, heads, hw, dev, stream)
     ref_eng = SpikformerEngine(p, batch=B, T=4, embed=embed, heads=heads, depth=depth, in_hw=hw, device=dev,
                                stream=stream)
+    assert any(getattr(k, "tail", False) for k in eng.kernels.values()) == tail == ref_eng.c2.tail
     assert eng.n_launches == ref_eng.launches, (eng.n_launches, ref_eng.launches)
     names = eng.launch_names()
     assert len(names) == eng.n_launches and any("(attn: attend)" in n for n in names), names

@@ -174,10 +174,14 @@ def sf_case():
     return p, x, logits, xs
 
 
-@pytest.mark.parametrize("stream", ["f16", "planes"])
-def test_engine_sps_and_blocks_teacher_forced(dev, sf_case, stream):
+@pytest.mark.parametrize("stream,tail", [("f16", False), ("planes", False), ("f16", True)])
+def test_engine_sps_and_blocks_teacher_forced(dev, env, sf_case, stream, tail):
+    """SPS stages and blocks against the oracle; tail: proj_conv2 (32 channels padded to 64) on
+    the opt-in paired-tail call."""
     p, x, _, xs = sf_case
+    env("SENGINE_AMD_TAIL", int(tail))
     eng = SpikformerEngine(p, batch=2, T=4, embed=128, heads=2, depth=4, in_hw=(32, 32), device=dev, stream=stream)
+    assert eng.c2.tail == tail
     eng.forward(x.to(dev))
     torch.cuda.synchronize()
     rates = _check_sps(eng, p, x, 4, 2, 128)
@@ -205,16 +209,19 @@ def test_engine_end_to_end_graph(dev, sf_case, stream):
     assert eng.launches == 7 + 6 * 4 + (2 if stream == "f16" else 1)
 
 
-@pytest.mark.parametrize("batch,nblocks,stream", [(1, 1, "f16"), (4, 2, "f16"), (1, 1, "planes")])
-def test_engine_cfg4_shape(dev, batch, nblocks, stream):
+@pytest.mark.parametrize("batch,nblocks,stream,tail", [(1, 1, "f16", False), (4, 2, "f16", False),
+                                                       (1, 1, "planes", False), (1, 0, "f16", True)])
+def test_engine_cfg4_shape(dev, env, batch, nblocks, stream, tail):
     """BASELINE config 4's shape: 3x224x224 pixels ~N(0,1), T=4, embed 384, 8 heads, MLP ratio
     4, 8 blocks (3,136 tokens), 1000 classes, on one image and on four; the SPS stages and
     the first `nblocks` blocks teacher-forced against the oracle, graph replays equal to the
-    eager run."""
+    eager run.  tail: proj_conv2 (96 channels padded to 128) on the opt-in paired-tail call."""
+    env("SENGINE_AMD_TAIL", int(tail))
     p = sf.make_params(41, embed=384, depth=8, num_classes=1000)
     x = torch.randn(batch, 3, 224, 224, generator=torch.Generator().manual_seed(42))
     eng = SpikformerEngine(p, batch=batch, T=4, embed=384, heads=8, depth=8, in_hw=(224, 224), device=dev,
                            stream=stream)
+    assert eng.c2.tail == tail
     assert eng.N == 3136 and eng.final_planes == (5 if stream == "planes" else 0)
     eager = eng.forward(x.to(dev)).clone()
     eng.capture()
