@@ -219,13 +219,37 @@ __device__ __forceinline__ void fast_epilogue_stateless(const float4_t (&acc)[T]
 // spikes plus an fp16 residual, out, reading the folded BN coefficients from LDS where they are
 // used (16 registers instead of 48 held across the timesteps: the persistent kernels keep the
 // next step's operands live meanwhile).  Lanes with `valid` false compute but store nothing.
-template <int MODE, int OUT_ENC>
+// PRELOAD (fp16 output): the residual rows of all T steps are loaded before the first store --
+// one memory round trip per call instead of one per step (the rows may alias the output, so a
+// later step's load cannot move above an earlier step's store) -- and without a residual
+// stream the same loads read the lane's own output rows and are discarded (a uniform branch
+// around the loads would make the compiler's wait after the join cover the operand loads the
+// persistent kernels have in flight).  32 more registers: taken by the persistent 1x1 kernel
+// (Spikformer's proj and fc2 1-2 % faster), not by the direct-staged one (it would spill).
+template <int MODE, int OUT_ENC, bool PRELOAD = false>
 __device__ __forceinline__ void lean_epilogue_stateless(const float4_t (&acc)[4][4], bool valid, int m, int F, int cob,
                                                  const NeuronParams& np, const float* fsc, const float* fbi,
                                                  uint8_t* __restrict__ out, int M, const SewAdd& sa) {
   constexpr int T = 4;
+  constexpr bool PRE = PRELOAD && OUT_ENC == SENGINE_ENC_F16;
   // Spike bits take no SEW residual here (the callers route residual layers elsewhere).
   const SpikeDst sd = spike_dst(sa, out, F, cob);
+  half8_t rr[PRE ? T : 1][2];
+  if constexpr (PRE) {
+    const bool r16 = sa.res16 != nullptr;
+    const _Float16* src = r16 ? sa.res16 : reinterpret_cast<const _Float16*>(out);
+    const int mr = valid ? m : 0;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const half8_t* r = reinterpret_cast<const half8_t*>(src + ((size_t)t * M + mr) * F + cob);
+      rr[t][0] = r[0];
+      rr[t][1] = r[1];
+    }
+    if (!r16) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) rr[t][0] = rr[t][1] = half8_t{};
+    }
+  }
   float v[16];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -247,8 +271,18 @@ __device__ __forceinline__ void lean_epilogue_stateless(const float4_t (&acc)[4]
       }
     }
     if (!valid) continue;
-    if (OUT_ENC == SENGINE_ENC_BITS) {
+    if constexpr (OUT_ENC == SENGINE_ENC_BITS) {
       *reinterpret_cast<uint16_t*>(sd.out + ((((size_t)t * M + m) * sd.F + sd.cob) >> 3)) = (uint16_t)word;
+    } else if constexpr (PRE) {
+      half8_t o0 = rr[t][0], o1 = rr[t][1];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        o0[j] += (word >> j) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+        o1[j] += (word >> (8 + j)) & 1u ? (_Float16)1.0f : (_Float16)0.0f;
+      }
+      half8_t* dst = reinterpret_cast<half8_t*>(reinterpret_cast<_Float16*>(out) + ((size_t)t * M + m) * F + cob);
+      dst[0] = o0;
+      dst[1] = o1;
     } else {
       const uint32_t zr[kResWords] = {};
       store_spike_f16(word, ((size_t)t * M + m) * F + cob, out, sa, zr);

@@ -269,7 +269,7 @@ void fused_tile1ps_kernel(TileParams p, int npg, int nsb) {
           lean_epilogue_state<MODE, OUT_ENC>(acc[h], true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl],
                                              &sCoef[1][cl], p.out, p.M, p.sew, p.state);
         else
-          lean_epilogue_stateless<MODE, OUT_ENC>(acc[h], true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl],
+          lean_epilogue_stateless<MODE, OUT_ENC, true>(acc[h], true, m, p.F, G0 * 64 + g * 16, np, &sCoef[0][cl],
                                                  &sCoef[1][cl], p.out, p.M, p.sew);
       }
 #pragma unroll
