@@ -51,9 +51,12 @@ __device__ __forceinline__ half16_t expand_bits16(uint32_t x) {
   return __builtin_bit_cast(half16_t, r);
 }
 
-// Same for 8 bits -> 8 fp16 values (dense 16x16x32 B fragment).
+// Same for 8 bits -> 8 fp16 values (dense 16x16x32 B fragment).  X is hidden from the
+// optimizer: for an 8-bit x it would rewrite each X << k as a multiplication by a 30-bit
+// constant, which runs on the quarter-rate integer multiplier instead of two full-rate ops.
 __device__ __forceinline__ half8_t expand_bits8(uint32_t x) {
-  const uint32_t X = x | (x << 15);
+  uint32_t X = x | (x << 15);
+  asm("" : "+v"(X));
   u32x4_t r;
   r[0] = (X << 14) & 0x40004000u;
   r[1] = (X << 12) & 0x40004000u;

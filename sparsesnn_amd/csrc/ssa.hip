@@ -318,12 +318,21 @@ __global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits
       if (base + r * 256 < T * ntok) sq[base + r * 256] = qs[r];
   }
   __syncthreads();
+  // per-step strides, hoisted out of the tile loop (the loop otherwise recomputes the 32- and
+  // 64-bit products for every step, on the quarter-rate integer multiplier)
+  const size_t out_tstride = (size_t)p.B * p.N * p.C / 16;  // u16 words per timestep
+  uint16_t* const out_bh = p.out + ((size_t)b * p.N * p.C + h * D) / 16;
   for (int tile = tile0 + wave; tile < tile_end; tile += 4) {
     uint64_t qcur[T];
+    const uint64_t* sqt = sq + (tile - tile0) * 16 + c;
 #pragma unroll
-    for (int t = 0; t < T; ++t) qcur[t] = sq[t * ntok + (tile - tile0) * 16 + c];
+    for (int t = 0; t < T; ++t) {
+      qcur[t] = *sqt;
+      sqt += ntok;
+    }
     const int n = tile * 16 + c;  // this lane's token (MFMA column)
     const bool nvalid = n < p.N;
+    uint16_t* o = out_bh + (size_t)n * (p.C / 16);
     float v[JT][4];  // membrane per (j tile, row e)
 #pragma unroll
     for (int jt = 0; jt < JT; ++jt)
@@ -377,10 +386,10 @@ __global__ __launch_bounds__(256) void ssa_attend_kernel(SsaParams p, int splits
         word[jt] = nib | (n1 << 4) | (n2 << 8) | (n3 << 12);
       }
       if (g == 0 && nvalid) {
-        uint16_t* o = p.out + (((size_t)(t * p.B + b) * p.N + n) * p.C + h * D) / 16;
 #pragma unroll
         for (int jt = 0; jt < JT; ++jt) o[jt] = (uint16_t)word[jt];
       }
+      o += out_tstride;
     }
   }
 }
