@@ -58,24 +58,29 @@ constexpr int kSsaKvWaves = 16;
 // holds column c (bit l = row l's bit c).  Six butterfly stages swap the off-diagonal blocks of
 // every 2d x 2d block: at stage d, a lane with bit d clear keeps the low d bits of each 2d-bit
 // field and takes its partner's low d bits above them, a lane with bit d set keeps the high d
-// bits and takes its partner's high d bits below them.
+// bits and takes its partner's high d bits below them.  Branch-free: the partner's word rotated
+// left by d (bit d clear) or right by d (set) -- one v_alignbit with a per-lane amount -- has
+// the wanted bits where the lane does not keep its own, and the bits the rotation wraps around
+// fall where it does; one bit-select merges them (as two selects of whole expressions, the
+// stages compiled to divergent branches with the permute waits inside them).
 __device__ __forceinline__ uint64_t transpose64(uint64_t x, int lane) {
   uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
   {  // d = 32: whole words
     const bool up = lane & 32;
     const uint32_t r = (uint32_t)__shfl_xor((int)(up ? lo : hi), 32, 64);
-    if (up) lo = r;
-    else hi = r;
+    lo = up ? r : lo;
+    hi = up ? hi : r;
   }
   constexpr uint32_t kMask[5] = {0x0000ffffu, 0x00ff00ffu, 0x0f0f0f0fu, 0x33333333u, 0x55555555u};
 #pragma unroll
   for (int st = 0; st < 5; ++st) {
     const int d = 16 >> st;
-    const uint32_t m = kMask[st];
     const bool clear = (lane & d) == 0;
+    const uint32_t keep = clear ? kMask[st] : ~kMask[st];  // the lane's own bits
+    const uint32_t sh = clear ? 32u - d : (uint32_t)d;     // alignbit(x, x, sh): rotl by d or rotr by d
     const uint32_t plo = (uint32_t)__shfl_xor((int)lo, d, 64), phi = (uint32_t)__shfl_xor((int)hi, d, 64);
-    lo = clear ? ((lo & m) | ((plo << d) & ~m)) : ((lo & ~m) | ((plo >> d) & m));
-    hi = clear ? ((hi & m) | ((phi << d) & ~m)) : ((hi & ~m) | ((phi >> d) & m));
+    lo = (lo & keep) | (__builtin_amdgcn_alignbit(plo, plo, sh) & ~keep);
+    hi = (hi & keep) | (__builtin_amdgcn_alignbit(phi, phi, sh) & ~keep);
   }
   return ((uint64_t)hi << 32) | lo;
 }
